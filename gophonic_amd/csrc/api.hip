@@ -1,0 +1,72 @@
+// extern "C" entry points of libgphq: argument validation in the reference's
+// order, then dispatch to the kernels. Declarations and reference citations
+// are in include/gphq.h.
+#include "common.h"
+
+namespace gphq {
+int gemv_launch(int fmt, const void *codes, const void *scales, const float *x, float *y, int K, int N,
+                hipStream_t stream);
+
+static thread_local int g_last_hip_error = 0;
+void set_hip_error(hipError_t e) { g_last_hip_error = (int)e; }
+}  // namespace gphq
+
+using namespace gphq;
+
+extern "C" {
+
+const char *gphq_error_string(int status) {
+    switch (status) {
+    case GPHQ_OK:
+        return "";
+    case GPHQ_ERR_INVALID_DIMENSIONS:
+        return "q8gemv: invalid dimensions";
+    case GPHQ_ERR_INVALID_WEIGHT_LENGTH:
+        return "q8gemv: invalid weight length";
+    case GPHQ_ERR_DIMENSIONS:
+        return "q8gemm: invalid dimensions or buffer length";
+    case GPHQ_ERR_NON_FINITE:
+        return "q8gemm: non-finite row scale";
+    case GPHQ_ERR_HIP:
+        return "gphq: HIP runtime error";
+    case GPHQ_ERR_UNSUPPORTED:
+        return "gphq: unsupported format or mode";
+    }
+    return "gphq: unknown status";
+}
+
+int gphq_last_hip_error(void) { return g_last_hip_error; }
+
+const char *gphq_version(void) { return "0.1.0"; }
+
+int gphq_q8gemv_mul_into(const float *x, int64_t x_len, const int8_t *q, int64_t q_len, const float *scales,
+                         int64_t scales_len, float *dst, int64_t dst_len, int64_t k, int64_t n, void *stream) {
+    // q8gemv/q8gemv.go:19-28, same checks in the same order.
+    if (k < 0 || n < 0 || x_len != k || scales_len != n || dst_len != n) return GPHQ_ERR_INVALID_DIMENSIONS;
+    if (k == 0) {
+        if (q_len != 0) return GPHQ_ERR_INVALID_WEIGHT_LENGTH;
+    } else if (q_len % k != 0 || q_len / k != n) {
+        return GPHQ_ERR_INVALID_WEIGHT_LENGTH;
+    }
+    // Device limits of this implementation (int row and column indices).
+    if (k > INT32_MAX || n > INT32_MAX) return GPHQ_ERR_INVALID_DIMENSIONS;
+    if (n == 0) return GPHQ_OK;
+    if (!x && k) return GPHQ_ERR_INVALID_DIMENSIONS;
+    if (!dst || !scales) return GPHQ_ERR_INVALID_DIMENSIONS;
+    return gemv_launch(GPHQ_FMT_Q8, q, scales, x, dst, (int)k, (int)n, (hipStream_t)stream);
+}
+
+int gphq_gemv(int fmt, const void *codes, const void *scales, const float *x, float *y, int64_t k, int64_t n,
+              void *stream) {
+    if (fmt != GPHQ_FMT_Q8 && fmt != GPHQ_FMT_Q8B && fmt != GPHQ_FMT_Q8B_F32 && fmt != GPHQ_FMT_Q4)
+        return GPHQ_ERR_UNSUPPORTED;
+    if (k < 0 || n < 0 || k > INT32_MAX || n > INT32_MAX) return GPHQ_ERR_DIMENSIONS;
+    if (fmt != GPHQ_FMT_Q8 && k % 32 != 0) return GPHQ_ERR_DIMENSIONS;
+    if (n == 0) return GPHQ_OK;
+    if (!y || !scales || (k && (!codes || !x))) return GPHQ_ERR_DIMENSIONS;
+    if (fmt != GPHQ_FMT_Q8 && k && ((uintptr_t)codes % 16 != 0 || (uintptr_t)x % 16 != 0))
+        return GPHQ_ERR_DIMENSIONS;
+    return gemv_launch(fmt, codes, scales, x, y, (int)k, (int)n, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,99 @@
+/*
+ * gphq.h — C ABI of libgphq, the MI355X (gfx950) implementation of
+ * gophonic's quantized matrix-product hot path.
+ *
+ * Every entry point takes plain pointers and sizes. Pointers named *_dev are
+ * device (HBM) addresses; everything is enqueued on `stream` (a hipStream_t,
+ * NULL for the default stream) and is complete when the stream reaches it.
+ * Entry points validate all arguments before enqueueing anything, and return
+ * GPHQ_OK (0) or a negative GPHQ_ERR_* code; gphq_error_string() gives the
+ * reference's own message for each code so a binding can raise the same
+ * panic or error value.
+ *
+ * Reference paths cited below are relative to the gophonic source tree.
+ */
+#ifndef GPHQ_H
+#define GPHQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+#define GPHQ_OK 0
+/* q8gemv/q8gemv.go:19-21 panic "q8gemv: invalid dimensions" */
+#define GPHQ_ERR_INVALID_DIMENSIONS (-1)
+/* q8gemv/q8gemv.go:22-28 panic "q8gemv: invalid weight length" */
+#define GPHQ_ERR_INVALID_WEIGHT_LENGTH (-2)
+/* q8gemm/packed.go:26 ErrDimensions "q8gemm: invalid dimensions or buffer length" */
+#define GPHQ_ERR_DIMENSIONS (-3)
+/* q8gemm/packed.go:27 ErrNonFinite "q8gemm: non-finite row scale" */
+#define GPHQ_ERR_NON_FINITE (-4)
+/* a HIP runtime call failed; gphq_last_hip_error() holds its hipError_t */
+#define GPHQ_ERR_HIP (-5)
+/* the format / mode argument is not one this library implements */
+#define GPHQ_ERR_UNSUPPORTED (-6)
+
+/* The reference message for a status code ("" for GPHQ_OK). Static storage. */
+const char *gphq_error_string(int status);
+/* The hipError_t of the most recent GPHQ_ERR_HIP on the calling thread. */
+int gphq_last_hip_error(void);
+/* Library version, "major.minor.patch". */
+const char *gphq_version(void);
+
+/* ---- weight formats of the qwen3lm GPU path ------------------------------
+ * qwen3lm/gpu.metal:50-61 (enum Q4 = 4, Q8 = 8, Q8B = 9). All are row-major
+ * over output rows [N][K]:
+ *   GPHQ_FMT_Q8     int8 codes [N][K], one fp32 scale per row (scales f32[N]);
+ *                   qwen3lm/gpu_darwin.go:582-594 quantizeRow, and the
+ *                   q8gemv.MulInto contract (q8gemv/q8gemv.go:13-30).
+ *   GPHQ_FMT_Q8B    int8 codes [N][K], one FP16 scale per 32 values
+ *                   (scales f16[N][K/32]); gpu_darwin.go:599-614.
+ *   GPHQ_FMT_Q8B_F32 int8 codes [N][K], one fp32 scale per 32 values
+ *                   (scales f32[N][K/32]); the Q8B arithmetic with fp32 block
+ *                   scales (the benchmark configuration's layout; it has no
+ *                   counterpart format name in the reference).
+ *   GPHQ_FMT_Q4     4-bit codes [N][K/2]: per 32 values, 16 bytes with value j
+ *                   in the low nibble of byte j and value j+16 in the high
+ *                   nibble, both stored plus 8; one FP16 scale per 32 values
+ *                   (scales f16[N][K/32]); gpu_darwin.go:616-658 and the
+ *                   cmd/qwen3-gptq 4-bit output (qwen3lm/gptq.go:703-766).
+ */
+#define GPHQ_FMT_Q4 4
+#define GPHQ_FMT_Q8 8
+#define GPHQ_FMT_Q8B 9
+#define GPHQ_FMT_Q8B_F32 10
+
+/* ---- q8gemv ---------------------------------------------------------------
+ * Replaces q8gemv.MulInto (q8gemv/q8gemv.go:18-30):
+ *   dst[j] = dot(x, float32(q[j*k:(j+1)*k])) * scales[j]
+ * The *_len arguments are the Go slice lengths; the same checks as the
+ * reference run first, in the same order, returning
+ * GPHQ_ERR_INVALID_DIMENSIONS or GPHQ_ERR_INVALID_WEIGHT_LENGTH where it
+ * panics. k == 0 is allowed (dst = 0 * scales). Inputs must not overlap dst.
+ * fp32 sums are reassociated across the wavefront (the reference's own SIMD
+ * kernel also reassociates, q8gemv/q8gemv.go:7-10). No allocation. */
+int gphq_q8gemv_mul_into(const float *x_dev, int64_t x_len, const int8_t *q_dev, int64_t q_len,
+                         const float *scales_dev, int64_t scales_len, float *dst_dev,
+                         int64_t dst_len, int64_t k, int64_t n, void *stream);
+
+/* ---- qwen3lm GEMV family --------------------------------------------------
+ * Replaces the store-epilogue GEMV kernels of the Metal backend,
+ * gemv<PRO_PLAIN, EPI_STORE, BITS, HEAD> (qwen3lm/gpu.metal:68-162, used as
+ * gemv_head and by the projection stream,
+ * gpu_projection_stream_darwin_test.go:22-111), dispatched from
+ * gpuWorkspace.gemv (qwen3lm/gpu_darwin.go:1386-1404):
+ *   y[j] = sum_k dequant(W)[j,k] * x[k]
+ * fmt is a GPHQ_FMT_* value. Block formats need k % 32 == 0. Per 16 values
+ * (8-bit) or 32 values (4-bit) the partial dot product is scaled once, as in
+ * gpu.metal:88-123. Returns GPHQ_ERR_DIMENSIONS on a bad shape. */
+int gphq_gemv(int fmt, const void *codes_dev, const void *scales_dev, const float *x_dev,
+              float *y_dev, int64_t k, int64_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GPHQ_H */
