@@ -6,6 +6,8 @@
 namespace gphq {
 int gemv_launch(int fmt, const void *codes, const void *scales, const float *x, float *y, int K, int N,
                 hipStream_t stream);
+int gemv_batch_launch(int fmt, const void *const *codes, const void *const *scales, const float *const *x,
+                      float *const *y, int count, int K, int N, hipStream_t stream);
 
 static thread_local int g_last_hip_error = 0;
 void set_hip_error(hipError_t e) { g_last_hip_error = (int)e; }
@@ -67,6 +69,22 @@ int gphq_gemv(int fmt, const void *codes, const void *scales, const float *x, fl
     if (fmt != GPHQ_FMT_Q8 && k && ((uintptr_t)codes % 16 != 0 || (uintptr_t)x % 16 != 0))
         return GPHQ_ERR_DIMENSIONS;
     return gemv_launch(fmt, codes, scales, x, y, (int)k, (int)n, (hipStream_t)stream);
+}
+
+int gphq_gemv_batch(int fmt, const void *const *codes, const void *const *scales, const float *const *x,
+                    float *const *y, int count, int64_t k, int64_t n, void *stream) {
+    if (fmt != GPHQ_FMT_Q8 && fmt != GPHQ_FMT_Q8B && fmt != GPHQ_FMT_Q8B_F32 && fmt != GPHQ_FMT_Q4)
+        return GPHQ_ERR_UNSUPPORTED;
+    if (count < 0 || count > GPHQ_GEMV_MAX_BATCH) return GPHQ_ERR_DIMENSIONS;
+    if (k < 0 || n < 0 || k > INT32_MAX || n > INT32_MAX) return GPHQ_ERR_DIMENSIONS;
+    if (k % (fmt == GPHQ_FMT_Q8 ? 16 : 32) != 0) return GPHQ_ERR_DIMENSIONS;
+    if (n == 0 || count == 0) return GPHQ_OK;
+    if (!codes || !scales || !x || !y) return GPHQ_ERR_DIMENSIONS;
+    for (int i = 0; i < count; ++i) {
+        if (!y[i] || !scales[i] || (k && (!codes[i] || !x[i]))) return GPHQ_ERR_DIMENSIONS;
+        if (k && ((uintptr_t)codes[i] % 16 != 0 || (uintptr_t)x[i] % 16 != 0)) return GPHQ_ERR_DIMENSIONS;
+    }
+    return gemv_batch_launch(fmt, codes, scales, x, y, count, (int)k, (int)n, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1,33 +1,47 @@
 // GEMV over quantized weight rows: y = dequant(W) . x, fp32 activations.
 //
-// Design (gfx950): a 64-lane wavefront owns R consecutive output rows. Lane l
-// streams bytes [16l, 16l+16) of each 1024-byte K step of every owned row with
-// one 128-bit load (one wavefront instruction covers 1 KiB of a row,
-// contiguous), so a row is read exactly once and the weight stream is fully
-// coalesced. B K-steps of all R rows are issued before any arithmetic, which
-// puts R*B 128-bit loads per lane in flight; the int8 codes are widened to
-// fp32 in registers and multiplied by the fp32 activations, which are read
-// through the L1/L2 (every wavefront of the chip reads the same x). Lane
-// partial sums are reduced with DPP row permutes plus four readlanes, so no
-// LDS and no barrier sits on the path.
+// Design (gfx950, measured on MI355X): a block of WPB wavefronts is SK K-slices
+// x (WPB/SK) row groups of RW rows. Lane l of a wavefront streams bytes
+// [16l, 16l+16) of each 1024-value K step of its RW rows with one 128-bit
+// non-temporal load (one wavefront instruction = 1 KiB of one row,
+// contiguous; every weight byte is read once). The wavefront's slice of x is
+// loaded first, into registers, and reused for all RW rows, so x crosses the
+// vector memory pipe once per row group rather than once per row; x and the
+// block scales are requested before the weights because one wavefront's
+// loads return in issue order. Codes are widened to fp32 in registers
+// (v_cvt_f32_i32 with SDWA byte select) and multiplied by fp32 x. Lane
+// partials are reduced with DPP row permutes plus four readlanes; the SK
+// slice totals of a row meet in LDS and are added in slice order, so results
+// are deterministic.
 //
-// Block formats scale each 16-value chunk's partial sum once
-// (acc = fma(d, t, acc)), which is the qwen3lm Metal arithmetic
-// (gpu.metal:88-100); Q8 adds chunk sums and applies the row scale after the
-// reduction (gpu.metal:98-129, q8gemv/scalar.go:13-15). Q4 consumes one
-// 32-value block per lane step: acc = fma(d, sum(nib*x) - 8*sum(x), acc)
-// (gpu.metal:102-123).
+// One launch can run up to kMaxBatch independent GEMVs of the same shape
+// (grid.y = GEMV), the equivalent of encoding several projections into one
+// command buffer in the reference's projection stream
+// (qwen3lm/gpu_projection_stream_darwin_test.go:75-90).
+//
+// Arithmetic per format follows qwen3lm/gpu.metal:85-129: block formats scale
+// each 16-value chunk's partial sum once (acc = fma(d, t, acc)); Q8 adds chunk
+// sums and applies the row scale after the reduction (also q8gemv/scalar.go);
+// Q4 takes one 32-value block per lane step and computes
+// acc = fma(d, sum(nib*x) - 8*sum(x), acc).
 #include "common.h"
 
 namespace gphq {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-struct GemvArgs {
+constexpr int kMaxBatch = 32;
+
+struct GemvSet {
     const void *codes;
     const void *scales;
     const float *x;
     float *y;
+};
+
+template <int MAXB>
+struct GemvBatch {
+    GemvSet set[MAXB];
     int K;
     int N;
 };
@@ -37,7 +51,7 @@ __device__ __forceinline__ float sext_byte_f(uint32_t v, int i) {
 }
 
 // Dot product of 16 int8 codes (one 128-bit load) with 16 fp32 activations,
-// as four 4-wide dot products summed, in the order of gpu.metal:91-92.
+// as four 4-wide dot products summed (gpu.metal:91-92).
 __device__ __forceinline__ float dot16(const u32x4 w, const float4 x0, const float4 x1, const float4 x2,
                                        const float4 x3) {
     float d0 = sext_byte_f(w.x, 0) * x0.x + sext_byte_f(w.x, 1) * x0.y + sext_byte_f(w.x, 2) * x0.z +
@@ -60,177 +74,217 @@ __device__ __forceinline__ float block_scale(const void *scales, size_t idx) {
     }
 }
 
-// 8-bit codes (Q8, Q8B, Q8B_F32); requires K % 16 == 0 and 16-byte aligned
-// codes, so every row starts 16-byte aligned.
-template <int FMT, int R, int B>
-__global__ __launch_bounds__(256) void gemv8_kernel(GemvArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int row0 = wave * R;
-    if (row0 >= a.N) return;
-    const int K = a.K;
-    const int8_t *W = (const int8_t *)a.codes;
-    const size_t kb = (size_t)(K >> 5);
-    int rows[R];
+// Adds the SK slice totals of each row (in slice order) and stores y.
+template <int FMT, int ROWS, int SK>
+__device__ __forceinline__ void finish_rows(float (*part)[SK], const GemvSet &s, int rowBlock, int N) {
+    __syncthreads();
+    if ((int)threadIdx.x < ROWS) {
+        const int row = rowBlock + threadIdx.x;
+        if (row < N) {
+            float t = part[threadIdx.x][0];
 #pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = min(row0 + r, a.N - 1);
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-    for (int base = 0; base < K; base += 1024 * B) {
-        u32x4 w[B][R];
-        float d[B][R];
-#pragma unroll
-        for (int j = 0; j < B; ++j) {
-            const int k0 = base + j * 1024 + lane * 16;
-            const bool ok = k0 < K;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                w[j][r] = ok ? __builtin_nontemporal_load((const u32x4 *)(W + (size_t)rows[r] * K + k0))
-                             : u32x4{0, 0, 0, 0};
-                if constexpr (FMT != GPHQ_FMT_Q8)
-                    d[j][r] = ok ? block_scale<FMT>(a.scales, (size_t)rows[r] * kb + (k0 >> 5)) : 0.0f;
-            }
+            for (int i = 1; i < SK; ++i) t += part[threadIdx.x][i];
+            if constexpr (FMT == GPHQ_FMT_Q8) t = t * ((const float *)s.scales)[row];
+            s.y[row] = t;
         }
-#pragma unroll
-        for (int j = 0; j < B; ++j) {
-            const int k0 = base + j * 1024 + lane * 16;
-            if (k0 < K) {
-                const float4 *xv = (const float4 *)(a.x + k0);
-                const float4 x0 = xv[0], x1 = xv[1], x2 = xv[2], x3 = xv[3];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const float t = dot16(w[j][r], x0, x1, x2, x3);
-                    if constexpr (FMT == GPHQ_FMT_Q8)
-                        acc[r] += t;
-                    else
-                        acc[r] = fmaf(d[j][r], t, acc[r]);
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float s = wave_sum(acc[r]);
-        if constexpr (FMT == GPHQ_FMT_Q8) s = s * ((const float *)a.scales)[rows[r]];
-        if (lane == r && row0 + r < a.N) a.y[row0 + r] = s;
     }
 }
 
-// 4-bit split-nibble codes; requires K % 32 == 0. Lane l takes block
-// (step*64 + l): 16 code bytes and 32 activations.
-template <int R, int B>
-__global__ __launch_bounds__(256) void gemv4_kernel(GemvArgs a) {
+// 8-bit codes (Q8, Q8B, Q8B_F32). Requires K % 16 == 0, 16-byte aligned codes
+// and x (every row then starts 16-byte aligned).
+template <int FMT, int RW, int SK, int WPB, int MAXB>
+__global__ __launch_bounds__(64 * WPB) void gemv8_kernel(const GemvBatch<MAXB> b) {
+    constexpr int RG = WPB / SK;
+    __shared__ float part[RG * RW][SK];
+    const GemvSet s = b.set[blockIdx.y];
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int row0 = wave * R;
-    if (row0 >= a.N) return;
-    const int K = a.K;
-    const uint8_t *W = (const uint8_t *)a.codes;
+    const int wv = threadIdx.x >> 6;
+    const int rg = wv / SK, ks = wv % SK;
+    const int rowBlock = blockIdx.x * (RG * RW);
+    const int row0 = rowBlock + rg * RW;
+    const int K = b.K;
+    const int steps = (K + SK * 1024 - 1) / (SK * 1024);
+    const int8_t *W = (const int8_t *)s.codes;
+    const size_t kb = (size_t)(K >> 5);
+    int rows[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) rows[r] = min(row0 + r, b.N - 1);
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+
+    for (int st = 0; st < steps; ++st) {
+        const int k0 = (ks * steps + st) * 1024 + lane * 16;
+        const bool ok = k0 < K;
+        float4 xr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[i] = ok ? *((const float4 *)(s.x + k0) + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        float d[RW];
+        if constexpr (FMT != GPHQ_FMT_Q8) {
+#pragma unroll
+            for (int r = 0; r < RW; ++r) d[r] = ok ? block_scale<FMT>(s.scales, (size_t)rows[r] * kb + (k0 >> 5)) : 0.0f;
+        }
+        u32x4 w[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+            w[r] = ok ? __builtin_nontemporal_load((const u32x4 *)(W + (size_t)rows[r] * K + k0)) : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            const float t = dot16(w[r], xr[0], xr[1], xr[2], xr[3]);
+            if constexpr (FMT == GPHQ_FMT_Q8)
+                acc[r] += t;
+            else
+                acc[r] = fmaf(d[r], t, acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const float t = wave_sum(acc[r]);
+        if (lane == 0) part[rg * RW + r][ks] = t;
+    }
+    finish_rows<FMT, RG * RW, SK>(part, s, rowBlock, b.N);
+}
+
+// 4-bit split-nibble codes; requires K % 32 == 0. Lane l takes the 32-value
+// block (step * 64 + l): 16 code bytes and 32 activations.
+template <int RW, int SK, int WPB, int MAXB>
+__global__ __launch_bounds__(64 * WPB) void gemv4_kernel(const GemvBatch<MAXB> b) {
+    constexpr int RG = WPB / SK;
+    __shared__ float part[RG * RW][SK];
+    const GemvSet s = b.set[blockIdx.y];
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int rg = wv / SK, ks = wv % SK;
+    const int rowBlock = blockIdx.x * (RG * RW);
+    const int row0 = rowBlock + rg * RW;
+    const int K = b.K;
+    const int steps = (K + SK * 2048 - 1) / (SK * 2048);
+    const uint8_t *W = (const uint8_t *)s.codes;
     const size_t kb = (size_t)(K >> 5);
     const size_t rowBytes = (size_t)(K >> 1);
-    int rows[R];
+    int rows[RW];
 #pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = min(row0 + r, a.N - 1);
-    float acc[R];
+    for (int r = 0; r < RW; ++r) rows[r] = min(row0 + r, b.N - 1);
+    float acc[RW];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
 
-    for (int base = 0; base < K; base += 2048 * B) {
-        u32x4 w[B][R];
-        float d[B][R];
+    for (int st = 0; st < steps; ++st) {
+        const int k0 = (ks * steps + st) * 2048 + lane * 32;
+        const bool ok = k0 < K;
+        float4 xs[8];
 #pragma unroll
-        for (int j = 0; j < B; ++j) {
-            const int k0 = base + j * 2048 + lane * 32;
-            const bool ok = k0 < K;
+        for (int i = 0; i < 8; ++i) xs[i] = ok ? *((const float4 *)(s.x + k0) + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        float d[RW];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                w[j][r] = ok ? __builtin_nontemporal_load((const u32x4 *)(W + (size_t)rows[r] * rowBytes + (k0 >> 1)))
-                             : u32x4{0, 0, 0, 0};
-                d[j][r] = ok ? block_scale<GPHQ_FMT_Q4>(a.scales, (size_t)rows[r] * kb + (k0 >> 5)) : 0.0f;
-            }
-        }
+        for (int r = 0; r < RW; ++r) d[r] = ok ? block_scale<GPHQ_FMT_Q4>(s.scales, (size_t)rows[r] * kb + (k0 >> 5)) : 0.0f;
+        u32x4 w[RW];
 #pragma unroll
-        for (int j = 0; j < B; ++j) {
-            const int k0 = base + j * 2048 + lane * 32;
-            if (k0 < K) {
-                const float4 *xv = (const float4 *)(a.x + k0);
-                float4 xs[8];
+        for (int r = 0; r < RW; ++r)
+            w[r] = ok ? __builtin_nontemporal_load((const u32x4 *)(W + (size_t)rows[r] * rowBytes + (k0 >> 1)))
+                      : u32x4{0, 0, 0, 0};
+        const float4 s4 = xs[0] + xs[1] + xs[2] + xs[3] + xs[4] + xs[5] + xs[6] + xs[7];
+        const float sx = (s4.x + s4.y + s4.z + s4.w) * 8.0f;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) xs[i] = xv[i];
-                float4 s4 = xs[0] + xs[1] + xs[2] + xs[3] + xs[4] + xs[5] + xs[6] + xs[7];
-                const float sx = (s4.x + s4.y + s4.z + s4.w) * 8.0f;
+        for (int r = 0; r < RW; ++r) {
+            const uint32_t ww[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const uint32_t ww[4] = {w[j][r].x, w[j][r].y, w[j][r].z, w[j][r].w};
-                    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            const uint32_t q = (ww[c] >> (4 * h)) & 0x0F0F0F0Fu;
-                            const float4 xv4 = xs[4 * h + c];
-                            t.x = fmaf((float)(q & 0xff), xv4.x, t.x);
-                            t.y = fmaf((float)((q >> 8) & 0xff), xv4.y, t.y);
-                            t.z = fmaf((float)((q >> 16) & 0xff), xv4.z, t.z);
-                            t.w = fmaf((float)(q >> 24), xv4.w, t.w);
-                        }
-                    }
-                    acc[r] = fmaf(d[j][r], (t.x + t.y + t.z + t.w) - sx, acc[r]);
+                for (int c = 0; c < 4; ++c) {
+                    const uint32_t q = (ww[c] >> (4 * h)) & 0x0F0F0F0Fu;
+                    const float4 xv4 = xs[4 * h + c];
+                    t.x = fmaf((float)(q & 0xff), xv4.x, t.x);
+                    t.y = fmaf((float)((q >> 8) & 0xff), xv4.y, t.y);
+                    t.z = fmaf((float)((q >> 16) & 0xff), xv4.z, t.z);
+                    t.w = fmaf((float)(q >> 24), xv4.w, t.w);
                 }
             }
+            acc[r] = fmaf(d[r], (t.x + t.y + t.z + t.w) - sx, acc[r]);
         }
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const float s = wave_sum(acc[r]);
-        if (lane == r && row0 + r < a.N) a.y[row0 + r] = s;
+    for (int r = 0; r < RW; ++r) {
+        const float t = wave_sum(acc[r]);
+        if (lane == 0) part[rg * RW + r][ks] = t;
     }
+    finish_rows<GPHQ_FMT_Q4, RG * RW, SK>(part, s, rowBlock, b.N);
 }
 
 // Any K, any alignment (Q8 only): one wavefront per row, lanes stride through
 // the row one code at a time. Used for shapes the vector path cannot take.
-__global__ __launch_bounds__(256) void gemv8_generic_kernel(GemvArgs a) {
+__global__ __launch_bounds__(256) void gemv8_generic_kernel(const GemvBatch<1> b) {
+    const GemvSet s = b.set[0];
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= a.N) return;
-    const int8_t *w = (const int8_t *)a.codes + (size_t)row * a.K;
+    if (row >= b.N) return;
+    const int8_t *w = (const int8_t *)s.codes + (size_t)row * b.K;
     float acc = 0.0f;
-    for (int k = lane; k < a.K; k += 64) acc = fmaf(a.x[k], (float)w[k], acc);
-    const float s = wave_sum(acc) * ((const float *)a.scales)[row];
-    if (lane == 0) a.y[row] = s;
+    for (int k = lane; k < b.K; k += 64) acc = fmaf(s.x[k], (float)w[k], acc);
+    const float t = wave_sum(acc) * ((const float *)s.scales)[row];
+    if (lane == 0) s.y[row] = t;
 }
 
-template <typename Kern>
-static int launch_rows(Kern kern, const GemvArgs &a, int rowsPerWave, hipStream_t stream) {
-    const int wavesPerBlock = 4;
-    const long waves = ((long)a.N + rowsPerWave - 1) / rowsPerWave;
-    const long blocks = (waves + wavesPerBlock - 1) / wavesPerBlock;
-    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * wavesPerBlock), 0, stream, a);
+// Tile geometry (measured on MI355X at 4096x4096): 4 rows per wavefront,
+// K split in 2 slices, 8 wavefronts per block = 16 rows per block.
+constexpr int kRW = 4, kSK = 2, kWPB = 8;
+constexpr int kRowsPerBlock = (kWPB / kSK) * kRW;
+// Q4: 2 rows per wavefront (32 activations per lane per step), 4 slices.
+constexpr int kRW4 = 2, kSK4 = 4, kWPB4 = 8;
+constexpr int kRowsPerBlock4 = (kWPB4 / kSK4) * kRW4;
+
+template <int MAXB>
+static int launch_batch(int fmt, const GemvBatch<MAXB> &b, int count, hipStream_t stream) {
+    const unsigned rowsPerBlock = fmt == GPHQ_FMT_Q4 ? kRowsPerBlock4 : kRowsPerBlock;
+    const dim3 grid((unsigned)((b.N + rowsPerBlock - 1) / rowsPerBlock), (unsigned)count);
+    switch (fmt) {
+    case GPHQ_FMT_Q8:
+        hipLaunchKernelGGL((gemv8_kernel<GPHQ_FMT_Q8, kRW, kSK, kWPB, MAXB>), grid, dim3(64 * kWPB), 0, stream, b);
+        break;
+    case GPHQ_FMT_Q8B:
+        hipLaunchKernelGGL((gemv8_kernel<GPHQ_FMT_Q8B, kRW, kSK, kWPB, MAXB>), grid, dim3(64 * kWPB), 0, stream, b);
+        break;
+    case GPHQ_FMT_Q8B_F32:
+        hipLaunchKernelGGL((gemv8_kernel<GPHQ_FMT_Q8B_F32, kRW, kSK, kWPB, MAXB>), grid, dim3(64 * kWPB), 0, stream,
+                           b);
+        break;
+    case GPHQ_FMT_Q4:
+        hipLaunchKernelGGL((gemv4_kernel<kRW4, kSK4, kWPB4, MAXB>), grid, dim3(64 * kWPB4), 0, stream, b);
+        break;
+    default:
+        return GPHQ_ERR_UNSUPPORTED;
+    }
     return launch_status();
 }
 
-// Chooses a kernel for (fmt, K, N). All arguments were validated by the caller.
+// One GEMV. Arguments were validated by the caller.
 int gemv_launch(int fmt, const void *codes, const void *scales, const float *x, float *y, int K, int N,
                 hipStream_t stream) {
     if (N == 0) return GPHQ_OK;
-    GemvArgs a{codes, scales, x, y, K, N};
-    constexpr int R = 2, B = 4;
-    switch (fmt) {
-    case GPHQ_FMT_Q8: {
+    GemvBatch<1> b{};
+    b.set[0] = GemvSet{codes, scales, x, y};
+    b.K = K;
+    b.N = N;
+    if (fmt == GPHQ_FMT_Q8) {
         const bool vec = (K % 16 == 0) && ((uintptr_t)codes % 16 == 0) && ((uintptr_t)x % 16 == 0);
-        if (!vec) return launch_rows(gemv8_generic_kernel, a, 1, stream);
-        return launch_rows(gemv8_kernel<GPHQ_FMT_Q8, R, B>, a, R, stream);
+        if (!vec) {
+            hipLaunchKernelGGL(gemv8_generic_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, b);
+            return launch_status();
+        }
     }
-    case GPHQ_FMT_Q8B:
-        return launch_rows(gemv8_kernel<GPHQ_FMT_Q8B, R, B>, a, R, stream);
-    case GPHQ_FMT_Q8B_F32:
-        return launch_rows(gemv8_kernel<GPHQ_FMT_Q8B_F32, R, B>, a, R, stream);
-    case GPHQ_FMT_Q4:
-        return launch_rows(gemv4_kernel<R, 2>, a, R, stream);
-    }
-    return GPHQ_ERR_UNSUPPORTED;
+    return launch_batch<1>(fmt, b, 1, stream);
+}
+
+// Up to kMaxBatch GEMVs of one shape and format in one launch.
+int gemv_batch_launch(int fmt, const void *const *codes, const void *const *scales, const float *const *x,
+                      float *const *y, int count, int K, int N, hipStream_t stream) {
+    if (N == 0 || count == 0) return GPHQ_OK;
+    GemvBatch<kMaxBatch> b{};
+    for (int i = 0; i < count; ++i) b.set[i] = GemvSet{codes[i], scales[i], x[i], y[i]};
+    b.K = K;
+    b.N = N;
+    return launch_batch<kMaxBatch>(fmt, b, count, stream);
 }
 
 }  // namespace gphq

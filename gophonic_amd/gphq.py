@@ -24,6 +24,7 @@ FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
+_vpp = ctypes.POINTER(ctypes.c_void_p)
 
 # name -> (restype, argtypes); every symbol include/gphq.h declares.
 SIGNATURES = {
@@ -32,7 +33,10 @@ SIGNATURES = {
     "gphq_version": (ctypes.c_char_p, []),
     "gphq_q8gemv_mul_into": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "gphq_gemv": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "gphq_gemv_batch": (ctypes.c_int, [ctypes.c_int, _vpp, _vpp, _vpp, _vpp, ctypes.c_int, _i64, _i64, _vp]),
 }
+
+GEMV_MAX_BATCH = 32
 
 
 class GphqError(RuntimeError):
@@ -99,3 +103,23 @@ def q8gemv_mul_into(x, q, scales, dst, k, n, stream=None):
 def gemv(fmt, codes, scales, x, y, k, n, stream=None):
     """qwen3lm gemv<PRO_PLAIN, EPI_STORE, fmt> (gpu.metal:68-162)."""
     return check(load().gphq_gemv(fmt, ptr(codes), ptr(scales), ptr(x), ptr(y), k, n, stream_handle(stream)))
+
+
+def _ptr_array(ts):
+    arr = (ctypes.c_void_p * max(1, len(ts)))()
+    for i, t in enumerate(ts):
+        arr[i] = ptr(t)
+    return arr
+
+
+def gemv_batch(fmt, codes, scales, xs, ys, k, n, stream=None):
+    """Several qwen3lm gemv dispatches of one shape in one launch (gphq_gemv_batch)."""
+    count = len(codes)
+    if not (len(scales) == len(xs) == len(ys) == count):
+        raise ValueError("gemv_batch: list lengths differ")
+    return check(
+        load().gphq_gemv_batch(
+            fmt, _ptr_array(codes), _ptr_array(scales), _ptr_array(xs), _ptr_array(ys), count, k, n,
+            stream_handle(stream),
+        )
+    )

@@ -210,3 +210,34 @@ def test_gemv_does_not_write_past_n():
     out = host(y)
     assert np.all(out[n:] == -7.0)
     assert np.isfinite(out[:n]).all()
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("count", [1, 5, 32])
+def test_gemv_batch_bit_identical_to_single(fmt, count):
+    # One launch over `count` independent GEMVs gives each one exactly the
+    # bits of its own gphq_gemv call (same per-GEMV arithmetic).
+    import torch
+
+    rng = np.random.default_rng(100 + count + fmt)
+    k, n = 1024, 80
+    sets = [make_block_weights(fmt, rng, n, k) for _ in range(count)]
+    xs = [dev(rng.standard_normal(k).astype(np.float32)) for _ in range(count)]
+    codes = [dev(c) for c, _ in sets]
+    scales = [dev(s) for _, s in sets]
+    ys = [empty_f32(n) for _ in range(count)]
+    gphq.gemv_batch(fmt, codes, scales, xs, ys, k, n)
+    for i in range(count):
+        single = empty_f32(n)
+        gphq.gemv(fmt, codes[i], scales[i], xs[i], single, k, n)
+        assert np.array_equal(host(single).view(np.uint32), host(ys[i]).view(np.uint32)), i
+        y64, _ = orc.gemv_f64(fmt, sets[i][0], sets[i][1], host(xs[i]), k, n)
+        assert rel_l2(host(ys[i]), y64) <= 1e-5
+
+
+def test_gemv_batch_rejects_bad_counts():
+    import torch
+
+    t = torch.zeros(64, device="cuda")
+    with pytest.raises(gphq.GphqError):
+        gphq.gemv_batch(orc.FMT_Q8B, [t] * 33, [t] * 33, [t] * 33, [t] * 33, 32, 2)
