@@ -1,0 +1,313 @@
+// int8 x int8 GEMM with exact int32 accumulation (q8gemm MulPanelsI8 /
+// MulStripsI8 semantics, q8gemm/int8.go:170-253):
+//   dst[m*stride + n] = (float32(sum_k qa[m,k]*qw[n,k]) * colScale[n]) * rowScale[m]
+// and the per-row activation quantizer of WorkspaceI8 (int8.go:100-168).
+//
+// Device layout ("tile layout"): an R x K int8 matrix is stored as
+// [ceil(R/16)][ceil(K/64)][64 lanes][16 bytes]; lane l of group (rt, kt) holds
+// row rt*16 + l%16, columns kt*64 + (l/16)*16 .. +16. One 1 KiB group is one
+// operand fragment of v_mfma_i32_16x16x64_i8 for both A (rows = activation
+// rows) and B (rows = weight rows / output columns), so every fragment load is
+// a single contiguous 1 KiB wavefront load. Padding (rows past R, K past the
+// logical K) is zero in the weights, so padded K never changes a sum.
+//
+// GEMM: a block is WM x WN x SK wavefronts; wavefront (wm, wn, ks) owns a
+// (16*TM) x (16*TN) output tile and the ks-th slice of the K tiles. It loads
+// U K-steps of A and B fragments straight from HBM/L2 into registers, then
+// issues TM*TN MFMAs per step. With SK > 1 the int32 partial tiles are added
+// in LDS (exact, so any split gives identical bits). The epilogue converts
+// int32 -> fp32 (round to nearest even, like Go's float32(int32)) and applies
+// the two scale multiplies in the reference's order. Blocks are renumbered so
+// that consecutive blocks on one XCD share a weight column tile, which is then
+// read from HBM once into that XCD's L2.
+#include "common.h"
+
+namespace gphq {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+__host__ __device__ inline size_t tile_offset(long r, long k, long kt) {
+    return ((size_t)(r >> 4) * kt + (k >> 6)) * 1024 + (size_t)((((k & 63) >> 4) << 4) + (r & 15)) * 16 + (k & 15);
+}
+
+// ---- weight packing: row-major int8 [rows][K] -> tile layout ---------------
+// One thread per 16-byte lane chunk of the destination; rows past `rows`
+// (inside the last 16-row tile) and K padding are written as zero.
+__global__ void i8_pack_tiles_kernel(const int8_t *__restrict__ src, int8_t *__restrict__ dst, int rows, int K,
+                                     int row0, int rowTiles, int kt) {
+    const size_t chunk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // 16-byte chunk index
+    const size_t total = (size_t)rowTiles * kt * 64;
+    if (chunk >= total) return;
+    const int lane = (int)(chunk & 63);
+    const size_t g = chunk >> 6;
+    const int ktile = (int)(g % kt);
+    const int rtile = (int)(g / kt) + (row0 >> 4);
+    const int r = rtile * 16 + (lane & 15);  // absolute row
+    const int kbase = ktile * 64 + (lane >> 4) * 16;
+    int8_t v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int k = kbase + i;
+        const int rr = r - row0;
+        v[i] = (rr >= 0 && rr < rows && k < K) ? src[(size_t)rr * K + k] : (int8_t)0;
+    }
+    int8_t *d = dst + ((size_t)rtile * kt + ktile) * 1024 + (size_t)lane * 16;
+    // Rows outside [row0, row0+rows) of a shared tile keep their bytes.
+    const int rr = r - row0;
+    if (rr >= 0 && rr < rows) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d[i] = v[i];
+    }
+}
+
+// ---- activation quantizer ---------------------------------------------------
+// quantize (int8.go:163-168): round half to even, saturate; a NaN (x * 0 for a
+// non-finite row) converts to 0, as Go's float->int8 conversion does on amd64
+// and arm64.
+__device__ __forceinline__ int8_t quantize_i8(float v) {
+    if (v != v) return 0;
+    const float r = rintf(v);
+    return (int8_t)fminf(fmaxf(r, -128.0f), 127.0f);
+}
+
+// SetRowScale (int8.go:106-112): max/127 and 127/max for finite positive max,
+// else 0 and 0. fp32 division is correctly rounded (hipcc default).
+__device__ __forceinline__ void i8_row_scale(float m, float &scale, float &inv) {
+    if (m > 0.0f && !isinf(m) && m == m) {
+        scale = m / 127.0f;
+        inv = 127.0f / m;
+    } else {
+        scale = 0.0f;
+        inv = 0.0f;
+    }
+}
+
+// Workspace Pack fused: per row (one block each), MaxAbs with NaN propagation
+// (gemm.go:138-150), SetRowScale, then quantize every column into the tile
+// layout (and zero the row's K padding).
+__global__ __launch_bounds__(256) void i8_pack_rows_kernel(const float *__restrict__ x, long stride, int K, int kt,
+                                                           int8_t *__restrict__ act, float *__restrict__ rowScale,
+                                                           float *__restrict__ rowInv) {
+    __shared__ float smax[4];
+    __shared__ int snan[4];
+    const int row = blockIdx.x;
+    const float *xr = x + (size_t)row * stride;
+    float m = 0.0f;
+    int nan = 0;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        const float v = xr[k];
+        nan |= (v != v);
+        m = fmaxf(m, fabsf(v));
+    }
+    // wave max / nan-any
+    for (int off = 32; off > 0; off >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, off));
+        nan |= __shfl_xor(nan, off);
+    }
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        smax[wv] = m;
+        snan[wv] = nan;
+    }
+    __syncthreads();
+    float mm = 0.0f;
+    int anyNan = 0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) {
+        mm = fmaxf(mm, smax[i]);
+        anyNan |= snan[i];
+    }
+    if (anyNan) mm = __builtin_nanf("");
+    float scale, inv;
+    i8_row_scale(mm, scale, inv);
+    if (threadIdx.x == 0) {
+        rowScale[row] = scale;
+        rowInv[row] = inv;
+    }
+    for (int k = threadIdx.x; k < kt * 64; k += blockDim.x) {
+        const int8_t q = k < K ? quantize_i8(__fmul_rn(xr[k], inv)) : (int8_t)0;
+        act[tile_offset(row, k, kt)] = q;
+    }
+}
+
+// PackRange (int8.go:116-163) with row scales already set: quantize columns
+// [k0, k1) of every prepared row; k1 == K also zeroes the K padding.
+__global__ __launch_bounds__(256) void i8_pack_range_kernel(const float *__restrict__ x, long stride, int K, int kt,
+                                                            int k0, int k1, int8_t *__restrict__ act,
+                                                            const float *__restrict__ rowInv) {
+    const int row = blockIdx.x;
+    const float inv = rowInv[row];
+    const float *xr = x + (size_t)row * stride;
+    const int kend = (k1 == K) ? kt * 64 : k1;
+    for (int k = k0 + threadIdx.x; k < kend; k += blockDim.x) {
+        const int8_t q = k < K ? quantize_i8(__fmul_rn(xr[k], inv)) : (int8_t)0;
+        act[tile_offset(row, k, kt)] = q;
+    }
+}
+
+// ---- GEMM ------------------------------------------------------------------
+struct I8GemmArgs {
+    const int8_t *A;      // activations, tile layout, MT x KT groups
+    const int8_t *B;      // weights, tile layout, NT x KT groups
+    const float *rowScale;  // [M]
+    const float *colScale;  // [N]
+    float *dst;
+    long stride;
+    int M, N, KT, NT;
+    int c0, c1;  // output columns [c0, c1)
+    int tileN0;  // first 16-column tile covered by the grid
+    int gridM, gridN;  // blocks along M and N
+};
+
+template <int TM, int TN, int WM, int WN, int SK, int U>
+__global__ __launch_bounds__(64 * WM * WN * SK) void i8gemm_kernel(const I8GemmArgs a) {
+    constexpr int NW = WM * WN * SK;
+    __shared__ i32x4 red[(SK > 1) ? (NW * TM * TN * 64) : 1];
+    // XCD-aware renumbering: hardware places block b on XCD b % 8. Give the
+    // blocks of one XCD consecutive logical ids, M fastest, so they share
+    // weight column tiles.
+    const int G = a.gridM * a.gridN;
+    const int b = blockIdx.x;
+    int logical = b;
+    if (G % 8 == 0) logical = (b % 8) * (G / 8) + b / 8;
+    const int bm = logical % a.gridM, bn = logical / a.gridM;
+
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int ks = wv % SK;
+    const int wn = (wv / SK) % WN;
+    const int wm = wv / (SK * WN);
+    const int mt0 = (bm * WM + wm) * TM;                      // first 16-row tile
+    const int nt0 = a.tileN0 + (bn * WN + wn) * TN;           // first 16-col tile
+    const int MT = (a.M + 15) >> 4;
+    const int KT = a.KT;
+    const int per = (KT + SK - 1) / SK;
+    const int kt0 = ks * per, kt1 = min(KT, kt0 + per);
+
+    size_t aoff[TM], boff[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) aoff[i] = (size_t)min(mt0 + i, MT - 1) * KT * 1024 + (size_t)lane * 16;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) boff[j] = (size_t)min(nt0 + j, a.NT - 1) * KT * 1024 + (size_t)lane * 16;
+
+    i32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+
+    for (int kt = kt0; kt < kt1; kt += U) {
+        i32x4 fa[U][TM], fb[U][TN];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool ok = kt + u < kt1;
+            const size_t ko = (size_t)(kt + u) * 1024;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                fa[u][i] = ok ? *(const i32x4 *)(a.A + aoff[i] + ko) : i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                fb[u][j] = ok ? __builtin_nontemporal_load((const i32x4 *)(a.B + boff[j] + ko)) : i32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][i], fb[u][j], acc[i][j], 0, 0, 0);
+    }
+
+    if constexpr (SK > 1) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) red[((wv * TM + i) * TN + j) * 64 + lane] = acc[i][j];
+        __syncthreads();
+        if (ks != 0) return;
+#pragma unroll
+        for (int s = 1; s < SK; ++s)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] += red[(((wv + s) * TM + i) * TN + j) * 64 + lane];
+    }
+
+    // Epilogue. Lane l of a 16x16 output tile holds rows 4*(l/16)+e, column l%16.
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        if (col < a.c0 || col >= a.c1) continue;
+        const float cs = a.colScale[col];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
+                if (row < a.M) {
+                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row]);
+                    a.dst[(size_t)row * a.stride + col] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int TM, int TN, int WM, int WN, int SK, int U>
+static int launch_i8gemm(I8GemmArgs a, hipStream_t stream) {
+    const int tiles = (a.c1 + 15) / 16 - a.tileN0;
+    a.gridN = (tiles + TN * WN - 1) / (TN * WN);
+    a.gridM = (a.M + 16 * TM * WM - 1) / (16 * TM * WM);
+    const unsigned blocks = (unsigned)(a.gridM * a.gridN);
+    hipLaunchKernelGGL((i8gemm_kernel<TM, TN, WM, WN, SK, U>), dim3(blocks), dim3(64 * WM * WN * SK), 0, stream, a);
+    return launch_status();
+}
+
+// Columns [c0, c1) of dst for M activation rows. Chooses a tile shape by M;
+// every shape gives identical bits (exact int32 sums, same epilogue).
+int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const float *colScale, float *dst,
+                  long stride, int M, int N, int KT, int c0, int c1, hipStream_t stream) {
+    if (M == 0 || c0 >= c1) return GPHQ_OK;
+    I8GemmArgs a{};
+    a.A = A;
+    a.B = B;
+    a.rowScale = rowScale;
+    a.colScale = colScale;
+    a.dst = dst;
+    a.stride = stride;
+    a.M = M;
+    a.N = N;
+    a.KT = KT;
+    a.NT = (N + 15) / 16;
+    a.c0 = c0;
+    a.c1 = c1;
+    a.tileN0 = c0 / 16;
+    if (M <= 16) return launch_i8gemm<1, 1, 1, 2, 4, 8>(a, stream);
+    if (M <= 64) return launch_i8gemm<4, 1, 1, 2, 4, 4>(a, stream);
+    if (M <= 192) return launch_i8gemm<2, 2, 2, 2, 1, 4>(a, stream);
+    return launch_i8gemm<4, 4, 2, 2, 1, 2>(a, stream);
+}
+
+int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {
+    if (rows == 0) return GPHQ_OK;
+    const int rowTiles = ((row0 + rows + 15) >> 4) - (row0 >> 4);
+    const size_t chunks = (size_t)rowTiles * kt * 64;
+    hipLaunchKernelGGL(i8_pack_tiles_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, src, dst,
+                       rows, K, row0, rowTiles, kt);
+    return launch_status();
+}
+
+int i8_pack_rows(const float *x, long stride, int rows, int K, int kt, int8_t *act, float *rowScale, float *rowInv,
+                 hipStream_t stream) {
+    if (rows == 0) return GPHQ_OK;
+    hipLaunchKernelGGL(i8_pack_rows_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, act, rowScale, rowInv);
+    return launch_status();
+}
+
+int i8_pack_range(const float *x, long stride, int rows, int K, int kt, int k0, int k1, int8_t *act,
+                  const float *rowInv, hipStream_t stream) {
+    if (rows == 0 || (k0 == k1 && k1 != K)) return GPHQ_OK;
+    hipLaunchKernelGGL(i8_pack_range_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, k0, k1, act, rowInv);
+    return launch_status();
+}
+
+}  // namespace gphq

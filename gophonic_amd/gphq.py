@@ -25,6 +25,7 @@ FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
 _vpp = ctypes.POINTER(ctypes.c_void_p)
+_i64p = ctypes.POINTER(ctypes.c_int64)
 
 # name -> (restype, argtypes); every symbol include/gphq.h declares.
 SIGNATURES = {
@@ -34,6 +35,23 @@ SIGNATURES = {
     "gphq_q8gemv_mul_into": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "gphq_gemv": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "gphq_gemv_batch": (ctypes.c_int, [ctypes.c_int, _vpp, _vpp, _vpp, _vpp, ctypes.c_int, _i64, _i64, _vp]),
+    "gphq_q8gemm_new_weights_i8": (ctypes.c_int, [_i64, _i64, _vpp]),
+    "gphq_q8gemm_weights_i8_free": (None, [_vp]),
+    "gphq_q8gemm_weights_i8_pack": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64]),
+    "gphq_q8gemm_weights_i8_pack_rows": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _i64]),
+    "gphq_q8gemm_weights_i8_dims": (ctypes.c_int, [_vp, _i64p, _i64p]),
+    "gphq_q8gemm_weights_i8_panels": (_i64, [_vp]),
+    "gphq_q8gemm_weights_i8_strips": (_i64, [_vp]),
+    "gphq_q8gemm_weights_i8_bytes": (_i64, [_vp]),
+    "gphq_q8gemm_new_workspace_i8": (ctypes.c_int, [_i64, _i64, _vpp]),
+    "gphq_q8gemm_workspace_i8_free": (None, [_vp]),
+    "gphq_q8gemm_workspace_i8_prepare": (ctypes.c_int, [_vp, _i64, _i64]),
+    "gphq_q8gemm_workspace_i8_set_row_scale": (ctypes.c_int, [_vp, _i64, ctypes.c_float]),
+    "gphq_q8gemm_workspace_i8_pack_range": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "gphq_q8gemm_workspace_i8_pack": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "gphq_q8gemm_workspace_i8_row_scales": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
+    "gphq_q8gemm_mul_panels_i8": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp]),
+    "gphq_q8gemm_mul_strips_i8": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp]),
 }
 
 GEMV_MAX_BATCH = 32
@@ -56,6 +74,12 @@ def load():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: run `python -m gophonic_amd.build` first")
+        # torch ships its own libamdhip64.so.7 (same soname as /opt/rocm's).
+        # The first one loaded serves the whole process, so load torch's before
+        # libgphq: the binding hands torch streams and device pointers to the
+        # library, and both sides must then talk to one HIP runtime.
+        import torch  # noqa: F401
+
         lib = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)
@@ -123,3 +147,108 @@ def gemv_batch(fmt, codes, scales, xs, ys, k, n, stream=None):
             stream_handle(stream),
         )
     )
+
+
+def _host(a, dtype):
+    import numpy as np
+
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a, a.ctypes.data
+
+
+class WeightsI8:
+    """q8gemm.WeightsI8 (int8.go:13-77), device resident."""
+
+    def __init__(self, k, n):
+        h = ctypes.c_void_p()
+        check(load().gphq_q8gemm_new_weights_i8(k, n, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            load().gphq_q8gemm_weights_i8_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def pack(self, q, scales):
+        import numpy as np
+
+        q, qp = _host(q, np.int8)
+        s, sp = _host(scales, np.float32)
+        return check(load().gphq_q8gemm_weights_i8_pack(self.h, qp, q.size, sp, s.size))
+
+    def pack_rows(self, q, scales, row0):
+        import numpy as np
+
+        q, qp = _host(q, np.int8)
+        s, sp = _host(scales, np.float32)
+        return check(load().gphq_q8gemm_weights_i8_pack_rows(self.h, qp, q.size, sp, s.size, row0))
+
+    def dims(self):
+        k, n = ctypes.c_int64(), ctypes.c_int64()
+        load().gphq_q8gemm_weights_i8_dims(self.h, ctypes.byref(k), ctypes.byref(n))
+        return k.value, n.value
+
+    def panels(self):
+        return load().gphq_q8gemm_weights_i8_panels(self.h)
+
+    def strips(self):
+        return load().gphq_q8gemm_weights_i8_strips(self.h)
+
+    def bytes(self):
+        return load().gphq_q8gemm_weights_i8_bytes(self.h)
+
+
+class WorkspaceI8:
+    """q8gemm.WorkspaceI8 (int8.go:79-168), device resident, up to max_rows rows."""
+
+    def __init__(self, k, max_rows=16):
+        h = ctypes.c_void_p()
+        check(load().gphq_q8gemm_new_workspace_i8(k, max_rows, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            load().gphq_q8gemm_workspace_i8_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prepare(self, rows, k):
+        return check(load().gphq_q8gemm_workspace_i8_prepare(self.h, rows, k))
+
+    def set_row_scale(self, row, max_abs):
+        return check(load().gphq_q8gemm_workspace_i8_set_row_scale(self.h, row, float(max_abs)))
+
+    def pack_range(self, x, stride, k0, k1, stream=None):
+        return check(
+            load().gphq_q8gemm_workspace_i8_pack_range(self.h, ptr(x), x.numel(), stride, k0, k1, stream_handle(stream))
+        )
+
+    def pack(self, x, rows, k, stride=None, stream=None):
+        stride = k if stride is None else stride
+        return check(
+            load().gphq_q8gemm_workspace_i8_pack(self.h, ptr(x), x.numel(), rows, k, stride, stream_handle(stream))
+        )
+
+    def row_scales(self, scale, inverse, stream=None):
+        return check(load().gphq_q8gemm_workspace_i8_row_scales(self.h, ptr(scale), ptr(inverse), stream_handle(stream)))
+
+
+def mul_panels_i8(dst, stride, ws, w, p0, p1, stream=None):
+    """q8gemm.MulPanelsI8 (int8.go:174-197)."""
+    return check(load().gphq_q8gemm_mul_panels_i8(ptr(dst), dst.numel(), stride, ws.h, w.h, p0, p1, stream_handle(stream)))
+
+
+def mul_strips_i8(dst, stride, ws, w, s0, s1, stream=None):
+    """q8gemm.MulStripsI8 (int8.go:224-241)."""
+    return check(load().gphq_q8gemm_mul_strips_i8(ptr(dst), dst.numel(), stride, ws.h, w.h, s0, s1, stream_handle(stream)))

@@ -106,6 +106,75 @@ int gphq_gemv_batch(int fmt, const void *const *codes_dev, const void *const *sc
                     const float *const *x_dev, float *const *y_dev, int count, int64_t k, int64_t n,
                     void *stream);
 
+/* ---- q8gemm: int8 x int8 with exact int32 accumulation ---------------------
+ * Replaces q8gemm.WeightsI8 / WorkspaceI8 / MulPanelsI8 / MulStripsI8
+ * (q8gemm/int8.go:13-253). Results are bit-identical to the reference's
+ * scalarMulPanelsI8 oracle (int8.go:199-211):
+ *   dst[r*stride + c] = float32(sum_k qa[r,k]*qw[c,k]) * scales[c] * rowScale[r]
+ * for any split of the columns into panels (64) or strips (16).
+ * Weights and workspaces live in device memory in a tile layout of this
+ * library's own ([16 rows][64 K] fragments); Pack takes the reference's
+ * row-major input. A workspace holds up to max_rows activation rows (the
+ * reference tile is fixed at 16 rows, ActivationRows, packed.go:19; a binding
+ * maps its tiles onto one prepared workspace). Handles may be used from any
+ * thread; calls on one workspace must not overlap (the reference's Prepare /
+ * PackRange contract, int8.go:80-83). */
+typedef struct gphq_weights_i8 gphq_weights_i8;
+typedef struct gphq_workspace_i8 gphq_workspace_i8;
+
+/* NewWeightsI8 (int8.go:20-32): zeroed device storage for an n x k matrix. */
+int gphq_q8gemm_new_weights_i8(int64_t k, int64_t n, gphq_weights_i8 **out);
+void gphq_q8gemm_weights_i8_free(gphq_weights_i8 *w);
+/* (*WeightsI8).Pack (int8.go:35-41): q_host row-major int8 [n][k], scales_host
+ * f32[n]; GPHQ_ERR_DIMENSIONS on a length mismatch, GPHQ_ERR_NON_FINITE on a
+ * NaN/Inf scale. Synchronous (one-time model setup). */
+int gphq_q8gemm_weights_i8_pack(gphq_weights_i8 *w, const int8_t *q_host, int64_t q_len,
+                                const float *scales_host, int64_t scales_len);
+/* (*WeightsI8).PackRows (int8.go:43-63): rows [row0, row0+rows) of freshly
+ * allocated weights; q_len must be k*rows. */
+int gphq_q8gemm_weights_i8_pack_rows(gphq_weights_i8 *w, const int8_t *q_host, int64_t q_len,
+                                     const float *scales_host, int64_t rows, int64_t row0);
+/* Dims / Panels / Strips / Bytes (int8.go:65-73, 216). Bytes counts this
+ * library's device bytes (codes in the tile layout plus fp32 scales). */
+int gphq_q8gemm_weights_i8_dims(const gphq_weights_i8 *w, int64_t *k, int64_t *n);
+int64_t gphq_q8gemm_weights_i8_panels(const gphq_weights_i8 *w);
+int64_t gphq_q8gemm_weights_i8_strips(const gphq_weights_i8 *w);
+int64_t gphq_q8gemm_weights_i8_bytes(const gphq_weights_i8 *w);
+
+/* NewWorkspaceI8 (int8.go:91-97) with a row capacity. */
+int gphq_q8gemm_new_workspace_i8(int64_t k, int64_t max_rows, gphq_workspace_i8 **out);
+void gphq_q8gemm_workspace_i8_free(gphq_workspace_i8 *ws);
+/* (*WorkspaceI8).Prepare (int8.go:100-108): rows <= max_rows, k <= capacity;
+ * clears the row scales. */
+int gphq_q8gemm_workspace_i8_prepare(gphq_workspace_i8 *ws, int64_t rows, int64_t k);
+/* (*WorkspaceI8).SetRowScale (int8.go:106-112): scale = max/127 and
+ * inverse = 127/max for finite positive max_abs, else 0 and 0 (host value,
+ * uploaded by the next pack_range). */
+int gphq_q8gemm_workspace_i8_set_row_scale(gphq_workspace_i8 *ws, int64_t row, float max_abs);
+/* (*WorkspaceI8).PackRange (int8.go:116-163): quantizes columns [k0, k1) of
+ * the prepared rows of x_dev (rows stride floats apart) with the set row
+ * scales: q = saturate_int8(round_half_even(x * inverse)). k0 and k1 must be
+ * multiples of 4 unless k1 == k. Waits for its own upload of host-set scales. */
+int gphq_q8gemm_workspace_i8_pack_range(gphq_workspace_i8 *ws, const float *x_dev, int64_t x_len,
+                                        int64_t stride, int64_t k0, int64_t k1, void *stream);
+/* Prepare(rows, k) + SetRowScale(r, MaxAbs(row r)) for every row +
+ * PackRange(0, k), computed on the device in one launch (the packI8 sequence
+ * of int8_test.go:32-43; MaxAbs as q8gemm/gemm.go:138-150). */
+int gphq_q8gemm_workspace_i8_pack(gphq_workspace_i8 *ws, const float *x_dev, int64_t x_len, int64_t rows,
+                                  int64_t k, int64_t stride, void *stream);
+/* The prepared rows' scale (max/127) and inverse (127/max) arrays, copied to
+ * device buffers of at least `rows` floats (either may be NULL). */
+int gphq_q8gemm_workspace_i8_row_scales(const gphq_workspace_i8 *ws, float *scale_dev,
+                                        float *inverse_dev, void *stream);
+/* MulPanelsI8 (int8.go:174-197): columns [p0*64, min(p1*64, n)) of dst_dev;
+ * other columns untouched. dst_len must be >= (rows-1)*stride + n. */
+int gphq_q8gemm_mul_panels_i8(float *dst_dev, int64_t dst_len, int64_t stride, const gphq_workspace_i8 *ws,
+                              const gphq_weights_i8 *w, int64_t p0, int64_t p1, void *stream);
+/* MulStripsI8 (int8.go:224-241): columns [s0*16, min(s1*16, n)), bit-identical
+ * to the panel form. */
+int gphq_q8gemm_mul_strips_i8(float *dst_dev, int64_t dst_len, int64_t stride, const gphq_workspace_i8 *ws,
+                              const gphq_weights_i8 *w, int64_t s0, int64_t s1, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
