@@ -33,6 +33,7 @@ def parse():
     ap.add_argument("--mode", choices=["batch", "graph", "eager"], default="batch")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the config-2 int8 GEMM lines")
     return ap.parse_args()
 
 
@@ -117,6 +118,73 @@ def gemv_config1(args, torch, gphq, mode):
     }
 
 
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, AMD published (POP/s)
+
+
+def gemm_config2(args, torch, gphq, ms=(1, 16, 128, 512), rotations=6, steps=20):
+    """Config 2 (reference semantics): x fp32 [M, 4096] quantized per row (WorkspaceI8),
+    int8 weights [12288, 4096] with fp32 per-row scales, exact int32 GEMM
+    (MulPanelsI8). Times the GEMM launch over `rotations` distinct weight sets
+    (> 256 MB) and, separately, the activation quantizer."""
+    K, N = 4096, 12288
+    rng = np.random.default_rng(2)
+    ws_list = []
+    for r in range(rotations):
+        w = gphq.WeightsI8(K, N)
+        w.pack(rng.integers(-127, 128, N * K, dtype=np.int8), (np.abs(rng.standard_normal(N)) * 0.01).astype(np.float32))
+        ws_list.append(w)
+    stream = torch.cuda.current_stream()
+    out = {}
+    for m in ms:
+        x = torch.randn((m, K), device="cuda")
+        ws = gphq.WorkspaceI8(K, m)
+        ws.pack(x, m, K, stream=stream)
+        dst = torch.empty((m, N), device="cuda")
+        for w in ws_list:
+            gphq.mul_panels_i8(dst, N, ws, w, 0, w.panels(), stream=stream)
+        torch.cuda.synchronize()
+        # Replay captured launches so host launch cost does not enter the timing.
+        g_gemm, g_quant = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_gemm):
+            cs = torch.cuda.current_stream()
+            for w in ws_list:
+                gphq.mul_panels_i8(dst, N, ws, w, 0, w.panels(), stream=cs)
+        with torch.cuda.graph(g_quant):
+            cs = torch.cuda.current_stream()
+            for _ in range(rotations):
+                ws.pack(x, m, K, stream=cs)
+        g_gemm.replay()
+        g_quant.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            g_gemm.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (steps * rotations)
+        e0.record(stream)
+        for _ in range(steps):
+            g_quant.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        q_us = e0.elapsed_time(e1) * 1e3 / (steps * rotations)
+        gemm_bytes = N * K + 4 * N + m * K + 4 * m + 4 * m * N
+        ops = 2.0 * m * N * K
+        out[f"M{m}"] = {
+            "gemm_us": round(us, 3),
+            "gemm_gbs": round(gemm_bytes / us / 1e3, 1),
+            "hbm_frac": round(gemm_bytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "tops": round(ops / us / 1e6, 1),
+            "int8_frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
+            "quantize_us": round(q_us, 3),
+        }
+        del ws
+    for w in ws_list:
+        w.close()
+    return out
+
+
 def cpu_baseline(seconds):
     """The reference's amd64 q8gemv path (scalarMulInto, single thread),
     restated in C (oracle), on the config-1 shape with per-row scales."""
@@ -160,6 +228,7 @@ def main():
     r = gemv_config1(args, torch, gphq, args.mode)
     single = gemv_config1(args, torch, gphq, "graph") if args.mode == "batch" else None
     value = r["value_gbs"]
+    gemm = None if args.no_gemm else gemm_config2(args, torch, gphq)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     kernel = "gemv8_kernel<Q8B_F32,4,2,8," + ("32>" if args.mode == "batch" else "1>")
     out = {
@@ -202,6 +271,7 @@ def main():
             "per_gemv_us": round(single["per_gemv_us"], 3),
             "mode": "one gphq_gemv launch per 4096x4096 GEMV, HIP graph of 32 launches",
         },
+        "gemm_config2": gemm,
         "decode_ms_per_token": None,
         "check": {"rel_l2_vs_float64": r["rel_l2"]},
     }

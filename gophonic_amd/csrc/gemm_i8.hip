@@ -94,10 +94,21 @@ __global__ __launch_bounds__(256) void i8_pack_rows_kernel(const float *__restri
     const float *xr = x + (size_t)row * stride;
     float m = 0.0f;
     int nan = 0;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) {
-        const float v = xr[k];
-        nan |= (v != v);
-        m = fmaxf(m, fabsf(v));
+    // Eight independent loads per thread per trip, so a row's reads are in
+    // flight together instead of one L2 round trip after another.
+    constexpr int UNR = 8;
+    for (int k0 = 0; k0 < K; k0 += 256 * UNR) {
+        float v[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int k = k0 + u * 256 + (int)threadIdx.x;
+            v[u] = k < K ? xr[k] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            nan |= (v[u] != v[u]);
+            m = fmaxf(m, fabsf(v[u]));
+        }
     }
     // wave max / nan-any
     for (int off = 32; off > 0; off >>= 1) {
@@ -123,9 +134,23 @@ __global__ __launch_bounds__(256) void i8_pack_rows_kernel(const float *__restri
         rowScale[row] = scale;
         rowInv[row] = inv;
     }
-    for (int k = threadIdx.x; k < kt * 64; k += blockDim.x) {
-        const int8_t q = k < K ? quantize_i8(__fmul_rn(xr[k], inv)) : (int8_t)0;
-        act[tile_offset(row, k, kt)] = q;
+    // Quantize: each thread takes 16 consecutive columns (one 16-byte lane
+    // chunk of the tile layout) and stores them with one 128-bit write.
+    for (int c = threadIdx.x; c < kt * 4; c += blockDim.x) {
+        const int kb = c * 16;
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int k = kb + 4 * j + i;
+                const int8_t q = k < K ? quantize_i8(__fmul_rn(xr[k], inv)) : (int8_t)0;
+                packed |= (uint32_t)(uint8_t)q << (8 * i);
+            }
+            w[j] = packed;
+        }
+        *(uint4 *)(act + tile_offset(row, kb, kt)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
@@ -195,8 +220,10 @@ __global__ __launch_bounds__(64 * WM * WN * SK) void i8gemm_kernel(const I8GemmA
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
 
-    for (int kt = kt0; kt < kt1; kt += U) {
-        i32x4 fa[U][TM], fb[U][TN];
+    // Two register buffers: the fragments of batch b+1 are requested before the
+    // MFMAs of batch b, so memory latency overlaps the matrix work. Fragments
+    // past the slice end are zero and add nothing.
+    auto load = [&](i32x4 (&fa)[U][TM], i32x4 (&fb)[U][TN], int kt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const bool ok = kt + u < kt1;
@@ -208,6 +235,8 @@ __global__ __launch_bounds__(64 * WM * WN * SK) void i8gemm_kernel(const I8GemmA
             for (int j = 0; j < TN; ++j)
                 fb[u][j] = ok ? __builtin_nontemporal_load((const i32x4 *)(a.B + boff[j] + ko)) : i32x4{0, 0, 0, 0};
         }
+    };
+    auto mma = [&](const i32x4 (&fa)[U][TM], const i32x4 (&fb)[U][TN]) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -215,6 +244,18 @@ __global__ __launch_bounds__(64 * WM * WN * SK) void i8gemm_kernel(const I8GemmA
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][i], fb[u][j], acc[i][j], 0, 0, 0);
+    };
+    i32x4 fa0[U][TM], fb0[U][TN], fa1[U][TM], fb1[U][TN];
+    int kt = kt0;
+    if (kt < kt1) load(fa0, fb0, kt);
+    while (kt < kt1) {
+        if (kt + U < kt1) load(fa1, fb1, kt + U);
+        mma(fa0, fb0);
+        kt += U;
+        if (kt >= kt1) break;
+        if (kt + U < kt1) load(fa0, fb0, kt + U);
+        mma(fa1, fb1);
+        kt += U;
     }
 
     if constexpr (SK > 1) {
@@ -252,6 +293,122 @@ __global__ __launch_bounds__(64 * WM * WN * SK) void i8gemm_kernel(const I8GemmA
     }
 }
 
+// LDS-staged variant for larger M: a block owns a BM x BN output tile; per
+// stage the block copies BKT K-tiles of its A rows and B columns (1 KiB
+// fragments, contiguous in the tile layout) from global memory into LDS with
+// 16-byte loads, double buffered: the next stage's global loads are in flight
+// while the wavefronts multiply the current stage out of LDS. Each fragment
+// then crosses the L2 -> CU path once per block instead of once per wavefront.
+template <int BM, int BN, int WM, int WN, int BKT>
+__global__ __launch_bounds__(64 * WM * WN) void i8gemm_lds_kernel(const I8GemmArgs a) {
+    constexpr int NT_ = 64 * WM * WN;
+    constexpr int TM = BM / 16 / WM, TN = BN / 16 / WN;
+    constexpr int AG = (BM / 16) * BKT, BG = (BN / 16) * BKT;  // 1 KiB groups per stage
+    constexpr int CH = (AG + BG) * 64;                          // 16-byte chunks per stage
+    constexpr int PER = (CH + NT_ - 1) / NT_;
+    __shared__ i32x4 lds[2][AG + BG][64];
+
+    const int G = a.gridM * a.gridN;
+    const int b = blockIdx.x;
+    int logical = b;
+    if (G % 8 == 0) logical = (b % 8) * (G / 8) + b / 8;
+    const int bm = logical % a.gridM, bn = logical / a.gridM;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wm = wv / WN, wn = wv % WN;
+    const int MT = (a.M + 15) >> 4, KT = a.KT;
+    const int rt0 = bm * (BM / 16), ct0 = a.tileN0 + bn * (BN / 16);
+
+    auto fetch = [&](int kt0, i32x4 (&reg)[PER]) {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int c = tid + p * NT_;
+            reg[p] = i32x4{0, 0, 0, 0};
+            if (c < CH) {
+                const int g = c >> 6, l = c & 63;
+                const int kk = (g < AG) ? (g % BKT) : ((g - AG) % BKT);
+                const int kt = kt0 + kk;
+                if (kt < KT) {
+                    if (g < AG) {
+                        const int rt = min(rt0 + g / BKT, MT - 1);
+                        reg[p] = *(const i32x4 *)(a.A + ((size_t)rt * KT + kt) * 1024 + (size_t)l * 16);
+                    } else {
+                        const int ct = min(ct0 + (g - AG) / BKT, a.NT - 1);
+                        reg[p] = __builtin_nontemporal_load(
+                            (const i32x4 *)(a.B + ((size_t)ct * KT + kt) * 1024 + (size_t)l * 16));
+                    }
+                }
+            }
+        }
+    };
+    auto stash = [&](int buf, const i32x4 (&reg)[PER]) {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int c = tid + p * NT_;
+            if (c < CH) lds[buf][c >> 6][c & 63] = reg[p];
+        }
+    };
+
+    i32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+
+    i32x4 reg[PER];
+    fetch(0, reg);
+    stash(0, reg);
+    __syncthreads();
+    int buf = 0;
+    for (int kt0 = 0; kt0 < KT; kt0 += BKT) {
+        const bool more = kt0 + BKT < KT;
+        if (more) fetch(kt0 + BKT, reg);
+#pragma unroll
+        for (int kk = 0; kk < BKT; ++kk) {
+            i32x4 fa[TM], fb[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) fa[i] = lds[buf][(wm * TM + i) * BKT + kk][lane];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) fb[j] = lds[buf][AG + (wn * TN + j) * BKT + kk][lane];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) stash(buf ^ 1, reg);
+        __syncthreads();
+        buf ^= 1;
+    }
+
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = (ct0 + wn * TN + j) * 16 + (lane & 15);
+        if (col < a.c0 || col >= a.c1) continue;
+        const float cs = a.colScale[col];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = (rt0 + wm * TM + i) * 16 + 4 * (lane >> 4) + e;
+                if (row < a.M) {
+                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row]);
+                    a.dst[(size_t)row * a.stride + col] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int BKT>
+static int launch_i8gemm_lds(I8GemmArgs a, hipStream_t stream) {
+    const int tiles = (a.c1 + 15) / 16 - a.tileN0;
+    a.gridN = (tiles * 16 + BN - 1) / BN;
+    a.gridM = (a.M + BM - 1) / BM;
+    const unsigned blocks = (unsigned)(a.gridM * a.gridN);
+    hipLaunchKernelGGL((i8gemm_lds_kernel<BM, BN, WM, WN, BKT>), dim3(blocks), dim3(64 * WM * WN), 0, stream, a);
+    return launch_status();
+}
+
 template <int TM, int TN, int WM, int WN, int SK, int U>
 static int launch_i8gemm(I8GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
@@ -281,10 +438,11 @@ int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const
     a.c0 = c0;
     a.c1 = c1;
     a.tileN0 = c0 / 16;
-    if (M <= 16) return launch_i8gemm<1, 1, 1, 2, 4, 8>(a, stream);
+    // Shapes picked by measurement on MI355X at K = 4096, N = 12288.
+    if (M <= 16) return launch_i8gemm<1, 2, 1, 2, 4, 4>(a, stream);
     if (M <= 64) return launch_i8gemm<4, 1, 1, 2, 4, 4>(a, stream);
-    if (M <= 192) return launch_i8gemm<2, 2, 2, 2, 1, 4>(a, stream);
-    return launch_i8gemm<4, 4, 2, 2, 1, 2>(a, stream);
+    if (M <= 192) return launch_i8gemm_lds<128, 64, 2, 2, 4>(a, stream);
+    return launch_i8gemm_lds<128, 64, 2, 2, 2>(a, stream);
 }
 
 int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {
