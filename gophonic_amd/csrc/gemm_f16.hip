@@ -1,0 +1,454 @@
+// FP16-operand GEMMs with fp32 accumulation on v_mfma_f32_16x16x32_f16:
+//
+//  * q8gemm MulPanels (q8gemm/gemm.go:228-286, scalar.go:9-20): FP16
+//    activations (each row scaled by an exact power of two into [2^14, 2^15))
+//    times int8 or FP16 weights, then acc * colScale[c] * rowInverse[r].
+//  * qwen3lm mm (gpu.metal:766-927, PRO_PLAIN / EPI_STORE): weights of a GPU
+//    format dequantized to FP16 per K step (Q8: half(code); Q8B: half(code) *
+//    half(d) rounded to half; Q4: (half(nib) - 8) * d rounded to half),
+//    activations half(x), fp32 accumulation; Q8 rows then scaled by their fp32
+//    row scale.
+//  * GPTQ int4 with group-128 FP16 scales and 4-bit zero points (8 codes per
+//    int32): (half(nib) - half(z)) * s rounded to half.
+//
+// Fragments: lane l of a 16x64 K step holds row (l % 16), columns
+// (l / 16) * 16 .. +16 of both operands (16 FP16 values = two 8-value MFMA
+// operands). The two MFMAs per step take values 0..7 and 8..15 of every lane;
+// A and B use the same K assignment, so C = A . B^T exactly as a plain K loop.
+// Activations are FP16 in the tile layout [M/16][K/64][64][16] (2 KiB per
+// group), written by f16_act_pack_kernel. Weights are read in their own
+// layout: the int8 tile layout of gemm_i8.hip, an FP16 tile layout, or the
+// qwen3lm row-major code arrays.
+#include "common.h"
+
+namespace gphq {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+enum WFmt {
+    W_I8_TILE = 0,    // q8gemm int8 weights, tile layout (1 KiB groups)
+    W_F16_TILE = 1,   // q8gemm FP16 weights, tile layout (2 KiB groups)
+    W_Q8_ROW = 2,     // qwen3lm Q8 codes [N][K] (fp32 row scales in the epilogue)
+    W_Q8B_ROW = 3,    // qwen3lm Q8B codes [N][K], f16 scales [N][K/32]
+    W_Q4_ROW = 4,     // qwen3lm Q4 codes [N][K/2], f16 scales [N][K/32]
+    W_GPTQ_ROW = 5,   // int32 [N][K/8] (nibble i of word j = k 8j+i), f16 scales and u8 zeros [N][K/128]
+};
+
+enum Epi { EPI_PANELS = 0, EPI_PLAIN = 1, EPI_ROWSCALE = 2 };
+
+struct F16GemmArgs {
+    const _Float16 *A;   // activations, FP16 tile layout, MT x KT groups
+    const void *B;       // weights (layout per WFmt)
+    const void *bScale;  // Q8B/Q4: f16 [N][K/32]; GPTQ: f16 [N][K/128]
+    const uint8_t *bZero;  // GPTQ: u8 [N][K/128]
+    const float *colScale;  // EPI_PANELS, EPI_ROWSCALE: fp32 [N]
+    const float *rowInv;    // EPI_PANELS: fp32 [M]
+    float *dst;
+    long stride;
+    int M, N, K, KT, NT;
+    int c0, c1, tileN0;
+    int gridM, gridN;
+};
+
+__device__ __forceinline__ _Float16 i8h(uint32_t v, int i) { return (_Float16)(int)((int32_t)(v << (24 - 8 * i)) >> 24); }
+
+// B fragment: 16 FP16 weights of row `n` (clamped in range), K step kt, lane
+// group g (values k = kt*64 + g*16 + 0..15), decoded per format.
+template <int WF>
+__device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int lane, f16x8 &lo, f16x8 &hi) {
+    const int g = lane >> 4;
+    const int k = kt * 64 + g * 16;
+    if constexpr (WF == W_I8_TILE) {
+        const u32x4 w = __builtin_nontemporal_load(
+            (const u32x4 *)((const int8_t *)a.B + ((size_t)(n >> 4) * a.KT + kt) * 1024 + (size_t)lane * 16));
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3);
+    } else if constexpr (WF == W_F16_TILE) {
+        const f16x8 *p = (const f16x8 *)((const _Float16 *)a.B + ((size_t)(n >> 4) * a.KT + kt) * 1024 + (size_t)lane * 16);
+        lo = __builtin_nontemporal_load(p);
+        hi = __builtin_nontemporal_load(p + 1);
+    } else if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW) {
+        u32x4 w = u32x4{0, 0, 0, 0};
+        if (k < a.K) w = __builtin_nontemporal_load((const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k));
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        if constexpr (WF == W_Q8_ROW) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3);
+        } else {
+            _Float16 d = (_Float16)0.0f;
+            if (k < a.K) d = __builtin_bit_cast(_Float16, ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3) * d;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3) * d;
+        }
+    } else if constexpr (WF == W_Q4_ROW) {
+        // Block (k / 32) is 16 bytes: value j in the low nibble of byte j,
+        // value j + 16 in the high nibble; this lane needs half (k / 16) % 2.
+        u32x4 w = u32x4{0, 0, 0, 0};
+        _Float16 d = (_Float16)0.0f;
+        if (k < a.K) {
+            w = __builtin_nontemporal_load((const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16));
+            d = __builtin_bit_cast(_Float16, ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)]);
+        }
+        const int sh = (g & 1) * 4;
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            lo[i] = ((_Float16)(int)((ww[i >> 2] >> (8 * (i & 3) + sh)) & 15) - (_Float16)8.0f) * d;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            hi[i] = ((_Float16)(int)((ww[2 + (i >> 2)] >> (8 * (i & 3) + sh)) & 15) - (_Float16)8.0f) * d;
+        if (k >= a.K) {
+            lo = f16x8{};
+            hi = f16x8{};
+        }
+    } else {  // W_GPTQ_ROW
+        uint32_t w0 = 0, w1 = 0;
+        _Float16 s = (_Float16)0.0f, z = (_Float16)0.0f;
+        if (k < a.K) {
+            const uint32_t *p = (const uint32_t *)a.B + (size_t)n * (a.K >> 3) + (k >> 3);
+            w0 = __builtin_nontemporal_load(p);
+            w1 = __builtin_nontemporal_load(p + 1);
+            const size_t gi = (size_t)n * (a.K >> 7) + (k >> 7);
+            s = __builtin_bit_cast(_Float16, ((const uint16_t *)a.bScale)[gi]);
+            z = (_Float16)(int)(a.bZero[gi] & 15);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lo[i] = ((_Float16)(int)((w0 >> (4 * i)) & 15) - z) * s;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hi[i] = ((_Float16)(int)((w1 >> (4 * i)) & 15) - z) * s;
+    }
+}
+
+template <int WF, int EPI, int TM, int TN, int WM, int WN, int SK, int U>
+__global__ __launch_bounds__(64 * WM * WN * SK) void f16gemm_kernel(const F16GemmArgs a) {
+    constexpr int NW = WM * WN * SK;
+    __shared__ f32x4 red[(SK > 1) ? (NW * TM * TN * 64) : 1];
+    const int G = a.gridM * a.gridN;
+    const int b = blockIdx.x;
+    int logical = b;
+    if (G % 8 == 0) logical = (b % 8) * (G / 8) + b / 8;
+    const int bm = logical % a.gridM, bn = logical / a.gridM;
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int ks = wv % SK;
+    const int wn = (wv / SK) % WN;
+    const int wm = wv / (SK * WN);
+    const int mt0 = (bm * WM + wm) * TM;
+    const int nt0 = a.tileN0 + (bn * WN + wn) * TN;
+    const int MT = (a.M + 15) >> 4;
+    const int KT = a.KT;
+    const int per = (KT + SK - 1) / SK;
+    const int kt0 = ks * per, kt1 = min(KT, kt0 + per);
+    int nrow[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) nrow[j] = min((nt0 + j) * 16 + (lane & 15), a.N - 1);
+    size_t aoff[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) aoff[i] = (size_t)min(mt0 + i, MT - 1) * KT * 1024 + (size_t)lane * 16;
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int kt = kt0; kt < kt1; kt += U) {
+        f16x8 fa[U][TM][2], fb[U][TN][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool ok = kt + u < kt1;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                if (ok) {
+                    const f16x8 *p = (const f16x8 *)(a.A + aoff[i] + (size_t)(kt + u) * 1024);
+                    fa[u][i][0] = p[0];
+                    fa[u][i][1] = p[1];
+                } else {
+                    fa[u][i][0] = f16x8{};
+                    fa[u][i][1] = f16x8{};
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                if (ok) {
+                    load_b<WF>(a, nrow[j], kt + u, lane, fb[u][j][0], fb[u][j][1]);
+                } else {
+                    fb[u][j][0] = f16x8{};
+                    fb[u][j][1] = f16x8{};
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[u][i][h], fb[u][j][h], acc[i][j], 0, 0, 0);
+    }
+
+    if constexpr (SK > 1) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) red[((wv * TM + i) * TN + j) * 64 + lane] = acc[i][j];
+        __syncthreads();
+        if (ks != 0) return;
+#pragma unroll
+        for (int s = 1; s < SK; ++s)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] += red[(((wv + s) * TM + i) * TN + j) * 64 + lane];
+    }
+
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        if (col < a.c0 || col >= a.c1) continue;
+        float cs = 1.0f;
+        if constexpr (EPI != EPI_PLAIN) cs = a.colScale[col];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
+                if (row < a.M) {
+                    float v = acc[i][j][e];
+                    if constexpr (EPI == EPI_PANELS) v = __fmul_rn(__fmul_rn(v, cs), a.rowInv[row]);
+                    if constexpr (EPI == EPI_ROWSCALE) v = __fmul_rn(v, cs);
+                    a.dst[(size_t)row * a.stride + col] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int WF, int EPI, int TM, int TN, int WM, int WN, int SK, int U>
+static int launch_f16gemm(F16GemmArgs a, hipStream_t stream) {
+    const int tiles = (a.c1 + 15) / 16 - a.tileN0;
+    a.gridN = (tiles + TN * WN - 1) / (TN * WN);
+    a.gridM = (a.M + 16 * TM * WM - 1) / (16 * TM * WM);
+    hipLaunchKernelGGL((f16gemm_kernel<WF, EPI, TM, TN, WM, WN, SK, U>), dim3((unsigned)(a.gridM * a.gridN)),
+                       dim3(64 * WM * WN * SK), 0, stream, a);
+    return launch_status();
+}
+
+template <int WF, int EPI>
+static int launch_by_m(const F16GemmArgs &a, hipStream_t stream) {
+    if (a.M <= 16) return launch_f16gemm<WF, EPI, 1, 2, 1, 2, 4, 2>(a, stream);
+    if (a.M <= 64) return launch_f16gemm<WF, EPI, 4, 1, 1, 2, 4, 2>(a, stream);
+    return launch_f16gemm<WF, EPI, 4, 2, 2, 2, 1, 1>(a, stream);
+}
+
+// Dispatch over weight format and epilogue. All arguments were validated.
+int f16gemm_launch(int wf, int epi, F16GemmArgs a, hipStream_t stream) {
+    if (a.M == 0 || a.c0 >= a.c1) return GPHQ_OK;
+    a.NT = (a.N + 15) / 16;
+    a.tileN0 = a.c0 / 16;
+#define GPHQ_F16_CASE(W, E) \
+    if (wf == W && epi == E) return launch_by_m<W, E>(a, stream);
+    GPHQ_F16_CASE(W_I8_TILE, EPI_PANELS)
+    GPHQ_F16_CASE(W_F16_TILE, EPI_PANELS)
+    GPHQ_F16_CASE(W_Q8_ROW, EPI_ROWSCALE)
+    GPHQ_F16_CASE(W_Q8B_ROW, EPI_PLAIN)
+    GPHQ_F16_CASE(W_Q4_ROW, EPI_PLAIN)
+    GPHQ_F16_CASE(W_GPTQ_ROW, EPI_PLAIN)
+#undef GPHQ_F16_CASE
+    return GPHQ_ERR_UNSUPPORTED;
+}
+
+// ---- activation packing ------------------------------------------------------
+// Row scale of q8gemm Workspace.SetRowScale (gemm.go:127-135): 2^e with
+// e = clamp(15 - exp(max), -100, 100) when max is finite and positive, else 1.
+__device__ __forceinline__ void f16_row_scale(float m, float &scale, float &inv) {
+    int e = 0;
+    if (m > 0.0f && !isinf(m) && m == m) {
+        int ex;
+        (void)frexpf(m, &ex);
+        e = min(max(15 - ex, -100), 100);
+    }
+    scale = ldexpf(1.0f, e);
+    inv = ldexpf(1.0f, -e);
+}
+
+// One block per row. mode 0: q8gemm Workspace.Pack (power-of-two row scale from
+// MaxAbs, then f16(x * scale)); mode 1: qwen3lm mm activations, half(x);
+// mode 2: PackRange with the row scales already on the device, converting only
+// columns [k0, k1) (and the K padding when k1 == K). Writes the FP16 tile
+// layout; modes 0 and 1 convert whole rows and zero the K padding.
+__global__ __launch_bounds__(256) void f16_act_pack_kernel(const float *__restrict__ x, long stride, int K, int kt,
+                                                           int mode, int k0, int k1, _Float16 *__restrict__ act,
+                                                           float *__restrict__ rowScale, float *__restrict__ rowInv) {
+    __shared__ float smax[4];
+    __shared__ int snan[4];
+    const int row = blockIdx.x;
+    const float *xr = x + (size_t)row * stride;
+    float scale = 1.0f, inv = 1.0f;
+    if (mode == 0) {
+        float m = 0.0f;
+        int nan = 0;
+        constexpr int UNR = 8;
+        for (int kb = 0; kb < K; kb += 256 * UNR) {
+            float v[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+                const int k = kb + u * 256 + (int)threadIdx.x;
+                v[u] = k < K ? xr[k] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+                nan |= (v[u] != v[u]);
+                m = fmaxf(m, fabsf(v[u]));
+            }
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            m = fmaxf(m, __shfl_xor(m, off));
+            nan |= __shfl_xor(nan, off);
+        }
+        if ((threadIdx.x & 63) == 0) {
+            smax[threadIdx.x >> 6] = m;
+            snan[threadIdx.x >> 6] = nan;
+        }
+        __syncthreads();
+        float mm = 0.0f;
+        int anyNan = 0;
+        for (int i = 0; i < (int)(blockDim.x >> 6); ++i) {
+            mm = fmaxf(mm, smax[i]);
+            anyNan |= snan[i];
+        }
+        if (anyNan) mm = __builtin_nanf("");
+        f16_row_scale(mm, scale, inv);
+        if (threadIdx.x == 0) {
+            rowScale[row] = scale;
+            rowInv[row] = inv;
+        }
+    } else if (mode == 2) {
+        scale = rowScale[row];
+    }
+    if (mode != 2) {
+        for (int c = threadIdx.x; c < kt * 4; c += blockDim.x) {
+            const int kb = c * 16;
+            f16x8 h[2];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int k = kb + i;
+                h[i >> 3][i & 7] = k < K ? (_Float16)__fmul_rn(xr[k], scale) : (_Float16)0.0f;
+            }
+            const size_t off =
+                ((size_t)(row >> 4) * kt + (kb >> 6)) * 1024 + (size_t)(((kb & 63) >> 4) * 16 + (row & 15)) * 16;
+            *(f16x8 *)(act + off) = h[0];
+            *(f16x8 *)(act + off + 8) = h[1];
+        }
+    } else {
+        const int kend = (k1 == K) ? kt * 64 : k1;
+        for (int k = k0 + (int)threadIdx.x; k < kend; k += blockDim.x) {
+            const size_t off = ((size_t)(row >> 4) * kt + (k >> 6)) * 1024 +
+                               (size_t)(((k & 63) >> 4) * 16 + (row & 15)) * 16 + (k & 15);
+            act[off] = k < K ? (_Float16)__fmul_rn(xr[k], scale) : (_Float16)0.0f;
+        }
+    }
+}
+
+int f16_act_pack(const float *x, long stride, int rows, int K, int kt, int mode, int k0, int k1, _Float16 *act,
+                 float *rowScale, float *rowInv, hipStream_t stream) {
+    if (rows == 0) return GPHQ_OK;
+    hipLaunchKernelGGL(f16_act_pack_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, mode, k0, k1, act,
+                       rowScale, rowInv);
+    return launch_status();
+}
+
+// PackBF16Rows arithmetic (q8gemm/packed.go:148-174) for rows already known to
+// be finite: per row, e = clamp(15 - exp(max|v|), -100, 100), values
+// f16(v * 2^e) (round to nearest even), stored row scale 2^-e, and a count of
+// values that did not convert exactly. One block per row; output row-major.
+__global__ __launch_bounds__(256) void bf16_rows_to_f16_kernel(const uint16_t *__restrict__ src, int K,
+                                                               uint16_t *__restrict__ dst, float *__restrict__ rowScale,
+                                                               unsigned long long *__restrict__ rounded) {
+    __shared__ float smax[4];
+    __shared__ unsigned long long scount[4];
+    const int row = blockIdx.x;
+    const uint16_t *s = src + (size_t)row * K;
+    float m = 0.0f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x)
+        m = fmaxf(m, fabsf(__builtin_bit_cast(float, (uint32_t)s[k] << 16)));
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    float mm = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) mm = fmaxf(mm, smax[i]);
+    int e = 0;
+    if (mm > 0.0f) {
+        int ex;
+        (void)frexpf(mm, &ex);
+        e = min(max(15 - ex, -100), 100);
+    }
+    const float scale = ldexpf(1.0f, e);
+    if (threadIdx.x == 0) rowScale[row] = ldexpf(1.0f, -e);
+    unsigned long long cnt = 0;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        const float v = __fmul_rn(__builtin_bit_cast(float, (uint32_t)s[k] << 16), scale);
+        const _Float16 h = (_Float16)v;
+        cnt += ((float)h != v);
+        dst[(size_t)row * K + k] = __builtin_bit_cast(uint16_t, h);
+    }
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off);
+    if ((threadIdx.x & 63) == 0) scount[threadIdx.x >> 6] = cnt;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long t = 0;
+        for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += scount[i];
+        atomicAdd(rounded, t);
+    }
+}
+
+int bf16_rows_to_f16(const uint16_t *src, int rows, int K, uint16_t *dst, float *rowScale, unsigned long long *rounded,
+                     hipStream_t stream) {
+    if (rows == 0) return GPHQ_OK;
+    hipLaunchKernelGGL(bf16_rows_to_f16_kernel, dim3(rows), dim3(256), 0, stream, src, K, dst, rowScale, rounded);
+    return launch_status();
+}
+
+// FP16 weights (raw bits, row-major [rows][K]) -> FP16 tile layout.
+__global__ void f16_pack_tiles_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ dst, int rows, int K,
+                                      int row0, int rowTiles, int kt) {
+    const size_t chunk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)rowTiles * kt * 64;
+    if (chunk >= total) return;
+    const int lane = (int)(chunk & 63);
+    const size_t g = chunk >> 6;
+    const int ktile = (int)(g % kt);
+    const int rtile = (int)(g / kt) + (row0 >> 4);
+    const int r = rtile * 16 + (lane & 15);
+    const int rr = r - row0;
+    if (rr < 0 || rr >= rows) return;
+    const int kbase = ktile * 64 + (lane >> 4) * 16;
+    uint16_t *d = dst + ((size_t)rtile * kt + ktile) * 1024 + (size_t)lane * 16;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int k = kbase + i;
+        d[i] = k < K ? src[(size_t)rr * K + k] : (uint16_t)0;
+    }
+}
+
+int f16_pack_tiles(const uint16_t *src, uint16_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {
+    if (rows == 0) return GPHQ_OK;
+    const int rowTiles = ((row0 + rows + 15) >> 4) - (row0 >> 4);
+    const size_t chunks = (size_t)rowTiles * kt * 64;
+    hipLaunchKernelGGL(f16_pack_tiles_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, src, dst,
+                       rows, K, row0, rowTiles, kt);
+    return launch_status();
+}
+
+}  // namespace gphq

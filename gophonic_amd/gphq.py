@@ -52,7 +52,35 @@ SIGNATURES = {
     "gphq_q8gemm_workspace_i8_row_scales": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
     "gphq_q8gemm_mul_panels_i8": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp]),
     "gphq_q8gemm_mul_strips_i8": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp]),
+    "gphq_q8gemm_new_weights": (ctypes.c_int, [_i64, _i64, _vpp]),
+    "gphq_q8gemm_new_weights_f16": (ctypes.c_int, [_i64, _i64, _vpp]),
+    "gphq_q8gemm_weights_f16_bytes": (_i64, [_i64, _i64]),
+    "gphq_q8gemm_new_weights_f16_buffer": (ctypes.c_int, [_i64, _i64, _vp, _i64, _vpp]),
+    "gphq_q8gemm_weights_free": (None, [_vp]),
+    "gphq_q8gemm_weights_pack": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64]),
+    "gphq_q8gemm_weights_pack_bf16": (ctypes.c_int, [_vp, _vp, _i64, _i64p]),
+    "gphq_q8gemm_weights_pack_bf16_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64p]),
+    "gphq_q8gemm_weights_dims": (ctypes.c_int, [_vp, _i64p, _i64p]),
+    "gphq_q8gemm_weights_panels": (_i64, [_vp]),
+    "gphq_q8gemm_weights_bytes": (_i64, [_vp]),
+    "gphq_q8gemm_weights_is_f16": (ctypes.c_int, [_vp]),
+    "gphq_q8gemm_new_workspace": (ctypes.c_int, [_i64, _i64, _vpp]),
+    "gphq_q8gemm_workspace_free": (None, [_vp]),
+    "gphq_q8gemm_workspace_prepare": (ctypes.c_int, [_vp, _i64, _i64]),
+    "gphq_q8gemm_workspace_prepare_row_f16": (ctypes.c_int, [_vp, _i64]),
+    "gphq_q8gemm_workspace_prepare_rows_f16": (ctypes.c_int, [_vp, _i64, _i64]),
+    "gphq_q8gemm_workspace_set_row_scale": (ctypes.c_int, [_vp, _i64, ctypes.c_float]),
+    "gphq_q8gemm_workspace_pack_range": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "gphq_q8gemm_workspace_pack": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "gphq_q8gemm_workspace_row_scales": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
+    "gphq_q8gemm_workspace_activations": (ctypes.c_int, [_vp, _vp, _vp]),
+    "gphq_q8gemm_mul_panels": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp]),
+    "gphq_q8gemm_mul_into": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "gphq_mm_workspace_bytes": (_i64, [_i64, _i64]),
+    "gphq_mm": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
 }
+
+FMT_GPTQ4_G128 = 12
 
 GEMV_MAX_BATCH = 32
 
@@ -252,3 +280,142 @@ def mul_panels_i8(dst, stride, ws, w, p0, p1, stream=None):
 def mul_strips_i8(dst, stride, ws, w, s0, s1, stream=None):
     """q8gemm.MulStripsI8 (int8.go:224-241)."""
     return check(load().gphq_q8gemm_mul_strips_i8(ptr(dst), dst.numel(), stride, ws.h, w.h, s0, s1, stream_handle(stream)))
+
+
+class Weights:
+    """q8gemm.Weights (packed.go:35-239): int8 (f16=False) or FP16 storage, device resident.
+    With `buffer` (a device tensor of weights_f16_bytes(k, n) bytes) it binds
+    caller-owned storage like NewWeightsF16Buffer."""
+
+    def __init__(self, k, n, f16=False, buffer=None):
+        h = ctypes.c_void_p()
+        self._buffer = buffer
+        if buffer is not None:
+            check(load().gphq_q8gemm_new_weights_f16_buffer(k, n, ptr(buffer), buffer.numel() * buffer.element_size(),
+                                                             ctypes.byref(h)))
+        elif f16:
+            check(load().gphq_q8gemm_new_weights_f16(k, n, ctypes.byref(h)))
+        else:
+            check(load().gphq_q8gemm_new_weights(k, n, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            load().gphq_q8gemm_weights_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def pack(self, q, scales):
+        import numpy as np
+
+        q, qp = _host(q, np.int8)
+        s, sp = _host(scales, np.float32)
+        return check(load().gphq_q8gemm_weights_pack(self.h, qp, q.size, sp, s.size))
+
+    def pack_bf16(self, bf16):
+        import numpy as np
+
+        b, bp = _host(bf16, np.uint16)
+        r = ctypes.c_int64()
+        check(load().gphq_q8gemm_weights_pack_bf16(self.h, bp, b.size, ctypes.byref(r)))
+        return r.value
+
+    def pack_bf16_rows(self, bf16, row0):
+        import numpy as np
+
+        b, bp = _host(bf16, np.uint16)
+        r = ctypes.c_int64()
+        check(load().gphq_q8gemm_weights_pack_bf16_rows(self.h, bp, b.size, row0, ctypes.byref(r)))
+        return r.value
+
+    def dims(self):
+        k, n = ctypes.c_int64(), ctypes.c_int64()
+        load().gphq_q8gemm_weights_dims(self.h, ctypes.byref(k), ctypes.byref(n))
+        return k.value, n.value
+
+    def panels(self):
+        return load().gphq_q8gemm_weights_panels(self.h)
+
+    def bytes(self):
+        return load().gphq_q8gemm_weights_bytes(self.h)
+
+    def f16(self):
+        return bool(load().gphq_q8gemm_weights_is_f16(self.h))
+
+
+def weights_f16_bytes(k, n):
+    return load().gphq_q8gemm_weights_f16_bytes(k, n)
+
+
+class Workspace:
+    """q8gemm.Workspace (gemm.go:20-226), device resident, up to max_rows rows."""
+
+    def __init__(self, k, max_rows=16):
+        h = ctypes.c_void_p()
+        check(load().gphq_q8gemm_new_workspace(k, max_rows, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            load().gphq_q8gemm_workspace_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prepare(self, rows, k):
+        return check(load().gphq_q8gemm_workspace_prepare(self.h, rows, k))
+
+    def prepare_row_f16(self, k):
+        return check(load().gphq_q8gemm_workspace_prepare_row_f16(self.h, k))
+
+    def prepare_rows_f16(self, rows, k):
+        return check(load().gphq_q8gemm_workspace_prepare_rows_f16(self.h, rows, k))
+
+    def set_row_scale(self, row, max_abs):
+        return check(load().gphq_q8gemm_workspace_set_row_scale(self.h, row, float(max_abs)))
+
+    def pack_range(self, x, stride, k0, k1, stream=None):
+        return check(
+            load().gphq_q8gemm_workspace_pack_range(self.h, ptr(x), x.numel(), stride, k0, k1, stream_handle(stream))
+        )
+
+    def pack(self, x, rows, k, stride=None, stream=None):
+        stride = k if stride is None else stride
+        return check(load().gphq_q8gemm_workspace_pack(self.h, ptr(x), x.numel(), rows, k, stride, stream_handle(stream)))
+
+    def row_scales(self, scale, inverse, stream=None):
+        return check(load().gphq_q8gemm_workspace_row_scales(self.h, ptr(scale), ptr(inverse), stream_handle(stream)))
+
+    def activations(self, out, stream=None):
+        return check(load().gphq_q8gemm_workspace_activations(self.h, ptr(out), stream_handle(stream)))
+
+
+def mul_panels(dst, stride, ws, w, p0, p1, stream=None):
+    """q8gemm.MulPanels (gemm.go:228-272)."""
+    return check(load().gphq_q8gemm_mul_panels(ptr(dst), dst.numel(), stride, ws.h, w.h, p0, p1, stream_handle(stream)))
+
+
+def mul_into(dst, x, rows, w, ws, stream=None):
+    """q8gemm.MulInto (gemm.go:274-286)."""
+    return check(load().gphq_q8gemm_mul_into(ptr(dst), dst.numel(), ptr(x), x.numel(), rows, w.h, ws.h, stream_handle(stream)))
+
+
+def mm_workspace_bytes(m, k):
+    return load().gphq_mm_workspace_bytes(m, k)
+
+
+def mm(fmt, codes, scales, x, y, m, k, n, work, zeros=None, stream=None):
+    """qwen3lm mm<PRO_PLAIN, EPI_STORE, fmt> (gpu.metal:766-927) or the GPTQ4_G128 variant."""
+    return check(
+        load().gphq_mm(fmt, ptr(codes), ptr(scales), ptr(zeros), ptr(x), ptr(y), m, k, n, ptr(work),
+                       work.numel() * work.element_size(), stream_handle(stream))
+    )

@@ -175,6 +175,96 @@ int gphq_q8gemm_mul_panels_i8(float *dst_dev, int64_t dst_len, int64_t stride, c
 int gphq_q8gemm_mul_strips_i8(float *dst_dev, int64_t dst_len, int64_t stride, const gphq_workspace_i8 *ws,
                               const gphq_weights_i8 *w, int64_t s0, int64_t s1, void *stream);
 
+/* ---- q8gemm: FP16 activations x int8 or FP16 weights -----------------------
+ * Replaces q8gemm.Weights / Workspace / MulPanels / MulInto
+ * (q8gemm/packed.go:35-239, gemm.go:20-286):
+ *   dst[r*stride + c] = (sum_k f16(x[r,k]*rowScale[r]) * w[c,k]) * scales[c] * rowInverse[r]
+ * with rowScale = 2^e placing each row's max|x| in [2^14, 2^15)
+ * (gemm.go:127-135). Products are exact in fp32; sums are fp32 on MFMA, in an
+ * order of the hardware's (the reference's SME kernel also reorders; its
+ * bound is 2e-5*sqrt(K) relative, q8gemm_test.go:58). Weights live in device
+ * memory in this library's [16 rows][64 K] tile layout. */
+typedef struct gphq_weights gphq_weights;
+typedef struct gphq_workspace gphq_workspace;
+
+/* NewWeights (packed.go:43-61): int8 storage. */
+int gphq_q8gemm_new_weights(int64_t k, int64_t n, gphq_weights **out);
+/* NewWeightsF16 (packed.go:63-76): FP16 storage, filled by pack_bf16. */
+int gphq_q8gemm_new_weights_f16(int64_t k, int64_t n, gphq_weights **out);
+/* WeightsF16Bytes (packed.go:78-93) for this library's device layout; a
+ * negative status for invalid dimensions. */
+int64_t gphq_q8gemm_weights_f16_bytes(int64_t k, int64_t n);
+/* NewWeightsF16Buffer (packed.go:95-121): binds caller-owned zeroed device
+ * storage (4-byte aligned, at least weights_f16_bytes). */
+int gphq_q8gemm_new_weights_f16_buffer(int64_t k, int64_t n, void *data_dev, int64_t data_len, gphq_weights **out);
+void gphq_q8gemm_weights_free(gphq_weights *w);
+/* (*Weights).Pack (packed.go:181-204): int8 row-major [n][k] + fp32 scales. */
+int gphq_q8gemm_weights_pack(gphq_weights *w, const int8_t *q_host, int64_t q_len, const float *scales_host,
+                             int64_t scales_len);
+/* (*Weights).PackBF16 / PackBF16Rows (packed.go:123-175): raw BF16 bits,
+ * row-major; *rounded receives the count of values FP16 could not hold
+ * exactly; GPHQ_ERR_NON_FINITE stops at the first row holding NaN/Inf. */
+int gphq_q8gemm_weights_pack_bf16(gphq_weights *w, const uint16_t *bf16_host, int64_t len, int64_t *rounded);
+int gphq_q8gemm_weights_pack_bf16_rows(gphq_weights *w, const uint16_t *bf16_host, int64_t len, int64_t row0,
+                                       int64_t *rounded);
+/* Dims / Panels / Bytes / F16 (packed.go:206-231). */
+int gphq_q8gemm_weights_dims(const gphq_weights *w, int64_t *k, int64_t *n);
+int64_t gphq_q8gemm_weights_panels(const gphq_weights *w);
+int64_t gphq_q8gemm_weights_bytes(const gphq_weights *w);
+int gphq_q8gemm_weights_is_f16(const gphq_weights *w);
+
+/* NewWorkspace (gemm.go:58-69) with a row capacity. */
+int gphq_q8gemm_new_workspace(int64_t k, int64_t max_rows, gphq_workspace **out);
+void gphq_q8gemm_workspace_free(gphq_workspace *ws);
+/* Prepare (gemm.go:79-89): row scales reset to 1. */
+int gphq_q8gemm_workspace_prepare(gphq_workspace *ws, int64_t rows, int64_t k);
+/* PrepareRowF16 / PrepareRowsF16 (gemm.go:91-122) need the reference's SME
+ * row kernel; without SME (amd64 included) the reference returns
+ * ErrDimensions, and so do these. */
+int gphq_q8gemm_workspace_prepare_row_f16(gphq_workspace *ws, int64_t k);
+int gphq_q8gemm_workspace_prepare_rows_f16(gphq_workspace *ws, int64_t rows, int64_t k);
+/* SetRowScale (gemm.go:124-136). */
+int gphq_q8gemm_workspace_set_row_scale(gphq_workspace *ws, int64_t row, float max_abs);
+/* PackRange (gemm.go:152-226): columns [k0, k1) (multiples of 2 unless
+ * k1 == k) of the prepared rows, f16(x * rowScale). */
+int gphq_q8gemm_workspace_pack_range(gphq_workspace *ws, const float *x_dev, int64_t x_len, int64_t stride,
+                                     int64_t k0, int64_t k1, void *stream);
+/* Pack (gemm.go:71-77): Prepare + SetRowScale(MaxAbs) + PackRange on the
+ * device in one launch. */
+int gphq_q8gemm_workspace_pack(gphq_workspace *ws, const float *x_dev, int64_t x_len, int64_t rows, int64_t k,
+                               int64_t stride, void *stream);
+/* The prepared rows' scales and inverses (device buffers, either NULL). */
+int gphq_q8gemm_workspace_row_scales(const gphq_workspace *ws, float *scale_dev, float *inverse_dev, void *stream);
+/* The packed FP16 activations as row-major [rows][k] bits (inspection;
+ * synchronizes the stream). */
+int gphq_q8gemm_workspace_activations(const gphq_workspace *ws, uint16_t *act_dev, void *stream);
+/* MulPanels (gemm.go:228-272): columns [p0*64, min(p1*64, n)); the portable
+ * path's scratch argument has no counterpart. */
+int gphq_q8gemm_mul_panels(float *dst_dev, int64_t dst_len, int64_t stride, gphq_workspace *ws,
+                           const gphq_weights *w, int64_t p0, int64_t p1, void *stream);
+/* MulInto (gemm.go:274-286): pack `rows` rows of x and multiply all panels. */
+int gphq_q8gemm_mul_into(float *dst_dev, int64_t dst_len, const float *x_dev, int64_t x_len, int64_t rows,
+                         const gphq_weights *w, gphq_workspace *ws, void *stream);
+
+/* ---- qwen3lm batched projection (mm) --------------------------------------
+ * Replaces mm<PRO_PLAIN, EPI_STORE, BITS> (qwen3lm/gpu.metal:766-927, run by
+ * gpuWorkspace.mmRun, gpu_darwin.go:1665-1699): y[M][N] = x[M][K] . W^T with
+ * each K step's weights dequantized to FP16 (Q8: half(code); Q8B:
+ * half(code)*half(d); Q4: (half(nib)-8)*d, each rounded to half), activations
+ * half(x), fp32 accumulation, and Q8 rows scaled by their fp32 scale after
+ * the sum. fmt: GPHQ_FMT_Q8, GPHQ_FMT_Q8B, GPHQ_FMT_Q4, or
+ * GPHQ_FMT_GPTQ4_G128: int32 codes [N][K/8] (nibble i of word j holds k = 8j+i,
+ * unsigned 0..15), FP16 scales [N][K/128] and zero points zeros_dev
+ * u8 [N][K/128] (low nibble), w = (q - z) * s -- the 4-bit group-128
+ * zero-point layout of the benchmark configuration (cmd/qwen3-gptq itself
+ * emits GPHQ_FMT_Q4). k must be a multiple of 32 (128 for GPTQ4_G128).
+ * work_dev is scratch of at least gphq_mm_workspace_bytes(m, k) bytes
+ * (16-byte aligned) for the FP16 activations. */
+#define GPHQ_FMT_GPTQ4_G128 12
+int64_t gphq_mm_workspace_bytes(int64_t m, int64_t k);
+int gphq_mm(int fmt, const void *codes_dev, const void *scales_dev, const uint8_t *zeros_dev, const float *x_dev,
+            float *y_dev, int64_t m, int64_t k, int64_t n, void *work_dev, int64_t work_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -543,3 +543,69 @@ void orc_f16_to_f32_array(const uint16_t *src, float *dst, int64_t n) {
 void orc_i8_quantize_array(const float *src, int8_t *dst, int64_t n) {
     for (int64_t i = 0; i < n; i++) dst[i] = orc_i8_quantize(src[i]);
 }
+
+/* ------------------------------------------------------------------ */
+/* qwen3lm mm semantics (gpu.metal:766-927, PRO_PLAIN / EPI_STORE) and the
+ * group-128 zero-point int4 variant. Each K step's weight tile is FP16:
+ * Q8 half(code) (exact), Q8B half(code)*half(d) and Q4 (half(nib)-8)*d,
+ * rounded to half (gpu.metal:836-861); activations half(x) (gpu.metal:
+ * 828-829, 863-865 with inv = 1). Products of two halves are exact in fp32 and
+ * float64; the sum here is float64 (the bound reference), and Q8 rows are
+ * then scaled by their fp32 scale (gpu.metal:898-899).
+ * fmt 12 (GPTQ4_G128): codes u32 [n][k/8], nibble i of word j = k 8j+i;
+ * scales f16 [n][k/128]; zeros u8 [n][k/128]; w = half((q - z) * s).
+ * Pinned by: the dequantization rule of gpu_darwin_test.go:44-56 (Q4) and
+ * exact float64 products; numpy float16 rounding in tests/test_oracle.py. */
+static float mm_weight(int fmt, const void *codes, const void *scales, const uint8_t *zeros, int64_t row,
+                       int64_t k, int64_t i) {
+    if (fmt == 8) return (float)((const int8_t *)codes)[row * k + i];
+    if (fmt == 9) {
+        float d = orc_f16_to_f32(((const uint16_t *)scales)[row * (k / 32) + i / 32]);
+        float c = (float)((const int8_t *)codes)[row * k + i];
+        return orc_f16_to_f32(orc_f32_to_f16(c * d));
+    }
+    if (fmt == 4) {
+        uint8_t b = ((const uint8_t *)codes)[row * (k / 2) + (i / 32) * 16 + i % 16];
+        int q = (i % 32 >= 16) ? (int)(b >> 4) : (int)(b & 15);
+        float d = orc_f16_to_f32(((const uint16_t *)scales)[row * (k / 32) + i / 32]);
+        return orc_f16_to_f32(orc_f32_to_f16((float)(q - 8) * d));
+    }
+    /* fmt 12 */
+    uint32_t wd = ((const uint32_t *)codes)[row * (k / 8) + i / 8];
+    int q = (int)((wd >> (4 * (i % 8))) & 15);
+    int z = zeros[row * (k / 128) + i / 128] & 15;
+    float s = orc_f16_to_f32(((const uint16_t *)scales)[row * (k / 128) + i / 128]);
+    return orc_f16_to_f32(orc_f32_to_f16((float)(q - z) * s));
+}
+
+void orc_mm_f64(int fmt, const void *codes, const void *scales, const uint8_t *zeros, const float *x, double *y,
+                double *abs_sum, int64_t m, int64_t k, int64_t n) {
+    for (int64_t c = 0; c < n; c++) {
+        for (int64_t r = 0; r < m; r++) {
+            double s = 0.0, a = 0.0;
+            for (int64_t i = 0; i < k; i++) {
+                double p = (double)orc_f16_to_f32(orc_f32_to_f16(x[r * k + i])) *
+                           (double)mm_weight(fmt, codes, scales, zeros, c, k, i);
+                s += p;
+                a += fabs(p);
+            }
+            if (fmt == 8) {
+                double sc = (double)((const float *)scales)[c];
+                s *= sc;
+                a *= fabs(sc);
+            }
+            y[r * n + c] = s;
+            if (abs_sum) abs_sum[r * n + c] = a;
+        }
+    }
+}
+
+/* The group-128 zero-point int4 weights without FP16 rounding, (q - z) * s in
+ * float64: the "true" dequantized matrix the 2e-3 tolerance refers to. */
+double orc_gptq_g128_weight(const uint32_t *codes, const uint16_t *scales, const uint8_t *zeros, int64_t row,
+                            int64_t k, int64_t i) {
+    uint32_t wd = codes[row * (k / 8) + i / 8];
+    int q = (int)((wd >> (4 * (i % 8))) & 15);
+    int z = zeros[row * (k / 128) + i / 128] & 15;
+    return (double)(q - z) * (double)orc_f16_to_f32(scales[row * (k / 128) + i / 128]);
+}

@@ -62,6 +62,7 @@ def _load():
         "orc_f32_to_f16_array": (None, [_f32p, _u16p, _i64]),
         "orc_f16_to_f32_array": (None, [_u16p, _f32p, _i64]),
         "orc_i8_quantize_array": (None, [_f32p, _i8p, _i64]),
+        "orc_mm_f64": (None, [ctypes.c_int, _vp, _vp, _u8p, _f32p, _f64p, _f64p, _i64, _i64, _i64]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -296,3 +297,19 @@ def pack_panels_quads(src, k, n):
     out = np.zeros(panels * quads * 256, dtype=np.int8)
     lib().orc_pack_panels_i8_quads(_p(src, _i8p), k, n, _p(out, _i8p))
     return out
+
+
+FMT_GPTQ4_G128 = 12
+
+
+def mm_f64(fmt, codes, scales, x, m, k, n, zeros=None):
+    """qwen3lm mm semantics (gpu.metal:766-927) in float64 -> (y[m,n], sum|a w|[m,n])."""
+    codes = np.ascontiguousarray(codes)
+    scales = np.ascontiguousarray(scales)
+    x = _c(x, np.float32)
+    z = None if zeros is None else _c(zeros, np.uint8)
+    y = np.zeros((m, n), dtype=np.float64)
+    a = np.zeros((m, n), dtype=np.float64)
+    lib().orc_mm_f64(fmt, codes.ctypes.data, scales.ctypes.data, None if z is None else _p(z, _u8p), _p(x, _f32p),
+                     _p(y, _f64p), _p(a, _f64p), m, k, n)
+    return y, a
