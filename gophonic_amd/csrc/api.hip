@@ -8,6 +8,9 @@ int gemv_launch(int fmt, const void *codes, const void *scales, const float *x, 
                 hipStream_t stream);
 int gemv_batch_launch(int fmt, const void *const *codes, const void *const *scales, const float *const *x,
                       float *const *y, int count, int K, int N, hipStream_t stream);
+size_t gemv_vec_workspace_bytes(int V, int K);
+int gemv_vec_launch(int fmt, const void *codes, const void *scales, const float *x, long xstride, float *y,
+                    long ystride, int V, int K, int N, void *work, hipStream_t stream);
 
 static thread_local int g_last_hip_error = 0;
 void set_hip_error(hipError_t e) { g_last_hip_error = (int)e; }
@@ -69,6 +72,27 @@ int gphq_gemv(int fmt, const void *codes, const void *scales, const float *x, fl
     if (fmt != GPHQ_FMT_Q8 && k && ((uintptr_t)codes % 16 != 0 || (uintptr_t)x % 16 != 0))
         return GPHQ_ERR_DIMENSIONS;
     return gemv_launch(fmt, codes, scales, x, y, (int)k, (int)n, (hipStream_t)stream);
+}
+
+int64_t gphq_gemv_vec_workspace_bytes(int64_t lanes, int64_t k) {
+    if (lanes < 0 || lanes > GPHQ_GEMV_VEC_MAX_LANES || k < 0 || k > INT32_MAX) return GPHQ_ERR_DIMENSIONS;
+    return (int64_t)gemv_vec_workspace_bytes((int)lanes, (int)k);
+}
+
+int gphq_gemv_vec(int fmt, const void *codes, const void *scales, const float *x, int64_t x_stride, float *y,
+                  int64_t y_stride, int64_t lanes, int64_t k, int64_t n, void *work, int64_t work_bytes,
+                  void *stream) {
+    if (fmt != GPHQ_FMT_Q8 && fmt != GPHQ_FMT_Q8B && fmt != GPHQ_FMT_Q8B_F32 && fmt != GPHQ_FMT_Q4)
+        return GPHQ_ERR_UNSUPPORTED;
+    if (lanes < 0 || lanes > GPHQ_GEMV_VEC_MAX_LANES || k < 0 || n < 0 || k > INT32_MAX || n > INT32_MAX)
+        return GPHQ_ERR_DIMENSIONS;
+    if (k % 32 != 0 || x_stride < k || y_stride < n) return GPHQ_ERR_DIMENSIONS;
+    if (lanes == 0 || n == 0) return GPHQ_OK;
+    if (work_bytes < gphq_gemv_vec_workspace_bytes(lanes, k)) return GPHQ_ERR_DIMENSIONS;
+    if (!y || !scales || !work || (uintptr_t)work % 16 != 0) return GPHQ_ERR_DIMENSIONS;
+    if (k && (!codes || !x || (uintptr_t)codes % 16 != 0)) return GPHQ_ERR_DIMENSIONS;
+    return gemv_vec_launch(fmt, codes, scales, x, (long)x_stride, y, (long)y_stride, (int)lanes, (int)k, (int)n, work,
+                           (hipStream_t)stream);
 }
 
 int gphq_gemv_batch(int fmt, const void *const *codes, const void *const *scales, const float *const *x,

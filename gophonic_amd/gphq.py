@@ -35,6 +35,8 @@ SIGNATURES = {
     "gphq_q8gemv_mul_into": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "gphq_gemv": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "gphq_gemv_batch": (ctypes.c_int, [ctypes.c_int, _vpp, _vpp, _vpp, _vpp, ctypes.c_int, _i64, _i64, _vp]),
+    "gphq_gemv_vec_workspace_bytes": (_i64, [_i64, _i64]),
+    "gphq_gemv_vec": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "gphq_q8gemm_new_weights_i8": (ctypes.c_int, [_i64, _i64, _vpp]),
     "gphq_q8gemm_weights_i8_free": (None, [_vp]),
     "gphq_q8gemm_weights_i8_pack": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64]),
@@ -418,4 +420,21 @@ def mm(fmt, codes, scales, x, y, m, k, n, work, zeros=None, stream=None):
     return check(
         load().gphq_mm(fmt, ptr(codes), ptr(scales), ptr(zeros), ptr(x), ptr(y), m, k, n, ptr(work),
                        work.numel() * work.element_size(), stream_handle(stream))
+    )
+
+
+GEMV_VEC_MAX_LANES = 32
+
+
+def gemv_vec_workspace_bytes(lanes, k):
+    return load().gphq_gemv_vec_workspace_bytes(lanes, k)
+
+
+def gemv_vec(fmt, codes, scales, x, y, lanes, k, n, work, x_stride=None, y_stride=None, stream=None):
+    """Multi-vector GEMV (qwen3lm gemvQ8BVector<V>, gpu.metal:239-314): x [lanes][k] -> y [lanes][n]."""
+    x_stride = k if x_stride is None else x_stride
+    y_stride = n if y_stride is None else y_stride
+    return check(
+        load().gphq_gemv_vec(fmt, ptr(codes), ptr(scales), ptr(x), x_stride, ptr(y), y_stride, lanes, k, n, ptr(work),
+                             work.numel() * work.element_size(), stream_handle(stream))
     )

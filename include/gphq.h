@@ -101,6 +101,24 @@ int gphq_gemv(int fmt, const void *codes_dev, const void *scales_dev, const floa
  * command buffer (qwen3lm/gpu_projection_stream_darwin_test.go:75-90); one
  * launch amortizes the fixed launch cost over all of them. Q8 here needs
  * k % 16 == 0. Outputs must not overlap each other or any input. */
+/* Multi-vector GEMV: `lanes` input vectors share one read of the weights,
+ * y_dev[v*y_stride + j] = sum_k dequant(W)[j,k] * x_dev[v*x_stride + k].
+ * Replaces gemvQ8BVector<V> (qwen3lm/gpu.metal:239-314) with its host side
+ * gpuDecodeBatchWorkspace.gemv (gpu_darwin.go:1121-1159); any lanes in
+ * 1..GPHQ_GEMV_VEC_MAX_LANES (the reference caps V at 8, decode_batch.go:31-33).
+ * Formats Q8, Q8B, Q8B_F32, Q4; k % 32 == 0. The vectors are split into FP16
+ * hi+lo parts after an exact power-of-two scaling and multiplied on MFMA
+ * (products exact, fp32 sums), so results agree with gphq_gemv to the
+ * reference's vector-vs-serial bound (1e-4 abs, 1e-5 rel,
+ * gpu_vector_batch_darwin_test.go:218) but not bit for bit. work_dev: scratch
+ * of at least gphq_gemv_vec_workspace_bytes(lanes, k) bytes, 16-byte aligned.
+ * A NaN or Inf in a vector makes that vector's outputs NaN. */
+#define GPHQ_GEMV_VEC_MAX_LANES 32
+int64_t gphq_gemv_vec_workspace_bytes(int64_t lanes, int64_t k);
+int gphq_gemv_vec(int fmt, const void *codes_dev, const void *scales_dev, const float *x_dev, int64_t x_stride,
+                  float *y_dev, int64_t y_stride, int64_t lanes, int64_t k, int64_t n, void *work_dev,
+                  int64_t work_bytes, void *stream);
+
 #define GPHQ_GEMV_MAX_BATCH 32
 int gphq_gemv_batch(int fmt, const void *const *codes_dev, const void *const *scales_dev,
                     const float *const *x_dev, float *const *y_dev, int count, int64_t k, int64_t n,
