@@ -36,6 +36,29 @@ const char *gphq_error_string(int status) {
         return "gphq: HIP runtime error";
     case GPHQ_ERR_UNSUPPORTED:
         return "gphq: unsupported format or mode";
+    case GPHQ_ERR_GEOMETRY:
+        return "qwen3: the GPU backend needs 128-wide heads, at most 8 query heads per key/value head, and 64-aligned "
+               "widths";
+    case GPHQ_ERR_FOREIGN_WORKSPACE:
+        return "qwen3: nil, closed, or foreign decode batch workspace";
+    case GPHQ_ERR_BATCH_SHAPE:
+        return "qwen3: decode batch has mismatched prefixes, tokens, hidden rows, logits rows, and next tokens";
+    case GPHQ_ERR_LANE_CAPACITY:
+        return "qwen3: decode batch lanes outside the workspace capacity";
+    case GPHQ_ERR_FOREIGN_PREFIX:
+        return "qwen3: decode prefix is nil, closed, or belongs to another evaluator";
+    case GPHQ_ERR_DUPLICATE_PREFIX:
+        return "qwen3: decode prefix is duplicated";
+    case GPHQ_ERR_PREFIX_FULL:
+        return "qwen3: decode prefix has no room for another token";
+    case GPHQ_ERR_TOKEN_RANGE:
+        return "qwen3: token in decode lane is outside vocabulary";
+    case GPHQ_ERR_OVERLAP:
+        return "qwen3: decode batch destinations overlap inputs";
+    case GPHQ_ERR_NON_FINITE_HIDDEN:
+        return "qwen3: non-finite batched hidden state";
+    case GPHQ_ERR_MODEL_INCOMPLETE:
+        return "qwen3: batched token decode requires a loaded language-model head; call LoadHead first";
     }
     return "gphq: unknown status";
 }

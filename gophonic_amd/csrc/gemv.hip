@@ -44,7 +44,17 @@ struct GemvBatch {
     GemvSet set[MAXB];
     int K;
     int N;
+    float eps;  // PRO_NORM only
 };
+
+// Prologue and epilogue of the decode-step GEMVs (qwen3lm/gpu.metal:63-64,
+// 72-80, 131-161). PRO_NORM scales the result by 1/sqrt(mean(x^2) + eps),
+// the RMSNorm of the input whose weight is folded into the rows; the sum of
+// squares comes from the x values the block already holds in registers.
+// EPI_ADD adds the result into y (the residual stream). EPI_SWIGLU takes
+// rows 2i (gate) and 2i+1 (up) and stores g/(1+exp(-g))*u at y[i].
+enum { PRO_PLAIN = 0, PRO_NORM = 1 };
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
 
 __device__ __forceinline__ float sext_byte_f(uint32_t v, int i) {
     return (float)((int32_t)(v << (24 - 8 * i)) >> 24);
@@ -74,28 +84,56 @@ __device__ __forceinline__ float block_scale(const void *scales, size_t idx) {
     }
 }
 
-// Adds the SK slice totals of each row (in slice order) and stores y.
-template <int FMT, int ROWS, int SK>
-__device__ __forceinline__ void finish_rows(float (*part)[SK], const GemvSet &s, int rowBlock, int N) {
+// Adds the SK slice totals of each row (in slice order), applies the
+// prologue's norm factor, the Q8 row scale and the epilogue. pss holds the SK
+// slice sums of x^2 (PRO_NORM).
+template <int FMT, int PRO, int EPI, int ROWS, int SK>
+__device__ __forceinline__ void finish_rows(float (*part)[SK], const float *pss, const GemvSet &s, int rowBlock,
+                                            int N, int K, float eps) {
     __syncthreads();
-    if ((int)threadIdx.x < ROWS) {
+    float inv = 1.0f;
+    if constexpr (PRO == PRO_NORM) {
+        float ss = pss[0];
+#pragma unroll
+        for (int i = 1; i < SK; ++i) ss += pss[i];
+        inv = 1.0f / sqrtf(ss / (float)K + eps);
+    }
+    auto total = [&](int r, int row) {
+        float t = part[r][0];
+#pragma unroll
+        for (int i = 1; i < SK; ++i) t += part[r][i];
+        t = t * inv;
+        if constexpr (FMT == GPHQ_FMT_Q8) t = t * ((const float *)s.scales)[row];
+        return t;
+    };
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int r = 2 * (int)threadIdx.x;
+        if (r < ROWS) {
+            const int row = rowBlock + r;
+            if (row + 1 < N) {
+                const float g = total(r, row), u = total(r + 1, row + 1);
+                s.y[row >> 1] = g / (1.0f + expf(-g)) * u;
+            }
+        }
+    } else if ((int)threadIdx.x < ROWS) {
         const int row = rowBlock + threadIdx.x;
         if (row < N) {
-            float t = part[threadIdx.x][0];
-#pragma unroll
-            for (int i = 1; i < SK; ++i) t += part[threadIdx.x][i];
-            if constexpr (FMT == GPHQ_FMT_Q8) t = t * ((const float *)s.scales)[row];
-            s.y[row] = t;
+            const float t = total(threadIdx.x, row);
+            if constexpr (EPI == EPI_ADD)
+                s.y[row] += t;
+            else
+                s.y[row] = t;
         }
     }
 }
 
 // 8-bit codes (Q8, Q8B, Q8B_F32). Requires K % 16 == 0, 16-byte aligned codes
 // and x (every row then starts 16-byte aligned).
-template <int FMT, int RW, int SK, int WPB, int MAXB>
+template <int FMT, int RW, int SK, int WPB, int MAXB, int PRO = PRO_PLAIN, int EPI = EPI_STORE>
 __global__ __launch_bounds__(64 * WPB) void gemv8_kernel(const GemvBatch<MAXB> b) {
     constexpr int RG = WPB / SK;
     __shared__ float part[RG * RW][SK];
+    __shared__ float pss[SK];
     const GemvSet s = b.set[blockIdx.y];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
@@ -112,6 +150,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv8_kernel(const GemvBatch<MAXB> b
     float acc[RW];
 #pragma unroll
     for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+    float ss = 0.0f;
 
     for (int st = 0; st < steps; ++st) {
         const int k0 = (ks * steps + st) * 1024 + lane * 16;
@@ -119,6 +158,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv8_kernel(const GemvBatch<MAXB> b
         float4 xr[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) xr[i] = ok ? *((const float4 *)(s.x + k0) + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ss += xr[i].x * xr[i].x + xr[i].y * xr[i].y + xr[i].z * xr[i].z + xr[i].w * xr[i].w;
+        }
         float d[RW];
         if constexpr (FMT != GPHQ_FMT_Q8) {
 #pragma unroll
@@ -142,15 +185,20 @@ __global__ __launch_bounds__(64 * WPB) void gemv8_kernel(const GemvBatch<MAXB> b
         const float t = wave_sum(acc[r]);
         if (lane == 0) part[rg * RW + r][ks] = t;
     }
-    finish_rows<FMT, RG * RW, SK>(part, s, rowBlock, b.N);
+    if constexpr (PRO == PRO_NORM) {
+        ss = wave_sum(ss);
+        if (rg == 0 && lane == 0) pss[ks] = ss;
+    }
+    finish_rows<FMT, PRO, EPI, RG * RW, SK>(part, pss, s, rowBlock, b.N, K, b.eps);
 }
 
 // 4-bit split-nibble codes; requires K % 32 == 0. Lane l takes the 32-value
 // block (step * 64 + l): 16 code bytes and 32 activations.
-template <int RW, int SK, int WPB, int MAXB>
+template <int RW, int SK, int WPB, int MAXB, int PRO = PRO_PLAIN, int EPI = EPI_STORE>
 __global__ __launch_bounds__(64 * WPB) void gemv4_kernel(const GemvBatch<MAXB> b) {
     constexpr int RG = WPB / SK;
     __shared__ float part[RG * RW][SK];
+    __shared__ float pss[SK];
     const GemvSet s = b.set[blockIdx.y];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
@@ -168,6 +216,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv4_kernel(const GemvBatch<MAXB> b
     float acc[RW];
 #pragma unroll
     for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+    float ss = 0.0f;
 
     for (int st = 0; st < steps; ++st) {
         const int k0 = (ks * steps + st) * 2048 + lane * 32;
@@ -175,6 +224,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv4_kernel(const GemvBatch<MAXB> b
         float4 xs[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) xs[i] = ok ? *((const float4 *)(s.x + k0) + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += xs[i].x * xs[i].x + xs[i].y * xs[i].y + xs[i].z * xs[i].z + xs[i].w * xs[i].w;
+        }
         float d[RW];
 #pragma unroll
         for (int r = 0; r < RW; ++r) d[r] = ok ? block_scale<GPHQ_FMT_Q4>(s.scales, (size_t)rows[r] * kb + (k0 >> 5)) : 0.0f;
@@ -209,7 +262,11 @@ __global__ __launch_bounds__(64 * WPB) void gemv4_kernel(const GemvBatch<MAXB> b
         const float t = wave_sum(acc[r]);
         if (lane == 0) part[rg * RW + r][ks] = t;
     }
-    finish_rows<GPHQ_FMT_Q4, RG * RW, SK>(part, s, rowBlock, b.N);
+    if constexpr (PRO == PRO_NORM) {
+        ss = wave_sum(ss);
+        if (rg == 0 && lane == 0) pss[ks] = ss;
+    }
+    finish_rows<GPHQ_FMT_Q4, PRO, EPI, RG * RW, SK>(part, pss, s, rowBlock, b.N, K, b.eps);
 }
 
 // Any K, any alignment (Q8 only): one wavefront per row, lanes stride through
@@ -285,6 +342,50 @@ int gemv_batch_launch(int fmt, const void *const *codes, const void *const *scal
     b.K = K;
     b.N = N;
     return launch_batch<kMaxBatch>(fmt, b, count, stream);
+}
+
+template <int PRO, int EPI>
+static int launch_fused(int fmt, const GemvBatch<1> &b, hipStream_t stream) {
+    const unsigned rowsPerBlock = fmt == GPHQ_FMT_Q4 ? kRowsPerBlock4 : kRowsPerBlock;
+    const dim3 grid((unsigned)((b.N + rowsPerBlock - 1) / rowsPerBlock));
+    switch (fmt) {
+    case GPHQ_FMT_Q8:
+        hipLaunchKernelGGL((gemv8_kernel<GPHQ_FMT_Q8, kRW, kSK, kWPB, 1, PRO, EPI>), grid, dim3(64 * kWPB), 0, stream,
+                           b);
+        break;
+    case GPHQ_FMT_Q8B:
+        hipLaunchKernelGGL((gemv8_kernel<GPHQ_FMT_Q8B, kRW, kSK, kWPB, 1, PRO, EPI>), grid, dim3(64 * kWPB), 0, stream,
+                           b);
+        break;
+    case GPHQ_FMT_Q8B_F32:
+        hipLaunchKernelGGL((gemv8_kernel<GPHQ_FMT_Q8B_F32, kRW, kSK, kWPB, 1, PRO, EPI>), grid, dim3(64 * kWPB), 0,
+                           stream, b);
+        break;
+    case GPHQ_FMT_Q4:
+        hipLaunchKernelGGL((gemv4_kernel<kRW4, kSK4, kWPB4, 1, PRO, EPI>), grid, dim3(64 * kWPB4), 0, stream, b);
+        break;
+    default:
+        return GPHQ_ERR_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
+// One decode-step GEMV with a fused prologue/epilogue (pro: PRO_*, epi:
+// EPI_*). K % 32 == 0, codes and x 16-byte aligned; for EPI_SWIGLU N is even
+// and y receives N/2 values. Arguments were validated by the caller.
+int gemv_fused_launch(int fmt, int pro, int epi, const void *codes, const void *scales, const float *x, float *y,
+                      int K, int N, float eps, hipStream_t stream) {
+    if (N == 0) return GPHQ_OK;
+    GemvBatch<1> b{};
+    b.set[0] = GemvSet{codes, scales, x, y};
+    b.K = K;
+    b.N = N;
+    b.eps = eps;
+    if (pro == PRO_PLAIN && epi == EPI_STORE) return launch_fused<PRO_PLAIN, EPI_STORE>(fmt, b, stream);
+    if (pro == PRO_NORM && epi == EPI_STORE) return launch_fused<PRO_NORM, EPI_STORE>(fmt, b, stream);
+    if (pro == PRO_PLAIN && epi == EPI_ADD) return launch_fused<PRO_PLAIN, EPI_ADD>(fmt, b, stream);
+    if (pro == PRO_NORM && epi == EPI_SWIGLU) return launch_fused<PRO_NORM, EPI_SWIGLU>(fmt, b, stream);
+    return GPHQ_ERR_UNSUPPORTED;
 }
 
 }  // namespace gphq

@@ -17,6 +17,12 @@
 //   * K is split over wavefronts; partial sums meet in LDS in slice order;
 //     y[v][n] = (acc_hi + acc_lo) * 2^-e_v (Q8: times the row scale).
 // VALU work per weight no longer grows with V.
+//
+// Decode-step forms (gemv_vec_fused_launch): with norm set, the prep pass
+// also sums x^2 and folds 1/sqrt(mean(x^2) + eps) into the vector's output
+// scale (PRO_NORM, gpu.metal:251-261); the epilogue stores, adds into y
+// (EPI_ADD) or pairs interleaved gate/up rows into g/(1+exp(-g))*u
+// (EPI_SWIGLU, gpu.metal:284-290), as gemvQ8BVector does per vector.
 #include "common.h"
 
 namespace gphq {
@@ -34,13 +40,16 @@ __host__ __device__ inline size_t vec_a_offset(int t, int kb, int KB, int lane) 
 }
 
 // One block per vector: power-of-two scale, hi/lo split, A-fragment layout.
+// With norm, inv also carries 1/sqrt(mean(x^2) + eps).
 __global__ __launch_bounds__(256) void vec_prep_kernel(const float *__restrict__ x, long stride, int V, int K, int KB,
-                                                       _Float16 *__restrict__ A, float *__restrict__ inv) {
+                                                       _Float16 *__restrict__ A, float *__restrict__ inv, int norm,
+                                                       float eps) {
     __shared__ float smax[4];
     __shared__ int snan[4];
+    __shared__ float sss[4];
     const int v = blockIdx.x;
     const float *xv = x + (size_t)v * stride;
-    float m = 0.0f;
+    float m = 0.0f, ss = 0.0f;
     int nan = 0;
     constexpr int UNR = 8;
     for (int k0 = 0; k0 < K; k0 += 256 * UNR) {
@@ -54,15 +63,18 @@ __global__ __launch_bounds__(256) void vec_prep_kernel(const float *__restrict__
         for (int u = 0; u < UNR; ++u) {
             nan |= (t[u] != t[u]);
             m = fmaxf(m, fabsf(t[u]));
+            ss += t[u] * t[u];
         }
     }
     for (int off = 32; off > 0; off >>= 1) {
         m = fmaxf(m, __shfl_xor(m, off));
         nan |= __shfl_xor(nan, off);
     }
+    ss = wave_sum(ss);
     if ((threadIdx.x & 63) == 0) {
         smax[threadIdx.x >> 6] = m;
         snan[threadIdx.x >> 6] = nan;
+        sss[threadIdx.x >> 6] = ss;
     }
     __syncthreads();
     float mm = 0.0f;
@@ -78,7 +90,11 @@ __global__ __launch_bounds__(256) void vec_prep_kernel(const float *__restrict__
         e = min(max(15 - ex, -100), 100);
     }
     const float s = ldexpf(1.0f, e);
-    if (threadIdx.x == 0) inv[v] = ldexpf(1.0f, -e);
+    if (threadIdx.x == 0) {
+        float f = ldexpf(1.0f, -e);
+        if (norm) f = f / sqrtf(((sss[0] + sss[1]) + (sss[2] + sss[3])) / (float)K + eps);
+        inv[v] = f;
+    }
     // Each thread writes one 8-value chunk of row 2v (hi) and of row 2v+1 (lo).
     const int rowHi = 2 * v, rowLo = 2 * v + 1;
     for (int c = threadIdx.x; c < KB * 4; c += blockDim.x) {
@@ -111,7 +127,9 @@ __device__ __forceinline__ _Float16 sext8h(uint32_t v, int i) { return (_Float16
 
 // MT M-tiles (16 A rows each = 8 vectors), SK K-slices per block, RG groups of
 // 16 weight rows per block.
-template <int FMT, int MT, int SK, int RG>
+enum { VEC_STORE = 0, VEC_ADD = 1, VEC_SWIGLU = 2 };
+
+template <int FMT, int MT, int SK, int RG, int EPI = VEC_STORE>
 __global__ __launch_bounds__(64 * SK * RG) void gemv_vec_kernel(const VecArgs a) {
     __shared__ f32x4 red[SK * RG * MT * 64];
     const int lane = threadIdx.x & 63;
@@ -174,16 +192,23 @@ __global__ __launch_bounds__(64 * SK * RG) void gemv_vec_kernel(const VecArgs a)
         for (int q = 1; q < SK; ++q) s += red[((rg * SK + q) * MT + t) * 64 + lane];
         // Rows 4*(l/16)+i of tile t: pairs (hi, lo) of vectors t*8 + 2*(l/16) + {0, 1}.
         const int col = n0 + (lane & 15);
-        if (col >= a.N) continue;
         float rs = 1.0f;
-        if constexpr (FMT == GPHQ_FMT_Q8) rs = ((const float *)a.scales)[col];
+        if constexpr (FMT == GPHQ_FMT_Q8) rs = ((const float *)a.scales)[min(col, a.N - 1)];
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const int v = t * 8 + 2 * (lane >> 4) + p;
-            if (v < a.V) {
-                float val = (s[2 * p] + s[2 * p + 1]) * a.inv[v];
-                if constexpr (FMT == GPHQ_FMT_Q8) val *= rs;
-                a.y[(size_t)v * a.ystride + col] = val;
+            float val = (s[2 * p] + s[2 * p + 1]) * a.inv[min(v, a.V - 1)];
+            if constexpr (FMT == GPHQ_FMT_Q8) val *= rs;
+            if constexpr (EPI == VEC_SWIGLU) {
+                // Lane l^1 holds column col^1: the up row of gate row col.
+                const float u = __shfl_xor(val, 1);
+                if (v < a.V && col < a.N && (col & 1) == 0)
+                    a.y[(size_t)v * a.ystride + (col >> 1)] = val / (1.0f + expf(-val)) * u;
+            } else if (v < a.V && col < a.N) {
+                if constexpr (EPI == VEC_ADD)
+                    a.y[(size_t)v * a.ystride + col] += val;
+                else
+                    a.y[(size_t)v * a.ystride + col] = val;
             }
         }
     }
@@ -195,22 +220,22 @@ size_t gemv_vec_workspace_bytes(int V, int K) {
     return (size_t)MT * KB * 1024 + (size_t)kMaxVecLanes * 4 + 256;
 }
 
-template <int FMT, int MT>
+template <int FMT, int MT, int EPI>
 static int launch_vec(const VecArgs &a, hipStream_t stream) {
     constexpr int SK = 4, RG = 2;
     const unsigned blocks = (unsigned)((a.N + 16 * RG - 1) / (16 * RG));
-    hipLaunchKernelGGL((gemv_vec_kernel<FMT, MT, SK, RG>), dim3(blocks), dim3(64 * SK * RG), 0, stream, a);
+    hipLaunchKernelGGL((gemv_vec_kernel<FMT, MT, SK, RG, EPI>), dim3(blocks), dim3(64 * SK * RG), 0, stream, a);
     return launch_status();
 }
 
-template <int FMT>
+template <int FMT, int EPI = VEC_STORE>
 static int launch_vec_fmt(const VecArgs &a, hipStream_t stream) {
     const int MT = (2 * a.V + 15) / 16;
     switch (MT) {
-    case 1: return launch_vec<FMT, 1>(a, stream);
-    case 2: return launch_vec<FMT, 2>(a, stream);
-    case 3: return launch_vec<FMT, 3>(a, stream);
-    case 4: return launch_vec<FMT, 4>(a, stream);
+    case 1: return launch_vec<FMT, 1, EPI>(a, stream);
+    case 2: return launch_vec<FMT, 2, EPI>(a, stream);
+    case 3: return launch_vec<FMT, 3, EPI>(a, stream);
+    case 4: return launch_vec<FMT, 4, EPI>(a, stream);
     }
     return GPHQ_ERR_UNSUPPORTED;
 }
@@ -225,7 +250,7 @@ int gemv_vec_launch(int fmt, const void *codes, const void *scales, const float 
     float *inv = (float *)((char *)work + (size_t)MT * KB * 1024);
     // A rows past 2V in the last M-tile are never written; they only feed the
     // matching C rows, which are never stored.
-    hipLaunchKernelGGL(vec_prep_kernel, dim3(V), dim3(256), 0, stream, x, xstride, V, K, KB, A, inv);
+    hipLaunchKernelGGL(vec_prep_kernel, dim3(V), dim3(256), 0, stream, x, xstride, V, K, KB, A, inv, 0, 0.0f);
     GPHQ_TRY(launch_status());
     VecArgs a{codes, scales, A, inv, y, ystride, V, K, N, KB};
     switch (fmt) {
@@ -235,6 +260,36 @@ int gemv_vec_launch(int fmt, const void *codes, const void *scales, const float 
     case GPHQ_FMT_Q4: return launch_vec_fmt<GPHQ_FMT_Q4>(a, stream);
     }
     return GPHQ_ERR_UNSUPPORTED;
+}
+
+template <int EPI>
+static int launch_vec_epi(int fmt, const VecArgs &a, hipStream_t stream) {
+    switch (fmt) {
+    case GPHQ_FMT_Q8: return launch_vec_fmt<GPHQ_FMT_Q8, EPI>(a, stream);
+    case GPHQ_FMT_Q8B: return launch_vec_fmt<GPHQ_FMT_Q8B, EPI>(a, stream);
+    case GPHQ_FMT_Q8B_F32: return launch_vec_fmt<GPHQ_FMT_Q8B_F32, EPI>(a, stream);
+    case GPHQ_FMT_Q4: return launch_vec_fmt<GPHQ_FMT_Q4, EPI>(a, stream);
+    }
+    return GPHQ_ERR_UNSUPPORTED;
+}
+
+// Decode-step multi-vector GEMV: norm (0/1) selects PRO_NORM, epi is 0 store,
+// 1 add, 2 SwiGLU (y then holds N/2 values per vector). V <= kMaxVecLanes,
+// K % 32 == 0; validated by the caller.
+int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const void *scales, const float *x,
+                          long xstride, float *y, long ystride, int V, int K, int N, float eps, void *work,
+                          hipStream_t stream) {
+    if (N == 0 || V == 0) return GPHQ_OK;
+    const int KB = (K + 31) / 32;
+    const int MT = (2 * V + 15) / 16;
+    _Float16 *A = (_Float16 *)work;
+    float *inv = (float *)((char *)work + (size_t)MT * KB * 1024);
+    hipLaunchKernelGGL(vec_prep_kernel, dim3(V), dim3(256), 0, stream, x, xstride, V, K, KB, A, inv, norm, eps);
+    GPHQ_TRY(launch_status());
+    VecArgs a{codes, scales, A, inv, y, ystride, V, K, N, KB};
+    if (epi == VEC_ADD) return launch_vec_epi<VEC_ADD>(fmt, a, stream);
+    if (epi == VEC_SWIGLU) return launch_vec_epi<VEC_SWIGLU>(fmt, a, stream);
+    return launch_vec_epi<VEC_STORE>(fmt, a, stream);
 }
 
 }  // namespace gphq

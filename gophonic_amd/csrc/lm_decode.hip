@@ -1,0 +1,1069 @@
+// qwen3lm GPU decode provider on MI355X: the lane API of the reference's Metal
+// backend (gpuModel / gpuPrefix / gpuDecodeBatchWorkspace,
+// qwen3lm/gpu_darwin.go:62-102, 800-893, 731-759, 1046-1281) rebuilt for one
+// gfx950 GPU.
+//
+// A step keeps everything on the device. The reference embeds tokens, applies
+// the final norm and rotates on the host between two command buffers per step
+// (gpu_darwin.go:1168-1258). Here:
+//   * tokens and positions live in device memory. A "seed" kernel sets them
+//     from the host arguments, and the argmax kernel writes each lane's next
+//     token and advances its position. So one step's launch sequence is
+//     identical from step to step, and a run of greedy steps needs no host
+//     round trip (it can be replayed as a HIP graph);
+//   * embedding gather + hidden rotation, final norm + rotations and the
+//     argmax are kernels;
+//   * per layer: QKV GEMV with the input RMSNorm fused (PRO_NORM),
+//     attention, O GEMV added into the residual, gate/up GEMV with norm and
+//     SwiGLU, the down input's Hadamard for Q8/Q4 weights, and the down GEMV
+//     added into the residual (gpu.metal:1-14 describes the same six
+//     dispatches);
+//   * attention splits each lane's context 0..pos over `splits` blocks per KV
+//     head (one launch fills the chip even at one lane). Each block runs a
+//     streaming softmax over its keys for all query heads of the KV head and
+//     writes a partial (max, sum, weighted V). The last block to finish,
+//     found with a device-scope counter, merges the partials in split order,
+//     so the result does not depend on which block finishes last.
+// Single-lane steps use the fp32 register GEMV (gemv.hip); steps with two or
+// more lanes use the multi-vector MFMA GEMV (gemv_vec.hip), which reads each
+// weight once for all lanes.
+#include <math.h>
+
+#include <vector>
+
+#include "common.h"
+
+namespace gphq {
+int gemv_fused_launch(int fmt, int pro, int epi, const void *codes, const void *scales, const float *x, float *y,
+                      int K, int N, float eps, hipStream_t stream);
+int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const void *scales, const float *x,
+                          long xstride, float *y, long ystride, int V, int K, int N, float eps, void *work,
+                          hipStream_t stream);
+size_t gemv_vec_workspace_bytes(int V, int K);
+}  // namespace gphq
+
+using namespace gphq;
+
+namespace {
+
+constexpr int kMaxLanes = GPHQ_DECODE_MAX_LANES;
+constexpr int kHeadDim = 128;
+constexpr int kPart = 2 + kHeadDim;  // one attention partial: max, sum, weighted V
+constexpr int kMaxSplits = 64;
+constexpr int kArgmaxBlocks = 64;
+constexpr int kMaxRotation = 4096;  // qwen3lm/hadamard.go:11
+constexpr int kMaxWidth = 16384;    // hidden and intermediate widths (LDS)
+
+enum { PRO_PLAIN = 0, PRO_NORM = 1 };
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
+
+// hadamard.go:24-47 newRotation: the block is the largest power of two up
+// to 4096 dividing k; sign i comes from the low bit of the i-th splitmix64
+// output with the state seeded by golden ^ k. Returns sign*scale per value
+// (multiplying by +-1 is exact, so x*(sign*scale) == (x*scale)*sign).
+int rotation_signs(int64_t k, std::vector<float> &out) {
+    int64_t block = 1;
+    while (block < kMaxRotation && k % (2 * block) == 0) block *= 2;
+    const float scale = (float)(1.0 / sqrt((double)block));
+    uint64_t state = 0x9e3779b97f4a7c15ull ^ (uint64_t)k;
+    out.resize(k);
+    for (int64_t i = 0; i < k; ++i) {
+        state += 0x9e3779b97f4a7c15ull;
+        uint64_t z = state;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        z ^= z >> 31;
+        out[i] = (z & 1) ? -scale : scale;
+    }
+    return (int)block;
+}
+
+// Bytes of one stored matrix's codes and scales (gpu_darwin.go:251-264).
+void matrix_bytes(int fmt, int64_t rows, int64_t k, int64_t *codes, int64_t *scales) {
+    *codes = fmt == GPHQ_FMT_Q4 ? rows * k / 2 : rows * k;
+    if (fmt == GPHQ_FMT_Q8)
+        *scales = 4 * rows;
+    else if (fmt == GPHQ_FMT_Q8B_F32)
+        *scales = 4 * rows * (k / 32);
+    else
+        *scales = 2 * rows * (k / 32);
+}
+
+int64_t align256(int64_t n) { return (n + 255) & ~(int64_t)255; }
+
+}  // namespace
+
+struct gphq_lm {
+    gphq_lm_config cfg;
+    int64_t qd, kvd, group, hblock, iblock, positions;
+    std::vector<gphq_lm_layer> layers;
+    std::vector<char> bound;
+    float *norms = nullptr;   // [layers][2][128]: q_norm, k_norm
+    float *rope = nullptr;    // [2][positions][64]: cos, then sin
+    float *hsigns = nullptr;  // hidden rotation sign*scale [hidden]
+    float *isigns = nullptr;  // intermediate rotation sign*scale [inter]
+    float *final_norm = nullptr;
+    const uint16_t *embed = nullptr;
+    const uint8_t *head = nullptr;
+    int64_t head_scale = 0, head_rows = 0;
+};
+
+struct gphq_prefix {
+    const gphq_lm *lm;
+    float *kc = nullptr, *vc = nullptr;  // [layers][capacity][kvd]
+    int64_t capacity = 0;
+};
+
+struct gphq_decode_batch {
+    const gphq_lm *lm;
+    int capacity;
+    float *h, *qkv, *ctx, *act, *hn, *hidden, *logits, *part;
+    unsigned *attn_cnt, *argmax_cnt;
+    uint32_t *akey, *aidx;
+    int32_t *tok, *pos, *start, *nonfinite;
+    void *vec_work;
+    size_t vec_bytes;
+    int vec_min_lanes = 2;  // lane count from which GEMVs use the MFMA multi-vector kernel
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+// ---- kernels ---------------------------------------------------------------
+
+// In-place unnormalized Walsh-Hadamard transform of each `block` run of
+// v[0..n), stage h = 1, 2, 4, ...: the butterfly network of hadamard.go:62-78
+// (each stage's butterflies are independent, so the fp32 result equals the
+// sequential network's bit for bit). All threads of the block take part.
+__device__ void lds_fwht(float *v, int n, int block) {
+    const int halfBlock = block >> 1;
+    for (int h = 1; h < block; h <<= 1) {
+        for (int idx = threadIdx.x; idx < (n >> 1); idx += blockDim.x) {
+            const int b = idx / halfBlock, i = idx - b * halfBlock;
+            const int j = b * block + (i / h) * 2 * h + (i % h);
+            const float a = v[j], c = v[j + h];
+            v[j] = a + c;
+            v[j + h] = a - c;
+        }
+        __syncthreads();
+    }
+}
+
+// Deterministic block sum (fixed tree over the block's waves).
+__device__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+struct SeedArgs {
+    int32_t tok[kMaxLanes];
+    int32_t pos[kMaxLanes];
+    int lanes;
+    int32_t *tok_dev, *pos_dev, *start_dev;
+};
+
+__global__ void lm_seed_kernel(const SeedArgs a) {
+    const int l = threadIdx.x;
+    if (l < a.lanes) {
+        a.tok_dev[l] = a.tok[l];
+        a.pos_dev[l] = a.pos[l];
+        a.start_dev[l] = a.pos[l];
+    }
+}
+
+// One block per lane: h = R . float32(bf16 embedding row of the lane's token)
+// (weights.go:614-619 embedRow, then rotation.apply, gpu_darwin.go:1172-1174).
+__global__ __launch_bounds__(1024) void lm_embed_kernel(const uint16_t *__restrict__ embed,
+                                                        const int32_t *__restrict__ tok, int vocab, int H,
+                                                        const float *__restrict__ signs, int block,
+                                                        float *__restrict__ h) {
+    extern __shared__ float v[];
+    const int lane = blockIdx.x;
+    const int t = min(max(tok[lane], 0), vocab - 1);
+    const uint16_t *row = embed + (size_t)t * H;
+    for (int i = threadIdx.x; i < H; i += blockDim.x)
+        v[i] = __builtin_bit_cast(float, (uint32_t)row[i] << 16) * signs[i];
+    __syncthreads();
+    lds_fwht(v, H, block);
+    for (int i = threadIdx.x; i < H; i += blockDim.x) h[(size_t)lane * H + i] = v[i];
+}
+
+// The online Hadamard of down's input (gpu.metal:339-367 rotate): grid
+// (n/block, lanes); x[lane][b*block ..] = H . (signs*scale . x).
+__global__ __launch_bounds__(256) void lm_rotate_kernel(float *__restrict__ x, int stride,
+                                                        const float *__restrict__ signs, int block) {
+    extern __shared__ float v[];
+    float *base = x + (size_t)blockIdx.y * stride + (size_t)blockIdx.x * block;
+    const float *sb = signs + (size_t)blockIdx.x * block;
+    for (int i = threadIdx.x; i < block; i += blockDim.x) v[i] = base[i] * sb[i];
+    __syncthreads();
+    lds_fwht(v, block, block);
+    for (int i = threadIdx.x; i < block; i += blockDim.x) base[i] = v[i];
+}
+
+// One block per lane (gpu_darwin.go:1241-1252): u = R^T h; hidden = u *
+// float32(1/sqrt(mean(u^2) + eps)) * w (ops.go:251-254, mean and root in
+// float64); hn = R hidden for the head. Flags a non-finite hidden value.
+__global__ __launch_bounds__(1024) void lm_final_kernel(const float *__restrict__ h, int H,
+                                                        const float *__restrict__ signs, int block,
+                                                        const float *__restrict__ w, float eps,
+                                                        float *__restrict__ hidden, float *__restrict__ hn,
+                                                        int32_t *__restrict__ nonfinite) {
+    extern __shared__ float v[];
+    __shared__ float red[16];
+    __shared__ int bad;
+    const int lane = blockIdx.x;
+    if (threadIdx.x == 0) bad = 0;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) v[i] = h[(size_t)lane * H + i];
+    __syncthreads();
+    lds_fwht(v, H, block);
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        const float u = v[i] * signs[i];
+        v[i] = u;
+        ss += u * u;
+    }
+    ss = block_sum(ss, red);
+    const float inv = (float)(1.0 / sqrt((double)ss / (double)H + (double)eps));
+    int any = 0;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        const float o = v[i] * inv * w[i];
+        any |= !isfinite(o);
+        hidden[(size_t)lane * H + i] = o;
+        v[i] = o * signs[i];
+    }
+    if (any) bad = 1;
+    __syncthreads();
+    lds_fwht(v, H, block);
+    for (int i = threadIdx.x; i < H; i += blockDim.x) hn[(size_t)lane * H + i] = v[i];
+    if (threadIdx.x == 0 && bad) nonfinite[lane] = 1;
+}
+
+struct AttnArgs {
+    const float *qkv;  // [lanes][qkvw]
+    float *kc[kMaxLanes];
+    float *vc[kMaxLanes];  // this layer's cache rows per lane, [capacity][kvd]
+    const float *qn, *kn;  // this layer's head norms [128]
+    const float *rope;     // cos [positions][64], then sin at +sin_off
+    const int32_t *pos;    // [lanes]
+    float *ctx;            // [lanes][qd]
+    float *part;           // [lanes][kvh][splits][GROUP][kPart]
+    unsigned *cnt;         // [lanes][kvh], zero between launches
+    float eps, scale;
+    int qkvw, qd, kvd, kvh, splits, sin_off;
+};
+
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge factor of a softmax state with max m into one with max mn.
+__device__ __forceinline__ float rescale(float m, float mn) { return m == -INFINITY ? 0.0f : expf(m - mn); }
+
+// attend1 (gpu.metal:392-466) split over the context: grid (splits, kvh,
+// lanes), 4 wavefronts. Each of the block's 16 row groups of 16 lanes takes
+// one key at a time; lane li of a group holds dims 4li..4li+3 and
+// 64+4li..64+4li+3 of the key and value rows (two 16-byte loads, a group
+// reads one 512-byte row).
+template <int GROUP, int KPI>
+__global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
+    __shared__ float qs[GROUP][kHeadDim];
+    __shared__ float knew[kHeadDim], vnew[kHeadDim];
+    __shared__ float wm[4][GROUP], wl[4][GROUP];
+    __shared__ float wacc[4][GROUP][kHeadDim];
+    __shared__ int amLast;
+    const int lid = blockIdx.z, g = blockIdx.y, sp = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int pos = a.pos[lid];
+    const int n = pos + 1;
+    int chunk = (n + a.splits - 1) / a.splits;
+    chunk = (chunk + 15) & ~15;
+    const int j0 = min(sp * chunk, n), j1 = min(n, j0 + chunk);
+    const float *qkv = a.qkv + (size_t)lid * a.qkvw;
+    float *kc = a.kc[lid] + g * kHeadDim;
+    float *vc = a.vc[lid] + g * kHeadDim;
+
+    // Head RMSNorm and RoPE of the new key and of the GROUP query heads
+    // (gpu.metal:380-388 normRopeAt). Lane l holds the rotary pair (l, l+64).
+    {
+        const float c = a.rope[(size_t)pos * 64 + lane], s = a.rope[a.sin_off + (size_t)pos * 64 + lane];
+        for (int item = wave; item <= GROUP; item += 4) {
+            const bool isKey = item == GROUP;
+            const float *src = isKey ? qkv + a.qd + g * kHeadDim : qkv + (size_t)(g * GROUP + item) * kHeadDim;
+            const float *w = isKey ? a.kn : a.qn;
+            float x0 = src[lane], x1 = src[lane + 64];
+            const float ss = wave_sum(x0 * x0 + x1 * x1);
+            const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
+            x0 = x0 * (inv * w[lane]);
+            x1 = x1 * (inv * w[lane + 64]);
+            const float y0 = x0 * c - x1 * s, y1 = x1 * c + x0 * s;
+            if (isKey) {
+                const float v0 = qkv[a.qd + a.kvd + g * kHeadDim + lane];
+                const float v1 = qkv[a.qd + a.kvd + g * kHeadDim + lane + 64];
+                knew[lane] = y0;
+                knew[lane + 64] = y1;
+                vnew[lane] = v0;
+                vnew[lane + 64] = v1;
+                if (j0 <= pos && pos < j1) {  // this block appends the token's K/V row
+                    float *kd = kc + (size_t)pos * a.kvd, *vd = vc + (size_t)pos * a.kvd;
+                    kd[lane] = y0;
+                    kd[lane + 64] = y1;
+                    vd[lane] = v0;
+                    vd[lane + 64] = v1;
+                }
+            } else {
+                qs[item][lane] = y0 * a.scale;
+                qs[item][lane + 64] = y1 * a.scale;
+            }
+        }
+    }
+    __syncthreads();
+
+    const int sub = lane >> 4, li = lane & 15;
+    const int rowgroup = wave * 4 + sub;  // 0..15
+    const int d0 = li * 4, d1 = 64 + li * 4;
+    float q[GROUP][8];
+#pragma unroll
+    for (int hh = 0; hh < GROUP; ++hh) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[hh][i] = qs[hh][d0 + i];
+            q[hh][4 + i] = qs[hh][d1 + i];
+        }
+    }
+    float m[GROUP], l[GROUP], acc[GROUP][8];
+#pragma unroll
+    for (int hh = 0; hh < GROUP; ++hh) {
+        m[hh] = -INFINITY;
+        l[hh] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[hh][i] = 0.0f;
+    }
+    const int iters = (j1 - j0 + 16 * KPI - 1) / (16 * KPI);
+    for (int it = 0; it < iters; ++it) {
+        float kr[KPI][8], vr[KPI][8];
+        bool valid[KPI];
+#pragma unroll
+        for (int u = 0; u < KPI; ++u) {
+            const int j = j0 + (it * KPI + u) * 16 + rowgroup;
+            valid[u] = j < j1;
+            const int jj = valid[u] ? j : j0;
+            const float4 k0 = *(const float4 *)(kc + (size_t)jj * a.kvd + d0);
+            const float4 k1 = *(const float4 *)(kc + (size_t)jj * a.kvd + d1);
+            const float4 v0 = *(const float4 *)(vc + (size_t)jj * a.kvd + d0);
+            const float4 v1 = *(const float4 *)(vc + (size_t)jj * a.kvd + d1);
+            kr[u][0] = k0.x, kr[u][1] = k0.y, kr[u][2] = k0.z, kr[u][3] = k0.w;
+            kr[u][4] = k1.x, kr[u][5] = k1.y, kr[u][6] = k1.z, kr[u][7] = k1.w;
+            vr[u][0] = v0.x, vr[u][1] = v0.y, vr[u][2] = v0.z, vr[u][3] = v0.w;
+            vr[u][4] = v1.x, vr[u][5] = v1.y, vr[u][6] = v1.z, vr[u][7] = v1.w;
+            if (jj == pos) {  // the new row: from registers of this block, not the cache
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    kr[u][i] = knew[d0 + i], kr[u][4 + i] = knew[d1 + i];
+                    vr[u][i] = vnew[d0 + i], vr[u][4 + i] = vnew[d1 + i];
+                }
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < GROUP; ++hh) {
+            float s[KPI];
+            float bm = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < KPI; ++u) {
+                float p = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) p = fmaf(q[hh][i], kr[u][i], p);
+                p = row16_sum(p);
+                s[u] = valid[u] ? p : -INFINITY;
+                bm = fmaxf(bm, s[u]);
+            }
+            const float mn = fmaxf(m[hh], bm);
+            if (mn == -INFINITY) continue;
+            const float c = rescale(m[hh], mn);
+            l[hh] *= c;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[hh][i] *= c;
+#pragma unroll
+            for (int u = 0; u < KPI; ++u) {
+                const float p = valid[u] ? expf(s[u] - mn) : 0.0f;
+                l[hh] += p;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[hh][i] = fmaf(p, vr[u][i], acc[hh][i]);
+            }
+            m[hh] = mn;
+        }
+    }
+    // Merge the wave's four row groups (lanes l, l^16, l^32, l^48 hold the
+    // same dims): xor 16, then xor 32.
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+        for (int hh = 0; hh < GROUP; ++hh) {
+            const float mo = __shfl_xor(m[hh], off), lo = __shfl_xor(l[hh], off);
+            const float mn = fmaxf(m[hh], mo);
+            const float c = rescale(m[hh], mn), co = rescale(mo, mn);
+            l[hh] = l[hh] * c + lo * co;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[hh][i] = acc[hh][i] * c + __shfl_xor(acc[hh][i], off) * co;
+            m[hh] = mn;
+        }
+    }
+    if (sub == 0) {
+#pragma unroll
+        for (int hh = 0; hh < GROUP; ++hh) {
+            if (li == 0) {
+                wm[wave][hh] = m[hh];
+                wl[wave][hh] = l[hh];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                wacc[wave][hh][d0 + i] = acc[hh][i];
+                wacc[wave][hh][d1 + i] = acc[hh][4 + i];
+            }
+        }
+    }
+    __syncthreads();
+    // The block's partial per query head, merged over its four waves.
+    float *bp = a.part + ((((size_t)lid * a.kvh + g) * a.splits + sp) * GROUP) * kPart;
+    for (int t = threadIdx.x; t < GROUP * kHeadDim; t += blockDim.x) {
+        const int hh = t / kHeadDim, d = t % kHeadDim;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][hh]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float c = rescale(wm[w][hh], M);
+            L += wl[w][hh] * c;
+            A += wacc[w][hh][d] * c;
+        }
+        st_agent(bp + hh * kPart + 2 + d, A);
+        if (d == 0) {
+            st_agent(bp + hh * kPart, M);
+            st_agent(bp + hh * kPart + 1, L);
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    unsigned *cnt = a.cnt + (size_t)lid * a.kvh + g;
+    if (threadIdx.x == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        amLast = prev == (unsigned)(a.splits - 1);
+    }
+    __syncthreads();
+    if (!amLast) return;
+    __threadfence();
+    // Last block of this (lane, KV head): merge all splits in split order.
+    const float *lp = a.part + (((size_t)lid * a.kvh + g) * a.splits) * GROUP * kPart;
+    for (int t = threadIdx.x; t < GROUP * kHeadDim; t += blockDim.x) {
+        const int hh = t / kHeadDim, d = t % kHeadDim;
+        float M = -INFINITY;
+        for (int s2 = 0; s2 < a.splits; ++s2) M = fmaxf(M, ld_agent(lp + ((size_t)s2 * GROUP + hh) * kPart));
+        float L = 0.0f, A = 0.0f;
+        for (int s2 = 0; s2 < a.splits; ++s2) {
+            const float *p = lp + ((size_t)s2 * GROUP + hh) * kPart;
+            const float c = rescale(ld_agent(p), M);
+            L += ld_agent(p + 1) * c;
+            A += ld_agent(p + 2 + d) * c;
+        }
+        a.ctx[(size_t)lid * a.qd + (size_t)(g * GROUP + hh) * kHeadDim + d] = A / L;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct ArgmaxArgs {
+    const float *logits;  // [lanes][stride]
+    int stride, vocab, lanes;
+    uint32_t *key, *idx;  // [lanes][kArgmaxBlocks]
+    unsigned *cnt;        // [lanes], zero between launches
+    int32_t *tok, *pos;
+    const int32_t *start;
+    int32_t *next;  // optional [lanes]
+    int32_t *run;   // optional [steps][lanes], indexed by pos - start
+};
+
+constexpr uint32_t kNone = 0xFFFFFFFFu;
+
+// Orders candidates as greedy_argmax_rows does (gpu.metal:192-237): larger
+// key first, then the smaller index; kNone never wins.
+__device__ __forceinline__ bool better(uint32_t k, uint32_t i, uint32_t bk, uint32_t bi) {
+    return i != kNone && (bi == kNone || k > bk || (k == bk && i < bi));
+}
+
+// First-maximum argmax of each lane's logits (decode_batch.go:182-191
+// greedyArgmax; NaNs never win, a NaN at index 0 keeps index 0): grid
+// (kArgmaxBlocks, lanes). The last block of a lane writes the next token,
+// feeds it back as the lane's current token and advances the lane's
+// position.
+__global__ __launch_bounds__(256) void lm_argmax_kernel(const ArgmaxArgs a) {
+    __shared__ uint32_t sk[256], si[256];
+    __shared__ int amLast;
+    const int lane = blockIdx.y;
+    const float *x = a.logits + (size_t)lane * a.stride;
+    const int per = (a.vocab + kArgmaxBlocks - 1) / kArgmaxBlocks;
+    const int c0 = blockIdx.x * per, c1 = min(a.vocab, c0 + per);
+    uint32_t bk = 0, bi = kNone;
+    for (int i = c0 + threadIdx.x; i < c1; i += blockDim.x) {
+        const uint32_t bits = __builtin_bit_cast(uint32_t, x[i]);
+        const uint32_t mag = bits & 0x7FFFFFFFu;
+        if (mag <= 0x7F800000u) {
+            const uint32_t key = mag == 0 ? 0x80000000u : ((bits & 0x80000000u) ? ~bits : bits ^ 0x80000000u);
+            if (better(key, (uint32_t)i, bk, bi)) bk = key, bi = (uint32_t)i;
+        }
+    }
+    sk[threadIdx.x] = bk;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int step = 128; step > 0; step >>= 1) {
+        if ((int)threadIdx.x < step && better(sk[threadIdx.x + step], si[threadIdx.x + step], sk[threadIdx.x], si[threadIdx.x])) {
+            sk[threadIdx.x] = sk[threadIdx.x + step];
+            si[threadIdx.x] = si[threadIdx.x + step];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const size_t o = (size_t)lane * kArgmaxBlocks + blockIdx.x;
+        __hip_atomic_store(a.key + o, sk[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.idx + o, si[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence();
+        const unsigned prev = __hip_atomic_fetch_add(a.cnt + lane, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        amLast = prev == (unsigned)(kArgmaxBlocks - 1);
+    }
+    __syncthreads();
+    if (!amLast || threadIdx.x != 0) return;
+    __threadfence();
+    uint32_t k = 0, best = kNone;
+    for (int b = 0; b < kArgmaxBlocks; ++b) {
+        const size_t o = (size_t)lane * kArgmaxBlocks + b;
+        const uint32_t kb = __hip_atomic_load(a.key + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t ib = __hip_atomic_load(a.idx + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (better(kb, ib, k, best)) k = kb, best = ib;
+    }
+    const uint32_t first = __builtin_bit_cast(uint32_t, x[0]) & 0x7FFFFFFFu;
+    const int32_t token = (first > 0x7F800000u || best == kNone) ? 0 : (int32_t)best;
+    const int32_t p = a.pos[lane];
+    if (a.run) a.run[(size_t)(p - a.start[lane]) * a.lanes + lane] = token;
+    if (a.next) a.next[lane] = token;
+    a.tok[lane] = token;
+    a.pos[lane] = p + 1;
+    __hip_atomic_store(a.cnt + lane, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- host orchestration ----------------------------------------------------
+
+template <int G>
+int launch_attend_g(const AttnArgs &a, int lanes, hipStream_t st) {
+    constexpr int KPI = G <= 4 ? 4 : 2;
+    hipLaunchKernelGGL((lm_attend_kernel<G, KPI>), dim3(a.splits, a.kvh, lanes), dim3(256), 0, st, a);
+    return launch_status();
+}
+
+int launch_attend(int group, const AttnArgs &a, int lanes, hipStream_t st) {
+    switch (group) {
+    case 1: return launch_attend_g<1>(a, lanes, st);
+    case 2: return launch_attend_g<2>(a, lanes, st);
+    case 3: return launch_attend_g<3>(a, lanes, st);
+    case 4: return launch_attend_g<4>(a, lanes, st);
+    case 5: return launch_attend_g<5>(a, lanes, st);
+    case 6: return launch_attend_g<6>(a, lanes, st);
+    case 7: return launch_attend_g<7>(a, lanes, st);
+    case 8: return launch_attend_g<8>(a, lanes, st);
+    }
+    return GPHQ_ERR_UNSUPPORTED;
+}
+
+int attention_splits(const gphq_lm *lm, int lanes) {
+    const int64_t work = lm->cfg.kv_heads * (int64_t)lanes;
+    return (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplits, 1024 / work));
+}
+
+// One projection GEMV of the step, single- or multi-lane.
+int gemv(gphq_decode_batch *ws, int lanes, int fmt, int pro, int epi, const uint8_t *buf, int64_t codes,
+         int64_t scales, const float *x, int64_t xs, float *y, int64_t ys, int64_t K, int64_t N, hipStream_t st) {
+    const float eps = (float)ws->lm->cfg.eps;
+    if (lanes < ws->vec_min_lanes) {
+        for (int l = 0; l < lanes; ++l)
+            GPHQ_TRY(gemv_fused_launch(fmt, pro, epi, buf + codes, buf + scales, x + (size_t)l * xs,
+                                       y + (size_t)l * ys, (int)K, (int)N, eps, st));
+        return GPHQ_OK;
+    }
+    return gemv_vec_fused_launch(fmt, pro == PRO_NORM, epi, buf + codes, buf + scales, x, (long)xs, y, (long)ys, lanes,
+                                 (int)K, (int)N, eps, ws->vec_work, st);
+}
+
+// Enqueues one decode step for `lanes` lanes whose tokens and positions are
+// already in ws->tok / ws->pos. head: run the final norm, head and argmax;
+// hidden_out receives each lane's post-final-norm state.
+int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool head, float *hidden_out,
+                int32_t *next_out, int32_t *run_out, hipStream_t st) {
+    const gphq_lm *lm = ws->lm;
+    const gphq_lm_config &c = lm->cfg;
+    const int64_t H = c.hidden, I = c.intermediate, qkvw = lm->qd + 2 * lm->kvd;
+    const int fmt = c.fmt;
+    hipLaunchKernelGGL(lm_embed_kernel, dim3(lanes), dim3(1024), H * sizeof(float), st, lm->embed, ws->tok,
+                       (int)c.vocab, (int)H, lm->hsigns, (int)lm->hblock, ws->h);
+    GPHQ_TRY(launch_status());
+    AttnArgs aa{};
+    aa.qkv = ws->qkv;
+    aa.rope = lm->rope;
+    aa.pos = ws->pos;
+    aa.ctx = ws->ctx;
+    aa.part = ws->part;
+    aa.cnt = ws->attn_cnt;
+    aa.eps = (float)c.eps;
+    aa.scale = (float)(1.0 / sqrt((double)c.head_dim));
+    aa.qkvw = (int)qkvw;
+    aa.qd = (int)lm->qd;
+    aa.kvd = (int)lm->kvd;
+    aa.kvh = (int)c.kv_heads;
+    aa.splits = attention_splits(lm, lanes);
+    aa.sin_off = (int)(lm->positions * 64);
+    for (int layer = 0; layer < c.layers; ++layer) {
+        const gphq_lm_layer &L = lm->layers[layer];
+        const uint8_t *buf = (const uint8_t *)L.buf_dev;
+        GPHQ_TRY(gemv(ws, lanes, fmt, PRO_NORM, EPI_STORE, buf, L.qkv, L.qkv_scale, ws->h, H, ws->qkv, qkvw, H, qkvw,
+                      st));
+        for (int l = 0; l < lanes; ++l) {
+            const size_t off = (size_t)layer * kvs[l]->capacity * lm->kvd;
+            aa.kc[l] = kvs[l]->kc + off;
+            aa.vc[l] = kvs[l]->vc + off;
+        }
+        aa.qn = lm->norms + (size_t)layer * 2 * kHeadDim;
+        aa.kn = aa.qn + kHeadDim;
+        GPHQ_TRY(launch_attend((int)lm->group, aa, lanes, st));
+        GPHQ_TRY(gemv(ws, lanes, fmt, PRO_PLAIN, EPI_ADD, buf, L.o, L.o_scale, ws->ctx, lm->qd, ws->h, H, lm->qd, H,
+                      st));
+        GPHQ_TRY(gemv(ws, lanes, fmt, PRO_NORM, EPI_SWIGLU, buf, L.gu, L.gu_scale, ws->h, H, ws->act, I, H, 2 * I,
+                      st));
+        if (fmt != GPHQ_FMT_Q8B) {  // gpu_darwin.go:209-215: Q8B skips down's input rotation
+            hipLaunchKernelGGL(lm_rotate_kernel, dim3((unsigned)(I / lm->iblock), lanes), dim3(256),
+                               lm->iblock * sizeof(float), st, ws->act, (int)I, lm->isigns, (int)lm->iblock);
+            GPHQ_TRY(launch_status());
+        }
+        GPHQ_TRY(gemv(ws, lanes, fmt, PRO_PLAIN, EPI_ADD, buf, L.d, L.d_scale, ws->act, I, ws->h, H, I, H, st));
+    }
+    if (!head) return GPHQ_OK;
+    hipLaunchKernelGGL(lm_final_kernel, dim3(lanes), dim3(1024), H * sizeof(float), st, ws->h, (int)H, lm->hsigns,
+                       (int)lm->hblock, lm->final_norm, (float)c.eps, hidden_out, ws->hn, ws->nonfinite);
+    GPHQ_TRY(launch_status());
+    GPHQ_TRY(gemv(ws, lanes, GPHQ_FMT_Q8B, PRO_PLAIN, EPI_STORE, lm->head, 0, lm->head_scale, ws->hn, H, ws->logits,
+                  lm->head_rows, H, lm->head_rows, st));
+    ArgmaxArgs ga{ws->logits, (int)lm->head_rows, (int)c.vocab, lanes, ws->akey, ws->aidx, ws->argmax_cnt,
+                  ws->tok, ws->pos, ws->start, next_out, run_out};
+    hipLaunchKernelGGL(lm_argmax_kernel, dim3(kArgmaxBlocks, lanes), dim3(256), 0, st, ga);
+    return launch_status();
+}
+
+int seed(gphq_decode_batch *ws, int lanes, const int64_t *positions, const int32_t *tokens, int64_t advance,
+         hipStream_t st) {
+    SeedArgs s{};
+    for (int l = 0; l < lanes; ++l) {
+        s.tok[l] = tokens[l];
+        s.pos[l] = (int32_t)(positions[l] + advance);
+    }
+    s.lanes = lanes;
+    s.tok_dev = ws->tok;
+    s.pos_dev = ws->pos;
+    s.start_dev = ws->start;
+    hipLaunchKernelGGL(lm_seed_kernel, dim3(1), dim3(64), 0, st, s);
+    return launch_status();
+}
+
+bool overlaps(const void *a, int64_t an, const void *b, int64_t bn) {
+    if (!a || !b || an <= 0 || bn <= 0) return false;
+    const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+    return a0 < b0 + (uintptr_t)bn && b0 < a0 + (uintptr_t)an;
+}
+
+// decode_batch.go:80-146 validateDecodeBatch, in the same order, for
+// `steps` consecutive tokens per lane.
+int validate(const gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
+             const int32_t *tokens, int64_t steps, const float *hidden, int64_t hidden_len, const float *logits,
+             const int32_t *next, bool need_head) {
+    if (!ws || !ws->lm) return GPHQ_ERR_FOREIGN_WORKSPACE;
+    const gphq_lm *lm = ws->lm;
+    if (lanes < 1 || !kvs || !positions || !tokens || (need_head && (logits == nullptr) == (next == nullptr)))
+        return GPHQ_ERR_BATCH_SHAPE;
+    if (lanes > ws->capacity) return GPHQ_ERR_LANE_CAPACITY;
+    for (int64_t l = 0; l < lanes; ++l) {
+        const gphq_prefix *kv = kvs[l];
+        if (!kv || kv->lm != lm || !kv->kc || kv->capacity < 1) return GPHQ_ERR_FOREIGN_PREFIX;
+        for (int64_t p = 0; p < l; ++p)
+            if (kvs[p] == kv) return GPHQ_ERR_DUPLICATE_PREFIX;
+        if (positions[l] < 0 || positions[l] + steps > kv->capacity || positions[l] + steps > lm->positions)
+            return GPHQ_ERR_PREFIX_FULL;
+    }
+    for (int64_t t = 0; t < steps; ++t)
+        for (int64_t l = 0; l < lanes; ++l)
+            if (tokens[t * lanes + l] < 0 || tokens[t * lanes + l] >= lm->cfg.vocab) return GPHQ_ERR_TOKEN_RANGE;
+    const int64_t hb = lanes * lm->cfg.hidden * 4, lb = lanes * lm->cfg.vocab * 4, nb = lanes * 4;
+    if (hidden && hidden_len < lanes * lm->cfg.hidden) return GPHQ_ERR_BATCH_SHAPE;
+    if (overlaps(next, nb, hidden, hb) || overlaps(hidden, hb, logits, lb)) return GPHQ_ERR_OVERLAP;
+    return GPHQ_OK;
+}
+
+bool model_ready(const gphq_lm *lm) {
+    if (!lm->embed || !lm->head || !lm->final_norm) return false;
+    for (char b : lm->bound)
+        if (!b) return false;
+    return true;
+}
+
+void free_batch(gphq_decode_batch *ws) {
+    for (void *p : ws->allocs) (void)hipFree(p);
+    delete ws;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gphq_lm_layer_layout(const gphq_lm_config *cfg, gphq_lm_layer *out, int64_t *bytes) {
+    if (!cfg || !out || !bytes) return GPHQ_ERR_DIMENSIONS;
+    const int fmt = cfg->fmt;
+    if (fmt != GPHQ_FMT_Q8 && fmt != GPHQ_FMT_Q8B && fmt != GPHQ_FMT_Q8B_F32 && fmt != GPHQ_FMT_Q4)
+        return GPHQ_ERR_UNSUPPORTED;
+    const int64_t h = cfg->hidden, qd = cfg->heads * cfg->head_dim, kvd = cfg->kv_heads * cfg->head_dim,
+                  inter = cfg->intermediate;
+    if (h <= 0 || qd <= 0 || kvd <= 0 || inter <= 0 || h % 32 || qd % 32 || inter % 32) return GPHQ_ERR_DIMENSIONS;
+    // gpu_darwin.go:251-283 place(): codes, then scales, each region 256-byte aligned.
+    int64_t at = 0;
+    auto place = [&](int64_t rows, int64_t k, int64_t *w, int64_t *s) {
+        int64_t cb, sb;
+        matrix_bytes(fmt, rows, k, &cb, &sb);
+        *w = at;
+        at = align256(at + cb);
+        *s = at;
+        at = align256(at + sb);
+    };
+    gphq_lm_layer L{};
+    place(qd + 2 * kvd, h, &L.qkv, &L.qkv_scale);
+    place(h, qd, &L.o, &L.o_scale);
+    place(2 * inter, h, &L.gu, &L.gu_scale);
+    place(h, inter, &L.d, &L.d_scale);
+    L.buf_bytes = at;
+    *out = L;
+    *bytes = at;
+    return GPHQ_OK;
+}
+
+int gphq_lm_head_layout(const gphq_lm_config *cfg, int64_t *rows, int64_t *scale_offset, int64_t *bytes) {
+    if (!cfg || !rows || !scale_offset || !bytes || cfg->hidden <= 0 || cfg->hidden % 32 || cfg->vocab <= 0)
+        return GPHQ_ERR_DIMENSIONS;
+    // gpu_darwin.go:340-346 loadHead: rows padded to 16, Q8B codes then FP16 scales.
+    const int64_t r = (cfg->vocab + 15) / 16 * 16;
+    *rows = r;
+    *scale_offset = align256(r * cfg->hidden);
+    *bytes = *scale_offset + 2 * r * (cfg->hidden / 32);
+    return GPHQ_OK;
+}
+
+int gphq_lm_new(const gphq_lm_config *cfg, gphq_lm **out) {
+    if (!cfg || !out) return GPHQ_ERR_DIMENSIONS;
+    *out = nullptr;
+    const gphq_lm_config c = *cfg;
+    if (c.fmt != GPHQ_FMT_Q8 && c.fmt != GPHQ_FMT_Q8B && c.fmt != GPHQ_FMT_Q8B_F32 && c.fmt != GPHQ_FMT_Q4)
+        return GPHQ_ERR_UNSUPPORTED;
+    // weights.go:672-680 readConfig plausibility.
+    if (c.hidden <= 0 || c.layers <= 0 || c.heads <= 0 || c.kv_heads <= 0 || c.head_dim <= 0 || c.intermediate <= 0 ||
+        c.vocab <= 0 || c.max_positions <= 0 || c.heads % c.kv_heads != 0 || c.head_dim % 2 != 0 || !(c.eps > 0) ||
+        !(c.rope_theta > 0))
+        return GPHQ_ERR_GEOMETRY;
+    // gpu_darwin.go:116-129 gpuGeometry.
+    const int64_t qd = c.heads * c.head_dim, kvd = c.kv_heads * c.head_dim, group = c.heads / c.kv_heads;
+    int64_t iblock = 1;
+    while (iblock < kMaxRotation && c.intermediate % (2 * iblock) == 0) iblock *= 2;
+    if (c.head_dim != kHeadDim || group > 8 || c.hidden % 64 || c.intermediate % 64 || (qd + 2 * kvd) % 64 ||
+        iblock < 64)
+        return GPHQ_ERR_GEOMETRY;
+    // Device limits of this implementation: one block holds a hidden vector
+    // in LDS; int32 row and column indices.
+    if (c.hidden > kMaxWidth || c.intermediate > kMaxWidth || qd > kMaxWidth || c.vocab > (1 << 28) ||
+        c.layers > 4096)
+        return GPHQ_ERR_GEOMETRY;
+    gphq_lm *lm = new gphq_lm();
+    lm->cfg = c;
+    lm->qd = qd;
+    lm->kvd = kvd;
+    lm->group = group;
+    lm->positions = std::min<int64_t>(c.max_positions, 1 << 16);  // gpu_darwin.go:33-35
+    lm->layers.assign(c.layers, gphq_lm_layer{});
+    lm->bound.assign(c.layers, 0);
+    std::vector<float> hs, is;
+    lm->hblock = rotation_signs(c.hidden, hs);
+    lm->iblock = rotation_signs(c.intermediate, is);
+    // gpu_darwin.go:232-241: float32(cos/sin(pos * invFreq[d])), float64 angles.
+    const int64_t half = kHeadDim / 2;
+    std::vector<float> rope((size_t)(2 * lm->positions * half));
+    for (int64_t d = 0; d < half; ++d) {
+        const double inv = 1.0 / pow(c.rope_theta, (double)(2 * d) / (double)c.head_dim);
+        for (int64_t p = 0; p < lm->positions; ++p) {
+            const double th = (double)p * inv;
+            rope[(size_t)(p * half + d)] = (float)cos(th);
+            rope[(size_t)(lm->positions * half + p * half + d)] = (float)sin(th);
+        }
+    }
+    auto upload = [](float **dst, const std::vector<float> &src) {
+        hipError_t e = hipMalloc(dst, src.size() * sizeof(float));
+        if (e == hipSuccess) e = hipMemcpy(*dst, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice);
+        return e;
+    };
+    hipError_t e = upload(&lm->rope, rope);
+    if (e == hipSuccess) e = upload(&lm->hsigns, hs);
+    if (e == hipSuccess) e = upload(&lm->isigns, is);
+    if (e == hipSuccess) e = hipMalloc(&lm->norms, (size_t)c.layers * 2 * kHeadDim * sizeof(float));
+    if (e != hipSuccess) {
+        gphq_lm_free(lm);
+        return hip_status(e);
+    }
+    *out = lm;
+    return GPHQ_OK;
+}
+
+void gphq_lm_free(gphq_lm *lm) {
+    if (!lm) return;
+    for (float *p : {lm->norms, lm->rope, lm->hsigns, lm->isigns, lm->final_norm})
+        if (p) (void)hipFree(p);
+    delete lm;
+}
+
+int gphq_lm_bind_layer(gphq_lm *lm, int64_t layer, const gphq_lm_layer *desc) {
+    if (!lm || !desc || layer < 0 || layer >= lm->cfg.layers || !desc->buf_dev || !desc->q_norm_host ||
+        !desc->k_norm_host)
+        return GPHQ_ERR_DIMENSIONS;
+    const gphq_lm_config &c = lm->cfg;
+    const int64_t h = c.hidden, inter = c.intermediate;
+    struct Region {
+        int64_t w, s, rows, k;
+    } regs[4] = {{desc->qkv, desc->qkv_scale, lm->qd + 2 * lm->kvd, h},
+                 {desc->o, desc->o_scale, h, lm->qd},
+                 {desc->gu, desc->gu_scale, 2 * inter, h},
+                 {desc->d, desc->d_scale, h, inter}};
+    if ((uintptr_t)desc->buf_dev % 256) return GPHQ_ERR_DIMENSIONS;
+    for (const Region &r : regs) {
+        int64_t cb, sb;
+        matrix_bytes(c.fmt, r.rows, r.k, &cb, &sb);
+        if (r.w < 0 || r.s < 0 || r.w % 16 || r.s % 4 || r.w + cb > desc->buf_bytes || r.s + sb > desc->buf_bytes)
+            return GPHQ_ERR_DIMENSIONS;
+    }
+    float norms[2 * kHeadDim];
+    for (int i = 0; i < kHeadDim; ++i) {
+        norms[i] = desc->q_norm_host[i];
+        norms[kHeadDim + i] = desc->k_norm_host[i];
+    }
+    GPHQ_TRY(hip_status(hipMemcpy(lm->norms + (size_t)layer * 2 * kHeadDim, norms, sizeof(norms),
+                                  hipMemcpyHostToDevice)));
+    lm->layers[layer] = *desc;
+    lm->layers[layer].q_norm_host = nullptr;
+    lm->layers[layer].k_norm_host = nullptr;
+    lm->bound[layer] = 1;
+    return GPHQ_OK;
+}
+
+int gphq_lm_bind_embed(gphq_lm *lm, const uint16_t *embed_dev, int64_t len) {
+    if (!lm || !embed_dev || len != lm->cfg.vocab * lm->cfg.hidden) return GPHQ_ERR_DIMENSIONS;
+    lm->embed = embed_dev;
+    return GPHQ_OK;
+}
+
+int gphq_lm_bind_head(gphq_lm *lm, const void *head_dev, int64_t bytes, const float *final_norm_host) {
+    if (!lm || !head_dev || !final_norm_host || (uintptr_t)head_dev % 256) return GPHQ_ERR_DIMENSIONS;
+    int64_t rows, so, need;
+    GPHQ_TRY(gphq_lm_head_layout(&lm->cfg, &rows, &so, &need));
+    if (bytes < need) return GPHQ_ERR_DIMENSIONS;
+    if (!lm->final_norm) GPHQ_TRY(hip_status(hipMalloc(&lm->final_norm, lm->cfg.hidden * sizeof(float))));
+    GPHQ_TRY(hip_status(
+        hipMemcpy(lm->final_norm, final_norm_host, lm->cfg.hidden * sizeof(float), hipMemcpyHostToDevice)));
+    lm->head = (const uint8_t *)head_dev;
+    lm->head_rows = rows;
+    lm->head_scale = so;
+    return GPHQ_OK;
+}
+
+int gphq_prefix_new(const gphq_lm *lm, int64_t capacity, gphq_prefix **out) {
+    if (!lm || !out || capacity < 1) return GPHQ_ERR_DIMENSIONS;
+    *out = nullptr;
+    gphq_prefix *p = new gphq_prefix();
+    p->lm = lm;
+    p->capacity = capacity;
+    const size_t n = (size_t)lm->cfg.layers * capacity * lm->kvd * sizeof(float);
+    hipError_t e = hipMalloc(&p->kc, n);
+    if (e == hipSuccess) e = hipMalloc(&p->vc, n);
+    if (e == hipSuccess) e = hipMemset(p->kc, 0, n);
+    if (e == hipSuccess) e = hipMemset(p->vc, 0, n);
+    if (e != hipSuccess) {
+        gphq_prefix_free(p);
+        return hip_status(e);
+    }
+    *out = p;
+    return GPHQ_OK;
+}
+
+void gphq_prefix_free(gphq_prefix *p) {
+    if (!p) return;
+    if (p->kc) (void)hipFree(p->kc);
+    if (p->vc) (void)hipFree(p->vc);
+    delete p;
+}
+
+int gphq_prefix_kv(const gphq_prefix *p, float **kc_dev, float **vc_dev, int64_t *capacity) {
+    if (!p) return GPHQ_ERR_DIMENSIONS;
+    if (kc_dev) *kc_dev = p->kc;
+    if (vc_dev) *vc_dev = p->vc;
+    if (capacity) *capacity = p->capacity;
+    return GPHQ_OK;
+}
+
+int gphq_prefix_copy(gphq_prefix *dst, const gphq_prefix *src, int64_t n, void *stream) {
+    if (!dst || !src || dst->lm != src->lm || n < 0 || n > dst->capacity || n > src->capacity)
+        return GPHQ_ERR_DIMENSIONS;
+    // gpu_darwin.go:873-881 copyFrom: the first n rows of each layer.
+    const int64_t kvd = dst->lm->kvd, layers = dst->lm->cfg.layers;
+    const size_t w = (size_t)n * kvd * sizeof(float);
+    if (w == 0) return GPHQ_OK;
+    const size_t dpitch = (size_t)dst->capacity * kvd * sizeof(float);
+    const size_t spitch = (size_t)src->capacity * kvd * sizeof(float);
+    GPHQ_TRY(hip_status(hipMemcpy2DAsync(dst->kc, dpitch, src->kc, spitch, w, (size_t)layers, hipMemcpyDeviceToDevice,
+                                         (hipStream_t)stream)));
+    return hip_status(hipMemcpy2DAsync(dst->vc, dpitch, src->vc, spitch, w, (size_t)layers, hipMemcpyDeviceToDevice,
+                                       (hipStream_t)stream));
+}
+
+int gphq_decode_batch_new(const gphq_lm *lm, int64_t capacity, gphq_decode_batch **out) {
+    if (!out) return GPHQ_ERR_DIMENSIONS;
+    *out = nullptr;
+    if (!lm) return GPHQ_ERR_FOREIGN_WORKSPACE;
+    if (capacity < 1 || capacity > kMaxLanes) return GPHQ_ERR_LANE_CAPACITY;
+    if (!model_ready(lm)) return GPHQ_ERR_MODEL_INCOMPLETE;
+    const gphq_lm_config &c = lm->cfg;
+    gphq_decode_batch *ws = new gphq_decode_batch();
+    ws->lm = lm;
+    ws->capacity = (int)capacity;
+    const int64_t H = c.hidden, I = c.intermediate, qkvw = lm->qd + 2 * lm->kvd;
+    const int64_t kmax = std::max({H, lm->qd, I});
+    ws->vec_bytes = gemv_vec_workspace_bytes((int)capacity, (int)kmax);
+    const size_t partFloats = (size_t)capacity * c.kv_heads * kMaxSplits * lm->group * kPart;
+    struct {
+        void **dst;
+        size_t bytes;
+    } bufs[] = {
+        {(void **)&ws->h, (size_t)capacity * H * 4},
+        {(void **)&ws->qkv, (size_t)capacity * qkvw * 4},
+        {(void **)&ws->ctx, (size_t)capacity * lm->qd * 4},
+        {(void **)&ws->act, (size_t)capacity * I * 4},
+        {(void **)&ws->hn, (size_t)capacity * H * 4},
+        {(void **)&ws->hidden, (size_t)capacity * H * 4},
+        {(void **)&ws->logits, (size_t)capacity * lm->head_rows * 4},
+        {(void **)&ws->part, partFloats * 4},
+        {(void **)&ws->attn_cnt, (size_t)capacity * c.kv_heads * 4},
+        {(void **)&ws->argmax_cnt, (size_t)capacity * 4},
+        {(void **)&ws->akey, (size_t)capacity * kArgmaxBlocks * 4},
+        {(void **)&ws->aidx, (size_t)capacity * kArgmaxBlocks * 4},
+        {(void **)&ws->tok, (size_t)capacity * 4},
+        {(void **)&ws->pos, (size_t)capacity * 4},
+        {(void **)&ws->start, (size_t)capacity * 4},
+        {(void **)&ws->nonfinite, (size_t)capacity * 4},
+        {(void **)&ws->vec_work, ws->vec_bytes},
+    };
+    for (auto &b : bufs) {
+        hipError_t e = hipMalloc(b.dst, b.bytes);
+        if (e == hipSuccess) {
+            ws->allocs.push_back(*b.dst);
+            e = hipMemset(*b.dst, 0, b.bytes);  // counters start at zero; scratch is defined
+        }
+        if (e != hipSuccess) {
+            free_batch(ws);
+            return hip_status(e);
+        }
+    }
+    *out = ws;
+    return GPHQ_OK;
+}
+
+void gphq_decode_batch_free(gphq_decode_batch *ws) {
+    if (ws) free_batch(ws);
+}
+
+int gphq_decode_batch_set_vec_min_lanes(gphq_decode_batch *ws, int64_t lanes) {
+    if (!ws || lanes < 1) return GPHQ_ERR_DIMENSIONS;
+    ws->vec_min_lanes = (int)std::min<int64_t>(lanes, kMaxLanes + 1);
+    return GPHQ_OK;
+}
+
+int gphq_decode_batch_into(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
+                           const int32_t *tokens, float *hidden_dev, int64_t hidden_len, float *logits_dev,
+                           int64_t logits_len, void *stream) {
+    GPHQ_TRY(validate(ws, kvs, lanes, positions, tokens, 1, hidden_dev, hidden_len, logits_dev, nullptr, true));
+    if (!hidden_dev || logits_len < lanes * ws->lm->cfg.vocab) return GPHQ_ERR_BATCH_SHAPE;
+    hipStream_t st = (hipStream_t)stream;
+    GPHQ_TRY(seed(ws, (int)lanes, positions, tokens, 0, st));
+    GPHQ_TRY(encode_step(ws, kvs, (int)lanes, true, hidden_dev, nullptr, nullptr, st));
+    const gphq_lm *lm = ws->lm;
+    return hip_status(hipMemcpy2DAsync(logits_dev, (size_t)lm->cfg.vocab * 4, ws->logits, (size_t)lm->head_rows * 4,
+                                       (size_t)lm->cfg.vocab * 4, (size_t)lanes, hipMemcpyDeviceToDevice, st));
+}
+
+int gphq_decode_batch_greedy_into(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes,
+                                  const int64_t *positions, const int32_t *tokens, float *hidden_dev,
+                                  int64_t hidden_len, int32_t *next_dev, void *stream) {
+    GPHQ_TRY(validate(ws, kvs, lanes, positions, tokens, 1, hidden_dev, hidden_len, nullptr, next_dev, true));
+    if (!hidden_dev) return GPHQ_ERR_BATCH_SHAPE;
+    hipStream_t st = (hipStream_t)stream;
+    GPHQ_TRY(seed(ws, (int)lanes, positions, tokens, 0, st));
+    return encode_step(ws, kvs, (int)lanes, true, hidden_dev, next_dev, nullptr, st);
+}
+
+int gphq_decode_greedy_run(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
+                           const int32_t *tokens, int64_t steps, int32_t *tokens_out_dev, int64_t tokens_out_len,
+                           float *hidden_dev, int64_t hidden_len, void *stream) {
+    if (steps < 1 || !tokens_out_dev || tokens_out_len < steps * lanes) return GPHQ_ERR_BATCH_SHAPE;
+    GPHQ_TRY(validate(ws, kvs, lanes, positions, tokens, 1, hidden_dev, hidden_len, nullptr, tokens_out_dev, true));
+    // Every step's position must fit the prefixes and the RoPE table.
+    for (int64_t l = 0; l < lanes; ++l)
+        if (positions[l] + steps > kvs[l]->capacity || positions[l] + steps > ws->lm->positions)
+            return GPHQ_ERR_PREFIX_FULL;
+    if (overlaps(tokens_out_dev, steps * lanes * 4, hidden_dev, lanes * ws->lm->cfg.hidden * 4))
+        return GPHQ_ERR_OVERLAP;
+    hipStream_t st = (hipStream_t)stream;
+    float *hid = hidden_dev ? hidden_dev : ws->hidden;
+    GPHQ_TRY(seed(ws, (int)lanes, positions, tokens, 0, st));
+    for (int64_t t = 0; t < steps; ++t) GPHQ_TRY(encode_step(ws, kvs, (int)lanes, true, hid, nullptr, tokens_out_dev, st));
+    return GPHQ_OK;
+}
+
+int gphq_decode_extend(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
+                       const int32_t *tokens, int64_t steps, void *stream) {
+    if (steps < 1) return GPHQ_ERR_BATCH_SHAPE;
+    GPHQ_TRY(validate(ws, kvs, lanes, positions, tokens, steps, nullptr, 0, nullptr, nullptr, false));
+    hipStream_t st = (hipStream_t)stream;
+    for (int64_t t = 0; t < steps; ++t) {
+        GPHQ_TRY(seed(ws, (int)lanes, positions, tokens + t * lanes, t, st));
+        GPHQ_TRY(encode_step(ws, kvs, (int)lanes, false, nullptr, nullptr, nullptr, st));
+    }
+    return GPHQ_OK;
+}
+
+int gphq_decode_batch_check(gphq_decode_batch *ws, void *stream) {
+    if (!ws) return GPHQ_ERR_FOREIGN_WORKSPACE;
+    int32_t flags[kMaxLanes];
+    GPHQ_TRY(hip_status(hipMemcpyAsync(flags, ws->nonfinite, ws->capacity * 4, hipMemcpyDeviceToHost,
+                                       (hipStream_t)stream)));
+    GPHQ_TRY(hip_status(hipStreamSynchronize((hipStream_t)stream)));
+    bool bad = false;
+    for (int l = 0; l < ws->capacity; ++l) bad |= flags[l] != 0;
+    if (!bad) return GPHQ_OK;
+    GPHQ_TRY(hip_status(hipMemsetAsync(ws->nonfinite, 0, ws->capacity * 4, (hipStream_t)stream)));
+    GPHQ_TRY(hip_status(hipStreamSynchronize((hipStream_t)stream)));
+    return GPHQ_ERR_NON_FINITE_HIDDEN;
+}
+
+}  // extern "C"

@@ -19,6 +19,17 @@ ERR_DIMENSIONS = -3
 ERR_NON_FINITE = -4
 ERR_HIP = -5
 ERR_UNSUPPORTED = -6
+ERR_GEOMETRY = -7
+ERR_FOREIGN_WORKSPACE = -8
+ERR_BATCH_SHAPE = -9
+ERR_LANE_CAPACITY = -10
+ERR_FOREIGN_PREFIX = -11
+ERR_DUPLICATE_PREFIX = -12
+ERR_PREFIX_FULL = -13
+ERR_TOKEN_RANGE = -14
+ERR_OVERLAP = -15
+ERR_NON_FINITE_HIDDEN = -16
+ERR_MODEL_INCOMPLETE = -17
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
 
@@ -80,6 +91,25 @@ SIGNATURES = {
     "gphq_q8gemm_mul_into": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp]),
     "gphq_mm_workspace_bytes": (_i64, [_i64, _i64]),
     "gphq_mm": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "gphq_lm_layer_layout": (ctypes.c_int, [_vp, _vp, _i64p]),
+    "gphq_lm_head_layout": (ctypes.c_int, [_vp, _i64p, _i64p, _i64p]),
+    "gphq_lm_new": (ctypes.c_int, [_vp, _vpp]),
+    "gphq_lm_free": (None, [_vp]),
+    "gphq_lm_bind_layer": (ctypes.c_int, [_vp, _i64, _vp]),
+    "gphq_lm_bind_embed": (ctypes.c_int, [_vp, _vp, _i64]),
+    "gphq_lm_bind_head": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "gphq_prefix_new": (ctypes.c_int, [_vp, _i64, _vpp]),
+    "gphq_prefix_free": (None, [_vp]),
+    "gphq_prefix_kv": (ctypes.c_int, [_vp, _vpp, _vpp, _i64p]),
+    "gphq_prefix_copy": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "gphq_decode_batch_new": (ctypes.c_int, [_vp, _i64, _vpp]),
+    "gphq_decode_batch_free": (None, [_vp]),
+    "gphq_decode_batch_set_vec_min_lanes": (ctypes.c_int, [_vp, _i64]),
+    "gphq_decode_batch_into": (ctypes.c_int, [_vp, _vpp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "gphq_decode_batch_greedy_into": (ctypes.c_int, [_vp, _vpp, _i64, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "gphq_decode_greedy_run": (ctypes.c_int, [_vp, _vpp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "gphq_decode_extend": (ctypes.c_int, [_vp, _vpp, _i64, _vp, _vp, _i64, _vp]),
+    "gphq_decode_batch_check": (ctypes.c_int, [_vp, _vp]),
 }
 
 FMT_GPTQ4_G128 = 12
@@ -438,3 +468,224 @@ def gemv_vec(fmt, codes, scales, x, y, lanes, k, n, work, x_stride=None, y_strid
         load().gphq_gemv_vec(fmt, ptr(codes), ptr(scales), ptr(x), x_stride, ptr(y), y_stride, lanes, k, n, ptr(work),
                              work.numel() * work.element_size(), stream_handle(stream))
     )
+
+
+# ---- qwen3lm decode provider (gphq_lm_* / gphq_prefix_* / gphq_decode_*) ----
+
+DECODE_MAX_LANES = 32
+
+
+class LmConfig(ctypes.Structure):
+    """gphq_lm_config: model geometry and the layer weight format."""
+
+    _fields_ = [(n, ctypes.c_int64) for n in ("hidden", "layers", "heads", "kv_heads", "head_dim", "intermediate",
+                                               "vocab", "max_positions")] + [
+        ("eps", ctypes.c_double), ("rope_theta", ctypes.c_double), ("fmt", ctypes.c_int32),
+        ("reserved", ctypes.c_int32)]
+
+
+class LmLayer(ctypes.Structure):
+    """gphq_lm_layer: one layer's device buffer, byte offsets and head norms."""
+
+    _fields_ = [("buf_dev", ctypes.c_void_p), ("buf_bytes", ctypes.c_int64)] + [
+        (n, ctypes.c_int64) for n in ("qkv", "qkv_scale", "o", "o_scale", "gu", "gu_scale", "d", "d_scale")] + [
+        ("q_norm_host", ctypes.c_void_p), ("k_norm_host", ctypes.c_void_p)]
+
+
+def lm_config(hidden, layers, heads, kv_heads, head_dim, intermediate, vocab, max_positions, fmt, eps=1e-6,
+              rope_theta=1e6):
+    return LmConfig(hidden, layers, heads, kv_heads, head_dim, intermediate, vocab, max_positions, eps, rope_theta,
+                    fmt, 0)
+
+
+def lm_layer_layout(cfg):
+    """gpu_darwin.go place(): (LmLayer with offsets, total bytes)."""
+    L, n = LmLayer(), ctypes.c_int64()
+    check(load().gphq_lm_layer_layout(ctypes.byref(cfg), ctypes.byref(L), ctypes.byref(n)))
+    return L, n.value
+
+
+def lm_head_layout(cfg):
+    """loadHead's buffer: (rows, scale_offset, bytes)."""
+    r, so, n = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    check(load().gphq_lm_head_layout(ctypes.byref(cfg), ctypes.byref(r), ctypes.byref(so), ctypes.byref(n)))
+    return r.value, so.value, n.value
+
+
+class Lm:
+    """gphq_lm: a device-resident qwen3lm model (gpuModel). Bound device
+    buffers are kept alive by this object."""
+
+    def __init__(self, cfg):
+        h = ctypes.c_void_p()
+        check(load().gphq_lm_new(ctypes.byref(cfg), ctypes.byref(h)))
+        self.h, self.cfg, self._keep = h, cfg, []
+
+    def close(self):
+        if self.h:
+            load().gphq_lm_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def bind_layer(self, layer, buf, desc, q_norm, k_norm):
+        """buf: uint8 device tensor laid out as desc (from lm_layer_layout)."""
+        import numpy as np
+
+        qn, qp = _host(q_norm, np.float32)
+        kn, kp = _host(k_norm, np.float32)
+        d = LmLayer.from_buffer_copy(desc)
+        d.buf_dev, d.buf_bytes = buf.data_ptr(), buf.numel() * buf.element_size()
+        d.q_norm_host, d.k_norm_host = qp, kp
+        check(load().gphq_lm_bind_layer(self.h, layer, ctypes.byref(d)))
+        self._keep.append(buf)
+
+    def bind_embed(self, embed):
+        """embed: int16/uint16-bit BF16 device tensor [vocab][hidden]."""
+        check(load().gphq_lm_bind_embed(self.h, embed.data_ptr(), embed.numel()))
+        self._keep.append(embed)
+
+    def bind_head(self, head, final_norm):
+        import numpy as np
+
+        fn, fp = _host(final_norm, np.float32)
+        check(load().gphq_lm_bind_head(self.h, head.data_ptr(), head.numel() * head.element_size(), fp))
+        self._keep.append(head)
+
+
+class Prefix:
+    """gphq_prefix: one lane's K/V cache (gpuPrefix)."""
+
+    def __init__(self, lm, capacity):
+        h = ctypes.c_void_p()
+        check(load().gphq_prefix_new(lm.h, capacity, ctypes.byref(h)))
+        self.h, self.lm, self.capacity = h, lm, capacity
+
+    def close(self):
+        if self.h:
+            load().gphq_prefix_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def kv(self):
+        """(kc, vc) device addresses and the capacity."""
+        k, v, c = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_int64()
+        check(load().gphq_prefix_kv(self.h, ctypes.byref(k), ctypes.byref(v), ctypes.byref(c)))
+        return k.value, v.value, c.value
+
+    def copy_from(self, src, n, stream=None):
+        check(load().gphq_prefix_copy(self.h, src.h, n, stream_handle(stream)))
+
+
+def _prefix_array(kvs):
+    arr = (ctypes.c_void_p * len(kvs))()
+    for i, p in enumerate(kvs):
+        arr[i] = p.h.value if p is not None and p.h else None
+    return arr
+
+
+class DecodeBatch:
+    """gphq_decode_batch: scratch for up to `capacity` lanes (gpuDecodeBatchWorkspace)."""
+
+    def __init__(self, lm, capacity):
+        h = ctypes.c_void_p()
+        check(load().gphq_decode_batch_new(lm.h, capacity, ctypes.byref(h)))
+        self.h, self.lm, self.capacity = h, lm, capacity
+
+    def close(self):
+        if self.h:
+            load().gphq_decode_batch_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_vec_min_lanes(self, lanes):
+        check(load().gphq_decode_batch_set_vec_min_lanes(self.h, lanes))
+
+    @staticmethod
+    def _args(positions, tokens):
+        import numpy as np
+
+        pos, pp = _host(positions, np.int64)
+        tok, tp = _host(tokens, np.int32)
+        return pos, pp, tok, tp
+
+    def into(self, kvs, positions, tokens, hidden, logits, stream=None):
+        """DecodeBatchInto: hidden [lanes][hidden], logits [lanes][vocab] device tensors."""
+        pos, pp, tok, tp = self._args(positions, tokens)
+        check(load().gphq_decode_batch_into(self.h, _prefix_array(kvs), len(kvs), pp, tp, ptr(hidden),
+                                            0 if hidden is None else hidden.numel(), ptr(logits),
+                                            0 if logits is None else logits.numel(), stream_handle(stream)))
+
+    def greedy_into(self, kvs, positions, tokens, hidden, next_tokens, stream=None):
+        """DecodeBatchGreedyInto: next_tokens int32 [lanes] device tensor."""
+        pos, pp, tok, tp = self._args(positions, tokens)
+        check(load().gphq_decode_batch_greedy_into(self.h, _prefix_array(kvs), len(kvs), pp, tp, ptr(hidden),
+                                                   0 if hidden is None else hidden.numel(), ptr(next_tokens),
+                                                   stream_handle(stream)))
+
+    def greedy_run(self, kvs, positions, tokens, steps, tokens_out, hidden=None, stream=None):
+        """`steps` chained greedy steps; tokens_out int32 [steps][lanes] device tensor."""
+        pos, pp, tok, tp = self._args(positions, tokens)
+        check(load().gphq_decode_greedy_run(self.h, _prefix_array(kvs), len(kvs), pp, tp, steps, ptr(tokens_out),
+                                            tokens_out.numel(), ptr(hidden), 0 if hidden is None else hidden.numel(),
+                                            stream_handle(stream)))
+
+    def extend(self, kvs, positions, tokens, stream=None):
+        """Teacher-forced steps; tokens [steps][lanes] host array."""
+        import numpy as np
+
+        pos, pp = _host(positions, np.int64)
+        tok = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1, len(kvs))
+        check(load().gphq_decode_extend(self.h, _prefix_array(kvs), len(kvs), pp, tok.ctypes.data, tok.shape[0],
+                                        stream_handle(stream)))
+
+    def check(self, stream=None):
+        return check(load().gphq_decode_batch_check(self.h, stream_handle(stream)))
+
+
+def lm_from_stored(geom_kwargs, fmt, layers, embed_bf16, final_norm, head, device="cuda"):
+    """Builds a device model from stored (already quantized) host weights, as
+    loadGPU uploads prepareGPU's buffers: per layer one buffer with the
+    reference's placement. layers: objects with .qkv/.o/.gu/.down = (codes,
+    scales) numpy arrays and .q_norm/.k_norm; head = (codes, scales) of the
+    padded Q8B head."""
+    import numpy as np
+    import torch
+
+    cfg = lm_config(fmt=fmt, **geom_kwargs)
+    desc, nbytes = lm_layer_layout(cfg)
+    lm = Lm(cfg)
+
+    def put(buf, off, a):
+        b = np.ascontiguousarray(a).view(np.uint8).reshape(-1)
+        buf[off:off + b.size] = torch.from_numpy(b.copy())
+
+    for i, L in enumerate(layers):
+        host = torch.zeros(nbytes, dtype=torch.uint8)
+        for (c, sc), (wo, so) in zip((L.qkv, L.o, L.gu, L.down), ((desc.qkv, desc.qkv_scale), (desc.o, desc.o_scale),
+                                                                   (desc.gu, desc.gu_scale), (desc.d, desc.d_scale))):
+            put(host, wo, c)
+            put(host, so, sc)
+        lm.bind_layer(i, host.to(device), desc, L.q_norm, L.k_norm)
+    emb = torch.from_numpy(np.ascontiguousarray(embed_bf16).view(np.int16).reshape(cfg.vocab, cfg.hidden).copy())
+    lm.bind_embed(emb.to(device))
+    rows, so, hb = lm_head_layout(cfg)
+    host = torch.zeros(hb, dtype=torch.uint8)
+    put(host, 0, head[0])
+    put(host, so, head[1])
+    lm.bind_head(host.to(device), final_norm)
+    return lm

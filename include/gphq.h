@@ -36,6 +36,32 @@ extern "C" {
 #define GPHQ_ERR_HIP (-5)
 /* the format / mode argument is not one this library implements */
 #define GPHQ_ERR_UNSUPPORTED (-6)
+/* qwen3lm/gpu_darwin.go:124-126 "qwen3: the GPU backend needs 128-wide heads, at
+ * most 8 query heads per key/value head, and 64-aligned widths" (also the
+ * readConfig plausibility checks, weights.go:672-680) */
+#define GPHQ_ERR_GEOMETRY (-7)
+/* decode_batch.go:81-83 "qwen3: nil, closed, or foreign decode batch workspace" */
+#define GPHQ_ERR_FOREIGN_WORKSPACE (-8)
+/* decode_batch.go:85-89 "qwen3: decode batch has mismatched prefixes, tokens,
+ * hidden rows, logits rows, and next tokens" */
+#define GPHQ_ERR_BATCH_SHAPE (-9)
+/* decode_batch.go:90-92 (and :31-33 at creation) lanes beyond the workspace capacity */
+#define GPHQ_ERR_LANE_CAPACITY (-10)
+/* decode_batch.go:95-97 "qwen3: decode prefix is nil, closed, or belongs to another evaluator" */
+#define GPHQ_ERR_FOREIGN_PREFIX (-11)
+/* decode_batch.go:98-102 "qwen3: decode prefix is duplicated" */
+#define GPHQ_ERR_DUPLICATE_PREFIX (-12)
+/* decode_batch.go:103-105 "qwen3: decode prefix has no room for another token" */
+#define GPHQ_ERR_PREFIX_FULL (-13)
+/* decode_batch.go:106-108 "qwen3: token in decode lane is outside vocabulary" */
+#define GPHQ_ERR_TOKEN_RANGE (-14)
+/* decode_batch.go:112-125 "qwen3: decode batch destinations overlap inputs" */
+#define GPHQ_ERR_OVERLAP (-15)
+/* gpu_darwin.go:1245-1249 "qwen3: non-finite batched hidden state" */
+#define GPHQ_ERR_NON_FINITE_HIDDEN (-16)
+/* decode_batch.go / gpu_darwin.go:1048-1069: the model has no head (LoadHead)
+ * or a layer / the embedding table is not bound */
+#define GPHQ_ERR_MODEL_INCOMPLETE (-17)
 
 /* The reference message for a status code ("" for GPHQ_OK). Static storage. */
 const char *gphq_error_string(int status);
@@ -282,6 +308,117 @@ int gphq_q8gemm_mul_into(float *dst_dev, int64_t dst_len, const float *x_dev, in
 int64_t gphq_mm_workspace_bytes(int64_t m, int64_t k);
 int gphq_mm(int fmt, const void *codes_dev, const void *scales_dev, const uint8_t *zeros_dev, const float *x_dev,
             float *y_dev, int64_t m, int64_t k, int64_t n, void *work_dev, int64_t work_bytes, void *stream);
+
+/* ---- qwen3lm GPU decode provider (the lane API) ----------------------------
+ * Replaces the Metal provider's single-token decode: gpuModel
+ * (qwen3lm/gpu_darwin.go:62-102, loadGPU 161-338, loadHead 340-373),
+ * gpuPrefix (800-893) and gpuDecodeBatchWorkspace (731-759, 1046-1281) behind
+ * Evaluator.NewDecodeBatchWorkspace / DecodeBatchInto /
+ * DecodeBatchGreedyInto (decode_batch.go:23-78). A step runs wholly on the
+ * device: embedding + hidden rotation, per layer QKV (RMSNorm fused) ->
+ * attention (head RMSNorm, RoPE, K/V append, softmax over 0..pos) -> O
+ * (+ residual) -> gate/up (RMSNorm, SwiGLU) -> [down input Hadamard for Q8/Q4]
+ * -> down (+ residual), then final norm, Q8B head and first-maximum argmax.
+ * fp32 arithmetic; results agree with the reference's float64 semantics to
+ * the reference GPU tests' bounds (gpu_decode_batch_darwin_test.go:121-131),
+ * not bit for bit. */
+#define GPHQ_DECODE_MAX_LANES 32
+
+/* The model geometry (config.json fields the reference reads, weights.go:
+ * 621-700) and the layer weight format (gpuModel.bits: GPHQ_FMT_Q8, Q8B or
+ * Q4; GPHQ_FMT_Q8B_F32 is Q8B with fp32 block scales). */
+typedef struct gphq_lm_config {
+    int64_t hidden, layers, heads, kv_heads, head_dim, intermediate, vocab, max_positions;
+    double eps, rope_theta;
+    int32_t fmt;
+    int32_t reserved;
+} gphq_lm_config;
+
+/* One layer (gpuLayer, gpu_darwin.go:45-56): a device buffer holding the
+ * quantized projections as prepareGPU writes them (gpu_darwin.go:392-569):
+ * fused QKV rows [q_dim + 2 kv_dim][hidden] = W.diag(input_norm).R^T (value
+ * rows may carry the per-head Hadamard), O [hidden][q_dim], gate/up rows
+ * interleaved [2 inter][hidden] (row 2i gate, 2i+1 up, post-attention norm
+ * folded), down [hidden][inter]; each region's codes then scales at the byte
+ * offsets given, the buffer 256-byte aligned. q_norm / k_norm: host float[128]
+ * (copied at bind). */
+typedef struct gphq_lm_layer {
+    const void *buf_dev;
+    int64_t buf_bytes;
+    int64_t qkv, qkv_scale, o, o_scale, gu, gu_scale, d, d_scale;
+    const float *q_norm_host, *k_norm_host;
+} gphq_lm_layer;
+
+typedef struct gphq_lm gphq_lm;
+typedef struct gphq_prefix gphq_prefix;
+typedef struct gphq_decode_batch gphq_decode_batch;
+
+/* The reference's per-layer placement (gpu_darwin.go:243-283 place): fills the
+ * offsets and buf_bytes of *out (buf_dev and norms untouched). */
+int gphq_lm_layer_layout(const gphq_lm_config *cfg, gphq_lm_layer *out, int64_t *bytes);
+/* loadHead's buffer (gpu_darwin.go:340-346): rows = vocab padded to 16, Q8B
+ * codes [rows][hidden], FP16 scales at scale_offset. */
+int gphq_lm_head_layout(const gphq_lm_config *cfg, int64_t *rows, int64_t *scale_offset, int64_t *bytes);
+/* gpuGeometry check (gpu_darwin.go:116-129), RoPE table (232-241: float32 of
+ * float64 cos/sin, min(max_positions, 65536) rows) and rotation signs
+ * (hadamard.go:24-47). Weights are bound afterwards. */
+int gphq_lm_new(const gphq_lm_config *cfg, gphq_lm **out);
+void gphq_lm_free(gphq_lm *lm);
+int gphq_lm_bind_layer(gphq_lm *lm, int64_t layer, const gphq_lm_layer *desc);
+/* The embedding table as raw BF16 bits [vocab][hidden] in device memory
+ * (Weights.embed, weights.go:614-619), unrotated. */
+int gphq_lm_bind_embed(gphq_lm *lm, const uint16_t *embed_dev, int64_t len);
+/* The Q8B head W.R^T (loadHead) and the final norm weight (host float[hidden]). */
+int gphq_lm_bind_head(gphq_lm *lm, const void *head_dev, int64_t bytes, const float *final_norm_host);
+
+/* gpuPrefix: a lane's private fp32 K/V cache [layers][capacity][kv_dim] each,
+ * zeroed. The token count lives with the caller (PrefixKV.tokens), who passes
+ * it as the lane's position. */
+int gphq_prefix_new(const gphq_lm *lm, int64_t capacity, gphq_prefix **out);
+void gphq_prefix_free(gphq_prefix *p);
+int gphq_prefix_kv(const gphq_prefix *p, float **kc_dev, float **vc_dev, int64_t *capacity);
+/* copyFrom (gpu_darwin.go:873-881): the first n rows of every layer. */
+int gphq_prefix_copy(gphq_prefix *dst, const gphq_prefix *src, int64_t n, void *stream);
+
+/* NewDecodeBatchWorkspace (decode_batch.go:27-39; gpu_darwin.go:1046-1108):
+ * scratch for 1..GPHQ_DECODE_MAX_LANES lanes (the reference caps at 8). */
+int gphq_decode_batch_new(const gphq_lm *lm, int64_t capacity, gphq_decode_batch **out);
+void gphq_decode_batch_free(gphq_decode_batch *ws);
+/* Lane count from which the step's GEMVs use the multi-vector MFMA kernel
+ * (default 2; a larger value keeps the per-lane fp32 GEMV). */
+int gphq_decode_batch_set_vec_min_lanes(gphq_decode_batch *ws, int64_t lanes);
+/* DecodeBatchInto (decode_batch.go:41-59): lane l at position positions[l]
+ * (its prefix's token count) takes host token tokens[l]; writes the lane's
+ * post-final-norm hidden state to hidden_dev[l*hidden..] and its logits to
+ * logits_dev[l*vocab..], and appends the K/V row. Validation follows
+ * decode_batch.go:80-146 in order, before any device work. */
+int gphq_decode_batch_into(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
+                           const int32_t *tokens, float *hidden_dev, int64_t hidden_len, float *logits_dev,
+                           int64_t logits_len, void *stream);
+/* DecodeBatchGreedyInto (decode_batch.go:61-78): as above, but next_dev[l]
+ * receives the first-maximum token (greedy_argmax_rows, gpu.metal:192-237)
+ * instead of the logits. */
+int gphq_decode_batch_greedy_into(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes,
+                                  const int64_t *positions, const int32_t *tokens, float *hidden_dev,
+                                  int64_t hidden_len, int32_t *next_dev, void *stream);
+/* `steps` chained greedy steps: step t of lane l consumes the token step t-1
+ * chose (tokens[l] first) at position positions[l] + t; tokens_out_dev
+ * [steps][lanes] receives every chosen token, hidden_dev (or NULL) the last
+ * step's hidden states. The device keeps tokens and positions between
+ * steps, so the host enqueues without waiting (the reference's Decoder run,
+ * gpu_darwin.go:1913-2006, chains steps in one command buffer the same way). */
+int gphq_decode_greedy_run(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
+                           const int32_t *tokens, int64_t steps, int32_t *tokens_out_dev, int64_t tokens_out_len,
+                           float *hidden_dev, int64_t hidden_len, void *stream);
+/* Teacher-forced extension of each lane's prefix by tokens [steps][lanes]
+ * (the one-token-at-a-time pass of encodeTokens, gpu_darwin.go:1768-1814):
+ * appends K/V rows; no head. */
+int gphq_decode_extend(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
+                       const int32_t *tokens, int64_t steps, void *stream);
+/* Waits for the stream and reports GPHQ_ERR_NON_FINITE_HIDDEN if a step since
+ * the last check produced a non-finite hidden value (the reference's error,
+ * gpu_darwin.go:1245-1249, which it raises before returning). */
+int gphq_decode_batch_check(gphq_decode_batch *ws, void *stream);
 
 #ifdef __cplusplus
 }

@@ -609,3 +609,59 @@ double orc_gptq_g128_weight(const uint32_t *codes, const uint16_t *scales, const
     int z = zeros[row * (k / 128) + i / 128] & 15;
     return (double)(q - z) * (double)orc_f16_to_f32(scales[row * (k / 128) + i / 128]);
 }
+
+/* ------------------------------------------------------------------ */
+/* Randomized Hadamard rotation of the qwen3lm GPU residual stream.
+ * Pinned by: splitmix64 against its published first outputs; apply against
+ * the dense matrix scale*H*diag(signs) (scipy's Sylvester Hadamard) in
+ * float64; orthogonality and dot-product preservation as
+ * qwen3lm/kernels_test.go:73-111; unapply(apply(x)) == x (tests/test_oracle_lm.py). */
+
+/* One splitmix64 step (Steele, Lea and Flood 2014), as hadamard.go:33-38:
+ * state += golden; z = state; two xor-shift-multiply rounds; z ^= z >> 31. */
+uint64_t orc_splitmix64_next(uint64_t *state) {
+    *state += 0x9e3779b97f4a7c15ull;
+    uint64_t z = *state;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+/* hadamard.go:24-47 newRotation: block is the largest power of two up to
+ * 4096 dividing k; sign i is -1 when the low bit of the i-th splitmix64
+ * output (state seeded with golden ^ k) is set; scale = float32(1/sqrt(block)).
+ * Returns the block; writes k signs and the scale. */
+int64_t orc_rotation(int64_t k, float *signs, float *scale) {
+    int64_t block = 1;
+    while (block < 4096 && k % (2 * block) == 0) block *= 2;
+    uint64_t state = 0x9e3779b97f4a7c15ull ^ (uint64_t)k;
+    for (int64_t i = 0; i < k; ++i) signs[i] = (orc_splitmix64_next(&state) & 1) ? -1.0f : 1.0f;
+    *scale = (float)(1.0 / sqrt((double)block));
+    return block;
+}
+
+/* hadamard.go:62-78 fwht: the unnormalized Walsh-Hadamard butterfly network
+ * in natural (Sylvester) order, stage h = 1, 2, 4, ...: (a, b) -> (a+b, a-b). */
+void orc_fwht(float *v, int64_t n) {
+    for (int64_t h = 1; h < n; h *= 2)
+        for (int64_t i = 0; i < n; i += 2 * h)
+            for (int64_t j = i; j < i + h; ++j) {
+                float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+}
+
+/* hadamard.go:51-58 apply: per block, v = (v * scale) * sign, then fwht. */
+void orc_rotation_apply(const float *signs, int64_t block, float scale, float *x, int64_t k) {
+    for (int64_t b = 0; b < k; b += block) {
+        for (int64_t i = b; i < b + block; ++i) x[i] = x[i] * scale * signs[i];
+        orc_fwht(x + b, block);
+    }
+}
+
+/* hadamard.go:80-86 unapply: fwht per block, then (v * scale) * sign. */
+void orc_rotation_unapply(const float *signs, int64_t block, float scale, float *x, int64_t k) {
+    for (int64_t b = 0; b < k; b += block) orc_fwht(x + b, block);
+    for (int64_t i = 0; i < k; ++i) x[i] = x[i] * scale * signs[i];
+}

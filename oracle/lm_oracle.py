@@ -1,0 +1,258 @@
+"""float64 restatement of one qwen3lm GPU decode step (the lane API's
+DecodeBatchInto / DecodeBatchGreedyInto), for parity tests.
+
+TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module; the product library never does.
+
+What is restated (reference paths are relative to the gophonic tree):
+
+* The residual stream lives in the hidden rotation's basis R = scale*H*diag(s)
+  (qwen3lm/hadamard.go:13-86, gpu_darwin.go:57-61). The token's BF16
+  embedding row is rotated on entry (gpu_darwin.go:1170-1175).
+* Per layer (gpu_darwin.go:1193-1235, kernels gpu.metal:68-162, 339-466):
+  QKV GEMV over the RMS-normalized residual (PRO_NORM: the input RMSNorm
+  weight is folded into the stored rows), attend1 (head RMSNorm with q_norm /
+  k_norm, RoPE from a float32 table, K/V append at row `pos`, softmax over
+  rows 0..pos), O GEMV added to the residual (EPI_ADD), gate/up GEMV over the
+  normalized residual with interleaved gate/up rows and SwiGLU (EPI_SWIGLU),
+  the down input's online Hadamard for Q8 and Q4 weights (rotate, skipped for
+  Q8B, gpu_darwin.go:209-215), down GEMV added to the residual.
+* After the layers (gpu_darwin.go:1241-1280): R^T, final RMSNorm with the
+  final norm weight (ops.go:251-254) -> the hidden output; R again; the Q8B
+  head GEMV over vocab rows; first-maximum argmax (decode_batch.go:182-191).
+
+Everything is float64 on the dequantized weights (the kernels' per-block
+scaling is exact in float64), so this is the precision target the fp32 device
+path is measured against. Pinned against Hugging Face transformers' Qwen3 in
+float64 (tests/test_oracle_lm.py), with the unrotated weights the stored ones
+imply.
+"""
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import oracle as orc
+
+FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
+
+
+@dataclass(frozen=True)
+class Geometry:
+    """A dense Qwen3 decoder's shape (lmtest.Geometry, lmtest/lmtest.go:22-24)."""
+
+    hidden: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    inter: int
+    vocab: int
+    max_pos: int
+    eps: float = 1e-6
+    theta: float = 1e6
+
+    @property
+    def qd(self):
+        return self.heads * self.head_dim
+
+    @property
+    def kvd(self):
+        return self.kv_heads * self.head_dim
+
+    @property
+    def head_rows(self):
+        # gpuModel.loadHead pads the vocabulary to 16 rows (gpu_darwin.go:343).
+        return (self.vocab + 15) // 16 * 16
+
+
+def rotation(k):
+    """hadamard.go:24-47 newRotation: (signs float32[k], block, scale)."""
+    signs = np.empty(k, np.float32)
+    scale = np.zeros(1, np.float32)
+    block = orc.lib().orc_rotation(k, orc._p(signs, orc._f32p), orc._p(scale, orc._f32p))
+    return signs, int(block), float(scale[0])
+
+
+def hadamard_f64(v, block):
+    """Unnormalized Walsh-Hadamard transform of each `block` run of the last
+    axis, in natural order (the network of hadamard.go:62-78), float64."""
+    v = np.array(v, dtype=np.float64, copy=True)
+    shape = v.shape
+    v = v.reshape(-1, block)
+    h = 1
+    while h < block:
+        w = v.reshape(v.shape[0], -1, 2, h)
+        a, b = w[:, :, 0, :].copy(), w[:, :, 1, :].copy()
+        w[:, :, 0, :] = a + b
+        w[:, :, 1, :] = a - b
+        h *= 2
+    return v.reshape(shape)
+
+
+def rot_apply(x, rot):
+    signs, block, scale = rot
+    return hadamard_f64(np.asarray(x, np.float64) * scale * signs, block)
+
+
+def rot_unapply(x, rot):
+    signs, block, scale = rot
+    return hadamard_f64(x, block) * scale * signs
+
+
+def rot_matrix(rot):
+    """The dense orthogonal matrix R with R @ x == rot_apply(x, rot)."""
+    signs, block, scale = rot
+    k = len(signs)
+    return rot_apply(np.eye(k), rot).T
+
+
+def bf16_to_f64(bits):
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def dequant(fmt, codes, scales, n, k):
+    """float64 [n][k] of a qwen3lm weight matrix (gpu.metal:46-61 formats)."""
+    if fmt == FMT_Q4:
+        b = np.asarray(codes, np.uint8).reshape(n, k // 32, 16)
+        v = np.concatenate([(b & 15), (b >> 4)], axis=2).astype(np.float64) - 8.0
+        d = np.asarray(scales, np.uint16).view(np.float16).astype(np.float64).reshape(n, k // 32, 1)
+        return (v * d).reshape(n, k)
+    q = np.asarray(codes, np.int8).reshape(n, k).astype(np.float64)
+    if fmt == FMT_Q8:
+        return q * np.asarray(scales, np.float32).astype(np.float64).reshape(n, 1)
+    if fmt == FMT_Q8B:
+        d = np.asarray(scales, np.uint16).view(np.float16).astype(np.float64)
+    elif fmt == FMT_Q8B_F32:
+        d = np.asarray(scales, np.float32).astype(np.float64)
+    else:
+        raise ValueError(f"format {fmt}")
+    return (q.reshape(n, k // 32, 32) * d.reshape(n, k // 32, 1)).reshape(n, k)
+
+
+def rope_table(geom, positions):
+    """gpu_darwin.go:232-241: float32(cos/sin(pos * invFreq[d])) with
+    invFreq[d] = 1/theta^(2d/headDim) in float64 (weights.go:685-688)."""
+    half = geom.head_dim // 2
+    inv = 1.0 / np.power(geom.theta, (2.0 * np.arange(half)) / geom.head_dim)
+    ang = np.arange(positions, dtype=np.float64)[:, None] * inv[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+@dataclass
+class Layer:
+    """One layer's stored projections (gpuLayer, gpu_darwin.go:45-56):
+    (codes, scales) of the fused QKV rows [qd+2kvd][hidden], O [hidden][qd],
+    interleaved gate/up [2*inter][hidden] (row 2i gate, 2i+1 up) and down
+    [hidden][inter]; q_norm / k_norm float32[head_dim]."""
+
+    qkv: tuple
+    o: tuple
+    gu: tuple
+    down: tuple
+    q_norm: np.ndarray
+    k_norm: np.ndarray
+
+
+class DecodeOracle:
+    """float64 single-token decode over stored qwen3lm GPU weights."""
+
+    def __init__(self, geom, fmt, layers, embed_bf16, final_norm, head):
+        g = geom
+        self.g, self.fmt = g, fmt
+        self.hrot, self.irot = rotation(g.hidden), rotation(g.inter)
+        self.embed = np.asarray(embed_bf16, np.uint16).reshape(g.vocab, g.hidden)
+        self.final_norm = np.asarray(final_norm, np.float32).astype(np.float64)
+        self.W = []
+        for L in layers:
+            self.W.append(dict(
+                qkv=dequant(fmt, *L.qkv, g.qd + 2 * g.kvd, g.hidden),
+                o=dequant(fmt, *L.o, g.hidden, g.qd),
+                gu=dequant(fmt, *L.gu, 2 * g.inter, g.hidden),
+                down=dequant(fmt, *L.down, g.hidden, g.inter),
+                qn=np.asarray(L.q_norm, np.float32).astype(np.float64),
+                kn=np.asarray(L.k_norm, np.float32).astype(np.float64),
+            ))
+        self.head = dequant(FMT_Q8B, *head, g.head_rows, g.hidden)[: g.vocab]
+        cos, sin = rope_table(g, g.max_pos)
+        self.cos, self.sin = cos.astype(np.float64), sin.astype(np.float64)
+
+    def new_cache(self, capacity):
+        g = self.g
+        return [(np.zeros((capacity, g.kvd)), np.zeros((capacity, g.kvd))) for _ in range(g.layers)]
+
+    def _norm(self, v, w=None):
+        inv = 1.0 / np.sqrt(np.dot(v, v) / len(v) + self.g.eps)
+        return v * inv if w is None else v * inv * w
+
+    def _rope(self, v, pos):
+        half = self.g.head_dim // 2
+        c, s = self.cos[pos], self.sin[pos]
+        a, b = v[:half].copy(), v[half:].copy()
+        return np.concatenate([a * c - b * s, b * c + a * s])
+
+    def embed_row(self, token):
+        """The rotated input row (gpu_darwin.go:1172-1174)."""
+        return rot_apply(bf16_to_f64(self.embed[token]), self.hrot)
+
+    def layers(self, cache, pos, h):
+        """Runs every layer on residual h (rotated basis) at position pos,
+        appending K/V to cache; returns the new residual."""
+        g = self.g
+        grp = g.heads // g.kv_heads
+        scale = 1.0 / np.sqrt(g.head_dim)
+        hd = g.head_dim
+        for li, W in enumerate(self.W):
+            qkv = W["qkv"] @ self._norm(h)
+            kc, vc = cache[li]
+            for kh in range(g.kv_heads):
+                k = qkv[g.qd + kh * hd: g.qd + (kh + 1) * hd]
+                v = qkv[g.qd + g.kvd + kh * hd: g.qd + g.kvd + (kh + 1) * hd]
+                kc[pos, kh * hd:(kh + 1) * hd] = self._rope(self._norm(k, W["kn"]), pos)
+                vc[pos, kh * hd:(kh + 1) * hd] = v
+            ctx = np.empty(g.qd)
+            for qh in range(g.heads):
+                kh = qh // grp
+                q = self._rope(self._norm(qkv[qh * hd:(qh + 1) * hd], W["qn"]), pos) * scale
+                s = kc[: pos + 1, kh * hd:(kh + 1) * hd] @ q
+                p = np.exp(s - s.max())
+                ctx[qh * hd:(qh + 1) * hd] = (p / p.sum()) @ vc[: pos + 1, kh * hd:(kh + 1) * hd]
+            h = h + W["o"] @ ctx
+            gu = W["gu"] @ self._norm(h)
+            gate, up = gu[0::2], gu[1::2]
+            act = gate / (1.0 + np.exp(-gate)) * up
+            if self.fmt != FMT_Q8B:
+                act = rot_apply(act, self.irot)
+            h = h + W["down"] @ act
+        return h
+
+    def finish(self, h):
+        """(hidden, logits): R^T, final RMSNorm, R, head (first vocab rows)."""
+        hu = rot_unapply(h, self.hrot)
+        hidden = self._norm(hu, self.final_norm)
+        logits = self.head @ rot_apply(hidden, self.hrot)
+        return hidden, logits
+
+    def step(self, cache, pos, token):
+        """One decode step for one lane: (hidden, logits, next_token)."""
+        h = self.layers(cache, pos, self.embed_row(token))
+        hidden, logits = self.finish(h)
+        return hidden, logits, greedy_argmax(logits)
+
+
+def greedy_argmax(values):
+    """decode_batch.go:182-191: strict greater-than scan from index 0; ties
+    keep the first index; NaNs never replace the best."""
+    best, at = values[0], 0
+    for i in range(1, len(values)):
+        if values[i] > best:
+            best, at = values[i], i
+    return at
+
+
+def greedy_argmax_np(values):
+    """The same rule, vectorized (NaN at index 0 keeps index 0)."""
+    v = np.asarray(values)
+    if np.isnan(v[0]):
+        return 0
+    w = np.where(np.isnan(v), -np.inf, v)
+    return int(np.argmax(w))

@@ -63,6 +63,11 @@ def _load():
         "orc_f16_to_f32_array": (None, [_u16p, _f32p, _i64]),
         "orc_i8_quantize_array": (None, [_f32p, _i8p, _i64]),
         "orc_mm_f64": (None, [ctypes.c_int, _vp, _vp, _u8p, _f32p, _f64p, _f64p, _i64, _i64, _i64]),
+        "orc_splitmix64_next": (ctypes.c_uint64, [ctypes.POINTER(ctypes.c_uint64)]),
+        "orc_rotation": (_i64, [_i64, _f32p, _f32p]),
+        "orc_fwht": (None, [_f32p, _i64]),
+        "orc_rotation_apply": (None, [_f32p, _i64, ctypes.c_float, _f32p, _i64]),
+        "orc_rotation_unapply": (None, [_f32p, _i64, ctypes.c_float, _f32p, _i64]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -313,3 +318,25 @@ def mm_f64(fmt, codes, scales, x, m, k, n, zeros=None):
     lib().orc_mm_f64(fmt, codes.ctypes.data, scales.ctypes.data, None if z is None else _p(z, _u8p), _p(x, _f32p),
                      _p(y, _f64p), _p(a, _f64p), m, k, n)
     return y, a
+
+
+def splitmix64_outputs(seed, count):
+    """The first `count` outputs of splitmix64 from state `seed`."""
+    st = ctypes.c_uint64(seed)
+    return [lib().orc_splitmix64_next(ctypes.byref(st)) for _ in range(count)]
+
+
+def rotation_apply_f32(x, rot):
+    """hadamard.go:51-58 rotation.apply in float32 (rot = (signs, block, scale))."""
+    signs, block, scale = rot
+    v = _c(x, np.float32).copy()
+    lib().orc_rotation_apply(_p(_c(signs, np.float32), _f32p), block, scale, _p(v, _f32p), len(v))
+    return v
+
+
+def rotation_unapply_f32(x, rot):
+    """hadamard.go:80-86 rotation.unapply in float32."""
+    signs, block, scale = rot
+    v = _c(x, np.float32).copy()
+    lib().orc_rotation_unapply(_p(_c(signs, np.float32), _f32p), block, scale, _p(v, _f32p), len(v))
+    return v

@@ -77,3 +77,50 @@ def test_gemv_rejects_bad_formats_and_shapes():
     assert lib.gphq_gemv(gphq.FMT_Q8B, p, p, p, p, -32, 4, None) == gphq.ERR_DIMENSIONS
     assert lib.gphq_gemv(gphq.FMT_Q8B, ctypes.c_void_p(8), p, p, p, 64, 4, None) == gphq.ERR_DIMENSIONS  # alignment
     assert lib.gphq_gemv(gphq.FMT_Q8B, p, p, p, p, 64, 0, None) == gphq.OK  # nothing to do
+
+
+def _lm_cfg(**kw):
+    base = dict(hidden=4096, layers=36, heads=32, kv_heads=8, head_dim=128, intermediate=12288, vocab=151936,
+                max_positions=40960, fmt=gphq.FMT_Q8B)
+    base.update(kw)
+    return gphq.lm_config(**base)
+
+
+def test_lm_layer_layout_qwen3_8b_q8b():
+    # gpu_darwin.go:251-283 place(): codes then scales, 256-byte aligned regions.
+    L, n = gphq.lm_layer_layout(_lm_cfg())
+    qkv_rows = 4096 + 2 * 1024
+    assert (L.qkv, L.qkv_scale) == (0, qkv_rows * 4096)
+    assert L.o == qkv_rows * 4096 + 2 * qkv_rows * 128
+    assert L.gu_scale - L.gu == 24576 * 4096
+    assert L.d_scale - L.d == 4096 * 12288
+    assert n == L.d_scale + 2 * 4096 * 384 == 204996608
+    # Q8 keeps one fp32 scale per row; Q4 halves the codes.
+    L8, n8 = gphq.lm_layer_layout(_lm_cfg(fmt=gphq.FMT_Q8))
+    assert L8.o - L8.qkv_scale == 4 * qkv_rows
+    L4, _ = gphq.lm_layer_layout(_lm_cfg(fmt=gphq.FMT_Q4))
+    assert L4.qkv_scale == qkv_rows * 2048
+
+
+def test_lm_head_layout_pads_vocab_to_16():
+    rows, so, n = gphq.lm_head_layout(_lm_cfg(vocab=151937))
+    assert rows == 151952 and so == (151952 * 4096 + 255) // 256 * 256 and n == so + 2 * 151952 * 128
+
+
+@pytest.mark.parametrize("kw", [dict(head_dim=64, heads=64), dict(heads=72, kv_heads=8), dict(hidden=4000),
+                                dict(intermediate=12320), dict(heads=30, kv_heads=8), dict(eps=0.0),
+                                dict(intermediate=96 * 5)])
+def test_lm_new_rejects_geometry_before_device_work(kw):
+    # gpu_darwin.go:116-129 gpuGeometry and weights.go:678-680.
+    lib = gphq.load()
+    h = ctypes.c_void_p()
+    assert lib.gphq_lm_new(ctypes.byref(_lm_cfg(**kw)), ctypes.byref(h)) == gphq.ERR_GEOMETRY
+    assert not h.value
+
+
+def test_decode_entry_points_reject_null_workspace():
+    lib = gphq.load()
+    p = ctypes.c_void_p(256)
+    assert lib.gphq_decode_batch_into(None, None, 1, p, p, p, 1, p, 1, None) == gphq.ERR_FOREIGN_WORKSPACE
+    assert lib.gphq_decode_batch_new(None, 1, ctypes.byref(ctypes.c_void_p())) == gphq.ERR_FOREIGN_WORKSPACE
+    assert gphq.error_string(gphq.ERR_PREFIX_FULL) == "qwen3: decode prefix has no room for another token"

@@ -1,0 +1,258 @@
+"""GPU parity of the qwen3lm decode provider (gphq_lm / gphq_prefix /
+gphq_decode_*), through the C ABI, against the float64 oracle
+(oracle/lm_oracle.py, itself pinned to transformers' Qwen3).
+
+Bounds are the reference GPU decode test's (gpu_decode_batch_darwin_test.go:
+121-131: hidden relative 1e-5, logits relative 1e-5), applied as relative L2
+against float64, plus a max-abs bound scaled to the vector's magnitude (the
+reference's absolute 1e-4 / 2e-4 assume real-checkpoint magnitudes of about
+1; these random-weight models run at about 30-100x that).
+"""
+import numpy as np
+import pytest
+
+from gophonic_amd import gphq
+from oracle import lm_oracle as lo
+from tests import lm_common as lc
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5
+
+
+def geom_kwargs(g):
+    return dict(hidden=g.hidden, layers=g.layers, heads=g.heads, kv_heads=g.kv_heads, head_dim=g.head_dim,
+                intermediate=g.inter, vocab=g.vocab, max_positions=g.max_pos, eps=g.eps, rope_theta=g.theta)
+
+
+def device_model(model):
+    return gphq.lm_from_stored(geom_kwargs(model["geom"]), model["fmt"], model["layers"], model["embed"],
+                               model["final_norm"], model["head"])
+
+
+def err(want, got):
+    want, got = np.asarray(want, np.float64), np.asarray(got, np.float64)
+    assert np.isfinite(got).all()
+    d = want - got
+    return float(np.sqrt((d ** 2).sum() / (want ** 2).sum())), float(np.abs(d).max() / np.abs(want).max())
+
+
+def top_gap(logits):
+    s = np.sort(np.asarray(logits, np.float64))
+    return s[-1] - s[-2]
+
+
+_CACHE = {}
+
+
+def setup(geom, fmt, seed):
+    key = (geom, fmt, seed)
+    if key not in _CACHE:
+        model = lc.random_model(geom, fmt, seed)
+        _CACHE.clear()
+        _CACHE[key] = (model, lc.oracle_for(model), device_model(model))
+    return _CACHE[key]
+
+
+def prefill(oracle, ws, kvs, prompts):
+    """Extends each lane by its prompt (teacher-forced), on the device and in
+    the oracle; returns the oracle caches and positions."""
+    caches = [oracle.new_cache(kv.capacity) for kv in kvs]
+    lanes = len(kvs)
+    pos = [0] * lanes
+    steps = max(len(p) for p in prompts)
+    for t in range(steps):
+        active = [i for i in range(lanes) if t < len(prompts[i])]
+        if not active:
+            continue
+        ws.extend([kvs[i] for i in active], [pos[i] for i in active], [[prompts[i][t] for i in active]])
+        for i in active:
+            oracle.layers(caches[i], pos[i], oracle.embed_row(prompts[i][t]))
+            pos[i] += 1
+    return caches, pos
+
+
+@pytest.mark.parametrize("fmt", lc.FMTS)
+@pytest.mark.parametrize("lanes", [1, 3])
+def test_decode_batch_into_matches_oracle(fmt, lanes):
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, fmt, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(100 + lanes)
+    ws = gphq.DecodeBatch(lm, 4)
+    kvs = [gphq.Prefix(lm, 64) for _ in range(lanes)]
+    prompts = [list(rng.integers(0, g.vocab, n)) for n in (0, 5, 17)[:lanes]]
+    caches, pos = prefill(oracle, ws, kvs, prompts)
+    tokens = list(rng.integers(0, g.vocab, lanes))
+    hidden = torch.full((lanes, g.hidden), -5.0, device="cuda")
+    logits = torch.full((lanes, g.vocab), -5.0, device="cuda")
+    ws.into(kvs, pos, tokens, hidden, logits)
+    ws.check()
+    hid, lg = hidden.cpu().numpy(), logits.cpu().numpy()
+    for i in range(lanes):
+        wh, wl, _ = oracle.step(caches[i], pos[i], tokens[i])
+        rh, ah = err(wh, hid[i])
+        rl, al = err(wl, lg[i])
+        assert rh <= REL and rl <= REL, (i, rh, rl)
+        assert ah <= 10 * REL and al <= 10 * REL, (i, ah, al)
+        # The appended K/V row equals the oracle's (the cache the next step reads).
+        kc, vc, cap = kvs[i].kv()
+        for layer in (0, g.layers - 1):
+            for name, base, want in (("k", kc, caches[i][layer][0]), ("v", vc, caches[i][layer][1])):
+                got = _read_dev_floats(base + ((layer * cap + pos[i]) * g.kvd) * 4, g.kvd)
+                r, _ = err(want[pos[i]], got)
+                assert r <= REL, (name, layer, r)
+
+
+def _read_dev_floats(addr, n):
+    """Copies n floats from a raw device address (a prefix's cache)."""
+    import ctypes
+
+    import torch
+
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    # The HIP runtime torch loaded (same soname), so device addresses agree.
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    torch.cuda.synchronize()
+    assert hip.hipMemcpy(out.data_ptr(), addr, n * 4, 3) == 0  # hipMemcpyDeviceToDevice
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt", [lo.FMT_Q8B, lo.FMT_Q8])
+def test_decode_06b_widths_long_context(fmt):
+    # Qwen3-0.6B widths (16 query / 8 KV heads, hidden 1024, inter 3072) with a
+    # 300-token context: many attention splits and more than one block per
+    # split's key range.
+    import torch
+
+    model, oracle, lm = setup(lc.SMALL_06B, fmt, seed=9)
+    g = model["geom"]
+    rng = np.random.default_rng(7)
+    ws = gphq.DecodeBatch(lm, 2)
+    kvs = [gphq.Prefix(lm, 400), gphq.Prefix(lm, 320)]
+    prompts = [list(rng.integers(0, g.vocab, 300)), list(rng.integers(0, g.vocab, 41))]
+    caches, pos = prefill(oracle, ws, kvs, prompts)
+    for lanes in (1, 2):
+        tokens = list(rng.integers(0, g.vocab, lanes))
+        hidden = torch.empty((lanes, g.hidden), device="cuda")
+        logits = torch.empty((lanes, g.vocab), device="cuda")
+        ws.into(kvs[:lanes], pos[:lanes], tokens, hidden, logits)
+        hid, lg = hidden.cpu().numpy(), logits.cpu().numpy()
+        for i in range(lanes):
+            wh, wl, _ = oracle.step(caches[i], pos[i], tokens[i])
+            rh, _ = err(wh, hid[i])
+            rl, _ = err(wl, lg[i])
+            assert rh <= REL and rl <= REL, (lanes, i, rh, rl)
+            pos[i] += 1
+
+
+@pytest.mark.parametrize("lanes", [1, 2, 5])
+def test_greedy_into_and_run_match_oracle(lanes):
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(31 + lanes)
+    ws = gphq.DecodeBatch(lm, 8)
+    steps = 12
+    kvs = [gphq.Prefix(lm, 80) for _ in range(lanes)]
+    prompts = [list(rng.integers(0, g.vocab, 3 + 4 * i)) for i in range(lanes)]
+    caches, pos0 = prefill(oracle, ws, kvs, prompts)
+    # Copies of the prefixes for the chained run.
+    kvs2 = [gphq.Prefix(lm, 80) for _ in range(lanes)]
+    for a, b in zip(kvs2, kvs):
+        a.copy_from(b, max(pos0))
+    first = list(rng.integers(0, g.vocab, lanes))
+    # Step by step through greedy_into.
+    hidden = torch.empty((lanes, g.hidden), device="cuda")
+    nxt = torch.empty(lanes, dtype=torch.int32, device="cuda")
+    toks, pos, seq = list(first), list(pos0), []
+    for _ in range(steps):
+        ws.greedy_into(kvs, pos, toks, hidden, nxt)
+        toks = nxt.cpu().numpy().tolist()
+        seq.append(toks)
+        pos = [p + 1 for p in pos]
+    hid_step = hidden.cpu().numpy()
+    # The chained run on the copies gives the same tokens and hidden states.
+    out = torch.full((steps, lanes), -1, dtype=torch.int32, device="cuda")
+    hidden2 = torch.empty((lanes, g.hidden), device="cuda")
+    ws.greedy_run(kvs2, pos0, first, steps, out, hidden2)
+    ws.check()
+    assert out.cpu().numpy().tolist() == seq
+    np.testing.assert_array_equal(hidden2.cpu().numpy(), hid_step)
+    # Each chosen token is the oracle's argmax, teacher-forced with the GPU's
+    # choices (a near tie within the bound may go either way).
+    for i in range(lanes):
+        t = first[i]
+        for s in range(steps):
+            _, wl, want = oracle.step(caches[i], pos0[i] + s, t)
+            got = seq[s][i]
+            assert got == want or wl[want] - wl[got] <= 1e-4 * np.abs(wl).max(), (i, s, got, want)
+            t = got
+
+
+def test_lanes_together_match_lanes_alone():
+    # gpu_vector_batch_darwin_test.go:217-220: batched lanes agree with
+    # single-lane decodes to max_abs 1e-4 (scaled) and relative 1e-5.
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(77)
+    lanes = 6
+    ws = gphq.DecodeBatch(lm, lanes)
+    prompts = [list(rng.integers(0, g.vocab, 2 + i)) for i in range(lanes)]
+    tokens = list(rng.integers(0, g.vocab, lanes))
+    kvs_a = [gphq.Prefix(lm, 32) for _ in range(lanes)]
+    kvs_b = [gphq.Prefix(lm, 32) for _ in range(lanes)]
+    _, pos = prefill(oracle, ws, kvs_a, prompts)
+    for a, b in zip(kvs_b, kvs_a):
+        a.copy_from(b, max(pos))
+    hid = torch.empty((lanes, g.hidden), device="cuda")
+    lg = torch.empty((lanes, g.vocab), device="cuda")
+    ws.into(kvs_a, pos, tokens, hid, lg)
+    for i in range(lanes):
+        h1 = torch.empty((1, g.hidden), device="cuda")
+        l1 = torch.empty((1, g.vocab), device="cuda")
+        ws.into([kvs_b[i]], [pos[i]], [tokens[i]], h1, l1)
+        rh, ah = err(h1.cpu().numpy()[0], hid.cpu().numpy()[i])
+        rl, al = err(l1.cpu().numpy()[0], lg.cpu().numpy()[i])
+        assert rh <= REL and rl <= REL and ah <= 10 * REL and al <= 10 * REL, (i, rh, rl, ah, al)
+
+
+def test_validation_errors():
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    ws = gphq.DecodeBatch(lm, 2)
+    a, b = gphq.Prefix(lm, 4), gphq.Prefix(lm, 4)
+    hid = torch.empty((3, g.hidden), device="cuda")
+    nxt = torch.empty(3, dtype=torch.int32, device="cuda")
+
+    def status(fn):
+        try:
+            fn()
+        except gphq.GphqError as e:
+            return e.status
+        return gphq.OK
+
+    assert status(lambda: ws.greedy_into([a, b, gphq.Prefix(lm, 4)], [0, 0, 0], [1, 1, 1], hid, nxt)) == \
+        gphq.ERR_LANE_CAPACITY
+    assert status(lambda: ws.greedy_into([a, a], [0, 0], [1, 1], hid, nxt)) == gphq.ERR_DUPLICATE_PREFIX
+    assert status(lambda: ws.greedy_into([a], [4], [1], hid, nxt)) == gphq.ERR_PREFIX_FULL
+    assert status(lambda: ws.greedy_into([a], [0], [g.vocab], hid, nxt)) == gphq.ERR_TOKEN_RANGE
+    assert status(lambda: ws.greedy_into([a], [0], [-1], hid, nxt)) == gphq.ERR_TOKEN_RANGE
+    other = gphq.lm_from_stored(geom_kwargs(g), lo.FMT_Q8B, model["layers"], model["embed"], model["final_norm"],
+                                model["head"])
+    assert status(lambda: ws.greedy_into([gphq.Prefix(other, 4)], [0], [1], hid, nxt)) == gphq.ERR_FOREIGN_PREFIX
+    assert status(lambda: ws.greedy_run([a], [2], [1], 3, torch.empty(3, dtype=torch.int32, device="cuda"))) == \
+        gphq.ERR_PREFIX_FULL
+    # Nothing was enqueued by the rejected calls: the prefixes are untouched.
+    kc, vc, cap = a.kv()
+    assert not _read_dev_floats(kc, g.kvd * cap).any()
+    # A model without a head cannot make a workspace.
+    bare = gphq.Lm(gphq.lm_config(fmt=lo.FMT_Q8B, **geom_kwargs(g)))
+    assert status(lambda: gphq.DecodeBatch(bare, 1)) == gphq.ERR_MODEL_INCOMPLETE

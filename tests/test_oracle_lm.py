@@ -1,0 +1,184 @@
+"""Pins the decode oracle (oracle/lm_oracle.py and the rotation functions of
+oracle/gphq_oracle.c) without retyping its formulas:
+
+* splitmix64 against the published first outputs of the generator;
+* the rotation against the dense matrix scale*H*diag(signs) built from
+  scipy's Sylvester Hadamard, orthogonality and dot-product preservation
+  (qwen3lm/kernels_test.go:73-111), and the block rule of that test;
+* the float64 decode step against Hugging Face transformers' Qwen3 (an
+  independent implementation of the same architecture) in float64, with the
+  unrotated weights that the stored, rotated ones imply;
+* the RoPE table against transformers' own rotary embedding.
+"""
+import numpy as np
+import pytest
+import scipy.linalg
+
+from oracle import lm_oracle as lo
+from oracle import oracle as orc
+from tests import lm_common as lc
+
+
+def test_splitmix64_published_outputs():
+    # The first outputs of splitmix64 from state 0 (Vigna's reference
+    # generator, also java.util.SplittableRandom's mixing function).
+    got = orc.splitmix64_outputs(0, 3)
+    assert got == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+
+
+@pytest.mark.parametrize("k", [8, 96, 136, 1024, 3072, 4096, 12288])
+def test_rotation_block_rule(k):
+    # kernels_test.go:75-78: block = min(4096, k & -k).
+    signs, block, scale = lo.rotation(k)
+    assert block == min(4096, k & -k)
+    assert scale == np.float32(1 / np.sqrt(block))
+    assert set(np.unique(signs)) <= {-1.0, 1.0}
+    # Signs are not degenerate: roughly half are negative.
+    assert 0.3 < np.mean(signs < 0) < 0.7 or k < 64
+
+
+@pytest.mark.parametrize("k", [96, 1024, 3072])
+def test_rotation_matches_dense_hadamard(k):
+    signs, block, scale = rot = lo.rotation(k)
+    H = scipy.linalg.hadamard(block).astype(np.float64)
+    R = np.zeros((k, k))
+    for b in range(0, k, block):
+        R[b:b + block, b:b + block] = scale * H @ np.diag(signs[b:b + block].astype(np.float64))
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal(k).astype(np.float32)
+    want = R @ x.astype(np.float64)
+    np.testing.assert_allclose(lo.rot_apply(x, rot), want, rtol=0, atol=1e-12 * np.abs(want).max())
+    got32 = orc.rotation_apply_f32(x, rot).astype(np.float64)
+    assert np.abs(got32 - want).max() <= 1e-6 * np.abs(want).max()
+    # The inverse is the transpose.
+    back = orc.rotation_unapply_f32(got32.astype(np.float32), rot).astype(np.float64)
+    assert np.abs(back - x).max() <= 1e-6 * np.abs(x).max()
+    np.testing.assert_allclose(lo.rot_unapply(want, rot), x, atol=1e-12 * np.abs(x).max())
+    np.testing.assert_allclose(lo.rot_matrix(rot), R, atol=1e-15)
+
+
+@pytest.mark.parametrize("k", [8, 96, 136, 4096, 12288])
+def test_rotation_orthogonal_as_reference(k):
+    # kernels_test.go:80-110, the same vectors and bounds.
+    rot = lo.rotation(k)
+    i = np.arange(k)
+    x = (np.sin(i * 1.7).astype(np.float32) * (1 + i % 9).astype(np.float32)).astype(np.float32)
+    norm = float(np.dot(x.astype(np.float64), x))
+    y = orc.rotation_apply_f32(x, rot)
+    rotated = float(np.dot(y.astype(np.float64), y))
+    assert abs(rotated - norm) <= 1e-5 * norm
+    w = np.cos(i).astype(np.float32)
+    dot = float(np.dot(w.astype(np.float64), x))
+    rw = orc.rotation_apply_f32(w, rot)
+    got = float(np.dot(rw.astype(np.float64), y))
+    assert abs(got - dot) <= 1e-4 * np.sqrt(norm) * np.sqrt(k)
+
+
+def test_fwht_float32_network_matches_float64():
+    # The float32 network agrees with the float64 transform to rounding.
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(4096).astype(np.float32)
+    a = v.copy()
+    orc.lib().orc_fwht(orc._p(a, orc._f32p), len(a))
+    want = lo.hadamard_f64(v, 4096)
+    assert np.abs(a - want).max() <= 64 * 2 ** -24 * np.abs(want).max() * 12
+
+
+def _hf_model(model):
+    """transformers Qwen3ForCausalLM in float64 holding the unrotated weights
+    that the stored ones imply (stored = W.R^T for q/k/v/gate/up and the head;
+    R.W (Q8B down) or R.W.Ri^T (Q8/Q4 down) and R.W for o)."""
+    torch = pytest.importorskip("torch")
+    tr = pytest.importorskip("transformers")
+    g, fmt = model["geom"], model["fmt"]
+    cfg = tr.Qwen3Config(
+        vocab_size=g.vocab, hidden_size=g.hidden, intermediate_size=g.inter, num_hidden_layers=g.layers,
+        num_attention_heads=g.heads, num_key_value_heads=g.kv_heads, head_dim=g.head_dim,
+        max_position_embeddings=g.max_pos, rms_norm_eps=g.eps,
+        rope_parameters={"rope_type": "default", "rope_theta": g.theta},
+        tie_word_embeddings=False, attention_bias=False)
+    cfg._attn_implementation = "eager"
+    m = tr.Qwen3ForCausalLM(cfg).double().eval()
+    R = lo.rot_matrix(lo.rotation(g.hidden))
+    Ri = lo.rot_matrix(lo.rotation(g.inter))
+    sd = {"model.embed_tokens.weight": lo.bf16_to_f64(model["embed"]).reshape(g.vocab, g.hidden),
+          "model.norm.weight": model["final_norm"].astype(np.float64),
+          "lm_head.weight": lo.dequant(lo.FMT_Q8B, *model["head"], g.head_rows, g.hidden)[: g.vocab] @ R}
+    for li, L in enumerate(model["layers"]):
+        p = f"model.layers.{li}."
+        qkv = lo.dequant(fmt, *L.qkv, g.qd + 2 * g.kvd, g.hidden) @ R
+        gu = lo.dequant(fmt, *L.gu, 2 * g.inter, g.hidden) @ R
+        down = R.T @ lo.dequant(fmt, *L.down, g.hidden, g.inter)
+        if fmt != lo.FMT_Q8B:
+            down = down @ Ri
+        sd.update({
+            p + "self_attn.q_proj.weight": qkv[: g.qd],
+            p + "self_attn.k_proj.weight": qkv[g.qd: g.qd + g.kvd],
+            p + "self_attn.v_proj.weight": qkv[g.qd + g.kvd:],
+            p + "self_attn.o_proj.weight": R.T @ lo.dequant(fmt, *L.o, g.hidden, g.qd),
+            p + "self_attn.q_norm.weight": L.q_norm.astype(np.float64),
+            p + "self_attn.k_norm.weight": L.k_norm.astype(np.float64),
+            p + "input_layernorm.weight": np.ones(g.hidden),
+            p + "post_attention_layernorm.weight": np.ones(g.hidden),
+            p + "mlp.gate_proj.weight": gu[0::2],
+            p + "mlp.up_proj.weight": gu[1::2],
+            p + "mlp.down_proj.weight": down,
+        })
+    state = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in sd.items()}
+    missing, unexpected = m.load_state_dict(state, strict=False)
+    assert not unexpected and not [k for k in missing if "rotary" not in k]
+    return m
+
+
+@pytest.mark.parametrize("fmt", [lo.FMT_Q8B, lo.FMT_Q8, lo.FMT_Q4])
+def test_decode_oracle_matches_transformers_qwen3(fmt):
+    torch = pytest.importorskip("torch")
+    model = lc.random_model(lc.GPU_SHAPE, fmt, seed=11 + fmt)
+    g = model["geom"]
+    orc_ = lc.oracle_for(model)
+    hf = _hf_model(model)
+    tokens = [5, 17, 3, 90, 44, 44, 0]
+    with torch.no_grad():
+        ids = torch.tensor([tokens])
+        hid = hf.model(ids).last_hidden_state[0].numpy()
+        logits = hf.lm_head(torch.from_numpy(hid)).numpy()
+    cache = orc_.new_cache(16)
+    for pos, t in enumerate(tokens):
+        hidden, lg, nxt = orc_.step(cache, pos, t)
+        # transformers computes RMSNorm, RoPE angles and softmax in float32,
+        # so agreement is to float32 rounding, far below any structural error.
+        rel_h = np.linalg.norm(hidden - hid[pos]) / np.linalg.norm(hid[pos])
+        rel_l = np.linalg.norm(lg - logits[pos]) / np.linalg.norm(logits[pos])
+        assert rel_h < 2e-5 and rel_l < 2e-5, (pos, rel_h, rel_l)
+        assert nxt == int(np.argmax(logits[pos])) or np.sort(logits[pos])[-1] - np.sort(logits[pos])[-2] < 1e-3
+
+
+def test_rope_table_matches_transformers():
+    torch = pytest.importorskip("torch")
+    tr = pytest.importorskip("transformers")
+    g = lc.GPU_SHAPE
+    cfg = tr.Qwen3Config(hidden_size=g.hidden, num_attention_heads=g.heads, num_key_value_heads=g.kv_heads,
+                         head_dim=g.head_dim, max_position_embeddings=g.max_pos,
+                         rope_parameters={"rope_type": "default", "rope_theta": g.theta})
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RotaryEmbedding
+
+    emb = Qwen3RotaryEmbedding(cfg)
+    pos = torch.arange(64)[None, :]
+    cos, sin = emb(torch.zeros(1, dtype=torch.float32), pos)
+    c, s = lo.rope_table(g, 64)
+    half = g.head_dim // 2
+    # transformers forms the angle in float32; positions < 64 keep it within 1e-5.
+    np.testing.assert_allclose(cos[0, :, :half].numpy(), c, atol=1e-5)
+    np.testing.assert_allclose(cos[0, :, half:].numpy(), c, atol=1e-5)
+    np.testing.assert_allclose(sin[0, :, :half].numpy(), s, atol=1e-5)
+
+
+def test_greedy_argmax_rules():
+    # decode_batch.go:182-191: first maximum, NaN never wins, NaN at 0 keeps 0.
+    nan = float("nan")
+    assert lo.greedy_argmax([1.0, 3.0, 3.0, 2.0]) == 1
+    assert lo.greedy_argmax([nan, 5.0, 6.0]) == 0
+    assert lo.greedy_argmax([1.0, nan, 0.5, 7.0]) == 3
+    assert lo.greedy_argmax([-0.0, 0.0]) == 0
+    for v in ([1.0, 3.0, 3.0, 2.0], [nan, 5.0, 6.0], [1.0, nan, 0.5, 7.0], [-np.inf, -np.inf]):
+        assert lo.greedy_argmax_np(v) == lo.greedy_argmax(v)
