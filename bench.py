@@ -34,6 +34,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true", help="skip the config-2 int8 GEMM lines")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-3/4b decode lines")
+    ap.add_argument("--decode-fmt", choices=["q8b", "q8b_f32", "q8", "q4"], default="q8b",
+                    help="layer weight format of the decode models (the reference's decode batch uses Q8B)")
+    ap.add_argument("--decode-eager", action="store_true", help="launch decode steps without the HIP graph")
     return ap.parse_args()
 
 
@@ -185,6 +189,128 @@ def gemm_config2(args, torch, gphq, ms=(1, 16, 128, 512), rotations=6, steps=20)
     return out
 
 
+QWEN3_06B = dict(hidden=1024, layers=28, heads=16, kv_heads=8, head_dim=128, intermediate=3072, vocab=151936,
+                 max_positions=40960)
+QWEN3_8B = dict(hidden=4096, layers=36, heads=32, kv_heads=8, head_dim=128, intermediate=12288, vocab=151936,
+                max_positions=40960)
+
+
+def decode_model(torch, gphq, geom, fmt, seed):
+    """A random-init Qwen3-shaped model in the qwen3lm GPU layout, generated on
+    the device: int8 codes U[-127,127] (Q4: bytes U[0,255]), scales |N(0,1)|*0.02,
+    norms 1 + N(0,0.02), BF16 embeddings N(0,1), a Q8B head padded to 16 rows.
+    Returns (lm, algorithmic weight bytes read per step)."""
+    cfg = gphq.lm_config(fmt=fmt, **geom)
+    desc, nbytes = gphq.lm_layer_layout(cfg)
+    lm = gphq.Lm(cfg)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    H, I = geom["hidden"], geom["intermediate"]
+    qd, kvd = geom["heads"] * 128, geom["kv_heads"] * 128
+    regions = [(desc.qkv, desc.qkv_scale, qd + 2 * kvd, H), (desc.o, desc.o_scale, H, qd),
+               (desc.gu, desc.gu_scale, 2 * I, H), (desc.d, desc.d_scale, H, I)]
+
+    def fill(buf, w, s, rows, k, f):
+        if f == gphq.FMT_Q4:
+            nc = rows * k // 2
+            buf[w:w + nc].copy_(torch.randint(0, 256, (nc,), dtype=torch.uint8, device="cuda", generator=gen))
+        else:
+            nc = rows * k
+            buf[w:w + nc].view(torch.int8).copy_(
+                torch.randint(-127, 128, (nc,), dtype=torch.int8, device="cuda", generator=gen))
+        ns = rows if f == gphq.FMT_Q8 else rows * k // 32
+        sc = torch.randn(ns, device="cuda", generator=gen).abs() * 0.02
+        if f in (gphq.FMT_Q8, gphq.FMT_Q8B_F32):
+            buf[s:s + 4 * ns].view(torch.float32).copy_(sc)
+            return nc + 4 * ns
+        buf[s:s + 2 * ns].view(torch.float16).copy_(sc.half())
+        return nc + 2 * ns
+
+    weight_bytes = 0
+    for layer in range(geom["layers"]):
+        buf = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+        for w, s_, rows, k in regions:
+            weight_bytes += fill(buf, w, s_, rows, k, fmt)
+        lm.bind_layer(layer, buf, desc, (1 + 0.02 * rng.standard_normal(128)).astype(np.float32),
+                      (1 + 0.02 * rng.standard_normal(128)).astype(np.float32))
+    emb = torch.randn((geom["vocab"], H), device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    lm.bind_embed(emb)
+    rows, so, hb = gphq.lm_head_layout(cfg)
+    head = torch.zeros(hb, dtype=torch.uint8, device="cuda")
+    weight_bytes += fill(head, 0, so, geom["vocab"], H, gphq.FMT_Q8B)  # rows past vocab stay zero
+    lm.bind_head(head, (1 + 0.02 * rng.standard_normal(H)).astype(np.float32))
+    torch.cuda.synchronize()
+    return lm, weight_bytes
+
+
+def decode_config(torch, gphq, lm, weight_bytes, geom, lanes, ctx, steps, warmup, graph, label):
+    """Greedy decode of `steps` tokens per lane at context `ctx` (the K/V
+    cache prefilled by teacher-forced steps over random ids, lane 0's prefix
+    copied to the others), timed with HIP events on the launch stream."""
+    stream = torch.cuda.current_stream()
+    ws = gphq.DecodeBatch(lm, lanes)
+    ws.set_graph(graph)
+    cap = ctx + max(steps, warmup) + 1
+    kvs = [gphq.Prefix(lm, cap) for _ in range(lanes)]
+    rng = np.random.default_rng(ctx + lanes)
+    t0 = time.perf_counter()
+    ws.extend(kvs[:1], [0], rng.integers(0, geom["vocab"], (ctx, 1)))
+    for kv in kvs[1:]:
+        kv.copy_from(kvs[0], ctx)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    first = rng.integers(0, geom["vocab"], lanes)
+    out = torch.empty((max(steps, warmup), lanes), dtype=torch.int32, device="cuda")
+    ws.greedy_run(kvs, [ctx] * lanes, first, warmup, out[:warmup])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    ws.greedy_run(kvs, [ctx] * lanes, first, steps, out[:steps])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ws.check()
+    ms = e0.elapsed_time(e1)
+    toks = out[:steps].cpu().numpy()
+    layers, kvd = geom["layers"], geom["kv_heads"] * 128
+    mean_ctx = ctx + (steps + 1) / 2.0  # keys read per layer, averaged over the timed steps
+    kv_bytes = lanes * layers * 2 * kvd * 4 * mean_ctx
+    step_bytes = weight_bytes + kv_bytes
+    ms_tok = ms / steps
+    return {
+        "workload": label,
+        "lanes": lanes,
+        "context": ctx,
+        "steps": steps,
+        "ms_per_step": round(ms_tok, 4),
+        "tokens_per_s": round(lanes * steps / (ms / 1e3), 1),
+        "bytes_per_step": int(step_bytes),
+        "achieved_gbs": round(step_bytes / (ms_tok / 1e3) / 1e9, 1),
+        "hbm_frac": round(step_bytes / (ms_tok / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+        "graph": bool(graph),
+        "prefill_s": round(prefill_s, 2),
+        "distinct_tokens": int(len(np.unique(toks))),
+    }
+
+
+def decode_benchmarks(args, torch, gphq):
+    fmt = {"q8b": gphq.FMT_Q8B, "q8b_f32": gphq.FMT_Q8B_F32, "q8": gphq.FMT_Q8, "q4": gphq.FMT_Q4}[args.decode_fmt]
+    graph = not args.decode_eager
+    res = {"fmt": args.decode_fmt}
+    lm, wb = decode_model(torch, gphq, QWEN3_06B, fmt, 3)
+    res["config3"] = decode_config(torch, gphq, lm, wb, QWEN3_06B, 1, 1024, 256, 16, graph,
+                                   "config 3: Qwen3-0.6B-shaped, batch 1, 1024-token K/V prefill, 256 greedy steps")
+    del lm
+    torch.cuda.empty_cache()
+    lm, wb = decode_model(torch, gphq, QWEN3_8B, fmt, 4)
+    res["config4b_1"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 1, 4096, 64, 8, graph,
+                                      "config 4b: Qwen3-8B-shaped decode at context 4096, 1 lane")
+    res["config4b_16"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 16, 4096, 32, 4, graph,
+                                       "config 4b: Qwen3-8B-shaped decode at context 4096, 16 lanes")
+    del lm
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(seconds):
     """The reference's amd64 q8gemv path (scalarMulInto, single thread),
     restated in C (oracle), on the config-1 shape with per-row scales."""
@@ -229,6 +355,7 @@ def main():
     single = gemv_config1(args, torch, gphq, "graph") if args.mode == "batch" else None
     value = r["value_gbs"]
     gemm = None if args.no_gemm else gemm_config2(args, torch, gphq)
+    decode = None if args.no_decode else decode_benchmarks(args, torch, gphq)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     kernel = "gemv8_kernel<Q8B_F32,4,2,8," + ("32>" if args.mode == "batch" else "1>")
     out = {
@@ -272,7 +399,8 @@ def main():
             "mode": "one gphq_gemv launch per 4096x4096 GEMV, HIP graph of 32 launches",
         },
         "gemm_config2": gemm,
-        "decode_ms_per_token": None,
+        "decode_ms_per_token": None if decode is None else decode["config4b_1"]["ms_per_step"],
+        "decode": decode,
         "check": {"rel_l2_vs_float64": r["rel_l2"]},
     }
     print(json.dumps(out), flush=True)

@@ -129,7 +129,9 @@ __device__ __forceinline__ void finish_rows(float (*part)[SK], const float *pss,
 
 // 8-bit codes (Q8, Q8B, Q8B_F32). Requires K % 16 == 0, 16-byte aligned codes
 // and x (every row then starts 16-byte aligned).
-template <int FMT, int RW, int SK, int WPB, int MAXB, int PRO = PRO_PLAIN, int EPI = EPI_STORE>
+// U > 1 issues the loads of U consecutive K steps before using any of them
+// (more bytes in flight per wavefront for short, latency-bound GEMVs).
+template <int FMT, int RW, int SK, int WPB, int MAXB, int PRO = PRO_PLAIN, int EPI = EPI_STORE, int U = 1>
 __global__ __launch_bounds__(64 * WPB) void gemv8_kernel(const GemvBatch<MAXB> b) {
     constexpr int RG = WPB / SK;
     __shared__ float part[RG * RW][SK];
@@ -152,32 +154,43 @@ __global__ __launch_bounds__(64 * WPB) void gemv8_kernel(const GemvBatch<MAXB> b
     for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
     float ss = 0.0f;
 
-    for (int st = 0; st < steps; ++st) {
-        const int k0 = (ks * steps + st) * 1024 + lane * 16;
-        const bool ok = k0 < K;
-        float4 xr[4];
+    for (int st0 = 0; st0 < steps; st0 += U) {
+        float4 xr[U][4];
+        float d[U][RW];
+        u32x4 w[U][RW];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xr[i] = ok ? *((const float4 *)(s.x + k0) + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-        if constexpr (PRO == PRO_NORM) {
+        for (int u = 0; u < U; ++u) {
+            const int k0 = (ks * steps + st0 + u) * 1024 + lane * 16;
+            const bool ok = st0 + u < steps && k0 < K;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ss += xr[i].x * xr[i].x + xr[i].y * xr[i].y + xr[i].z * xr[i].z + xr[i].w * xr[i].w;
+            for (int i = 0; i < 4; ++i)
+                xr[u][i] = ok ? *((const float4 *)(s.x + k0) + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (FMT != GPHQ_FMT_Q8) {
+#pragma unroll
+                for (int r = 0; r < RW; ++r)
+                    d[u][r] = ok ? block_scale<FMT>(s.scales, (size_t)rows[r] * kb + (k0 >> 5)) : 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                w[u][r] = ok ? __builtin_nontemporal_load((const u32x4 *)(W + (size_t)rows[r] * K + k0))
+                             : u32x4{0, 0, 0, 0};
         }
-        float d[RW];
-        if constexpr (FMT != GPHQ_FMT_Q8) {
 #pragma unroll
-            for (int r = 0; r < RW; ++r) d[r] = ok ? block_scale<FMT>(s.scales, (size_t)rows[r] * kb + (k0 >> 5)) : 0.0f;
-        }
-        u32x4 w[RW];
+        for (int u = 0; u < U; ++u) {
+            if constexpr (PRO == PRO_NORM) {
 #pragma unroll
-        for (int r = 0; r < RW; ++r)
-            w[r] = ok ? __builtin_nontemporal_load((const u32x4 *)(W + (size_t)rows[r] * K + k0)) : u32x4{0, 0, 0, 0};
+                for (int i = 0; i < 4; ++i)
+                    ss += xr[u][i].x * xr[u][i].x + xr[u][i].y * xr[u][i].y + xr[u][i].z * xr[u][i].z +
+                          xr[u][i].w * xr[u][i].w;
+            }
 #pragma unroll
-        for (int r = 0; r < RW; ++r) {
-            const float t = dot16(w[r], xr[0], xr[1], xr[2], xr[3]);
-            if constexpr (FMT == GPHQ_FMT_Q8)
-                acc[r] += t;
-            else
-                acc[r] = fmaf(d[r], t, acc[r]);
+            for (int r = 0; r < RW; ++r) {
+                const float t = dot16(w[u][r], xr[u][0], xr[u][1], xr[u][2], xr[u][3]);
+                if constexpr (FMT == GPHQ_FMT_Q8)
+                    acc[r] += t;
+                else
+                    acc[r] = fmaf(d[u][r], t, acc[r]);
+            }
         }
     }
 #pragma unroll
@@ -344,26 +357,41 @@ int gemv_batch_launch(int fmt, const void *const *codes, const void *const *scal
     return launch_batch<kMaxBatch>(fmt, b, count, stream);
 }
 
+// Tile shape of a decode-step GEMV, chosen from the matrix shape (measured
+// on MI355X with rotated weights over 256 MB, one launch per GEMV):
+// very tall matrices (the head) take 16-row blocks of four unsplit
+// wavefronts; tall ones (gate/up) 16-row blocks with K in two slices; long
+// rows (down) 16-row blocks with K in four slices and two steps in flight;
+// short, wide-K matrices (o, 0.6B down) 8-row blocks with K in four slices;
+// the rest (qkv) 8-row blocks with K in two slices.
+template <int FMT, int PRO, int EPI>
+static void launch_fused8(const GemvBatch<1> &b, hipStream_t stream) {
+    auto go = [&](auto kern, int rows, int threads) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)((b.N + rows - 1) / rows)), dim3(threads), 0, stream, b);
+    };
+    if (b.N >= 65536)
+        go(gemv8_kernel<FMT, 4, 1, 4, 1, PRO, EPI, 1>, 16, 256);
+    else if (b.N >= 16384)
+        go(gemv8_kernel<FMT, 4, 2, 8, 1, PRO, EPI, 1>, 16, 512);
+    else if (b.K >= 8192)
+        go(gemv8_kernel<FMT, 4, 4, 8, 1, PRO, EPI, 2>, 8, 512);
+    else if (b.N <= 4096 && b.K >= 2048)
+        go(gemv8_kernel<FMT, 2, 4, 8, 1, PRO, EPI, 1>, 4, 512);
+    else
+        go(gemv8_kernel<FMT, 2, 2, 8, 1, PRO, EPI, 1>, 8, 512);
+}
+
 template <int PRO, int EPI>
 static int launch_fused(int fmt, const GemvBatch<1> &b, hipStream_t stream) {
-    const unsigned rowsPerBlock = fmt == GPHQ_FMT_Q4 ? kRowsPerBlock4 : kRowsPerBlock;
-    const dim3 grid((unsigned)((b.N + rowsPerBlock - 1) / rowsPerBlock));
     switch (fmt) {
-    case GPHQ_FMT_Q8:
-        hipLaunchKernelGGL((gemv8_kernel<GPHQ_FMT_Q8, kRW, kSK, kWPB, 1, PRO, EPI>), grid, dim3(64 * kWPB), 0, stream,
-                           b);
-        break;
-    case GPHQ_FMT_Q8B:
-        hipLaunchKernelGGL((gemv8_kernel<GPHQ_FMT_Q8B, kRW, kSK, kWPB, 1, PRO, EPI>), grid, dim3(64 * kWPB), 0, stream,
-                           b);
-        break;
-    case GPHQ_FMT_Q8B_F32:
-        hipLaunchKernelGGL((gemv8_kernel<GPHQ_FMT_Q8B_F32, kRW, kSK, kWPB, 1, PRO, EPI>), grid, dim3(64 * kWPB), 0,
-                           stream, b);
-        break;
-    case GPHQ_FMT_Q4:
+    case GPHQ_FMT_Q8: launch_fused8<GPHQ_FMT_Q8, PRO, EPI>(b, stream); break;
+    case GPHQ_FMT_Q8B: launch_fused8<GPHQ_FMT_Q8B, PRO, EPI>(b, stream); break;
+    case GPHQ_FMT_Q8B_F32: launch_fused8<GPHQ_FMT_Q8B_F32, PRO, EPI>(b, stream); break;
+    case GPHQ_FMT_Q4: {
+        const dim3 grid((unsigned)((b.N + kRowsPerBlock4 - 1) / kRowsPerBlock4));
         hipLaunchKernelGGL((gemv4_kernel<kRW4, kSK4, kWPB4, 1, PRO, EPI>), grid, dim3(64 * kWPB4), 0, stream, b);
         break;
+    }
     default:
         return GPHQ_ERR_UNSUPPORTED;
     }

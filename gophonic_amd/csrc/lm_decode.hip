@@ -18,17 +18,19 @@
 //     SwiGLU, the down input's Hadamard for Q8/Q4 weights, and the down GEMV
 //     added into the residual (gpu.metal:1-14 describes the same six
 //     dispatches);
-//   * attention splits each lane's context 0..pos over `splits` blocks per KV
-//     head (one launch fills the chip even at one lane). Each block runs a
-//     streaming softmax over its keys for all query heads of the KV head and
-//     writes a partial (max, sum, weighted V). The last block to finish,
-//     found with a device-scope counter, merges the partials in split order,
-//     so the result does not depend on which block finishes last.
+//   * attention splits each lane's context 0..pos over up to `splits` blocks
+//     per KV head (one launch fills the chip even at one lane). Each block
+//     runs a streaming softmax over its keys for all query heads of the KV
+//     head and writes a partial (max, sum, weighted V); a second small kernel
+//     merges the partials of each query head in split order. (Merging in the
+//     last block to finish needs device-scope fences and atomics, which cost
+//     more on MI355X's per-XCD L2 caches than the extra launch.)
 // Single-lane steps use the fp32 register GEMV (gemv.hip); steps with two or
 // more lanes use the multi-vector MFMA GEMV (gemv_vec.hip), which reads each
 // weight once for all lanes.
 #include <math.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "common.h"
@@ -50,7 +52,7 @@ constexpr int kMaxLanes = GPHQ_DECODE_MAX_LANES;
 constexpr int kHeadDim = 128;
 constexpr int kPart = 2 + kHeadDim;  // one attention partial: max, sum, weighted V
 constexpr int kMaxSplits = 64;
-constexpr int kArgmaxBlocks = 64;
+constexpr int kMinChunk = 64;  // keys per attention block, at least
 constexpr int kMaxRotation = 4096;  // qwen3lm/hadamard.go:11
 constexpr int kMaxWidth = 16384;    // hidden and intermediate widths (LDS)
 
@@ -118,13 +120,20 @@ struct gphq_decode_batch {
     const gphq_lm *lm;
     int capacity;
     float *h, *qkv, *ctx, *act, *hn, *hidden, *logits, *part;
-    unsigned *attn_cnt, *argmax_cnt;
-    uint32_t *akey, *aidx;
     int32_t *tok, *pos, *start, *nonfinite;
     void *vec_work;
     size_t vec_bytes;
     int vec_min_lanes = 2;  // lane count from which GEMVs use the MFMA multi-vector kernel
     std::vector<void *> allocs;
+    // One captured greedy step (gphq_decode_greedy_run), valid for the lane
+    // prefixes and output pointers it was captured with.
+    bool use_graph = true;
+    hipStream_t capture = nullptr;
+    hipGraphExec_t step_exec = nullptr;
+    std::vector<gphq_prefix *> graph_kvs;
+    float *graph_hidden = nullptr;
+    int32_t *graph_out = nullptr;
+    int graph_vec_min = 0;
 };
 
 namespace {
@@ -245,6 +254,18 @@ __global__ __launch_bounds__(1024) void lm_final_kernel(const float *__restrict_
     if (threadIdx.x == 0 && bad) nonfinite[lane] = 1;
 }
 
+// Keys per attention block for a context of n keys: n spread over at most
+// `splits` blocks, at least kMinChunk each, a multiple of 16. The blocks in
+// use, ceil(n / chunk), are never empty.
+__device__ __forceinline__ int attn_chunk(int n, int splits) {
+    const int chunk = (n + splits - 1) / splits;
+    return max(kMinChunk, (chunk + 15) & ~15);
+}
+__device__ __forceinline__ int attn_used_splits(int n, int splits) {
+    const int chunk = attn_chunk(n, splits);
+    return (n + chunk - 1) / chunk;
+}
+
 struct AttnArgs {
     const float *qkv;  // [lanes][qkvw]
     float *kc[kMaxLanes];
@@ -254,17 +275,9 @@ struct AttnArgs {
     const int32_t *pos;    // [lanes]
     float *ctx;            // [lanes][qd]
     float *part;           // [lanes][kvh][splits][GROUP][kPart]
-    unsigned *cnt;         // [lanes][kvh], zero between launches
     float eps, scale;
     int qkvw, qd, kvd, kvh, splits, sin_off;
 };
-
-__device__ __forceinline__ float ld_agent(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Merge factor of a softmax state with max m into one with max mn.
 __device__ __forceinline__ float rescale(float m, float mn) { return m == -INFINITY ? 0.0f : expf(m - mn); }
@@ -273,24 +286,49 @@ __device__ __forceinline__ float rescale(float m, float mn) { return m == -INFIN
 // lanes), 4 wavefronts. Each of the block's 16 row groups of 16 lanes takes
 // one key at a time; lane li of a group holds dims 4li..4li+3 and
 // 64+4li..64+4li+3 of the key and value rows (two 16-byte loads, a group
-// reads one 512-byte row).
+// reads one 512-byte row). The first keys' loads are issued before the
+// query/key norms are computed, so the two overlap.
 template <int GROUP, int KPI>
 __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     __shared__ float qs[GROUP][kHeadDim];
     __shared__ float knew[kHeadDim], vnew[kHeadDim];
     __shared__ float wm[4][GROUP], wl[4][GROUP];
     __shared__ float wacc[4][GROUP][kHeadDim];
-    __shared__ int amLast;
     const int lid = blockIdx.z, g = blockIdx.y, sp = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int pos = a.pos[lid];
     const int n = pos + 1;
-    int chunk = (n + a.splits - 1) / a.splits;
-    chunk = (chunk + 15) & ~15;
-    const int j0 = min(sp * chunk, n), j1 = min(n, j0 + chunk);
+    const int chunk = attn_chunk(n, a.splits);
+    const int used = (n + chunk - 1) / chunk;
+    if (sp >= used) return;
+    const int j0 = sp * chunk, j1 = min(n, j0 + chunk);
     const float *qkv = a.qkv + (size_t)lid * a.qkvw;
     float *kc = a.kc[lid] + g * kHeadDim;
     float *vc = a.vc[lid] + g * kHeadDim;
+    const int sub = lane >> 4, li = lane & 15;
+    const int rowgroup = wave * 4 + sub;  // 0..15
+    const int d0 = li * 4, d1 = 64 + li * 4;
+    const int iters = (j1 - j0 + 16 * KPI - 1) / (16 * KPI);
+
+    float kr[KPI][8], vr[KPI][8];
+    bool valid[KPI];
+    auto load_keys = [&](int it) {
+#pragma unroll
+        for (int u = 0; u < KPI; ++u) {
+            const int j = j0 + (it * KPI + u) * 16 + rowgroup;
+            valid[u] = j < j1;
+            const int jj = valid[u] ? j : j0;
+            const float4 k0 = *(const float4 *)(kc + (size_t)jj * a.kvd + d0);
+            const float4 k1 = *(const float4 *)(kc + (size_t)jj * a.kvd + d1);
+            const float4 v0 = *(const float4 *)(vc + (size_t)jj * a.kvd + d0);
+            const float4 v1 = *(const float4 *)(vc + (size_t)jj * a.kvd + d1);
+            kr[u][0] = k0.x, kr[u][1] = k0.y, kr[u][2] = k0.z, kr[u][3] = k0.w;
+            kr[u][4] = k1.x, kr[u][5] = k1.y, kr[u][6] = k1.z, kr[u][7] = k1.w;
+            vr[u][0] = v0.x, vr[u][1] = v0.y, vr[u][2] = v0.z, vr[u][3] = v0.w;
+            vr[u][4] = v1.x, vr[u][5] = v1.y, vr[u][6] = v1.z, vr[u][7] = v1.w;
+        }
+    };
+    if (iters > 0) load_keys(0);
 
     // Head RMSNorm and RoPE of the new key and of the GROUP query heads
     // (gpu.metal:380-388 normRopeAt). Lane l holds the rotary pair (l, l+64).
@@ -328,9 +366,6 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     }
     __syncthreads();
 
-    const int sub = lane >> 4, li = lane & 15;
-    const int rowgroup = wave * 4 + sub;  // 0..15
-    const int d0 = li * 4, d1 = 64 + li * 4;
     float q[GROUP][8];
 #pragma unroll
     for (int hh = 0; hh < GROUP; ++hh) {
@@ -348,24 +383,11 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[hh][i] = 0.0f;
     }
-    const int iters = (j1 - j0 + 16 * KPI - 1) / (16 * KPI);
     for (int it = 0; it < iters; ++it) {
-        float kr[KPI][8], vr[KPI][8];
-        bool valid[KPI];
+        if (it > 0) load_keys(it);
 #pragma unroll
         for (int u = 0; u < KPI; ++u) {
-            const int j = j0 + (it * KPI + u) * 16 + rowgroup;
-            valid[u] = j < j1;
-            const int jj = valid[u] ? j : j0;
-            const float4 k0 = *(const float4 *)(kc + (size_t)jj * a.kvd + d0);
-            const float4 k1 = *(const float4 *)(kc + (size_t)jj * a.kvd + d1);
-            const float4 v0 = *(const float4 *)(vc + (size_t)jj * a.kvd + d0);
-            const float4 v1 = *(const float4 *)(vc + (size_t)jj * a.kvd + d1);
-            kr[u][0] = k0.x, kr[u][1] = k0.y, kr[u][2] = k0.z, kr[u][3] = k0.w;
-            kr[u][4] = k1.x, kr[u][5] = k1.y, kr[u][6] = k1.z, kr[u][7] = k1.w;
-            vr[u][0] = v0.x, vr[u][1] = v0.y, vr[u][2] = v0.z, vr[u][3] = v0.w;
-            vr[u][4] = v1.x, vr[u][5] = v1.y, vr[u][6] = v1.z, vr[u][7] = v1.w;
-            if (jj == pos) {  // the new row: from registers of this block, not the cache
+            if (j0 + (it * KPI + u) * 16 + rowgroup == pos) {  // the new row, from this block's LDS
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     kr[u][i] = knew[d0 + i], kr[u][4 + i] = knew[d1 + i];
@@ -446,45 +468,54 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
             L += wl[w][hh] * c;
             A += wacc[w][hh][d] * c;
         }
-        st_agent(bp + hh * kPart + 2 + d, A);
+        bp[hh * kPart + 2 + d] = A;
         if (d == 0) {
-            st_agent(bp + hh * kPart, M);
-            st_agent(bp + hh * kPart + 1, L);
+            bp[hh * kPart] = M;
+            bp[hh * kPart + 1] = L;
         }
     }
-    __threadfence();
-    __syncthreads();
-    unsigned *cnt = a.cnt + (size_t)lid * a.kvh + g;
-    if (threadIdx.x == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        amLast = prev == (unsigned)(a.splits - 1);
+}
+
+// The merge of attention's split partials (grid: q_heads, lanes; 128
+// threads, thread d owns dim d): weights exp(m_s - max) per split, then
+// ctx = sum_s w_s A_s / sum_s w_s l_s, splits in order.
+__global__ __launch_bounds__(128) void lm_attn_merge_kernel(const AttnArgs a, int group) {
+    __shared__ float cw[kMaxSplits];
+    __shared__ float linv;
+    const int h = blockIdx.x, lid = blockIdx.y;
+    const int g = h / group, hh = h - g * group;
+    const int used = attn_used_splits(a.pos[lid] + 1, a.splits);
+    const float *lp = a.part + (((size_t)lid * a.kvh + g) * a.splits * group + hh) * kPart;
+    const size_t stride = (size_t)group * kPart;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const bool has = lane < used;
+        const float ms = has ? lp[lane * stride] : -INFINITY;
+        const float ls = has ? lp[lane * stride + 1] : 0.0f;
+        float M = ms;
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        const float c = has ? rescale(ms, M) : 0.0f;
+        const float L = wave_sum(ls * c);
+        cw[lane] = c;
+        if (lane == 0) linv = 1.0f / L;
     }
     __syncthreads();
-    if (!amLast) return;
-    __threadfence();
-    // Last block of this (lane, KV head): merge all splits in split order.
-    const float *lp = a.part + (((size_t)lid * a.kvh + g) * a.splits) * GROUP * kPart;
-    for (int t = threadIdx.x; t < GROUP * kHeadDim; t += blockDim.x) {
-        const int hh = t / kHeadDim, d = t % kHeadDim;
-        float M = -INFINITY;
-        for (int s2 = 0; s2 < a.splits; ++s2) M = fmaxf(M, ld_agent(lp + ((size_t)s2 * GROUP + hh) * kPart));
-        float L = 0.0f, A = 0.0f;
-        for (int s2 = 0; s2 < a.splits; ++s2) {
-            const float *p = lp + ((size_t)s2 * GROUP + hh) * kPart;
-            const float c = rescale(ld_agent(p), M);
-            L += ld_agent(p + 1) * c;
-            A += ld_agent(p + 2 + d) * c;
-        }
-        a.ctx[(size_t)lid * a.qd + (size_t)(g * GROUP + hh) * kHeadDim + d] = A / L;
+    const int d = threadIdx.x;
+    const float *p = lp + 2 + d;
+    float A = 0.0f;
+    for (int s0 = 0; s0 < used; s0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = s0 + i < used ? p[(size_t)(s0 + i) * stride] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) A = fmaf(cw[min(s0 + i, kMaxSplits - 1)], v[i], A);
     }
-    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    a.ctx[(size_t)lid * a.qd + (size_t)h * kHeadDim + d] = A * linv;
 }
 
 struct ArgmaxArgs {
-    const float *logits;  // [lanes][stride]
+    const float *logits;  // [lanes][stride], stride a multiple of 4
     int stride, vocab, lanes;
-    uint32_t *key, *idx;  // [lanes][kArgmaxBlocks]
-    unsigned *cnt;        // [lanes], zero between launches
     int32_t *tok, *pos;
     const int32_t *start;
     int32_t *next;  // optional [lanes]
@@ -499,63 +530,63 @@ __device__ __forceinline__ bool better(uint32_t k, uint32_t i, uint32_t bk, uint
     return i != kNone && (bi == kNone || k > bk || (k == bk && i < bi));
 }
 
+__device__ __forceinline__ void consider(float v, int i, uint32_t &bk, uint32_t &bi) {
+    const uint32_t bits = __builtin_bit_cast(uint32_t, v);
+    const uint32_t mag = bits & 0x7FFFFFFFu;
+    if (mag <= 0x7F800000u) {  // NaNs never win; signed zeros tie
+        const uint32_t key = mag == 0 ? 0x80000000u : ((bits & 0x80000000u) ? ~bits : bits ^ 0x80000000u);
+        if (better(key, (uint32_t)i, bk, bi)) bk = key, bi = (uint32_t)i;
+    }
+}
+
 // First-maximum argmax of each lane's logits (decode_batch.go:182-191
-// greedyArgmax; NaNs never win, a NaN at index 0 keeps index 0): grid
-// (kArgmaxBlocks, lanes). The last block of a lane writes the next token,
-// feeds it back as the lane's current token and advances the lane's
-// position.
-__global__ __launch_bounds__(256) void lm_argmax_kernel(const ArgmaxArgs a) {
-    __shared__ uint32_t sk[256], si[256];
-    __shared__ int amLast;
-    const int lane = blockIdx.y;
+// greedyArgmax; a NaN at index 0 keeps index 0): one block per lane. Writes
+// the next token, feeds it back as the lane's current token and advances the
+// lane's position.
+__global__ __launch_bounds__(1024) void lm_argmax_kernel(const ArgmaxArgs a) {
+    __shared__ uint32_t sk[16], si[16];
+    const int lane = blockIdx.x;
     const float *x = a.logits + (size_t)lane * a.stride;
-    const int per = (a.vocab + kArgmaxBlocks - 1) / kArgmaxBlocks;
-    const int c0 = blockIdx.x * per, c1 = min(a.vocab, c0 + per);
     uint32_t bk = 0, bi = kNone;
-    for (int i = c0 + threadIdx.x; i < c1; i += blockDim.x) {
-        const uint32_t bits = __builtin_bit_cast(uint32_t, x[i]);
-        const uint32_t mag = bits & 0x7FFFFFFFu;
-        if (mag <= 0x7F800000u) {
-            const uint32_t key = mag == 0 ? 0x80000000u : ((bits & 0x80000000u) ? ~bits : bits ^ 0x80000000u);
-            if (better(key, (uint32_t)i, bk, bi)) bk = key, bi = (uint32_t)i;
+    const int n4 = a.vocab >> 2;
+    for (int c0 = threadIdx.x; c0 < n4; c0 += 4 * blockDim.x) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = c0 + u * blockDim.x;
+            v[u] = c < n4 ? *((const float4 *)x + c) : make_float4(NAN, NAN, NAN, NAN);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = 4 * (c0 + u * blockDim.x);
+            consider(v[u].x, i, bk, bi);
+            consider(v[u].y, i + 1, bk, bi);
+            consider(v[u].z, i + 2, bk, bi);
+            consider(v[u].w, i + 3, bk, bi);
         }
     }
-    sk[threadIdx.x] = bk;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int step = 128; step > 0; step >>= 1) {
-        if ((int)threadIdx.x < step && better(sk[threadIdx.x + step], si[threadIdx.x + step], sk[threadIdx.x], si[threadIdx.x])) {
-            sk[threadIdx.x] = sk[threadIdx.x + step];
-            si[threadIdx.x] = si[threadIdx.x + step];
-        }
-        __syncthreads();
+    for (int i = 4 * n4 + threadIdx.x; i < a.vocab; i += blockDim.x) consider(x[i], i, bk, bi);
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t ko = __shfl_xor(bk, off), io = __shfl_xor(bi, off);
+        if (better(ko, io, bk, bi)) bk = ko, bi = io;
     }
-    if (threadIdx.x == 0) {
-        const size_t o = (size_t)lane * kArgmaxBlocks + blockIdx.x;
-        __hip_atomic_store(a.key + o, sk[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.idx + o, si[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __threadfence();
-        const unsigned prev = __hip_atomic_fetch_add(a.cnt + lane, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        amLast = prev == (unsigned)(kArgmaxBlocks - 1);
+    if ((threadIdx.x & 63) == 0) {
+        sk[threadIdx.x >> 6] = bk;
+        si[threadIdx.x >> 6] = bi;
     }
     __syncthreads();
-    if (!amLast || threadIdx.x != 0) return;
-    __threadfence();
-    uint32_t k = 0, best = kNone;
-    for (int b = 0; b < kArgmaxBlocks; ++b) {
-        const size_t o = (size_t)lane * kArgmaxBlocks + b;
-        const uint32_t kb = __hip_atomic_load(a.key + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t ib = __hip_atomic_load(a.idx + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (better(kb, ib, k, best)) k = kb, best = ib;
-    }
+    if (threadIdx.x != 0) return;
+    bk = sk[0];
+    bi = si[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+        if (better(sk[w], si[w], bk, bi)) bk = sk[w], bi = si[w];
     const uint32_t first = __builtin_bit_cast(uint32_t, x[0]) & 0x7FFFFFFFu;
-    const int32_t token = (first > 0x7F800000u || best == kNone) ? 0 : (int32_t)best;
+    const int32_t token = (first > 0x7F800000u || bi == kNone) ? 0 : (int32_t)bi;
     const int32_t p = a.pos[lane];
     if (a.run) a.run[(size_t)(p - a.start[lane]) * a.lanes + lane] = token;
     if (a.next) a.next[lane] = token;
     a.tok[lane] = token;
     a.pos[lane] = p + 1;
-    __hip_atomic_store(a.cnt + lane, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host orchestration ----------------------------------------------------
@@ -618,7 +649,6 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool 
     aa.pos = ws->pos;
     aa.ctx = ws->ctx;
     aa.part = ws->part;
-    aa.cnt = ws->attn_cnt;
     aa.eps = (float)c.eps;
     aa.scale = (float)(1.0 / sqrt((double)c.head_dim));
     aa.qkvw = (int)qkvw;
@@ -640,6 +670,9 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool 
         aa.qn = lm->norms + (size_t)layer * 2 * kHeadDim;
         aa.kn = aa.qn + kHeadDim;
         GPHQ_TRY(launch_attend((int)lm->group, aa, lanes, st));
+        hipLaunchKernelGGL(lm_attn_merge_kernel, dim3((unsigned)c.heads, lanes), dim3(kHeadDim), 0, st, aa,
+                           (int)lm->group);
+        GPHQ_TRY(launch_status());
         GPHQ_TRY(gemv(ws, lanes, fmt, PRO_PLAIN, EPI_ADD, buf, L.o, L.o_scale, ws->ctx, lm->qd, ws->h, H, lm->qd, H,
                       st));
         GPHQ_TRY(gemv(ws, lanes, fmt, PRO_NORM, EPI_SWIGLU, buf, L.gu, L.gu_scale, ws->h, H, ws->act, I, H, 2 * I,
@@ -657,9 +690,8 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool 
     GPHQ_TRY(launch_status());
     GPHQ_TRY(gemv(ws, lanes, GPHQ_FMT_Q8B, PRO_PLAIN, EPI_STORE, lm->head, 0, lm->head_scale, ws->hn, H, ws->logits,
                   lm->head_rows, H, lm->head_rows, st));
-    ArgmaxArgs ga{ws->logits, (int)lm->head_rows, (int)c.vocab, lanes, ws->akey, ws->aidx, ws->argmax_cnt,
-                  ws->tok, ws->pos, ws->start, next_out, run_out};
-    hipLaunchKernelGGL(lm_argmax_kernel, dim3(kArgmaxBlocks, lanes), dim3(256), 0, st, ga);
+    ArgmaxArgs ga{ws->logits, (int)lm->head_rows, (int)c.vocab, lanes, ws->tok, ws->pos, ws->start, next_out, run_out};
+    hipLaunchKernelGGL(lm_argmax_kernel, dim3(lanes), dim3(1024), 0, st, ga);
     return launch_status();
 }
 
@@ -718,9 +750,47 @@ bool model_ready(const gphq_lm *lm) {
     return true;
 }
 
+void drop_graph(gphq_decode_batch *ws) {
+    if (ws->step_exec) (void)hipGraphExecDestroy(ws->step_exec);
+    ws->step_exec = nullptr;
+    ws->graph_kvs.clear();
+}
+
 void free_batch(gphq_decode_batch *ws) {
+    drop_graph(ws);
+    if (ws->capture) (void)hipStreamDestroy(ws->capture);
     for (void *p : ws->allocs) (void)hipFree(p);
     delete ws;
+}
+
+// Captures one chained greedy step (embed .. argmax) on the workspace's own
+// stream into an executable graph, unless the cached one matches. Capture
+// records the launches without running them.
+int step_graph(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, float *hidden, int32_t *out) {
+    if (ws->step_exec && (int)ws->graph_kvs.size() == lanes && ws->graph_hidden == hidden && ws->graph_out == out &&
+        ws->graph_vec_min == ws->vec_min_lanes && std::equal(kvs, kvs + lanes, ws->graph_kvs.begin()))
+        return GPHQ_OK;
+    drop_graph(ws);
+    if (!ws->capture) GPHQ_TRY(hip_status(hipStreamCreateWithFlags(&ws->capture, hipStreamNonBlocking)));
+    GPHQ_TRY(hip_status(hipStreamBeginCapture(ws->capture, hipStreamCaptureModeRelaxed)));
+    const int st = encode_step(ws, kvs, lanes, true, hidden, nullptr, out, ws->capture);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(ws->capture, &graph);
+    if (st != GPHQ_OK || e != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return st != GPHQ_OK ? st : hip_status(e);
+    }
+    const hipError_t ie = hipGraphInstantiate(&ws->step_exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ie != hipSuccess) {
+        ws->step_exec = nullptr;
+        return hip_status(ie);
+    }
+    ws->graph_kvs.assign(kvs, kvs + lanes);
+    ws->graph_hidden = hidden;
+    ws->graph_out = out;
+    ws->graph_vec_min = ws->vec_min_lanes;
+    return GPHQ_OK;
 }
 
 }  // namespace
@@ -964,10 +1034,6 @@ int gphq_decode_batch_new(const gphq_lm *lm, int64_t capacity, gphq_decode_batch
         {(void **)&ws->hidden, (size_t)capacity * H * 4},
         {(void **)&ws->logits, (size_t)capacity * lm->head_rows * 4},
         {(void **)&ws->part, partFloats * 4},
-        {(void **)&ws->attn_cnt, (size_t)capacity * c.kv_heads * 4},
-        {(void **)&ws->argmax_cnt, (size_t)capacity * 4},
-        {(void **)&ws->akey, (size_t)capacity * kArgmaxBlocks * 4},
-        {(void **)&ws->aidx, (size_t)capacity * kArgmaxBlocks * 4},
         {(void **)&ws->tok, (size_t)capacity * 4},
         {(void **)&ws->pos, (size_t)capacity * 4},
         {(void **)&ws->start, (size_t)capacity * 4},
@@ -1035,8 +1101,21 @@ int gphq_decode_greedy_run(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64
         return GPHQ_ERR_OVERLAP;
     hipStream_t st = (hipStream_t)stream;
     float *hid = hidden_dev ? hidden_dev : ws->hidden;
+    if (ws->use_graph) GPHQ_TRY(step_graph(ws, kvs, (int)lanes, hid, tokens_out_dev));
     GPHQ_TRY(seed(ws, (int)lanes, positions, tokens, 0, st));
-    for (int64_t t = 0; t < steps; ++t) GPHQ_TRY(encode_step(ws, kvs, (int)lanes, true, hid, nullptr, tokens_out_dev, st));
+    for (int64_t t = 0; t < steps; ++t) {
+        if (ws->use_graph)
+            GPHQ_TRY(hip_status(hipGraphLaunch(ws->step_exec, st)));
+        else
+            GPHQ_TRY(encode_step(ws, kvs, (int)lanes, true, hid, nullptr, tokens_out_dev, st));
+    }
+    return GPHQ_OK;
+}
+
+int gphq_decode_batch_set_graph(gphq_decode_batch *ws, int on) {
+    if (!ws) return GPHQ_ERR_FOREIGN_WORKSPACE;
+    ws->use_graph = on != 0;
+    if (!ws->use_graph) drop_graph(ws);
     return GPHQ_OK;
 }
 

@@ -110,6 +110,7 @@ SIGNATURES = {
     "gphq_decode_greedy_run": (ctypes.c_int, [_vp, _vpp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "gphq_decode_extend": (ctypes.c_int, [_vp, _vpp, _i64, _vp, _vp, _i64, _vp]),
     "gphq_decode_batch_check": (ctypes.c_int, [_vp, _vp]),
+    "gphq_decode_batch_set_graph": (ctypes.c_int, [_vp, ctypes.c_int]),
 }
 
 FMT_GPTQ4_G128 = 12
@@ -614,6 +615,9 @@ class DecodeBatch:
 
     def set_vec_min_lanes(self, lanes):
         check(load().gphq_decode_batch_set_vec_min_lanes(self.h, lanes))
+
+    def set_graph(self, on):
+        check(load().gphq_decode_batch_set_graph(self.h, 1 if on else 0))
 
     @staticmethod
     def _args(positions, tokens):

@@ -410,6 +410,12 @@ int gphq_decode_batch_greedy_into(gphq_decode_batch *ws, gphq_prefix *const *kvs
 int gphq_decode_greedy_run(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
                            const int32_t *tokens, int64_t steps, int32_t *tokens_out_dev, int64_t tokens_out_len,
                            float *hidden_dev, int64_t hidden_len, void *stream);
+/* Whether gphq_decode_greedy_run replays one captured step as a HIP graph
+ * (default 1) or launches each step's kernels (0). The graph is captured on
+ * the workspace's own stream at the first run and kept while the lane
+ * prefixes, hidden_dev and tokens_out_dev stay the same; it is launched on
+ * the caller's stream. */
+int gphq_decode_batch_set_graph(gphq_decode_batch *ws, int on);
 /* Teacher-forced extension of each lane's prefix by tokens [steps][lanes]
  * (the one-token-at-a-time pass of encodeTokens, gpu_darwin.go:1768-1814):
  * appends K/V rows; no head. */

@@ -256,3 +256,44 @@ def test_validation_errors():
     # A model without a head cannot make a workspace.
     bare = gphq.Lm(gphq.lm_config(fmt=lo.FMT_Q8B, **geom_kwargs(g)))
     assert status(lambda: gphq.DecodeBatch(bare, 1)) == gphq.ERR_MODEL_INCOMPLETE
+
+
+def test_run_graph_replays_match_eager_launches():
+    # The chained run replays one captured step as a HIP graph. Several runs,
+    # with eager decode work and synchronizations between them and a
+    # recapture for new prefixes, must each equal the eager launches.
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(5)
+    lanes, steps = 3, 7
+    ws = gphq.DecodeBatch(lm, 4)
+    base = [gphq.Prefix(lm, 40) for _ in range(lanes)]
+    prompts = [list(rng.integers(0, g.vocab, 4 + i)) for i in range(lanes)]
+    _, pos = prefill(oracle, ws, base, prompts)
+    first = list(rng.integers(0, g.vocab, lanes))
+
+    def run(graph, kvs):
+        for a, b in zip(kvs, base):
+            a.copy_from(b, max(pos))
+        ws.set_graph(graph)
+        out = torch.full((steps, lanes), -1, dtype=torch.int32, device="cuda")
+        hid = torch.empty((lanes, g.hidden), device="cuda")
+        ws.greedy_run(kvs, pos, first, steps, out, hid)
+        torch.cuda.synchronize()
+        return out.cpu().numpy(), hid.cpu().numpy()
+
+    kv1 = [gphq.Prefix(lm, 40) for _ in range(lanes)]
+    kv2 = [gphq.Prefix(lm, 40) for _ in range(lanes)]
+    want_t, want_h = run(False, kv1)
+    other = gphq.Prefix(lm, 40)
+    for rep in range(3):
+        got_t, got_h = run(True, kv1 if rep < 2 else kv2)
+        np.testing.assert_array_equal(got_t, want_t)
+        np.testing.assert_array_equal(got_h, want_h)
+        # Eager work on the same workspace between replays.
+        h1 = torch.empty((1, g.hidden), device="cuda")
+        l1 = torch.empty((1, g.vocab), device="cuda")
+        ws.into([other], [rep], [int(first[0])], h1, l1)
+        torch.cuda.synchronize()
