@@ -109,8 +109,9 @@ int gphq_gemv_vec(int fmt, const void *codes, const void *scales, const float *x
         return GPHQ_ERR_UNSUPPORTED;
     if (lanes < 0 || lanes > GPHQ_GEMV_VEC_MAX_LANES || k < 0 || n < 0 || k > INT32_MAX || n > INT32_MAX)
         return GPHQ_ERR_DIMENSIONS;
-    if (k % 32 != 0 || x_stride < k || y_stride < n) return GPHQ_ERR_DIMENSIONS;
+    if (k % 32 != 0 || x_stride < k || y_stride < n || x_stride % 4 != 0) return GPHQ_ERR_DIMENSIONS;
     if (lanes == 0 || n == 0) return GPHQ_OK;
+    if (k && (uintptr_t)x % 16 != 0) return GPHQ_ERR_DIMENSIONS;
     if (work_bytes < gphq_gemv_vec_workspace_bytes(lanes, k)) return GPHQ_ERR_DIMENSIONS;
     if (!y || !scales || !work || (uintptr_t)work % 16 != 0) return GPHQ_ERR_DIMENSIONS;
     if (k && (!codes || !x || (uintptr_t)codes % 16 != 0)) return GPHQ_ERR_DIMENSIONS;

@@ -132,8 +132,9 @@ int gphq_gemv(int fmt, const void *codes_dev, const void *scales_dev, const floa
  * Replaces gemvQ8BVector<V> (qwen3lm/gpu.metal:239-314) with its host side
  * gpuDecodeBatchWorkspace.gemv (gpu_darwin.go:1121-1159); any lanes in
  * 1..GPHQ_GEMV_VEC_MAX_LANES (the reference caps V at 8, decode_batch.go:31-33).
- * Formats Q8, Q8B, Q8B_F32, Q4; k % 32 == 0. The vectors are split into FP16
- * hi+lo parts after an exact power-of-two scaling and multiplied on MFMA
+ * Formats Q8, Q8B, Q8B_F32, Q4; k % 32 == 0; x_dev 16-byte aligned and
+ * x_stride a multiple of 4. Each 32-value block of each vector is split into
+ * FP16 hi+lo parts after an exact power-of-two scaling and multiplied on MFMA
  * (products exact, fp32 sums), so results agree with gphq_gemv to the
  * reference's vector-vs-serial bound (1e-4 abs, 1e-5 rel,
  * gpu_vector_batch_darwin_test.go:218) but not bit for bit. work_dev: scratch

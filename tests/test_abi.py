@@ -124,3 +124,13 @@ def test_decode_entry_points_reject_null_workspace():
     assert lib.gphq_decode_batch_into(None, None, 1, p, p, p, 1, p, 1, None) == gphq.ERR_FOREIGN_WORKSPACE
     assert lib.gphq_decode_batch_new(None, 1, ctypes.byref(ctypes.c_void_p())) == gphq.ERR_FOREIGN_WORKSPACE
     assert gphq.error_string(gphq.ERR_PREFIX_FULL) == "qwen3: decode prefix has no room for another token"
+
+
+def test_gemv_vec_rejects_misaligned_vectors():
+    lib = gphq.load()
+    p = ctypes.c_void_p(256)
+    big = 1 << 30
+    # x_stride not a multiple of 4, then x not 16-byte aligned: rejected before any device work.
+    assert lib.gphq_gemv_vec(gphq.FMT_Q8B, p, p, p, 66, p, 64, 2, 64, 64, p, big, None) == gphq.ERR_DIMENSIONS
+    assert lib.gphq_gemv_vec(gphq.FMT_Q8B, p, p, ctypes.c_void_p(260), 64, p, 64, 2, 64, 64, p, big, None) == \
+        gphq.ERR_DIMENSIONS
