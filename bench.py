@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--decode-fmt", choices=["q8b", "q8b_f32", "q8", "q4"], default="q8b",
                     help="layer weight format of the decode models (the reference's decode batch uses Q8B)")
     ap.add_argument("--decode-eager", action="store_true", help="launch decode steps without the HIP graph")
+    ap.add_argument("--decode-configs", default="3,4b1,4b16",
+                    help="decode lines to run: 3 (Qwen3-0.6B), 4b1 / 4b16 (Qwen3-8B, 1 / 16 lanes)")
     return ap.parse_args()
 
 
@@ -295,20 +297,37 @@ def decode_config(torch, gphq, lm, weight_bytes, geom, lanes, ctx, steps, warmup
 def decode_benchmarks(args, torch, gphq):
     fmt = {"q8b": gphq.FMT_Q8B, "q8b_f32": gphq.FMT_Q8B_F32, "q8": gphq.FMT_Q8, "q4": gphq.FMT_Q4}[args.decode_fmt]
     graph = not args.decode_eager
+    want = set(args.decode_configs.split(","))
     res = {"fmt": args.decode_fmt}
-    lm, wb = decode_model(torch, gphq, QWEN3_06B, fmt, 3)
-    res["config3"] = decode_config(torch, gphq, lm, wb, QWEN3_06B, 1, 1024, 256, 16, graph,
-                                   "config 3: Qwen3-0.6B-shaped, batch 1, 1024-token K/V prefill, 256 greedy steps")
-    del lm
-    torch.cuda.empty_cache()
-    lm, wb = decode_model(torch, gphq, QWEN3_8B, fmt, 4)
-    res["config4b_1"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 1, 4096, 64, 8, graph,
-                                      "config 4b: Qwen3-8B-shaped decode at context 4096, 1 lane")
-    res["config4b_16"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 16, 4096, 32, 4, graph,
-                                       "config 4b: Qwen3-8B-shaped decode at context 4096, 16 lanes")
-    del lm
-    torch.cuda.empty_cache()
+    if "3" in want:
+        lm, wb = decode_model(torch, gphq, QWEN3_06B, fmt, 3)
+        res["config3"] = decode_config(torch, gphq, lm, wb, QWEN3_06B, 1, 1024, 256, 16, graph,
+                                       "config 3: Qwen3-0.6B-shaped, batch 1, 1024-token K/V prefill, 256 greedy steps")
+        del lm
+        torch.cuda.empty_cache()
+    if want & {"4b1", "4b16"}:
+        lm, wb = decode_model(torch, gphq, QWEN3_8B, fmt, 4)
+        if "4b1" in want:
+            res["config4b_1"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 1, 4096, 64, 8, graph,
+                                              "config 4b: Qwen3-8B-shaped decode at context 4096, 1 lane")
+        if "4b16" in want:
+            res["config4b_16"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 16, 4096, 32, 4, graph,
+                                               "config 4b: Qwen3-8B-shaped decode at context 4096, 16 lanes")
+        del lm
+        torch.cuda.empty_cache()
     return res
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed FETCH_SIZE / WRITE_SIZE
+    profile (profiles/gemv8_config1_traffic.md), or None."""
+    path = os.path.join(ROOT, "profiles", "gemv8_config1_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return rec["traffic_bytes_per_launch"] if rec.get("kernel") == kernel else None
 
 
 def cpu_baseline(seconds):
@@ -358,6 +377,7 @@ def main():
     decode = None if args.no_decode else decode_benchmarks(args, torch, gphq)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     kernel = "gemv8_kernel<Q8B_F32,4,2,8," + ("32>" if args.mode == "batch" else "1>")
+    traffic = measured_traffic(kernel) if args.rotations == 32 else None
     out = {
         "metric": "Q8 GEMV HBM GB/s (% of peak) + Qwen3-8B Q8 decode ms/token, 1 MI355X",
         "value": round(value, 2),
@@ -386,7 +406,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel": kernel,
             "per_launch_us": round(r["per_launch_us"], 3),
             "bytes_per_launch": r["bytes_per_launch"],
@@ -399,7 +419,7 @@ def main():
             "mode": "one gphq_gemv launch per 4096x4096 GEMV, HIP graph of 32 launches",
         },
         "gemm_config2": gemm,
-        "decode_ms_per_token": None if decode is None else decode["config4b_1"]["ms_per_step"],
+        "decode_ms_per_token": (decode or {}).get("config4b_1", {}).get("ms_per_step"),
         "decode": decode,
         "check": {"rel_l2_vs_float64": r["rel_l2"]},
     }
