@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <vector>
 
 #include "../../include/gphq.h"
 
@@ -51,6 +52,31 @@ __device__ __forceinline__ float wave_sum(float v) {
     float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
     return (a + b) + (c + d);
 }
+
+// In-place unnormalized Walsh-Hadamard transform of each `block` run of
+// v[0..n) in LDS, stage h = 1, 2, 4, ...: the butterfly network of
+// qwen3lm/hadamard.go:62-78 (each stage's butterflies are independent, so the
+// fp32 result equals the sequential network's bit for bit). All threads of
+// the block take part; ends with a barrier.
+__device__ inline void lds_fwht(float *v, int n, int block) {
+    const int halfBlock = block >> 1;
+    for (int h = 1; h < block; h <<= 1) {
+        for (int idx = threadIdx.x; idx < (n >> 1); idx += blockDim.x) {
+            const int b = idx / halfBlock, i = idx - b * halfBlock;
+            const int j = b * block + (i / h) * 2 * h + (i % h);
+            const float a = v[j], c = v[j + h];
+            v[j] = a + c;
+            v[j + h] = a - c;
+        }
+        __syncthreads();
+    }
+}
+
+// qwen3lm/hadamard.go:24-47 newRotation(k): fills k signs (+-1) and returns
+// the block (the largest power of two up to 4096 dividing k); the scale is
+// 1/sqrt(block) rounded to float32.
+int rotation_signs_pm1(int64_t k, std::vector<float> &signs);
+inline float rotation_scale(int64_t block) { return (float)(1.0 / __builtin_sqrt((double)block)); }
 
 // IEEE half bits -> float (exact), for FP16 scales stored as raw uint16.
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {

@@ -361,9 +361,10 @@ int gemv_batch_launch(int fmt, const void *const *codes, const void *const *scal
 // on MI355X with rotated weights over 256 MB, one launch per GEMV):
 // very tall matrices (the head) take 16-row blocks of four unsplit
 // wavefronts; tall ones (gate/up) 16-row blocks with K in two slices; long
-// rows (down) 16-row blocks with K in four slices and two steps in flight;
-// short, wide-K matrices (o, 0.6B down) 8-row blocks with K in four slices;
-// the rest (qkv) 8-row blocks with K in two slices.
+// rows (down) 8-row blocks with K in four slices and two steps in flight;
+// short, wide-K matrices 4-row blocks with K in four slices (2-row blocks of
+// one row per wavefront up to 2048 rows: Qwen3-0.6B's o and down); the rest
+// (qkv) 8-row blocks with K in two slices.
 template <int FMT, int PRO, int EPI>
 static void launch_fused8(const GemvBatch<1> &b, hipStream_t stream) {
     auto go = [&](auto kern, int rows, int threads) {
@@ -375,6 +376,8 @@ static void launch_fused8(const GemvBatch<1> &b, hipStream_t stream) {
         go(gemv8_kernel<FMT, 4, 2, 8, 1, PRO, EPI, 1>, 16, 512);
     else if (b.K >= 8192)
         go(gemv8_kernel<FMT, 4, 4, 8, 1, PRO, EPI, 2>, 8, 512);
+    else if (b.N <= 2048 && b.K >= 2048)
+        go(gemv8_kernel<FMT, 1, 4, 8, 1, PRO, EPI, 1>, 2, 512);
     else if (b.N <= 4096 && b.K >= 2048)
         go(gemv8_kernel<FMT, 2, 4, 8, 1, PRO, EPI, 1>, 4, 512);
     else

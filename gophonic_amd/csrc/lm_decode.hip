@@ -59,25 +59,13 @@ constexpr int kMaxWidth = 16384;    // hidden and intermediate widths (LDS)
 enum { PRO_PLAIN = 0, PRO_NORM = 1 };
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
 
-// hadamard.go:24-47 newRotation: the block is the largest power of two up
-// to 4096 dividing k; sign i comes from the low bit of the i-th splitmix64
-// output with the state seeded by golden ^ k. Returns sign*scale per value
-// (multiplying by +-1 is exact, so x*(sign*scale) == (x*scale)*sign).
+// Sign*scale per value of newRotation(k) (multiplying by +-1 is exact, so
+// x*(sign*scale) == (x*scale)*sign); returns the block.
 int rotation_signs(int64_t k, std::vector<float> &out) {
-    int64_t block = 1;
-    while (block < kMaxRotation && k % (2 * block) == 0) block *= 2;
-    const float scale = (float)(1.0 / sqrt((double)block));
-    uint64_t state = 0x9e3779b97f4a7c15ull ^ (uint64_t)k;
-    out.resize(k);
-    for (int64_t i = 0; i < k; ++i) {
-        state += 0x9e3779b97f4a7c15ull;
-        uint64_t z = state;
-        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-        z ^= z >> 31;
-        out[i] = (z & 1) ? -scale : scale;
-    }
-    return (int)block;
+    const int block = rotation_signs_pm1(k, out);
+    const float scale = rotation_scale(block);
+    for (float &v : out) v *= scale;
+    return block;
 }
 
 // Bytes of one stored matrix's codes and scales (gpu_darwin.go:251-264).
@@ -139,24 +127,6 @@ struct gphq_decode_batch {
 namespace {
 
 // ---- kernels ---------------------------------------------------------------
-
-// In-place unnormalized Walsh-Hadamard transform of each `block` run of
-// v[0..n), stage h = 1, 2, 4, ...: the butterfly network of hadamard.go:62-78
-// (each stage's butterflies are independent, so the fp32 result equals the
-// sequential network's bit for bit). All threads of the block take part.
-__device__ void lds_fwht(float *v, int n, int block) {
-    const int halfBlock = block >> 1;
-    for (int h = 1; h < block; h <<= 1) {
-        for (int idx = threadIdx.x; idx < (n >> 1); idx += blockDim.x) {
-            const int b = idx / halfBlock, i = idx - b * halfBlock;
-            const int j = b * block + (i / h) * 2 * h + (i % h);
-            const float a = v[j], c = v[j + h];
-            v[j] = a + c;
-            v[j + h] = a - c;
-        }
-        __syncthreads();
-    }
-}
 
 // Deterministic block sum (fixed tree over the block's waves).
 __device__ float block_sum(float v, float *red) {

@@ -111,6 +111,8 @@ SIGNATURES = {
     "gphq_decode_extend": (ctypes.c_int, [_vp, _vpp, _i64, _vp, _vp, _i64, _vp]),
     "gphq_decode_batch_check": (ctypes.c_int, [_vp, _vp]),
     "gphq_decode_batch_set_graph": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "gphq_prepare_work_bytes": (_i64, [_i64, _i64]),
+    "gphq_prepare_projection": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
 }
 
 FMT_GPTQ4_G128 = 12
@@ -692,4 +694,129 @@ def lm_from_stored(geom_kwargs, fmt, layers, embed_bf16, final_norm, head, devic
     put(host, 0, head[0])
     put(host, so, head[1])
     lm.bind_head(host.to(device), final_norm)
+    return lm
+
+
+# ---- weight preparation (gphq_prepare_projection) ----------------------------
+
+
+class RotationSpec(ctypes.Structure):
+    _fields_ = [("width", ctypes.c_int64), ("tile", ctypes.c_int64)]
+
+
+class PrepareJob(ctypes.Structure):
+    _fields_ = [("src_bf16_dev", ctypes.c_void_p), ("n", ctypes.c_int64), ("k", ctypes.c_int64),
+                ("norm_host", ctypes.c_void_p), ("in_rot", RotationSpec), ("out_rot", RotationSpec),
+                ("fmt", ctypes.c_int32), ("reserved", ctypes.c_int32), ("dst_dev", ctypes.c_void_p),
+                ("dst_bytes", ctypes.c_int64), ("base", ctypes.c_int64), ("sc", ctypes.c_int64),
+                ("step", ctypes.c_int64), ("row0", ctypes.c_int64), ("scale_mul", ctypes.c_float)]
+
+
+def prepare_work_bytes(n, k):
+    return load().gphq_prepare_work_bytes(n, k)
+
+
+def prepare_projection(src_bf16, n, k, fmt, dst, base, sc, norm=None, in_rot=(0, 0), out_rot=(0, 0), step=1, row0=0,
+                       scale_mul=1.0, work=None, stream=None):
+    """One prepareGPU job: src_bf16 device int16 tensor [n][k] -> quantized rows in dst
+    (a uint8 device tensor) at byte offsets base (codes) and sc (scales)."""
+    import numpy as np
+    import torch
+
+    if work is None:
+        work = torch.empty(prepare_work_bytes(n, k), dtype=torch.uint8, device=dst.device)
+    nh = None
+    if norm is not None:
+        nh = np.ascontiguousarray(norm, dtype=np.float32)
+    job = PrepareJob(src_bf16.data_ptr(), n, k, None if nh is None else nh.ctypes.data, RotationSpec(*in_rot),
+                     RotationSpec(*out_rot), fmt, 0, dst.data_ptr(), dst.numel() * dst.element_size(), base, sc,
+                     step, row0, scale_mul)
+    check(load().gphq_prepare_projection(ctypes.byref(job), work.data_ptr(), work.numel() * work.element_size(),
+                                         stream_handle(stream)))
+
+
+def _bf16_device(bits, shape, device):
+    """BF16 bits (numpy uint16/int16 or a device int16 tensor) as a contiguous device int16 tensor."""
+    import numpy as np
+    import torch
+
+    if isinstance(bits, torch.Tensor):
+        return bits.reshape(shape).contiguous().to(device)
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16).reshape(shape).copy()).to(device)
+
+
+def _bf16_host_f32(bits):
+    import numpy as np
+    import torch
+
+    if isinstance(bits, torch.Tensor):
+        bits = bits.cpu().numpy()
+    return (np.asarray(bits).view(np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(-1)
+
+
+def prepare_lm(geom_kwargs, fmt, tensors, device="cuda", prefix="model.", head_name="lm_head.weight"):
+    """prepareGPU (gpu_darwin.go:392-567) for a dense Qwen3 checkpoint, on the
+    device: every projection of every layer quantized into its layer buffer
+    (the placement of gphq_lm_layer_layout), the head into its own buffer
+    (Q8B, in chunks of max(inter, 4096) rows), and the model bound.
+
+    tensors maps checkpoint names (model.layers.N.self_attn.q_proj.weight, ...,
+    model.embed_tokens.weight, model.norm.weight, lm_head.weight) to BF16 bits:
+    numpy uint16/int16 arrays or device int16 tensors. Returns an Lm.
+
+    The job list is the reference's: q/k/v over the input-normalized,
+    hidden-rotated rows (v's rows also rotated per head), o with the per-head
+    input rotation and the hidden output rotation, gate/up over the
+    post-attention-normalized rows interleaved with step 2, down with the
+    intermediate input rotation (none for Q8B) and the hidden output rotation,
+    and the head over hidden-rotated rows.
+    """
+    import torch
+
+    cfg = lm_config(fmt=fmt, **geom_kwargs)
+    desc, nbytes = lm_layer_layout(cfg)
+    h, qd, inter, hd = cfg.hidden, cfg.heads * cfg.head_dim, cfg.intermediate, cfg.head_dim
+    kv = cfg.kv_heads * hd
+    hidden_rot, head_rot = (h, 0), (0, hd)
+    down_in = (0, 0) if fmt == FMT_Q8B else (inter, 0)
+    lm = Lm(cfg)
+    jobs_per_layer = []
+    for i in range(cfg.layers):
+        p = f"{prefix}layers.{i}."
+        an = _bf16_host_f32(tensors[p + "input_layernorm.weight"])
+        mn = _bf16_host_f32(tensors[p + "post_attention_layernorm.weight"])
+        jobs_per_layer.append([
+            # name, n, k, norm, in, out, base, sc, step, row0
+            (p + "self_attn.q_proj.weight", qd, h, an, hidden_rot, (0, 0), desc.qkv, desc.qkv_scale, 1, 0),
+            (p + "self_attn.k_proj.weight", kv, h, an, hidden_rot, (0, 0), desc.qkv, desc.qkv_scale, 1, qd),
+            (p + "self_attn.v_proj.weight", kv, h, an, hidden_rot, head_rot, desc.qkv, desc.qkv_scale, 1, qd + kv),
+            (p + "self_attn.o_proj.weight", h, qd, None, head_rot, hidden_rot, desc.o, desc.o_scale, 1, 0),
+            (p + "mlp.gate_proj.weight", inter, h, mn, hidden_rot, (0, 0), desc.gu, desc.gu_scale, 2, 0),
+            (p + "mlp.up_proj.weight", inter, h, mn, hidden_rot, (0, 0), desc.gu, desc.gu_scale, 2, 1),
+            (p + "mlp.down_proj.weight", h, inter, None, down_in, hidden_rot, desc.d, desc.d_scale, 1, 0),
+        ])
+    rows, head_sc, head_bytes = lm_head_layout(cfg)
+    chunk = max(inter, 4096)
+    wmax = max([prepare_work_bytes(j[1], j[2]) for js in jobs_per_layer for j in js] +
+               [prepare_work_bytes(min(chunk, cfg.vocab), h)])
+    work = torch.empty(wmax, dtype=torch.uint8, device=device)
+    for i, js in enumerate(jobs_per_layer):
+        buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        for name, n, k, norm, rin, rout, base, sc, step, row0 in js:
+            src = _bf16_device(tensors[name], (n, k), device)
+            prepare_projection(src, n, k, fmt, buf, base, sc, norm=norm, in_rot=rin, out_rot=rout, step=step,
+                               row0=row0, work=work)
+            del src
+        p = f"{prefix}layers.{i}."
+        lm.bind_layer(i, buf, desc, _bf16_host_f32(tensors[p + "self_attn.q_norm.weight"]),
+                      _bf16_host_f32(tensors[p + "self_attn.k_norm.weight"]))
+    lm.bind_embed(_bf16_device(tensors[prefix + "embed_tokens.weight"], (cfg.vocab, h), device))
+    head_buf = torch.zeros(head_bytes, dtype=torch.uint8, device=device)
+    head_src = tensors[head_name]
+    for r in range(0, cfg.vocab, chunk):
+        n = min(r + chunk, cfg.vocab) - r
+        src = _bf16_device(head_src.reshape(cfg.vocab, h)[r:r + n], (n, h), device)
+        prepare_projection(src, n, h, FMT_Q8B, head_buf, 0, head_sc, in_rot=hidden_rot, row0=r, work=work)
+    lm.bind_head(head_buf, _bf16_host_f32(tensors[prefix + "norm.weight"]))
+    torch.cuda.synchronize()
     return lm

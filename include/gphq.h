@@ -427,6 +427,44 @@ int gphq_decode_extend(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t l
  * gpu_darwin.go:1245-1249, which it raises before returning). */
 int gphq_decode_batch_check(gphq_decode_batch *ws, void *stream);
 
+/* ---- weight preparation (prepareGPU's jobs) ---------------------------------
+ * Replaces the body of one gpuJob of qwen3lm's prepareGPU
+ * (qwen3lm/gpu_darwin.go:375-391, 511-567): BF16 rows [n][k] -> float32 ->
+ * times the folded RMSNorm weight -> input rotation R.row -> output rotation
+ * along the rows -> quantization into the layer buffer (Q8 quantizeRow, Q8B
+ * quantizeRowQ8B, Q4 quantizeRowQ4; gpu_darwin.go:582-658), every step in the
+ * reference's float32 operation order, so codes and scales are bit-identical
+ * to the host path's. GPHQ_FMT_Q8B_F32 stores the Q8B codes of d = max/127
+ * with fp32 scales (no counterpart in the reference).
+ * A rotation is newRotation(width) (hadamard.go:24-47), or with tile > 0 the
+ * signs of newRotation(tile) repeated every tile values (the per-head
+ * rotation of value rows and o inputs, gpu_darwin.go:217-221); {0, 0} is
+ * none. The input rotation spans k, the output rotation n (n a multiple of
+ * its block). Source row r is written to destination row row0 + r*step
+ * (gate/up interleave: step 2, row0 0 or 1), codes at byte offset base and
+ * scales at sc of dst_dev (dst_bytes long). One-time setup: the call waits
+ * for its stream. */
+typedef struct gphq_rotation_spec {
+    int64_t width, tile;
+} gphq_rotation_spec;
+
+typedef struct gphq_prepare_job {
+    const uint16_t *src_bf16_dev; /* [n][k] BF16 bits */
+    int64_t n, k;
+    const float *norm_host;       /* k weights folded into every row, or NULL */
+    gphq_rotation_spec in_rot, out_rot;
+    int32_t fmt;
+    int32_t reserved;
+    void *dst_dev;
+    int64_t dst_bytes;
+    int64_t base, sc, step, row0;
+    float scale_mul;
+} gphq_prepare_job;
+
+/* Scratch for gphq_prepare_projection: float32 rows plus tables (n*k*4 + ...). */
+int64_t gphq_prepare_work_bytes(int64_t n, int64_t k);
+int gphq_prepare_projection(const gphq_prepare_job *job, void *work_dev, int64_t work_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -665,3 +665,70 @@ void orc_rotation_unapply(const float *signs, int64_t block, float scale, float 
     for (int64_t b = 0; b < k; b += block) orc_fwht(x + b, block);
     for (int64_t i = 0; i < k; ++i) x[i] = x[i] * scale * signs[i];
 }
+
+/* hadamard.go:88-104 applyRows: the n x k matrix a becomes R.a, rotating along
+ * the row index: each row times its sign, the butterfly network across rows
+ * of each block (stage h = 1, 2, ...), then every value times scale. */
+void orc_rotation_apply_rows(const float *signs, int64_t block, float scale, float *a, int64_t n, int64_t k) {
+    for (int64_t i = 0; i < n; ++i)
+        for (int64_t c = 0; c < k; ++c) a[i * k + c] *= signs[i];
+    for (int64_t b = 0; b < n; b += block)
+        for (int64_t h = 1; h < block; h *= 2)
+            for (int64_t i = b; i < b + block; i += 2 * h)
+                for (int64_t j = i; j < i + h; ++j)
+                    for (int64_t c = 0; c < k; ++c) {
+                        float x = a[j * k + c], y = a[(j + h) * k + c];
+                        a[j * k + c] = x + y;
+                        a[(j + h) * k + c] = x - y;
+                    }
+    for (int64_t i = 0; i < n * k; ++i) a[i] *= scale;
+}
+
+/* One gpuJob of prepareGPU (qwen3lm/gpu_darwin.go:511-567) on the CPU: rows of
+ * BF16 bits [n][k] widened to float32; each row times the folded norm (if
+ * any), then rotated by the input rotation (if any); then the output rotation
+ * along the rows (if any); then each row quantized in format fmt (8 = Q8 with
+ * an fp32 row scale times scale_mul, 9 = Q8B, 4 = Q4, 10 = Q8B with fp32 block
+ * scales) into dst at byte offsets base (codes) and sc (scales), source row r
+ * landing on destination row row0 + r*step. in_signs/out_signs may be NULL. */
+void orc_prepare_projection(const uint16_t *bf16, int64_t n, int64_t k, const float *norm, const float *in_signs,
+                            int64_t in_block, float in_scale, const float *out_signs, int64_t out_block,
+                            float out_scale, int fmt, uint8_t *dst, int64_t base, int64_t sc, int64_t step,
+                            int64_t row0, float scale_mul, float *work) {
+    for (int64_t i = 0; i < n * k; ++i) work[i] = orc_bf16_to_f32(bf16[i]);
+    for (int64_t r = 0; r < n; ++r) {
+        float *row = work + r * k;
+        if (norm)
+            for (int64_t i = 0; i < k; ++i) row[i] *= norm[i];
+        if (in_signs) orc_rotation_apply(in_signs, in_block, in_scale, row, k);
+    }
+    if (out_signs) orc_rotation_apply_rows(out_signs, out_block, out_scale, work, n, k);
+    for (int64_t r = 0; r < n; ++r) {
+        const float *row = work + r * k;
+        const int64_t d = row0 + r * step;
+        if (fmt == 8) {
+            float s = orc_quantize_row_q8(row, k, (int8_t *)(dst + base + d * k));
+            float v = s * scale_mul;
+            memcpy(dst + sc + d * 4, &v, 4);
+        } else if (fmt == 9) {
+            orc_quantize_row_q8b(row, k, (int8_t *)(dst + base + d * k), (uint16_t *)(dst + sc + d * (k / 32) * 2),
+                                 scale_mul);
+        } else if (fmt == 4) {
+            orc_quantize_row_q4(row, k, dst + base + d * (k / 2), (uint16_t *)(dst + sc + d * (k / 32) * 2),
+                                scale_mul);
+        } else if (fmt == 10) {
+            int8_t *q = (int8_t *)(dst + base + d * k);
+            float *s = (float *)(dst + sc + d * (k / 32) * 4);
+            for (int64_t b = 0; b < k / 32; b++) {
+                float dd = orc_max_abs(row + b * 32, 32) / 127.0f;
+                s[b] = dd * scale_mul;
+                for (int i = 0; i < 32; i++) {
+                    double q0 = dd == 0.0f ? 0.0 : nearbyint((double)(row[b * 32 + i] / dd));
+                    if (q0 > 127) q0 = 127;
+                    if (q0 < -127) q0 = -127;
+                    q[b * 32 + i] = (int8_t)q0;
+                }
+            }
+        }
+    }
+}

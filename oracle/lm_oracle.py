@@ -99,6 +99,13 @@ def rot_unapply(x, rot):
     return hadamard_f64(x, block) * scale * signs
 
 
+def head_rotation(head_dim, length):
+    """The per-head rotation of value rows and o inputs (gpu_darwin.go:217-221):
+    newRotation(head_dim)'s signs repeated over `length` values."""
+    signs, block, scale = rotation(head_dim)
+    return np.tile(signs, length // head_dim), block, scale
+
+
 def rot_matrix(rot):
     """The dense orthogonal matrix R with R @ x == rot_apply(x, rot)."""
     signs, block, scale = rot

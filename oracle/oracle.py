@@ -68,6 +68,10 @@ def _load():
         "orc_fwht": (None, [_f32p, _i64]),
         "orc_rotation_apply": (None, [_f32p, _i64, ctypes.c_float, _f32p, _i64]),
         "orc_rotation_unapply": (None, [_f32p, _i64, ctypes.c_float, _f32p, _i64]),
+        "orc_rotation_apply_rows": (None, [_f32p, _i64, ctypes.c_float, _f32p, _i64, _i64]),
+        "orc_prepare_projection": (None, [_u16p, _i64, _i64, _f32p, _f32p, _i64, ctypes.c_float, _f32p, _i64,
+                                          ctypes.c_float, ctypes.c_int, _u8p, _i64, _i64, _i64, _i64,
+                                          ctypes.c_float, _f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -340,3 +344,29 @@ def rotation_unapply_f32(x, rot):
     v = _c(x, np.float32).copy()
     lib().orc_rotation_unapply(_p(_c(signs, np.float32), _f32p), block, scale, _p(v, _f32p), len(v))
     return v
+
+
+def rotation_apply_rows_f32(a, rot):
+    """hadamard.go:88-104 rotation.applyRows in float32 on an n x k array (rot = (signs, block, scale))."""
+    signs, block, scale = rot
+    m = np.array(a, dtype=np.float32, copy=True, order="C")
+    n, k = m.shape
+    lib().orc_rotation_apply_rows(_p(_c(signs[:n], np.float32), _f32p), block, scale, _p(m, _f32p), n, k)
+    return m
+
+
+def prepare_projection(bf16, n, k, fmt, dst, base, sc, norm=None, in_rot=None, out_rot=None, step=1, row0=0,
+                       scale_mul=1.0):
+    """One prepareGPU job (gpu_darwin.go:511-567) on the CPU, writing into the uint8 array dst.
+    in_rot / out_rot: (signs, block, scale) or None."""
+    src = _c(bf16, np.uint16)
+    work = np.empty(n * k, np.float32)
+    nrm = None if norm is None else _c(norm, np.float32)
+    ins = None if in_rot is None else _c(in_rot[0][:k], np.float32)
+    outs = None if out_rot is None else _c(out_rot[0][:n], np.float32)
+    lib().orc_prepare_projection(
+        _p(src, _u16p), n, k, None if nrm is None else _p(nrm, _f32p),
+        None if ins is None else _p(ins, _f32p), 0 if in_rot is None else in_rot[1],
+        0.0 if in_rot is None else in_rot[2], None if outs is None else _p(outs, _f32p),
+        0 if out_rot is None else out_rot[1], 0.0 if out_rot is None else out_rot[2], fmt, _p(dst, _u8p), base, sc,
+        step, row0, scale_mul, _p(work, _f32p))

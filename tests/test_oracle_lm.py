@@ -182,3 +182,37 @@ def test_greedy_argmax_rules():
     assert lo.greedy_argmax([-0.0, 0.0]) == 0
     for v in ([1.0, 3.0, 3.0, 2.0], [nan, 5.0, 6.0], [1.0, nan, 0.5, 7.0], [-np.inf, -np.inf]):
         assert lo.greedy_argmax_np(v) == lo.greedy_argmax(v)
+
+
+@pytest.mark.parametrize("n,k,rot_k,tile", [(256, 8, 256, 0), (1024, 3, 1024, 0), (256, 5, 0, 128)])
+def test_rotation_apply_rows_matches_dense(n, k, rot_k, tile):
+    # hadamard.go:88-104: applyRows(a) == R @ a, rotating along the row index.
+    rot = lo.head_rotation(tile, n) if tile else lo.rotation(rot_k)
+    R = lo.rot_matrix(rot)
+    rng = np.random.default_rng(n + k)
+    a = rng.standard_normal((n, k)).astype(np.float32)
+    got = orc.rotation_apply_rows_f32(a, rot).astype(np.float64)
+    want = R @ a.astype(np.float64)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    # Rows of the identity become the columns of R.
+    np.testing.assert_allclose(orc.rotation_apply_rows_f32(np.eye(n, dtype=np.float32), rot), R, atol=1e-6)
+
+
+def test_prepare_projection_oracle_roundtrip():
+    # A prepared job dequantizes back to R_out . (W diag(norm)) . R_in^T within the
+    # quantizer's bound: every stored row is the rotated row to half a step.
+    g = lc.GPU_SHAPE
+    rng = np.random.default_rng(4)
+    n, k = g.hidden, g.qd
+    w = (rng.standard_normal((n, k)) * 0.1).astype(np.float32)
+    bf = lc.bf16_bits(w)
+    wf = lo.bf16_to_f64(bf).reshape(n, k)
+    hin = lo.head_rotation(g.head_dim, k)
+    hout = lo.rotation(g.hidden)
+    dst = np.zeros(n * k + n * (k // 32) * 2, np.uint8)
+    orc.prepare_projection(bf, n, k, lo.FMT_Q8B, dst, 0, n * k, in_rot=hin, out_rot=hout)
+    deq = lo.dequant(lo.FMT_Q8B, dst[:n * k], dst[n * k:].view(np.uint16), n, k)
+    want = lo.rot_matrix(hout) @ wf @ lo.rot_matrix(hin).T
+    step = np.abs(want).reshape(n, k // 32, 32).max(axis=2, keepdims=True) / 127
+    err = np.abs(deq - want).reshape(n, k // 32, 32)
+    assert (err <= 0.5 * step * 1.01 + 1e-6).all()
