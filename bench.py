@@ -320,8 +320,8 @@ def decode_benchmarks(args, torch, gphq):
 
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed FETCH_SIZE / WRITE_SIZE
-    profile (profiles/gemv8_config1_traffic.md), or None."""
-    path = os.path.join(ROOT, "profiles", "gemv8_config1_traffic.json")
+    profile (profiles/gemvp_config1_traffic.md), or None."""
+    path = os.path.join(ROOT, "profiles", "gemvp_config1_traffic.json")
     try:
         with open(path) as f:
             rec = json.load(f)
@@ -376,7 +376,9 @@ def main():
     gemm = None if args.no_gemm else gemm_config2(args, torch, gphq)
     decode = None if args.no_decode else decode_benchmarks(args, torch, gphq)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
-    kernel = "gemv8_kernel<Q8B_F32,4,2,8," + ("32>" if args.mode == "batch" else "1>")
+    # The persistent GEMV's template shape for config 1 (gemv.hip persistent_shape):
+    # <format, K steps per wave, rows per group, K slices, waves per block, GEMVs per launch>.
+    kernel = "gemvp_kernel<Q8B_F32,2,4,2,4,32>" if args.mode == "batch" else "gemvp_kernel<Q8B_F32,2,4,2,8,1>"
     traffic = measured_traffic(kernel) if args.rotations == 32 else None
     out = {
         "metric": "Q8 GEMV HBM GB/s (% of peak) + Qwen3-8B Q8 decode ms/token, 1 MI355X",
