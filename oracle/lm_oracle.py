@@ -226,7 +226,8 @@ class DecodeOracle:
             h = h + W["o"] @ ctx
             gu = W["gu"] @ self._norm(h)
             gate, up = gu[0::2], gu[1::2]
-            act = gate / (1.0 + np.exp(-gate)) * up
+            with np.errstate(over="ignore"):  # exp(-gate) = inf gives act = -0, as in float32
+                act = gate / (1.0 + np.exp(-gate)) * up
             if self.fmt != FMT_Q8B:
                 act = rot_apply(act, self.irot)
             h = h + W["down"] @ act

@@ -297,3 +297,35 @@ def test_run_graph_replays_match_eager_launches():
         l1 = torch.empty((1, g.vocab), device="cuda")
         ws.into([other], [rep], [int(first[0])], h1, l1)
         torch.cuda.synchronize()
+
+
+# One layer at Qwen3-8B widths: the GEMVs take the K = 4096 shapes with two
+# and four K slices (the norm prologue's cross-slice sum included) and
+# down's K = 12288 in six slices.
+QWEN3_8B_LAYER = lo.Geometry(hidden=4096, layers=1, heads=32, kv_heads=8, head_dim=128, inter=12288, vocab=1000,
+                             max_pos=64)
+
+
+@pytest.mark.parametrize("fmt", [lo.FMT_Q8B, lo.FMT_Q8])
+def test_decode_8b_widths(fmt):
+    import torch
+
+    model, oracle, lm = setup(QWEN3_8B_LAYER, fmt, seed=21)
+    g = model["geom"]
+    rng = np.random.default_rng(8)
+    ws = gphq.DecodeBatch(lm, 2)
+    kvs = [gphq.Prefix(lm, 32), gphq.Prefix(lm, 32)]
+    caches, pos = prefill(oracle, ws, kvs, [list(rng.integers(0, g.vocab, 9)), list(rng.integers(0, g.vocab, 4))])
+    for lanes in (1, 2):
+        tokens = list(rng.integers(0, g.vocab, lanes))
+        hidden = torch.empty((lanes, g.hidden), device="cuda")
+        logits = torch.empty((lanes, g.vocab), device="cuda")
+        ws.into(kvs[:lanes], pos[:lanes], tokens, hidden, logits)
+        hid, lg = hidden.cpu().numpy(), logits.cpu().numpy()
+        for i in range(lanes):
+            wh, wl, _ = oracle.step(caches[i], pos[i], tokens[i])
+            rh, ah = err(wh, hid[i])
+            rl, al = err(wl, lg[i])
+            assert rh <= REL and rl <= REL, (lanes, i, rh, rl)
+            assert ah <= 10 * REL and al <= 10 * REL, (lanes, i, ah, al)
+            pos[i] += 1
