@@ -51,7 +51,7 @@ namespace {
 constexpr int kMaxLanes = GPHQ_DECODE_MAX_LANES;
 constexpr int kHeadDim = 128;
 constexpr int kPart = 2 + kHeadDim;  // one attention partial: max, sum, weighted V
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 32;  // attention blocks per (KV head, lane), at most
 constexpr int kMinChunk = 64;  // keys per attention block, at least
 constexpr int kMaxRotation = 4096;  // qwen3lm/hadamard.go:11
 constexpr int kMaxWidth = 16384;    // hidden and intermediate widths (LDS)
@@ -448,7 +448,9 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
 
 // The merge of attention's split partials (grid: q_heads, lanes; 128
 // threads, thread d owns dim d): weights exp(m_s - max) per split, then
-// ctx = sum_s w_s A_s / sum_s w_s l_s, splits in order.
+// ctx = sum_s w_s A_s / sum_s w_s l_s, splits in order. Every load is issued
+// up front (thread d reads dim d of each used split, 64 threads read the
+// maxima and sums), so the kernel waits for memory once.
 __global__ __launch_bounds__(128) void lm_attn_merge_kernel(const AttnArgs a, int group) {
     __shared__ float cw[kMaxSplits];
     __shared__ float linv;
@@ -457,6 +459,10 @@ __global__ __launch_bounds__(128) void lm_attn_merge_kernel(const AttnArgs a, in
     const int used = attn_used_splits(a.pos[lid] + 1, a.splits);
     const float *lp = a.part + (((size_t)lid * a.kvh + g) * a.splits * group + hh) * kPart;
     const size_t stride = (size_t)group * kPart;
+    const int d = threadIdx.x;
+    float v[kMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) v[s] = s < used ? lp[(size_t)s * stride + 2 + d] : 0.0f;
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
         const bool has = lane < used;
@@ -466,20 +472,13 @@ __global__ __launch_bounds__(128) void lm_attn_merge_kernel(const AttnArgs a, in
         for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
         const float c = has ? rescale(ms, M) : 0.0f;
         const float L = wave_sum(ls * c);
-        cw[lane] = c;
+        if (lane < kMaxSplits) cw[lane] = c;
         if (lane == 0) linv = 1.0f / L;
     }
     __syncthreads();
-    const int d = threadIdx.x;
-    const float *p = lp + 2 + d;
     float A = 0.0f;
-    for (int s0 = 0; s0 < used; s0 += 8) {
-        float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = s0 + i < used ? p[(size_t)(s0 + i) * stride] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) A = fmaf(cw[min(s0 + i, kMaxSplits - 1)], v[i], A);
-    }
+    for (int s = 0; s < kMaxSplits; ++s) A = fmaf(cw[s], v[s], A);
     a.ctx[(size_t)lid * a.qd + (size_t)h * kHeadDim + d] = A * linv;
 }
 
@@ -582,9 +581,12 @@ int launch_attend(int group, const AttnArgs &a, int lanes, hipStream_t st) {
     return GPHQ_ERR_UNSUPPORTED;
 }
 
+// Attention blocks per (KV head, lane): about 256 blocks in all, at most
+// kMaxSplits per head (measured on MI355X at contexts 512-4096 for 1, 4 and
+// 16 lanes: more splits add merge work faster than they add bandwidth).
 int attention_splits(const gphq_lm *lm, int lanes) {
     const int64_t work = lm->cfg.kv_heads * (int64_t)lanes;
-    return (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplits, 1024 / work));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplits, 256 / work));
 }
 
 // One projection GEMV of the step, single- or multi-lane.
