@@ -34,6 +34,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true", help="skip the config-2 int8 GEMM lines")
+    ap.add_argument("--no-gptq", action="store_true", help="skip the config-5 GPTQ int4 lines")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3/4b decode lines")
     ap.add_argument("--decode-fmt", choices=["q8b", "q8b_f32", "q8", "q4"], default="q8b",
                     help="layer weight format of the decode models (the reference's decode batch uses Q8B)")
@@ -125,6 +126,7 @@ def gemv_config1(args, torch, gphq, mode):
 
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, AMD published (POP/s)
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, AMD published
 
 
 def gemm_config2(args, torch, gphq, ms=(1, 16, 128, 512), rotations=6, steps=20):
@@ -188,6 +190,61 @@ def gemm_config2(args, torch, gphq, ms=(1, 16, 128, 512), rotations=6, steps=20)
         del ws
     for w in ws_list:
         w.close()
+    return out
+
+
+def gptq_config5(args, torch, gphq, ms=(1, 256), steps=20):
+    """Config 5: GPTQ int4 dequant-matmul at the Qwen3-8B shapes K=4096 -> N=12288 and
+    K=12288 -> N=4096 (gphq_mm, GPHQ_FMT_GPTQ4_G128: nibbles U[0,15] 8 per int32 along K,
+    fp16 group-128 scales |N(0,1)|*0.01, 4-bit zero points U[0,15]); activations fp32
+    N(0,1) converted to FP16 inside the call, fp32 accumulation. Each shape rotates
+    through distinct weight sets totalling > 256 MB."""
+    out = {}
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    for k, n in ((4096, 12288), (12288, 4096)):
+        per = n * k // 2 + n * (k // 128) * 3
+        rotations = (320 << 20) // per + 1
+        sets = []
+        for _ in range(rotations):
+            codes = torch.randint(0, 2 ** 31 - 1, (n, k // 8), dtype=torch.int32, device="cuda", generator=g)
+            scales = (torch.randn((n, k // 128), device="cuda", generator=g).abs() * 0.01).half()
+            zeros = torch.randint(0, 16, (n, k // 128), dtype=torch.uint8, device="cuda", generator=g)
+            sets.append((codes, scales, zeros))
+        for m in ms:
+            x = torch.randn((m, k), device="cuda", generator=g)
+            y = torch.empty((m, n), device="cuda")
+            work = torch.empty(gphq.mm_workspace_bytes(m, k), dtype=torch.uint8, device="cuda")
+            for c, sc, z in sets:
+                gphq.mm(gphq.FMT_GPTQ4_G128, c, sc, x, y, m, k, n, work, zeros=z, stream=stream)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                cs = torch.cuda.current_stream()
+                for c, sc, z in sets:
+                    gphq.mm(gphq.FMT_GPTQ4_G128, c, sc, x, y, m, k, n, work, zeros=z, stream=cs)
+            graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(steps):
+                graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (steps * rotations)
+            nbytes = per + 4 * m * k + 4 * m * n
+            flops = 2.0 * m * n * k
+            out[f"K{k}_N{n}_M{m}"] = {
+                "us": round(us, 3),
+                "gbs": round(nbytes / us / 1e3, 1),
+                "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                "tflops": round(flops / us / 1e6, 2),
+                "fp16_frac": round(flops / us / 1e6 / FP16_PEAK_TFLOPS, 4),
+                "rotations": rotations,
+            }
+        del sets
+        torch.cuda.empty_cache()
     return out
 
 
@@ -374,6 +431,7 @@ def main():
     single = gemv_config1(args, torch, gphq, "graph") if args.mode == "batch" else None
     value = r["value_gbs"]
     gemm = None if args.no_gemm else gemm_config2(args, torch, gphq)
+    gptq = None if args.no_gptq else gptq_config5(args, torch, gphq)
     decode = None if args.no_decode else decode_benchmarks(args, torch, gphq)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     # The persistent GEMV's template shape for config 1 (gemv.hip persistent_shape):
@@ -421,6 +479,7 @@ def main():
             "mode": "one gphq_gemv launch per 4096x4096 GEMV, HIP graph of 32 launches",
         },
         "gemm_config2": gemm,
+        "gptq_config5": gptq,
         "decode_ms_per_token": (decode or {}).get("config4b_1", {}).get("ms_per_step"),
         "decode": decode,
         "check": {"rel_l2_vs_float64": r["rel_l2"]},

@@ -29,6 +29,7 @@
 namespace gphq {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxBatch = 32;
 
@@ -453,6 +454,169 @@ __global__ __launch_bounds__(64 * WPB) void gemvp_kernel(const GemvBatch<MAXB> b
             }
         }
     }
+}
+
+// GPTQ int4 GEMV (GPHQ_FMT_GPTQ4_G128 at one activation row): codes int32
+// [N][K/8] (nibble i of word j is k = 8j + i), FP16 scales [N][K/128], 4-bit
+// zero points u8 [N][K/128]; y[n] = sum_g s_g * sum_{k in g} (q - z_g) *
+// half(x[k]), fp32 arithmetic, weights not rounded (the mm path rounds each
+// dequantized weight to FP16 first; this path is within 1e-4 relative of the
+// float64 value with un-rounded weights, the mm path within about 2^-11).
+//
+// Persistent like gemvp_kernel: a wavefront holds its K slice of half(x) in
+// registers (NS steps of 2048 values; lane l takes values 32l..32l+31 of a
+// step, one 16-byte load of codes) and walks row groups. Per code word the
+// low and high nibbles of its bytes are masked out and placed under the FP16
+// exponent of 1024 by v_perm_b32, giving pairs (1024 + q), and
+// v_dot2_f32_f16 adds their products with the matching half(x) pairs in fp32
+// (exact products). Per 128-value group (four lanes) the lane's part is
+// s * (dot - (1024 + z) * sum(half(x))), which removes the bias and the zero
+// point in one step: about one VALU operation per weight.
+template <int NS, int RW, int SK, int WPB>
+__global__ __launch_bounds__(64 * WPB) void gemv_gptq_kernel(const uint32_t *__restrict__ codes,
+                                                             const uint16_t *__restrict__ scales,
+                                                             const uint8_t *__restrict__ zeros,
+                                                             const float *__restrict__ x, float *__restrict__ y, int K,
+                                                             int N, int iters) {
+    static_assert(WPB % SK == 0, "wave groups of SK waves");
+    constexpr int WG = WPB / SK;
+    __shared__ float part[2][WG][RW][SK];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wg = wv / SK, ks = wv - wg * SK;
+    const int kbase = ks * (NS * 2048) + lane * 32;
+    const int KG = K >> 7;  // groups per row
+    // half(x) pairs in the nibble order of one code word: (x0,x2), (x4,x6), (x1,x3), (x5,x7).
+    f16x2 xh[NS][4][4];
+    float sx[NS];
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float4 a = *(const float4 *)(x + kbase + st * 2048 + w * 8);
+            const float4 b = *(const float4 *)(x + kbase + st * 2048 + w * 8 + 4);
+            const _Float16 h[8] = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                                   (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+            xh[st][w][0] = f16x2{h[0], h[2]};
+            xh[st][w][1] = f16x2{h[4], h[6]};
+            xh[st][w][2] = f16x2{h[1], h[3]};
+            xh[st][w][3] = f16x2{h[5], h[7]};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sum += (float)h[i];
+        }
+        sx[st] = sum;
+    }
+    const int groups = (N + RW - 1) / RW;
+    const int stride = gridDim.x * WG;
+    int g = blockIdx.x * WG + wg;
+    for (int it = 0; it < iters; ++it, g += stride) {
+        const bool valid = g < groups;
+        if constexpr (SK == 1) {
+            if (!valid) break;
+        }
+        const int row0 = g * RW;
+        float acc[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+        if (valid) {
+            u32x4 w[NS][RW];
+            uint16_t sc[NS][RW];
+            uint8_t zp[NS][RW];
+#pragma unroll
+            for (int st = 0; st < NS; ++st)
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    const size_t row = (size_t)min(row0 + r, N - 1);
+                    const int gi = (kbase + st * 2048) >> 7;
+                    sc[st][r] = scales[row * KG + gi];
+                    zp[st][r] = zeros[row * KG + gi];
+                    w[st][r] = __builtin_nontemporal_load(
+                        (const u32x4 *)(codes + row * (size_t)(K >> 3) + ((kbase + st * 2048) >> 3)));
+                }
+#pragma unroll
+            for (int st = 0; st < NS; ++st)
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    const uint32_t ww[4] = {w[st][r].x, w[st][r].y, w[st][r].z, w[st][r].w};
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t lo = ww[q] & 0x0F0F0F0Fu, hi = (ww[q] >> 4) & 0x0F0F0F0Fu;
+                        const f16x2 p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u));
+                        const f16x2 p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u));
+                        const f16x2 p2 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u));
+                        const f16x2 p3 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u));
+                        dot = __builtin_amdgcn_fdot2(p0, xh[st][q][0], dot, false);
+                        dot = __builtin_amdgcn_fdot2(p1, xh[st][q][1], dot, false);
+                        dot = __builtin_amdgcn_fdot2(p2, xh[st][q][2], dot, false);
+                        dot = __builtin_amdgcn_fdot2(p3, xh[st][q][3], dot, false);
+                    }
+                    const float sg = half_bits_to_float(sc[st][r]);
+                    const float zb = 1024.0f + (float)(zp[st][r] & 15);
+                    acc[r] = fmaf(sg, fmaf(-zb, sx[st], dot), acc[r]);
+                }
+        }
+        float t[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) t[r] = wave_sum(acc[r]);
+        if constexpr (SK == 1) {
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < RW; ++r)
+                    if (row0 + r < N) y[row0 + r] = t[r];
+            }
+        } else {
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < RW; ++r) part[it & 1][wg][r][ks] = t[r];
+            }
+            __syncthreads();
+            if (ks == 0 && lane == 0 && valid) {
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    float v = part[it & 1][wg][r][0];
+#pragma unroll
+                    for (int i = 1; i < SK; ++i) v += part[it & 1][wg][r][i];
+                    if (row0 + r < N) y[row0 + r] = v;
+                }
+            }
+        }
+    }
+}
+
+static int device_cus();
+
+template <int NS, int RW, int SK, int WPB>
+static int go_gptq(const uint32_t *codes, const uint16_t *scales, const uint8_t *zeros, const float *x, float *y,
+                   int K, int N, int bpc, hipStream_t stream) {
+    constexpr int WG = WPB / SK;
+    const long groups = (N + RW - 1) / RW;
+    const long blocks = std::max(1L, std::min((groups + WG - 1) / WG, (long)device_cus() * bpc));
+    const int iters = (int)((groups + blocks * WG - 1) / (blocks * WG));
+    hipLaunchKernelGGL((gemv_gptq_kernel<NS, RW, SK, WPB>), dim3((unsigned)blocks), dim3(64 * WPB), 0, stream, codes,
+                       scales, zeros, x, y, K, N, iters);
+    return launch_status();
+}
+
+// One GPTQ4_G128 row (gphq_mm with m = 1) when K is a multiple of 2048 up to
+// 16 * 2048 and x is 16-byte aligned; GPHQ_ERR_UNSUPPORTED otherwise (the
+// caller then uses the mm kernel).
+int gemv_gptq_launch(const void *codes, const void *scales, const uint8_t *zeros, const float *x, float *y, int K,
+                     int N, hipStream_t stream) {
+    if (K % 2048 || (uintptr_t)x % 16) return GPHQ_ERR_UNSUPPORTED;
+    const uint32_t *c = (const uint32_t *)codes;
+    const uint16_t *s = (const uint16_t *)scales;
+    // Launch shapes from a sweep on MI355X at the config-5 shapes.
+    switch (K / 2048) {
+    case 1: return go_gptq<1, 4, 1, 4>(c, s, zeros, x, y, K, N, 2, stream);
+    case 2: return go_gptq<1, 4, 2, 8>(c, s, zeros, x, y, K, N, 2, stream);
+    case 3: return go_gptq<1, 2, 3, 6>(c, s, zeros, x, y, K, N, 2, stream);
+    case 4: return go_gptq<1, 2, 4, 8>(c, s, zeros, x, y, K, N, 1, stream);
+    case 6: return go_gptq<1, 2, 6, 12>(c, s, zeros, x, y, K, N, 1, stream);
+    case 8: return go_gptq<1, 2, 8, 16>(c, s, zeros, x, y, K, N, 1, stream);
+    }
+    return GPHQ_ERR_UNSUPPORTED;
 }
 
 // Any K, any alignment (Q8 only): one wavefront per row, lanes stride through

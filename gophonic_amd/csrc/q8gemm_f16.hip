@@ -24,6 +24,8 @@ struct F16GemmArgs {
     int gridM, gridN;
 };
 int f16gemm_launch(int wf, int epi, F16GemmArgs a, hipStream_t stream);
+int gemv_gptq_launch(const void *codes, const void *scales, const uint8_t *zeros, const float *x, float *y, int K,
+                     int N, hipStream_t stream);
 int f16_act_pack(const float *x, long stride, int rows, int K, int kt, int mode, int k0, int k1, _Float16 *act,
                  float *rowScale, float *rowInv, hipStream_t stream);
 int f16_pack_tiles(const uint16_t *src, uint16_t *dst, int rows, int K, int row0, int kt, hipStream_t stream);
@@ -473,6 +475,11 @@ int gphq_mm(int fmt, const void *codes, const void *scales, const uint8_t *zeros
     if (k == 0) return fill_zero_columns(y, (long)n, (int)m, 0, (int)n, s);
     if (!codes || !x || !work || (uintptr_t)codes % 16 != 0 || (uintptr_t)work % 16 != 0) return GPHQ_ERR_DIMENSIONS;
     if (fmt == GPHQ_FMT_GPTQ4_G128 && !zeros) return GPHQ_ERR_DIMENSIONS;
+    if (fmt == GPHQ_FMT_GPTQ4_G128 && m == 1) {
+        // One activation row: the GEMV kernel (same arithmetic, fp32 sums).
+        const int st = gemv_gptq_launch(codes, scales, zeros, x, y, (int)k, (int)n, s);
+        if (st != GPHQ_ERR_UNSUPPORTED) return st;
+    }
     const int64_t kt = ceil_div(k, 64);
     GPHQ_TRY(f16_act_pack(x, (long)k, (int)m, (int)k, (int)kt, 1, 0, (int)k, (_Float16 *)work, nullptr, nullptr, s));
     F16GemmArgs a{};
