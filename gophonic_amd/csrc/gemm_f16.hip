@@ -235,6 +235,186 @@ __global__ __launch_bounds__(64 * WM * WN * SK) void f16gemm_kernel(const F16Gem
     }
 }
 
+// ---- LDS-shared B tiles (qwen3lm row formats, M > 64) -------------------------
+// Raw codes of one B fragment (16 values of row n at k = kt*64 + g*16): the
+// code bytes (GPTQ: two words), and the scale bits (low half) and GPTQ zero
+// point (bits 16..23).
+struct RawB {
+    u32x4 w;
+    uint32_t sz;
+};
+
+template <int WF>
+__device__ __forceinline__ RawB load_raw(const F16GemmArgs &a, int n, int kt, int g) {
+    const int k = kt * 64 + g * 16;
+    RawB r{u32x4{0, 0, 0, 0}, 0};
+    if (k >= a.K) return r;
+    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW) {
+        r.w = __builtin_nontemporal_load((const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k));
+        if constexpr (WF == W_Q8B_ROW) r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
+    } else if constexpr (WF == W_Q4_ROW) {
+        r.w = __builtin_nontemporal_load((const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16));
+        r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
+    } else {  // W_GPTQ_ROW
+        const uint32_t *p = (const uint32_t *)a.B + (size_t)n * (a.K >> 3) + (k >> 3);
+        r.w.x = __builtin_nontemporal_load(p);
+        r.w.y = __builtin_nontemporal_load(p + 1);
+        const size_t gi = (size_t)n * (a.K >> 7) + (k >> 7);
+        r.sz = ((const uint16_t *)a.bScale)[gi] | ((uint32_t)(a.bZero[gi] & 15) << 16);
+    }
+    return r;
+}
+
+// The same FP16 values as load_b: Q8 half(code); Q8B half(code) * d; Q4
+// (half(nib) - 8) * d; GPTQ (half(nib) - half(z)) * s, each rounded to half.
+template <int WF>
+__device__ __forceinline__ void dequant(const RawB &r, int g, f16x8 &lo, f16x8 &hi) {
+    const uint32_t ww[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
+    if constexpr (WF == W_Q8_ROW) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3);
+    } else if constexpr (WF == W_Q8B_ROW) {
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3) * d;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3) * d;
+    } else if constexpr (WF == W_Q4_ROW) {
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
+        const int sh = (g & 1) * 4;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            lo[i] = ((_Float16)(int)((ww[i >> 2] >> (8 * (i & 3) + sh)) & 15) - (_Float16)8.0f) * d;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            hi[i] = ((_Float16)(int)((ww[2 + (i >> 2)] >> (8 * (i & 3) + sh)) & 15) - (_Float16)8.0f) * d;
+    } else {
+        const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
+        const _Float16 z = (_Float16)(int)(r.sz >> 16);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lo[i] = ((_Float16)(int)((ww[0] >> (4 * i)) & 15) - z) * s;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hi[i] = ((_Float16)(int)((ww[1] >> (4 * i)) & 15) - z) * s;
+    }
+}
+
+// Block tile (32*WTM) x (32*WTN), four wavefronts as 2 x 2, each
+// (16*WTM) x (16*WTN) of the output. Per 64-deep K step the block's threads
+// dequantize the B tile once into LDS in MFMA fragment order (tile j, lane
+// slot g*16 + n%16, 16 values), double-buffered; the raw codes of step kt+1
+// are loaded before the MFMAs of step kt run and written to the other buffer
+// after them, with one barrier per step. A fragments come straight from the
+// FP16 tile layout (two 16-byte loads per lane and tile), one step ahead.
+template <int WF, int EPI, int WTM, int WTN>
+__global__ __launch_bounds__(256) void f16gemm_lds_kernel(const F16GemmArgs a) {
+    constexpr int BN16 = 2 * WTN;                      // 16-row B tiles per block
+    constexpr int PAIRS = BN16 * 64 / 256;             // (row, lane group) pairs per thread and step
+    __shared__ f16x8 bs[2][BN16][64][2];
+    const int G = a.gridM * a.gridN;
+    const int b = blockIdx.x;
+    int logical = b;
+    if (G % 8 == 0) logical = (b % 8) * (G / 8) + b / 8;  // blocks of one XCD take neighbouring tiles
+    const int bm = logical % a.gridM, bn = logical / a.gridM;
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int wm = wv >> 1, wn = wv & 1;
+    const int mt0 = (bm * 2 + wm) * WTM;
+    const int nt0 = a.tileN0 + bn * BN16;
+    const int MT = (a.M + 15) >> 4;
+    const int KT = a.KT;
+    size_t aoff[WTM];
+#pragma unroll
+    for (int i = 0; i < WTM; ++i) aoff[i] = (size_t)min(mt0 + i, MT - 1) * KT * 1024 + (size_t)lane * 16;
+    // Loader assignment: pair p -> tile p / 64, lane slot p % 64 (row n = tile*16 + slot % 16, group slot / 16).
+    int pn[PAIRS], pg[PAIRS], pt[PAIRS], ps[PAIRS];
+#pragma unroll
+    for (int q = 0; q < PAIRS; ++q) {
+        const int p = threadIdx.x + 256 * q;
+        pt[q] = p >> 6;
+        ps[q] = p & 63;
+        pg[q] = ps[q] >> 4;
+        pn[q] = min((nt0 + pt[q]) * 16 + (ps[q] & 15), a.N - 1);
+    }
+    auto load_a = [&](int kt, f16x8 (&fa)[WTM][2]) {
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+            const f16x8 *p = (const f16x8 *)(a.A + aoff[i] + (size_t)kt * 1024);
+            fa[i][0] = p[0];
+            fa[i][1] = p[1];
+        }
+    };
+    f32x4 acc[WTM][WTN];
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    RawB raw[PAIRS];
+#pragma unroll
+    for (int q = 0; q < PAIRS; ++q) raw[q] = load_raw<WF>(a, pn[q], 0, pg[q]);
+    f16x8 fa[WTM][2], fn[WTM][2];
+    load_a(0, fa);
+#pragma unroll
+    for (int q = 0; q < PAIRS; ++q) dequant<WF>(raw[q], pg[q], bs[0][pt[q]][ps[q]][0], bs[0][pt[q]][ps[q]][1]);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < KT;
+        if (more) {
+#pragma unroll
+            for (int q = 0; q < PAIRS; ++q) raw[q] = load_raw<WF>(a, pn[q], kt + 1, pg[q]);
+            load_a(kt + 1, fn);
+        }
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            const f16x8 b0 = bs[cur][wn * WTN + j][lane][0], b1 = bs[cur][wn * WTN + j][lane][1];
+#pragma unroll
+            for (int i = 0; i < WTM; ++i) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i][0], b0, acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i][1], b1, acc[i][j], 0, 0, 0);
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int q = 0; q < PAIRS; ++q)
+                dequant<WF>(raw[q], pg[q], bs[cur ^ 1][pt[q]][ps[q]][0], bs[cur ^ 1][pt[q]][ps[q]][1]);
+#pragma unroll
+            for (int i = 0; i < WTM; ++i) fa[i][0] = fn[i][0], fa[i][1] = fn[i][1];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+        const int col = (nt0 + wn * WTN + j) * 16 + (lane & 15);
+        if (col < a.c0 || col >= a.c1) continue;
+        float cs = 1.0f;
+        if constexpr (EPI == EPI_ROWSCALE) cs = a.colScale[col];
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
+                if (row < a.M) {
+                    float v = acc[i][j][e];
+                    if constexpr (EPI == EPI_ROWSCALE) v = __fmul_rn(v, cs);
+                    a.dst[(size_t)row * a.stride + col] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int WF, int EPI, int WTM, int WTN>
+static int launch_f16gemm_lds(F16GemmArgs a, hipStream_t stream) {
+    const int tiles = (a.c1 + 15) / 16 - a.tileN0;
+    a.gridN = (tiles + 2 * WTN - 1) / (2 * WTN);
+    a.gridM = (a.M + 32 * WTM - 1) / (32 * WTM);
+    hipLaunchKernelGGL((f16gemm_lds_kernel<WF, EPI, WTM, WTN>), dim3((unsigned)(a.gridM * a.gridN)), dim3(256), 0,
+                       stream, a);
+    return launch_status();
+}
+
 template <int WF, int EPI, int TM, int TN, int WM, int WN, int SK, int U>
 static int launch_f16gemm(F16GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
@@ -249,6 +429,12 @@ template <int WF, int EPI>
 static int launch_by_m(const F16GemmArgs &a, hipStream_t stream) {
     if (a.M <= 16) return launch_f16gemm<WF, EPI, 1, 2, 1, 2, 4, 2>(a, stream);
     if (a.M <= 64) return launch_f16gemm<WF, EPI, 4, 1, 1, 2, 4, 2>(a, stream);
+    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q4_ROW || WF == W_GPTQ_ROW) {
+        // 128 x 128 block tiles when they fill the chip, else 128 x 64.
+        const long big = (long)((a.M + 127) / 128) * (((a.c1 + 15) / 16 - a.tileN0 + 7) / 8);
+        if (big >= 256) return launch_f16gemm_lds<WF, EPI, 4, 4>(a, stream);
+        return launch_f16gemm_lds<WF, EPI, 4, 2>(a, stream);
+    }
     return launch_f16gemm<WF, EPI, 4, 2, 2, 2, 1, 1>(a, stream);
 }
 
