@@ -59,6 +59,22 @@ const char *gphq_error_string(int status) {
         return "qwen3: non-finite batched hidden state";
     case GPHQ_ERR_MODEL_INCOMPLETE:
         return "qwen3: batched token decode requires a loaded language-model head; call LoadHead first";
+    case GPHQ_ERR_WORKSPACE:
+        return "qwen3: nil or foreign workspace";
+    case GPHQ_ERR_KEEP_RANGE:
+        return "qwen3: keep outside the stored tokens";
+    case GPHQ_ERR_PREFIX_CAPACITY:
+        return "qwen3: tokens exceed prefix capacity";
+    case GPHQ_ERR_EMPTY_SEQUENCE:
+        return "qwen3: empty token sequence";
+    case GPHQ_ERR_CONTEXT:
+        return "qwen3: tokens exceed the Qwen3 context";
+    case GPHQ_ERR_DEST_WIDTH:
+        return "qwen3: destination width does not match the hidden size";
+    case GPHQ_ERR_TOKEN_VOCAB:
+        return "qwen3: token is outside vocabulary";
+    case GPHQ_ERR_NON_FINITE_STATE:
+        return "qwen3: non-finite hidden state";
     }
     return "gphq: unknown status";
 }

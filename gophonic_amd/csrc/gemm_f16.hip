@@ -10,6 +10,10 @@
 //    row scale.
 //  * GPTQ int4 with group-128 FP16 scales and 4-bit zero points (8 codes per
 //    int32): (half(nib) - half(z)) * s rounded to half.
+//  * the qwen3lm batched pass's projections (mm_qkv / mm_o / mm_gateup /
+//    mm_down, gpu.metal:994-1025): the same tiles with the residual-add and
+//    SwiGLU epilogues (gpu.metal:897-927), and Q8B with fp32 block scales
+//    (half(code * d), one rounding).
 //
 // Fragments: lane l of a 16x64 K step holds row (l % 16), columns
 // (l / 16) * 16 .. +16 of both operands (16 FP16 values = two 8-value MFMA
@@ -34,9 +38,13 @@ enum WFmt {
     W_Q8B_ROW = 3,    // qwen3lm Q8B codes [N][K], f16 scales [N][K/32]
     W_Q4_ROW = 4,     // qwen3lm Q4 codes [N][K/2], f16 scales [N][K/32]
     W_GPTQ_ROW = 5,   // int32 [N][K/8] (nibble i of word j = k 8j+i), f16 scales and u8 zeros [N][K/128]
+    W_Q8BF_ROW = 6,   // qwen3lm Q8B codes [N][K] with fp32 scales [N][K/32]
 };
 
-enum Epi { EPI_PANELS = 0, EPI_PLAIN = 1, EPI_ROWSCALE = 2 };
+// EPI_ADD: dst += v (the residual stream). EPI_SWIGLU: columns 2i (gate) and
+// 2i+1 (up) give dst[row][i] = g / (1 + exp(-g)) * u. Both multiply by
+// colScale[col] first when it is set (Q8 row scales).
+enum Epi { EPI_PANELS = 0, EPI_PLAIN = 1, EPI_ROWSCALE = 2, EPI_ADD = 3, EPI_SWIGLU = 4 };
 
 struct F16GemmArgs {
     const _Float16 *A;   // activations, FP16 tile layout, MT x KT groups
@@ -53,6 +61,15 @@ struct F16GemmArgs {
 };
 
 __device__ __forceinline__ _Float16 i8h(uint32_t v, int i) { return (_Float16)(int)((int32_t)(v << (24 - 8 * i)) >> 24); }
+__device__ __forceinline__ float i8f(uint32_t v, int i) { return (float)((int32_t)(v << (24 - 8 * i)) >> 24); }
+// half of the fp32 value x. The asm barrier keeps a product feeding x a
+// separate fp32 multiply: without it the backend fuses multiply and convert
+// (v_fma_mix), which rounds the exact product to half once instead of the
+// fp32 product.
+__device__ __forceinline__ _Float16 f32_to_half(float x) {
+    asm volatile("" : "+v"(x));
+    return (_Float16)x;
+}
 
 // B fragment: 16 FP16 weights of row `n` (clamped in range), K step kt, lane
 // group g (values k = kt*64 + g*16 + 0..15), decoded per format.
@@ -89,6 +106,18 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
 #pragma unroll
             for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3) * d;
         }
+    } else if constexpr (WF == W_Q8BF_ROW) {
+        u32x4 w = u32x4{0, 0, 0, 0};
+        float d = 0.0f;
+        if (k < a.K) {
+            w = __builtin_nontemporal_load((const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k));
+            d = ((const float *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
+        }
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lo[i] = f32_to_half(i8f(ww[i >> 2], i & 3) * d);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hi[i] = f32_to_half(i8f(ww[2 + (i >> 2)], i & 3) * d);
     } else if constexpr (WF == W_Q4_ROW) {
         // Block (k / 32) is 16 bytes: value j in the low nibble of byte j,
         // value j + 16 in the high nibble; this lane needs half (k / 16) % 2.
@@ -125,6 +154,41 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
         for (int i = 0; i < 8; ++i) lo[i] = ((_Float16)(int)((w0 >> (4 * i)) & 15) - z) * s;
 #pragma unroll
         for (int i = 0; i < 8; ++i) hi[i] = ((_Float16)(int)((w1 >> (4 * i)) & 15) - z) * s;
+    }
+}
+
+// Epilogue of one lane's part of a 16x16 accumulator tile: rows row0 ..
+// row0 + 3 of column col. Columns outside [c0, c1) and rows past M are not
+// written. Every lane of the wavefront calls it (EPI_SWIGLU exchanges the
+// gate and up values of neighbouring lanes).
+template <int EPI>
+__device__ __forceinline__ void epilogue(const F16GemmArgs &a, const f32x4 &acc, int row0, int col) {
+    const bool colOk = col >= a.c0 && col < a.c1;
+    float cs = 1.0f;
+    if constexpr (EPI == EPI_PANELS || EPI == EPI_ROWSCALE) {
+        if (colOk) cs = a.colScale[col];
+    }
+    if constexpr (EPI == EPI_ADD || EPI == EPI_SWIGLU) {
+        if (colOk && a.colScale) cs = a.colScale[col];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int row = row0 + e;
+        float v = acc[e];
+        if constexpr (EPI == EPI_SWIGLU) {
+            if (a.colScale) v = __fmul_rn(v, cs);
+            const float u = __shfl_xor(v, 1);
+            if (colOk && !(col & 1) && row < a.M) a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
+        } else if (colOk && row < a.M) {
+            float *p = a.dst + (size_t)row * a.stride + col;
+            if constexpr (EPI == EPI_PANELS) v = __fmul_rn(__fmul_rn(v, cs), a.rowInv[row]);
+            if constexpr (EPI == EPI_ROWSCALE) v = __fmul_rn(v, cs);
+            if constexpr (EPI == EPI_ADD) {
+                if (a.colScale) v = __fmul_rn(v, cs);
+                v = *p + v;
+            }
+            *p = v;
+        }
     }
 }
 
@@ -214,31 +278,16 @@ __global__ __launch_bounds__(64 * WM * WN * SK) void f16gemm_kernel(const F16Gem
     }
 
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int col = (nt0 + j) * 16 + (lane & 15);
-        if (col < a.c0 || col >= a.c1) continue;
-        float cs = 1.0f;
-        if constexpr (EPI != EPI_PLAIN) cs = a.colScale[col];
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
-                if (row < a.M) {
-                    float v = acc[i][j][e];
-                    if constexpr (EPI == EPI_PANELS) v = __fmul_rn(__fmul_rn(v, cs), a.rowInv[row]);
-                    if constexpr (EPI == EPI_ROWSCALE) v = __fmul_rn(v, cs);
-                    a.dst[(size_t)row * a.stride + col] = v;
-                }
-            }
-        }
-    }
+        for (int i = 0; i < TM; ++i)
+            epilogue<EPI>(a, acc[i][j], (mt0 + i) * 16 + 4 * (lane >> 4), (nt0 + j) * 16 + (lane & 15));
 }
 
 // ---- LDS-shared B tiles (qwen3lm row formats, M > 64) -------------------------
 // Raw codes of one B fragment (16 values of row n at k = kt*64 + g*16): the
-// code bytes (GPTQ: two words), and the scale bits (low half) and GPTQ zero
-// point (bits 16..23).
+// code bytes (GPTQ: two words), and the scale bits (FP16 in the low half, or
+// all 32 bits of an fp32 scale) and GPTQ zero point (bits 16..23).
 struct RawB {
     u32x4 w;
     uint32_t sz;
@@ -249,9 +298,10 @@ __device__ __forceinline__ RawB load_raw(const F16GemmArgs &a, int n, int kt, in
     const int k = kt * 64 + g * 16;
     RawB r{u32x4{0, 0, 0, 0}, 0};
     if (k >= a.K) return r;
-    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW) {
+    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q8BF_ROW) {
         r.w = __builtin_nontemporal_load((const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k));
         if constexpr (WF == W_Q8B_ROW) r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
+        if constexpr (WF == W_Q8BF_ROW) r.sz = ((const uint32_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
     } else if constexpr (WF == W_Q4_ROW) {
         r.w = __builtin_nontemporal_load((const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16));
         r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
@@ -265,8 +315,9 @@ __device__ __forceinline__ RawB load_raw(const F16GemmArgs &a, int n, int kt, in
     return r;
 }
 
-// The same FP16 values as load_b: Q8 half(code); Q8B half(code) * d; Q4
-// (half(nib) - 8) * d; GPTQ (half(nib) - half(z)) * s, each rounded to half.
+// The same FP16 values as load_b: Q8 half(code); Q8B half(code) * d; Q8B
+// with fp32 scales half(code * d); Q4 (half(nib) - 8) * d; GPTQ
+// (half(nib) - half(z)) * s, each rounded to half.
 template <int WF>
 __device__ __forceinline__ void dequant(const RawB &r, int g, f16x8 &lo, f16x8 &hi) {
     const uint32_t ww[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
@@ -281,6 +332,12 @@ __device__ __forceinline__ void dequant(const RawB &r, int g, f16x8 &lo, f16x8 &
         for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3) * d;
 #pragma unroll
         for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3) * d;
+    } else if constexpr (WF == W_Q8BF_ROW) {
+        const float d = __builtin_bit_cast(float, r.sz);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lo[i] = f32_to_half(i8f(ww[i >> 2], i & 3) * d);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hi[i] = f32_to_half(i8f(ww[2 + (i >> 2)], i & 3) * d);
     } else if constexpr (WF == W_Q4_ROW) {
         const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
         const int sh = (g & 1) * 4;
@@ -385,24 +442,10 @@ __global__ __launch_bounds__(256) void f16gemm_lds_kernel(const F16GemmArgs a) {
         __syncthreads();
     }
 #pragma unroll
-    for (int j = 0; j < WTN; ++j) {
-        const int col = (nt0 + wn * WTN + j) * 16 + (lane & 15);
-        if (col < a.c0 || col >= a.c1) continue;
-        float cs = 1.0f;
-        if constexpr (EPI == EPI_ROWSCALE) cs = a.colScale[col];
+    for (int j = 0; j < WTN; ++j)
 #pragma unroll
-        for (int i = 0; i < WTM; ++i) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
-                if (row < a.M) {
-                    float v = acc[i][j][e];
-                    if constexpr (EPI == EPI_ROWSCALE) v = __fmul_rn(v, cs);
-                    a.dst[(size_t)row * a.stride + col] = v;
-                }
-            }
-        }
-    }
+        for (int i = 0; i < WTM; ++i)
+            epilogue<EPI>(a, acc[i][j], (mt0 + i) * 16 + 4 * (lane >> 4), (nt0 + wn * WTN + j) * 16 + (lane & 15));
 }
 
 template <int WF, int EPI, int WTM, int WTN>
@@ -429,7 +472,7 @@ template <int WF, int EPI>
 static int launch_by_m(const F16GemmArgs &a, hipStream_t stream) {
     if (a.M <= 16) return launch_f16gemm<WF, EPI, 1, 2, 1, 2, 4, 2>(a, stream);
     if (a.M <= 64) return launch_f16gemm<WF, EPI, 4, 1, 1, 2, 4, 2>(a, stream);
-    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q4_ROW || WF == W_GPTQ_ROW) {
+    if constexpr (WF != W_I8_TILE && WF != W_F16_TILE) {
         // 128 x 128 block tiles when they fill the chip, else 128 x 64.
         const long big = (long)((a.M + 127) / 128) * (((a.c1 + 15) / 16 - a.tileN0 + 7) / 8);
         if (big >= 256) return launch_f16gemm_lds<WF, EPI, 4, 4>(a, stream);
@@ -451,6 +494,15 @@ int f16gemm_launch(int wf, int epi, F16GemmArgs a, hipStream_t stream) {
     GPHQ_F16_CASE(W_Q8B_ROW, EPI_PLAIN)
     GPHQ_F16_CASE(W_Q4_ROW, EPI_PLAIN)
     GPHQ_F16_CASE(W_GPTQ_ROW, EPI_PLAIN)
+    GPHQ_F16_CASE(W_Q8BF_ROW, EPI_PLAIN)
+    GPHQ_F16_CASE(W_Q8_ROW, EPI_ADD)
+    GPHQ_F16_CASE(W_Q8B_ROW, EPI_ADD)
+    GPHQ_F16_CASE(W_Q8BF_ROW, EPI_ADD)
+    GPHQ_F16_CASE(W_Q4_ROW, EPI_ADD)
+    GPHQ_F16_CASE(W_Q8_ROW, EPI_SWIGLU)
+    GPHQ_F16_CASE(W_Q8B_ROW, EPI_SWIGLU)
+    GPHQ_F16_CASE(W_Q8BF_ROW, EPI_SWIGLU)
+    GPHQ_F16_CASE(W_Q4_ROW, EPI_SWIGLU)
 #undef GPHQ_F16_CASE
     return GPHQ_ERR_UNSUPPORTED;
 }
@@ -472,17 +524,31 @@ __device__ __forceinline__ void f16_row_scale(float m, float &scale, float &inv)
 // One block per row. mode 0: q8gemm Workspace.Pack (power-of-two row scale from
 // MaxAbs, then f16(x * scale)); mode 1: qwen3lm mm activations, half(x);
 // mode 2: PackRange with the row scales already on the device, converting only
-// columns [k0, k1) (and the K padding when k1 == K). Writes the FP16 tile
-// layout; modes 0 and 1 convert whole rows and zero the K padding.
+// columns [k0, k1) (and the K padding when k1 == K); mode 3: the qwen3lm
+// PRO_NORM prologue (gpu.metal:785-796, 825-826), half(x * f) with
+// f = 1/sqrt(sum(x^2)/K + eps). Writes the FP16 tile layout; modes 0, 1 and 3
+// convert whole rows and zero the K padding.
 __global__ __launch_bounds__(256) void f16_act_pack_kernel(const float *__restrict__ x, long stride, int K, int kt,
-                                                           int mode, int k0, int k1, _Float16 *__restrict__ act,
-                                                           float *__restrict__ rowScale, float *__restrict__ rowInv) {
+                                                           int mode, int k0, int k1, float eps,
+                                                           _Float16 *__restrict__ act, float *__restrict__ rowScale,
+                                                           float *__restrict__ rowInv) {
     __shared__ float smax[4];
     __shared__ int snan[4];
     const int row = blockIdx.x;
     const float *xr = x + (size_t)row * stride;
     float scale = 1.0f, inv = 1.0f;
-    if (mode == 0) {
+    if (mode == 3) {
+        float ss = 0.0f;
+        for (int k = 4 * (int)threadIdx.x; k < K; k += 1024) {
+            const float4 v = *(const float4 *)(xr + k);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        const float t = (smax[0] + smax[1]) + (smax[2] + smax[3]);
+        scale = 1.0f / sqrtf(t / (float)K + eps);
+    } else if (mode == 0) {
         float m = 0.0f;
         int nan = 0;
         constexpr int UNR = 8;
@@ -550,9 +616,57 @@ __global__ __launch_bounds__(256) void f16_act_pack_kernel(const float *__restri
 int f16_act_pack(const float *x, long stride, int rows, int K, int kt, int mode, int k0, int k1, _Float16 *act,
                  float *rowScale, float *rowInv, hipStream_t stream) {
     if (rows == 0) return GPHQ_OK;
-    hipLaunchKernelGGL(f16_act_pack_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, mode, k0, k1, act,
-                       rowScale, rowInv);
+    hipLaunchKernelGGL(f16_act_pack_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, mode, k0, k1, 0.0f,
+                       act, rowScale, rowInv);
     return launch_status();
+}
+
+// The qwen3lm batched pass's activation tiles: half(x) (norm false) or the
+// RMS-normalized half(x * f) (norm true). x rows are `stride` floats apart,
+// 16-byte aligned, K % 4 == 0.
+int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, _Float16 *act,
+                hipStream_t stream) {
+    if (rows == 0) return GPHQ_OK;
+    const int kt = (K + 63) / 64;
+    hipLaunchKernelGGL(f16_act_pack_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, norm ? 3 : 1, 0, K,
+                       eps, act, nullptr, nullptr);
+    return launch_status();
+}
+
+// One projection of the qwen3lm batched pass over M activation rows packed
+// by lm_act_pack: epi 0 stores y[M][N], 1 adds into y, 2 stores the SwiGLU of
+// interleaved gate/up columns into y[M][N/2]; y rows are y_stride floats
+// apart. fmt is a GPHQ_FMT_* layer format. Arguments were validated.
+int lm_mm_launch(int fmt, int epi, const void *codes, const void *scales, const _Float16 *act, float *y,
+                 long y_stride, int M, int K, int N, hipStream_t stream) {
+    F16GemmArgs a{};
+    int wf;
+    switch (fmt) {
+    case GPHQ_FMT_Q8: wf = W_Q8_ROW; break;
+    case GPHQ_FMT_Q8B: wf = W_Q8B_ROW; break;
+    case GPHQ_FMT_Q8B_F32: wf = W_Q8BF_ROW; break;
+    case GPHQ_FMT_Q4: wf = W_Q4_ROW; break;
+    default: return GPHQ_ERR_UNSUPPORTED;
+    }
+    const bool q8 = fmt == GPHQ_FMT_Q8;
+    int e;
+    if (epi == 0)
+        e = q8 ? EPI_ROWSCALE : EPI_PLAIN;
+    else
+        e = epi == 1 ? EPI_ADD : EPI_SWIGLU;
+    a.A = act;
+    a.B = codes;
+    a.bScale = scales;
+    a.colScale = q8 ? (const float *)scales : nullptr;
+    a.dst = y;
+    a.stride = y_stride;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.KT = (K + 63) / 64;
+    a.c0 = 0;
+    a.c1 = N;
+    return f16gemm_launch(wf, e, a, stream);
 }
 
 // PackBF16Rows arithmetic (q8gemm/packed.go:148-174) for rows already known to

@@ -34,6 +34,7 @@
 #include <vector>
 
 #include "common.h"
+#include "lm_model.h"
 
 namespace gphq {
 int gemv_fused_launch(int fmt, int pro, int epi, const void *codes, const void *scales, const float *x, float *y,
@@ -49,7 +50,7 @@ using namespace gphq;
 namespace {
 
 constexpr int kMaxLanes = GPHQ_DECODE_MAX_LANES;
-constexpr int kHeadDim = 128;
+constexpr int kHeadDim = kLmHeadDim;
 constexpr int kPart = 2 + kHeadDim;  // one attention partial: max, sum, weighted V
 constexpr int kMaxSplits = 32;  // attention blocks per (KV head, lane), at most
 constexpr int kMinChunk = 64;  // keys per attention block, at least
@@ -82,27 +83,6 @@ void matrix_bytes(int fmt, int64_t rows, int64_t k, int64_t *codes, int64_t *sca
 int64_t align256(int64_t n) { return (n + 255) & ~(int64_t)255; }
 
 }  // namespace
-
-struct gphq_lm {
-    gphq_lm_config cfg;
-    int64_t qd, kvd, group, hblock, iblock, positions;
-    std::vector<gphq_lm_layer> layers;
-    std::vector<char> bound;
-    float *norms = nullptr;   // [layers][2][128]: q_norm, k_norm
-    float *rope = nullptr;    // [2][positions][64]: cos, then sin
-    float *hsigns = nullptr;  // hidden rotation sign*scale [hidden]
-    float *isigns = nullptr;  // intermediate rotation sign*scale [inter]
-    float *final_norm = nullptr;
-    const uint16_t *embed = nullptr;
-    const uint8_t *head = nullptr;
-    int64_t head_scale = 0, head_rows = 0;
-};
-
-struct gphq_prefix {
-    const gphq_lm *lm;
-    float *kc = nullptr, *vc = nullptr;  // [layers][capacity][kvd]
-    int64_t capacity = 0;
-};
 
 struct gphq_decode_batch {
     const gphq_lm *lm;
@@ -766,6 +746,34 @@ int step_graph(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, float 
 }
 
 }  // namespace
+
+namespace gphq {
+
+bool lm_model_ready(const gphq_lm *lm) { return model_ready(lm); }
+
+int lm_embed_launch(const gphq_lm *lm, const int32_t *tok, int rows, float *h, hipStream_t st) {
+    const int H = (int)lm->cfg.hidden;
+    hipLaunchKernelGGL(lm_embed_kernel, dim3(rows), dim3(1024), H * sizeof(float), st, lm->embed, tok,
+                       (int)lm->cfg.vocab, H, lm->hsigns, (int)lm->hblock, h);
+    return launch_status();
+}
+
+int lm_rotate_launch(const gphq_lm *lm, float *act, int rows, long stride, hipStream_t st) {
+    const int64_t I = lm->cfg.intermediate;
+    hipLaunchKernelGGL(lm_rotate_kernel, dim3((unsigned)(I / lm->iblock), rows), dim3(256),
+                       lm->iblock * sizeof(float), st, act, (int)stride, lm->isigns, (int)lm->iblock);
+    return launch_status();
+}
+
+int lm_final_launch(const gphq_lm *lm, const float *h, int rows, float *hidden, float *hn, int32_t *nonfinite,
+                    hipStream_t st) {
+    const int H = (int)lm->cfg.hidden;
+    hipLaunchKernelGGL(lm_final_kernel, dim3(rows), dim3(1024), H * sizeof(float), st, h, H, lm->hsigns,
+                       (int)lm->hblock, lm->final_norm, (float)lm->cfg.eps, hidden, hn, nonfinite);
+    return launch_status();
+}
+
+}  // namespace gphq
 
 extern "C" {
 

@@ -1,0 +1,458 @@
+// qwen3lm batched pass on MI355X: HiddenLastExtendInto's GPU path
+// (qwen3lm/evaluator.go:146-262 -> gpuWorkspace.batch / batchPacked / pass /
+// encodeBatch, gpu_darwin.go:1406-1480, 1574-1657, 1703-1764).
+//
+// A prefix-owned K/V cache is extended by n tokens in passes of up to the
+// workspace's row capacity (the reference's gpuPositions = 2048 rows; here
+// the caller picks it, e.g. a whole 4096-token prompt in one pass). A pass
+// runs, per layer:
+//   * the QKV projection over the RMS-normalized residual rows (the
+//     activation tile packer computes each row's norm, gpu.metal:785-796);
+//   * lm_qk_rope_kernel: head RMSNorm and RoPE of every query and key head,
+//     queries scaled by 1/sqrt(head_dim) in place, keys and values appended
+//     at cache rows base + m (gpu.metal:1027-1056 qkRope);
+//   * lm_flash_kernel: causal attention of each row m over cache rows
+//     0 .. base + m (gpu.metal:1099-1240 attendFlash);
+//   * the O projection added into the residual, the gate/up projection with
+//     the norm prologue and the SwiGLU epilogue, the down input's Hadamard
+//     (Q8 / Q4), and the down projection added into the residual.
+// Projections run on the FP16 MFMA GEMM of gemm_f16.hip (FP16 weight and
+// activation tiles, fp32 sums, the reference mm's arithmetic); a one-row pass
+// takes the fp32 GEMV instead, as the reference's encodeTokens does
+// (gpu_darwin.go:1605-1614). After the last pass the last row's final norm
+// gives the caller's hidden state.
+#include <math.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "common.h"
+#include "lm_model.h"
+
+namespace gphq {
+int gemv_fused_launch(int fmt, int pro, int epi, const void *codes, const void *scales, const float *x, float *y,
+                      int K, int N, float eps, hipStream_t stream);
+int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, _Float16 *act,
+                hipStream_t stream);
+int lm_mm_launch(int fmt, int epi, const void *codes, const void *scales, const _Float16 *act, float *y,
+                 long y_stride, int M, int K, int N, hipStream_t stream);
+}  // namespace gphq
+
+using namespace gphq;
+
+struct gphq_prefill {
+    const gphq_lm *lm;
+    int rows;  // tokens per pass, at most
+    float *h, *qkv, *ctx, *act, *hn;
+    _Float16 *a16;  // FP16 activation tiles [rows/16][K/64][64][16]
+    int32_t *tok, *nonfinite;
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+constexpr int kHeadDim = kLmHeadDim;
+enum { PRO_PLAIN = 0, PRO_NORM = 1 };
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+struct RopeArgs {
+    float *qkv;             // [rows][qkvw]
+    float *kc, *vc;         // this layer's cache [capacity][kvd]
+    const float *qn, *kn;   // head norm weights [128]
+    const float *rope;      // cos [positions][64], sin at +sin_off
+    float eps, qscale;
+    int qkvw, qd, kvd, heads, kvh, base, sin_off;
+};
+
+// qkRope (gpu.metal:1027-1056) for row m = blockIdx.y, head item blockIdx.x
+// (query heads, then key heads, then value heads); one wavefront, lane l
+// holding the rotary pair (l, l + 64). The same norm and rotation arithmetic
+// as the decode step's attention kernel.
+__global__ __launch_bounds__(64) void lm_qk_rope_kernel(const RopeArgs a) {
+    const int h = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+    float *row = a.qkv + (size_t)m * a.qkvw;
+    const int pos = a.base + m;
+    const size_t slot = (size_t)pos * a.kvd;
+    if (h < a.heads + a.kvh) {
+        const bool isQ = h < a.heads;
+        float *src = row + (size_t)h * kHeadDim;  // key head h - heads starts at qd + (h - heads) * 128
+        float x0 = src[lane], x1 = src[lane + 64];
+        const float ss = wave_sum(x0 * x0 + x1 * x1);
+        const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
+        const float *w = isQ ? a.qn : a.kn;
+        x0 = x0 * (inv * w[lane]);
+        x1 = x1 * (inv * w[lane + 64]);
+        const float c = a.rope[(size_t)pos * 64 + lane], s = a.rope[a.sin_off + (size_t)pos * 64 + lane];
+        const float y0 = x0 * c - x1 * s, y1 = x1 * c + x0 * s;
+        if (isQ) {
+            src[lane] = y0 * a.qscale;
+            src[lane + 64] = y1 * a.qscale;
+        } else {
+            float *d = a.kc + slot + (size_t)(h - a.heads) * kHeadDim;
+            d[lane] = y0;
+            d[lane + 64] = y1;
+        }
+        return;
+    }
+    const int vh = h - a.heads - a.kvh;
+    const float *src = row + a.qd + a.kvd + (size_t)vh * kHeadDim;
+    float *d = a.vc + slot + (size_t)vh * kHeadDim;
+    d[lane] = src[lane];
+    d[lane + 64] = src[lane + 64];
+}
+
+struct FlashArgs {
+    const float *qkv;        // [rows][qkvw], queries prepared by lm_qk_rope_kernel
+    const float *kc, *vc;    // this layer's cache [capacity][kvd]
+    float *ctx;              // [rows][qd]
+    int qkvw, qd, kvd, rows, base;
+};
+
+// Causal attention of pass rows m0 .. m0+31 (m0 = 32 * row block) for the
+// GROUP query heads of KV head g = blockIdx.y: wavefront w is query head
+// g*GROUP + w, and the block's waves share each 32-key tile of K and V,
+// staged through LDS as FP16. Row m attends cache rows 0 .. base + m.
+//
+// Per tile, on v_mfma_f32_32x32x16_f16 with fp32 accumulation:
+//   S^T (32 keys x 32 queries) = K . Q^T, so lane l holds query l % 32 and 16
+//     of its keys (the other 16 in lane l ^ 32): the online softmax needs one
+//     lane exchange per reduction;
+//   O^T (128 dims x 32 queries) += V^T . P^T, P^T taken straight from the
+//     S^T registers (the MFMA's K index runs over the lane's own keys; V^T is
+//     stored in LDS in the matching key order).
+// Queries enter as half(q * log2(e)) (q already carries 1/sqrt(head_dim)), so
+// the softmax is exp2(s - max); probabilities and values are FP16.
+template <int GROUP>
+__global__ __launch_bounds__(64 * GROUP) void lm_flash_kernel(const FlashArgs a) {
+    constexpr int NT = 64 * GROUP;
+    constexpr int KB = 32;             // keys per tile
+    constexpr int KS = kHeadDim + 8;   // K tile row stride (halves): conflict-free 16-byte reads
+    constexpr int VS = KB + 8;         // V^T row stride (halves)
+    constexpr int KITEMS = (KB * kHeadDim / 4 + NT - 1) / NT;  // float4 of K per thread
+    constexpr int VITEMS = (KB / 4 * kHeadDim + NT - 1) / NT;  // (dim, 4 keys) of V per thread
+    __shared__ _Float16 Ks[KB * KS];
+    __shared__ _Float16 Vt[kHeadDim * VS];
+    const int nmb = (a.rows + 31) >> 5;
+    const int mb = nmb - 1 - (int)blockIdx.x;  // longest rows first
+    const int g = blockIdx.y;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int q = lane & 31, hi = lane >> 5;
+    const int head = g * GROUP + wave;
+    const int m0 = mb * 32;
+    const int kvEnd = a.base + a.rows;  // cache rows written by this pass's qk_rope
+    const int lastKey = a.base + min(m0 + 31, a.rows - 1);
+    const int tiles = lastKey / KB + 1;
+    const int myLast = a.base + m0 + q;  // this lane's query sees keys 0..myLast
+    const float *kbase = a.kc + (size_t)g * kHeadDim;
+    const float *vbase = a.vc + (size_t)g * kHeadDim;
+
+    half8 qf[8];
+    {
+        const float *qrow = a.qkv + (size_t)min(m0 + q, a.rows - 1) * a.qkvw + (size_t)head * kHeadDim + 8 * hi;
+        constexpr float kLog2e = 1.4426950408889634f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 x0 = *(const float4 *)(qrow + 16 * c), x1 = *(const float4 *)(qrow + 16 * c + 4);
+            qf[c] = half8{(_Float16)(x0.x * kLog2e), (_Float16)(x0.y * kLog2e), (_Float16)(x0.z * kLog2e),
+                          (_Float16)(x0.w * kLog2e), (_Float16)(x1.x * kLog2e), (_Float16)(x1.y * kLog2e),
+                          (_Float16)(x1.z * kLog2e), (_Float16)(x1.w * kLog2e)};
+        }
+    }
+
+    float4 kr[KITEMS];
+    float4 vr[VITEMS];
+    auto load_tile = [&](int jb) {
+#pragma unroll
+        for (int i = 0; i < KITEMS; ++i) {
+            const int idx = tid + i * NT;
+            const int j = jb + (idx >> 5);
+            kr[i] = (idx < KB * kHeadDim / 4 && j < kvEnd)
+                        ? *(const float4 *)(kbase + (size_t)j * a.kvd + 4 * (idx & 31))
+                        : float4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int i = 0; i < VITEMS; ++i) {
+            const int idx = tid + i * NT;
+            const int d = idx & (kHeadDim - 1), j = jb + 4 * (idx >> 7);
+            float4 v{0.f, 0.f, 0.f, 0.f};
+            if (idx < KB / 4 * kHeadDim) {
+                const float *p = vbase + (size_t)j * a.kvd + d;
+                if (j < kvEnd) v.x = p[0];
+                if (j + 1 < kvEnd) v.y = p[a.kvd];
+                if (j + 2 < kvEnd) v.z = p[2 * (size_t)a.kvd];
+                if (j + 3 < kvEnd) v.w = p[3 * (size_t)a.kvd];
+            }
+            vr[i] = v;
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int i = 0; i < KITEMS; ++i) {
+            const int idx = tid + i * NT;
+            if (idx < KB * kHeadDim / 4) {
+                typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+                *(half4 *)(Ks + (idx >> 5) * KS + 4 * (idx & 31)) =
+                    half4{(_Float16)kr[i].x, (_Float16)kr[i].y, (_Float16)kr[i].z, (_Float16)kr[i].w};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VITEMS; ++i) {
+            const int idx = tid + i * NT;
+            if (idx < KB / 4 * kHeadDim) {
+                // Key group kg (keys 4kg..4kg+3) goes to position group
+                // 4*(kg/4) + {0, 2, 1, 3}[kg % 4]: in each 16-key half, LDS
+                // positions 0..7 hold keys 0-3, 8-11 and positions 8..15 keys
+                // 4-7, 12-15, the keys lanes 0-31 and 32-63 hold in S^T.
+                const int d = idx & (kHeadDim - 1), kg = idx >> 7;
+                const int r = kg & 3;
+                const int pg = (kg & ~3) + ((r == 1) ? 2 : (r == 2) ? 1 : r);
+                typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+                *(half4 *)(Vt + d * VS + 4 * pg) =
+                    half4{(_Float16)vr[i].x, (_Float16)vr[i].y, (_Float16)vr[i].z, (_Float16)vr[i].w};
+            }
+        }
+    };
+
+    f32x16 o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = f32x16{};
+    float mrun = -INFINITY, lrun = 0.0f;
+    load_tile(0);
+    for (int t = 0; t < tiles; ++t) {
+        const int jb = t * KB;
+        __syncthreads();  // the previous tile's LDS reads are done
+        store_tile();
+        __syncthreads();
+        if (t + 1 < tiles) load_tile(jb + KB);
+        f32x16 s = f32x16{};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const half8 kf = *(const half8 *)(Ks + q * KS + 16 * c + 8 * hi);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], s, 0, 0, 0);
+        }
+        // s[r] is key jb + 8*(r/4) + 4*hi + r%4 of query row m0 + q.
+        if (jb + KB - 1 > a.base + m0) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (jb + 8 * (r >> 2) + 4 * hi + (r & 3) > myLast) s[r] = -INFINITY;
+        }
+        float mx = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // Tile 0 holds key 0, which every query sees, so mnew is finite.
+        const float mnew = fmaxf(mrun, mx);
+        const float corr = exp2f(mrun - mnew);
+        mrun = mnew;
+        float p[16], rs = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            p[r] = exp2f(s[r] - mnew);
+            rs += p[r];
+        }
+        rs += __shfl_xor(rs, 32);
+        lrun = lrun * corr + rs;
+        half8 p0, p1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            p0[i] = (_Float16)p[i];
+            p1[i] = (_Float16)p[8 + i];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            o[c] *= corr;
+            const _Float16 *vrow = Vt + (32 * c + q) * VS + 8 * hi;
+            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)vrow, p0, o[c], 0, 0, 0);
+            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)(vrow + 16), p1, o[c], 0, 0, 0);
+        }
+    }
+    const int m = m0 + q;
+    if (m >= a.rows) return;
+    const float inv = 1.0f / lrun;
+    float *out = a.ctx + (size_t)m * a.qd + (size_t)head * kHeadDim + 4 * hi;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *(float4 *)(out + 32 * c + 8 * j) = float4{o[c][4 * j] * inv, o[c][4 * j + 1] * inv,
+                                                       o[c][4 * j + 2] * inv, o[c][4 * j + 3] * inv};
+}
+
+template <int G>
+int launch_flash_g(const FlashArgs &a, int kvh, hipStream_t st) {
+    hipLaunchKernelGGL((lm_flash_kernel<G>), dim3((unsigned)((a.rows + 31) / 32), (unsigned)kvh), dim3(64 * G), 0, st,
+                       a);
+    return launch_status();
+}
+
+int launch_flash(int group, const FlashArgs &a, int kvh, hipStream_t st) {
+    switch (group) {
+    case 1: return launch_flash_g<1>(a, kvh, st);
+    case 2: return launch_flash_g<2>(a, kvh, st);
+    case 3: return launch_flash_g<3>(a, kvh, st);
+    case 4: return launch_flash_g<4>(a, kvh, st);
+    case 5: return launch_flash_g<5>(a, kvh, st);
+    case 6: return launch_flash_g<6>(a, kvh, st);
+    case 7: return launch_flash_g<7>(a, kvh, st);
+    case 8: return launch_flash_g<8>(a, kvh, st);
+    }
+    return GPHQ_ERR_UNSUPPORTED;
+}
+
+// One projection of a pass over R rows: the fp32 GEMV for one row, else the
+// activation tiles (normalized for PRO_NORM) and the FP16 MFMA GEMM.
+int project(gphq_prefill *ws, int R, int pro, int epi, const uint8_t *buf, int64_t codes, int64_t scales,
+            const float *x, int64_t K, float *y, int64_t ystride, int64_t N, hipStream_t st) {
+    const gphq_lm_config &c = ws->lm->cfg;
+    const float eps = (float)c.eps;
+    if (R == 1) return gemv_fused_launch(c.fmt, pro, epi, buf + codes, buf + scales, x, y, (int)K, (int)N, eps, st);
+    GPHQ_TRY(lm_act_pack(x, (long)K, R, (int)K, pro == PRO_NORM, eps, ws->a16, st));
+    return lm_mm_launch(c.fmt, epi, buf + codes, buf + scales, ws->a16, y, (long)ystride, R, (int)K, (int)N, st);
+}
+
+// One pass: rows tokens already in ws->tok, continuing kv at cache row base.
+int encode_pass(gphq_prefill *ws, gphq_prefix *kv, int base, int R, hipStream_t st) {
+    const gphq_lm *lm = ws->lm;
+    const gphq_lm_config &c = lm->cfg;
+    const int64_t H = c.hidden, I = c.intermediate, qd = lm->qd, kvd = lm->kvd, qkvw = qd + 2 * kvd;
+    GPHQ_TRY(lm_embed_launch(lm, ws->tok, R, ws->h, st));
+    RopeArgs ra{};
+    ra.qkv = ws->qkv;
+    ra.rope = lm->rope;
+    ra.eps = (float)c.eps;
+    ra.qscale = (float)(1.0 / sqrt((double)c.head_dim));
+    ra.qkvw = (int)qkvw;
+    ra.qd = (int)qd;
+    ra.kvd = (int)kvd;
+    ra.heads = (int)c.heads;
+    ra.kvh = (int)c.kv_heads;
+    ra.base = base;
+    ra.sin_off = (int)(lm->positions * 64);
+    FlashArgs fa{};
+    fa.qkv = ws->qkv;
+    fa.ctx = ws->ctx;
+    fa.qkvw = (int)qkvw;
+    fa.qd = (int)qd;
+    fa.kvd = (int)kvd;
+    fa.rows = R;
+    fa.base = base;
+    for (int layer = 0; layer < c.layers; ++layer) {
+        const gphq_lm_layer &L = lm->layers[layer];
+        const uint8_t *buf = (const uint8_t *)L.buf_dev;
+        GPHQ_TRY(project(ws, R, PRO_NORM, EPI_STORE, buf, L.qkv, L.qkv_scale, ws->h, H, ws->qkv, qkvw, qkvw, st));
+        const size_t off = (size_t)layer * kv->capacity * kvd;
+        ra.kc = kv->kc + off;
+        ra.vc = kv->vc + off;
+        ra.qn = lm->norms + (size_t)layer * 2 * kHeadDim;
+        ra.kn = ra.qn + kHeadDim;
+        hipLaunchKernelGGL(lm_qk_rope_kernel, dim3((unsigned)(c.heads + 2 * c.kv_heads), (unsigned)R), dim3(64), 0,
+                           st, ra);
+        GPHQ_TRY(launch_status());
+        fa.kc = ra.kc;
+        fa.vc = ra.vc;
+        GPHQ_TRY(launch_flash((int)lm->group, fa, (int)c.kv_heads, st));
+        GPHQ_TRY(project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.o, L.o_scale, ws->ctx, qd, ws->h, H, H, st));
+        GPHQ_TRY(project(ws, R, PRO_NORM, EPI_SWIGLU, buf, L.gu, L.gu_scale, ws->h, H, ws->act, I, 2 * I, st));
+        if (c.fmt != GPHQ_FMT_Q8B) GPHQ_TRY(lm_rotate_launch(lm, ws->act, R, (long)I, st));
+        GPHQ_TRY(project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.d, L.d_scale, ws->act, I, ws->h, H, H, st));
+    }
+    return GPHQ_OK;
+}
+
+void free_prefill(gphq_prefill *ws) {
+    for (void *p : ws->allocs) (void)hipFree(p);
+    delete ws;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gphq_prefill_new(const gphq_lm *lm, int64_t rows, gphq_prefill **out) {
+    if (!out) return GPHQ_ERR_DIMENSIONS;
+    *out = nullptr;
+    if (!lm) return GPHQ_ERR_WORKSPACE;
+    if (rows < 1 || rows > GPHQ_PREFILL_MAX_ROWS) return GPHQ_ERR_DIMENSIONS;
+    if (!lm_model_ready(lm)) return GPHQ_ERR_MODEL_INCOMPLETE;
+    const gphq_lm_config &c = lm->cfg;
+    gphq_prefill *ws = new gphq_prefill();
+    ws->lm = lm;
+    ws->rows = (int)rows;
+    const int64_t H = c.hidden, I = c.intermediate, qkvw = lm->qd + 2 * lm->kvd;
+    const int64_t kmax = std::max({H, lm->qd, I});
+    const int64_t rpad = (rows + 15) / 16 * 16, kpad = (kmax + 63) / 64 * 64;
+    struct {
+        void **dst;
+        size_t bytes;
+    } bufs[] = {
+        {(void **)&ws->h, (size_t)rows * H * 4},      {(void **)&ws->qkv, (size_t)rows * qkvw * 4},
+        {(void **)&ws->ctx, (size_t)rows * lm->qd * 4}, {(void **)&ws->act, (size_t)rows * I * 4},
+        {(void **)&ws->hn, (size_t)H * 4},            {(void **)&ws->a16, (size_t)rpad * kpad * 2},
+        {(void **)&ws->tok, (size_t)rows * 4},        {(void **)&ws->nonfinite, 4},
+    };
+    for (auto &b : bufs) {
+        const hipError_t e = hipMalloc(b.dst, b.bytes);
+        if (e != hipSuccess) {
+            free_prefill(ws);
+            return hip_status(e);
+        }
+        ws->allocs.push_back(*b.dst);
+    }
+    const hipError_t e = hipMemset(ws->nonfinite, 0, 4);
+    if (e != hipSuccess) {
+        free_prefill(ws);
+        return hip_status(e);
+    }
+    *out = ws;
+    return GPHQ_OK;
+}
+
+void gphq_prefill_free(gphq_prefill *ws) {
+    if (ws) free_prefill(ws);
+}
+
+int gphq_prefill_rows(const gphq_prefill *ws) { return ws ? ws->rows : 0; }
+
+int gphq_prefill_extend(gphq_prefill *ws, gphq_prefix *kv, int64_t keep, const int32_t *tokens, int64_t n,
+                        float *hidden_dev, int64_t hidden_len, void *stream) {
+    // evaluator.go:178-194 then HiddenLastBatchInto's checks (540-560), in order.
+    if (!ws || !ws->lm) return GPHQ_ERR_WORKSPACE;
+    const gphq_lm *lm = ws->lm;
+    if (!kv || kv->lm != lm || !kv->kc) return GPHQ_ERR_FOREIGN_PREFIX;
+    if (keep < 0 || keep > kv->capacity) return GPHQ_ERR_KEEP_RANGE;
+    if (n < 0 || keep + n > kv->capacity) return GPHQ_ERR_PREFIX_CAPACITY;
+    if (n == 0 || !tokens) return GPHQ_ERR_EMPTY_SEQUENCE;
+    if (keep + n > lm->cfg.max_positions || keep + n > lm->positions) return GPHQ_ERR_CONTEXT;
+    if (!hidden_dev || hidden_len != lm->cfg.hidden) return GPHQ_ERR_DEST_WIDTH;
+    for (int64_t i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= lm->cfg.vocab) return GPHQ_ERR_TOKEN_VOCAB;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t H = lm->cfg.hidden;
+    // gpu_darwin.go:1460-1476: a sequence longer than a pass runs as
+    // consecutive passes, each continuing the cache where the last stopped.
+    int last = 0;
+    for (int64_t off = 0; off < n; off += ws->rows) {
+        const int R = (int)std::min<int64_t>(ws->rows, n - off);
+        GPHQ_TRY(hip_status(
+            hipMemcpyAsync(ws->tok, tokens + off, (size_t)R * sizeof(int32_t), hipMemcpyHostToDevice, st)));
+        GPHQ_TRY(encode_pass(ws, kv, (int)(keep + off), R, st));
+        last = R;
+    }
+    return lm_final_launch(lm, ws->h + (size_t)(last - 1) * H, 1, hidden_dev, ws->hn, ws->nonfinite, st);
+}
+
+int gphq_prefill_check(gphq_prefill *ws, void *stream) {
+    if (!ws) return GPHQ_ERR_WORKSPACE;
+    hipStream_t st = (hipStream_t)stream;
+    GPHQ_TRY(hip_status(hipStreamSynchronize(st)));
+    int32_t bad = 0;
+    GPHQ_TRY(hip_status(hipMemcpy(&bad, ws->nonfinite, 4, hipMemcpyDeviceToHost)));
+    if (!bad) return GPHQ_OK;
+    GPHQ_TRY(hip_status(hipMemset(ws->nonfinite, 0, 4)));
+    return GPHQ_ERR_NON_FINITE_STATE;
+}
+
+}  // extern "C"

@@ -40,7 +40,7 @@ using namespace gphq;
 static constexpr int64_t kOutputPanel = 64;  // q8gemm/packed.go:17
 static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-enum { W_I8_TILE = 0, W_F16_TILE = 1, W_Q8_ROW = 2, W_Q8B_ROW = 3, W_Q4_ROW = 4, W_GPTQ_ROW = 5 };
+enum { W_I8_TILE = 0, W_F16_TILE = 1, W_Q8_ROW = 2, W_Q8B_ROW = 3, W_Q4_ROW = 4, W_GPTQ_ROW = 5, W_Q8BF_ROW = 6 };
 enum { EPI_PANELS = 0, EPI_PLAIN = 1, EPI_ROWSCALE = 2 };
 
 struct gphq_weights {
@@ -456,6 +456,9 @@ int gphq_mm(int fmt, const void *codes, const void *scales, const uint8_t *zeros
         break;
     case GPHQ_FMT_Q8B:
         wf = W_Q8B_ROW;
+        break;
+    case GPHQ_FMT_Q8B_F32:
+        wf = W_Q8BF_ROW;
         break;
     case GPHQ_FMT_Q4:
         wf = W_Q4_ROW;

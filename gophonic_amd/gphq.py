@@ -30,6 +30,14 @@ ERR_TOKEN_RANGE = -14
 ERR_OVERLAP = -15
 ERR_NON_FINITE_HIDDEN = -16
 ERR_MODEL_INCOMPLETE = -17
+ERR_WORKSPACE = -18
+ERR_KEEP_RANGE = -19
+ERR_PREFIX_CAPACITY = -20
+ERR_EMPTY_SEQUENCE = -21
+ERR_CONTEXT = -22
+ERR_DEST_WIDTH = -23
+ERR_TOKEN_VOCAB = -24
+ERR_NON_FINITE_STATE = -25
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
 
@@ -113,6 +121,11 @@ SIGNATURES = {
     "gphq_decode_batch_set_graph": (ctypes.c_int, [_vp, ctypes.c_int]),
     "gphq_prepare_work_bytes": (_i64, [_i64, _i64]),
     "gphq_prepare_projection": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "gphq_prefill_new": (ctypes.c_int, [_vp, _i64, _vpp]),
+    "gphq_prefill_free": (None, [_vp]),
+    "gphq_prefill_rows": (ctypes.c_int, [_vp]),
+    "gphq_prefill_extend": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "gphq_prefill_check": (ctypes.c_int, [_vp, _vp]),
 }
 
 FMT_GPTQ4_G128 = 12
@@ -661,6 +674,40 @@ class DecodeBatch:
 
     def check(self, stream=None):
         return check(load().gphq_decode_batch_check(self.h, stream_handle(stream)))
+
+
+class Prefill:
+    """gphq_prefill: the batched pass's scratch for up to `rows` tokens per pass
+    (gpuWorkspace, gpu_darwin.go:895-960)."""
+
+    def __init__(self, lm, rows):
+        h = ctypes.c_void_p()
+        check(load().gphq_prefill_new(lm.h, rows, ctypes.byref(h)))
+        self.h, self.lm, self.rows = h, lm, rows
+
+    def close(self):
+        if self.h:
+            load().gphq_prefill_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def extend(self, kv, keep, tokens, hidden, stream=None):
+        """HiddenLastExtendInto (evaluator.go:146): tokens (host ints) continue
+        the first `keep` rows of kv; hidden [hidden] device tensor receives the
+        last token's post-final-norm state."""
+        import numpy as np
+
+        tok = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+        check(load().gphq_prefill_extend(self.h, kv.h if kv is not None else None, keep, tok.ctypes.data, tok.size,
+                                         ptr(hidden), 0 if hidden is None else hidden.numel(), stream_handle(stream)))
+
+    def check(self, stream=None):
+        return check(load().gphq_prefill_check(self.h, stream_handle(stream)))
 
 
 def lm_from_stored(geom_kwargs, fmt, layers, embed_bf16, final_norm, head, device="cuda"):

@@ -62,6 +62,22 @@ extern "C" {
 /* decode_batch.go / gpu_darwin.go:1048-1069: the model has no head (LoadHead)
  * or a layer / the embedding table is not bound */
 #define GPHQ_ERR_MODEL_INCOMPLETE (-17)
+/* evaluator.go:191-193 "qwen3: nil or foreign workspace" */
+#define GPHQ_ERR_WORKSPACE (-18)
+/* evaluator.go:185-187 "qwen3: keep outside the stored tokens" */
+#define GPHQ_ERR_KEEP_RANGE (-19)
+/* evaluator.go:188-190 "qwen3: tokens exceed prefix capacity" */
+#define GPHQ_ERR_PREFIX_CAPACITY (-20)
+/* evaluator.go:545-547 "qwen3: empty token sequence" */
+#define GPHQ_ERR_EMPTY_SEQUENCE (-21)
+/* evaluator.go:548-550 "qwen3: tokens exceed the Qwen3 context" */
+#define GPHQ_ERR_CONTEXT (-22)
+/* evaluator.go:551-553 "qwen3: destination width does not match the hidden size" */
+#define GPHQ_ERR_DEST_WIDTH (-23)
+/* evaluator.go:554-558 "qwen3: token is outside vocabulary" */
+#define GPHQ_ERR_TOKEN_VOCAB (-24)
+/* gpu_darwin.go:1636-1638, 1649-1652 "qwen3: non-finite hidden state" */
+#define GPHQ_ERR_NON_FINITE_STATE (-25)
 
 /* The reference message for a status code ("" for GPHQ_OK). Static storage. */
 const char *gphq_error_string(int status);
@@ -297,7 +313,8 @@ int gphq_q8gemm_mul_into(float *dst_dev, int64_t dst_len, const float *x_dev, in
  * each K step's weights dequantized to FP16 (Q8: half(code); Q8B:
  * half(code)*half(d); Q4: (half(nib)-8)*d, each rounded to half), activations
  * half(x), fp32 accumulation, and Q8 rows scaled by their fp32 scale after
- * the sum. fmt: GPHQ_FMT_Q8, GPHQ_FMT_Q8B, GPHQ_FMT_Q4, or
+ * the sum. fmt: GPHQ_FMT_Q8, GPHQ_FMT_Q8B, GPHQ_FMT_Q8B_F32 (half(code*d)
+ * from the fp32 product), GPHQ_FMT_Q4, or
  * GPHQ_FMT_GPTQ4_G128: int32 codes [N][K/8] (nibble i of word j holds k = 8j+i,
  * unsigned 0..15), FP16 scales [N][K/128] and zero points zeros_dev
  * u8 [N][K/128] (low nibble), w = (q - z) * s -- the 4-bit group-128
@@ -464,6 +481,41 @@ typedef struct gphq_prepare_job {
 /* Scratch for gphq_prepare_projection: float32 rows plus tables (n*k*4 + ...). */
 int64_t gphq_prepare_work_bytes(int64_t n, int64_t k);
 int gphq_prepare_projection(const gphq_prepare_job *job, void *work_dev, int64_t work_bytes, void *stream);
+
+/* ---- qwen3lm batched pass (prefill) ----------------------------------------
+ * Replaces the GPU path of Evaluator.HiddenLastExtendInto (evaluator.go:
+ * 146-262): gpuWorkspace.batchPacked with an unshared prefix, pass and
+ * encodeBatch (gpu_darwin.go:1449-1480, 1574-1657, 1703-1764). Per pass of up
+ * to `rows` tokens and per layer: QKV projection over RMS-normalized rows,
+ * qkRope (head norm, RoPE, K/V append), causal attention (attendFlash),
+ * O projection + residual, gate/up with norm and SwiGLU, the down input's
+ * Hadamard (Q8/Q4) and down + residual; projections use FP16 weight and
+ * activation tiles with fp32 sums (the reference mm's arithmetic), attention
+ * FP16 MFMA tiles with fp32 sums and softmax. A one-token pass uses the fp32
+ * GEMV (encodeTokens, gpu_darwin.go:1605-1614). Results agree with the
+ * token-by-token path to the reference's bound (cosine >= 0.99999,
+ * gpu_official_darwin_test.go:86), not bit for bit. */
+#define GPHQ_PREFILL_MAX_ROWS 65536
+typedef struct gphq_prefill gphq_prefill;
+
+/* The batched part of NewWorkspace (newWorkspace, gpu_darwin.go:895-960): device
+ * scratch for passes of up to `rows` tokens (the reference fixes 2048). */
+int gphq_prefill_new(const gphq_lm *lm, int64_t rows, gphq_prefill **out);
+void gphq_prefill_free(gphq_prefill *ws);
+int gphq_prefill_rows(const gphq_prefill *ws);
+/* HiddenLastExtendInto: evaluates tokens[0..n) (host array) as the
+ * continuation of the first `keep` cache rows of kv, writing K/V rows
+ * keep..keep+n-1, in passes of at most the workspace's rows; hidden_dev
+ * (hidden_len == hidden floats) receives the last token's post-final-norm
+ * state. The caller keeps the token count (keep + n afterwards). Validation
+ * follows evaluator.go:178-194, 540-560 in order, before any device work.
+ * Enqueued on `stream`; gphq_prefill_check waits and reports a non-finite
+ * hidden state. */
+int gphq_prefill_extend(gphq_prefill *ws, gphq_prefix *kv, int64_t keep, const int32_t *tokens, int64_t n,
+                        float *hidden_dev, int64_t hidden_len, void *stream);
+/* Waits for the stream; GPHQ_ERR_NON_FINITE_STATE if an extension since the
+ * last check produced a non-finite hidden value. */
+int gphq_prefill_check(gphq_prefill *ws, void *stream);
 
 #ifdef __cplusplus
 }

@@ -233,6 +233,54 @@ class DecodeOracle:
             h = h + W["down"] @ act
         return h
 
+    def _norm_rows(self, v, w=None):
+        inv = 1.0 / np.sqrt((v * v).sum(axis=1, keepdims=True) / v.shape[1] + self.g.eps)
+        return v * inv if w is None else v * inv * w
+
+    def _rope_rows(self, v, pos):
+        half = self.g.head_dim // 2
+        c, s = self.cos[pos], self.sin[pos]
+        a, b = v[:, :half], v[:, half:]
+        return np.concatenate([a * c - b * s, b * c + a * s], axis=1)
+
+    def prefill(self, cache, base, tokens):
+        """All rows of tokens at positions base.. at once (the batched pass,
+        gpu_darwin.go:1703-1764: each row attends cache rows 0..its own
+        position): appends K/V and returns the residual rows [T][hidden]. The
+        same float64 math as stepping layers() token by token."""
+        g = self.g
+        T = len(tokens)
+        hd = g.head_dim
+        grp = g.heads // g.kv_heads
+        scale = 1.0 / np.sqrt(hd)
+        pos = base + np.arange(T)
+        h = np.stack([self.embed_row(t) for t in tokens])
+        mask = np.arange(base + T)[None, :] <= pos[:, None]
+        for li, W in enumerate(self.W):
+            qkv = self._norm_rows(h) @ W["qkv"].T
+            kc, vc = cache[li]
+            for kh in range(g.kv_heads):
+                k = qkv[:, g.qd + kh * hd: g.qd + (kh + 1) * hd]
+                v = qkv[:, g.qd + g.kvd + kh * hd: g.qd + g.kvd + (kh + 1) * hd]
+                kc[pos, kh * hd:(kh + 1) * hd] = self._rope_rows(self._norm_rows(k, W["kn"]), pos)
+                vc[pos, kh * hd:(kh + 1) * hd] = v
+            ctx = np.empty((T, g.qd))
+            for qh in range(g.heads):
+                kh = qh // grp
+                q = self._rope_rows(self._norm_rows(qkv[:, qh * hd:(qh + 1) * hd], W["qn"]), pos) * scale
+                s = np.where(mask, q @ kc[: base + T, kh * hd:(kh + 1) * hd].T, -np.inf)
+                p = np.exp(s - s.max(axis=1, keepdims=True))
+                ctx[:, qh * hd:(qh + 1) * hd] = (p / p.sum(axis=1, keepdims=True)) @ vc[: base + T, kh * hd:(kh + 1) * hd]
+            h = h + ctx @ W["o"].T
+            gu = self._norm_rows(h) @ W["gu"].T
+            gate, up = gu[:, 0::2], gu[:, 1::2]
+            with np.errstate(over="ignore"):
+                act = gate / (1.0 + np.exp(-gate)) * up
+            if self.fmt != FMT_Q8B:
+                act = rot_apply(act, self.irot)
+            h = h + act @ W["down"].T
+        return h
+
     def finish(self, h):
         """(hidden, logits): R^T, final RMSNorm, R, head (first vocab rows)."""
         hu = rot_unapply(h, self.hrot)

@@ -46,6 +46,9 @@ def weights(fmt, rng, n, k):
     if fmt == orc.FMT_Q8B:
         return (rng.integers(-127, 128, n * k).astype(np.int8),
                 (np.abs(rng.standard_normal(n * k // 32)) * 0.02).astype(np.float16).view(np.uint16), None)
+    if fmt == orc.FMT_Q8B_F32:
+        return (rng.integers(-127, 128, n * k).astype(np.int8),
+                (np.abs(rng.standard_normal(n * k // 32)) * 0.02).astype(np.float32), None)
     if fmt == orc.FMT_Q4:
         return (rng.integers(0, 256, n * k // 2).astype(np.uint8),
                 (np.abs(rng.standard_normal(n * k // 32)) * 0.02).astype(np.float16).view(np.uint16), None)
@@ -55,7 +58,7 @@ def weights(fmt, rng, n, k):
             rng.integers(0, 16, n * k // 128).astype(np.uint8))
 
 
-FORMATS = [orc.FMT_Q8, orc.FMT_Q8B, orc.FMT_Q4, orc.FMT_GPTQ4_G128]
+FORMATS = [orc.FMT_Q8, orc.FMT_Q8B, orc.FMT_Q8B_F32, orc.FMT_Q4, orc.FMT_GPTQ4_G128]
 
 
 @pytest.mark.parametrize("fmt", FORMATS)

@@ -323,3 +323,49 @@ def test_pack_panels_quads_layout():
         for kk in range(k):
             assert out[(row // 64) * quads * 256 + (kk // 4) * 256 + (row % 64) * 4 + kk % 4] == src[row, kk]
     assert np.count_nonzero(out) == n * k
+
+
+@pytest.mark.parametrize("fmt", [orc.FMT_Q8, orc.FMT_Q8B, orc.FMT_Q8B_F32, orc.FMT_Q4, orc.FMT_GPTQ4_G128])
+def test_mm_f64_matches_numpy_fp16_tiles(fmt):
+    """The mm oracle's FP16 operands (gpu.metal:836-861 tile dequantization,
+    activations half(x)) rebuilt with numpy's float16 rounding and nibble
+    unpacking, summed in float64."""
+    rng = np.random.default_rng(fmt)
+    m, k, n = 3, 256, 5
+    x = rng.standard_normal(m * k).astype(np.float32)
+    # Values chosen so the fp16 rounding matters: scales with full fp32 / fp16 mantissas.
+    if fmt == orc.FMT_Q4:
+        codes = rng.integers(0, 256, n * k // 2).astype(np.uint8)
+        sc = (np.abs(rng.standard_normal(n * k // 32)) * 0.02).astype(np.float16)
+        b = codes.reshape(n, k // 32, 16)
+        q = np.concatenate([b & 15, b >> 4], axis=2).astype(np.float32) - 8
+        w = (q * sc.astype(np.float32).reshape(n, k // 32, 1)).astype(np.float16).reshape(n, k)
+        scales = sc.view(np.uint16)
+    elif fmt == orc.FMT_GPTQ4_G128:
+        codes = rng.integers(0, 2 ** 32, n * k // 8, dtype=np.uint64).astype(np.uint32)
+        sc = (np.abs(rng.standard_normal(n * k // 128)) * 0.01).astype(np.float16)
+        zeros = rng.integers(0, 16, n * k // 128).astype(np.uint8)
+        q = ((codes.reshape(n, k // 8, 1) >> (4 * np.arange(8, dtype=np.uint32))) & 15).reshape(n, k).astype(np.float32)
+        z = np.repeat(zeros.reshape(n, k // 128), 128, axis=1).astype(np.float32)
+        w = ((q - z) * np.repeat(sc.reshape(n, k // 128), 128, axis=1).astype(np.float32)).astype(np.float16)
+        scales = sc.view(np.uint16)
+    else:
+        codes = rng.integers(-127, 128, n * k).astype(np.int8)
+        c = codes.reshape(n, k).astype(np.float32)
+        if fmt == orc.FMT_Q8:
+            scales = (np.abs(rng.standard_normal(n)) * 0.01).astype(np.float32)
+            w = c.astype(np.float16)
+        elif fmt == orc.FMT_Q8B:
+            sc = (np.abs(rng.standard_normal(n * k // 32)) * 0.02).astype(np.float16)
+            w = (c * np.repeat(sc.reshape(n, k // 32), 32, axis=1).astype(np.float32)).astype(np.float16)
+            scales = sc.view(np.uint16)
+        else:
+            scales = (np.abs(rng.standard_normal(n * k // 32)) * 0.02).astype(np.float32)
+            w = (c * np.repeat(scales.reshape(n, k // 32), 32, axis=1)).astype(np.float16)
+    xh = x.astype(np.float16).astype(np.float64).reshape(m, k)
+    want = xh @ w.astype(np.float64).T
+    if fmt == orc.FMT_Q8:
+        want = want * scales.astype(np.float64)[None, :]
+    got, absum = orc.mm_f64(fmt, codes, scales, x, m, k, n, zeros=zeros if fmt == orc.FMT_GPTQ4_G128 else None)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+    assert np.all(absum >= np.abs(got) * (1 - 1e-12))

@@ -153,6 +153,34 @@ def test_decode_oracle_matches_transformers_qwen3(fmt):
         assert nxt == int(np.argmax(logits[pos])) or np.sort(logits[pos])[-1] - np.sort(logits[pos])[-2] < 1e-3
 
 
+@pytest.mark.parametrize("fmt", [lo.FMT_Q8B, lo.FMT_Q8])
+def test_batched_prefill_oracle_matches_stepping_and_transformers(fmt):
+    """The batched-pass restatement (DecodeOracle.prefill) against the
+    token-by-token step and against transformers' own batched causal pass,
+    with the prompt split into two passes (the second continuing the cache)."""
+    torch = pytest.importorskip("torch")
+    model = lc.random_model(lc.GPU_SHAPE, fmt, seed=21 + fmt)
+    g = model["geom"]
+    orc_ = lc.oracle_for(model)
+    tokens = [7, 1, 88, 88, 30, 2, 64, 11, 5, 93, 40]
+    split = 4
+    c1 = orc_.new_cache(16)
+    h1 = np.concatenate([orc_.prefill(c1, 0, tokens[:split]), orc_.prefill(c1, split, tokens[split:])])
+    c2 = orc_.new_cache(16)
+    for pos, t in enumerate(tokens):
+        h2 = orc_.layers(c2, pos, orc_.embed_row(t))
+        assert np.abs(h1[pos] - h2).max() <= 1e-9 * np.abs(h2).max(), pos
+    for (k1, v1), (k2, v2) in zip(c1, c2):
+        assert np.abs(k1 - k2).max() <= 1e-9 * np.abs(k2).max()
+        assert np.abs(v1 - v2).max() <= 1e-9 * np.abs(v2).max()
+    hf = _hf_model(model)
+    with torch.no_grad():
+        hid = hf.model(torch.tensor([tokens])).last_hidden_state[0].numpy()
+    for pos in range(len(tokens)):
+        hidden, _ = orc_.finish(h1[pos])
+        assert np.linalg.norm(hidden - hid[pos]) / np.linalg.norm(hid[pos]) < 2e-5, pos
+
+
 def test_rope_table_matches_transformers():
     torch = pytest.importorskip("torch")
     tr = pytest.importorskip("transformers")
