@@ -39,8 +39,9 @@ def parse():
     ap.add_argument("--decode-fmt", choices=["q8b", "q8b_f32", "q8", "q4"], default="q8b",
                     help="layer weight format of the decode models (the reference's decode batch uses Q8B)")
     ap.add_argument("--decode-eager", action="store_true", help="launch decode steps without the HIP graph")
-    ap.add_argument("--decode-configs", default="3,4b1,4b16",
-                    help="decode lines to run: 3 (Qwen3-0.6B), 4b1 / 4b16 (Qwen3-8B, 1 / 16 lanes)")
+    ap.add_argument("--decode-configs", default="3,4a,4b1,4b16",
+                    help="model lines to run: 3 (Qwen3-0.6B decode), 4a (Qwen3-8B 4096-token prefill), "
+                    "4b1 / 4b16 (Qwen3-8B decode, 1 / 16 lanes)")
     return ap.parse_args()
 
 
@@ -304,7 +305,7 @@ def decode_model(torch, gphq, geom, fmt, seed):
 
 def decode_config(torch, gphq, lm, weight_bytes, geom, lanes, ctx, steps, warmup, graph, label):
     """Greedy decode of `steps` tokens per lane at context `ctx` (the K/V
-    cache prefilled by teacher-forced steps over random ids, lane 0's prefix
+    cache prefilled by the batched pass over random ids, lane 0's prefix
     copied to the others), timed with HIP events on the launch stream."""
     stream = torch.cuda.current_stream()
     ws = gphq.DecodeBatch(lm, lanes)
@@ -313,7 +314,10 @@ def decode_config(torch, gphq, lm, weight_bytes, geom, lanes, ctx, steps, warmup
     kvs = [gphq.Prefix(lm, cap) for _ in range(lanes)]
     rng = np.random.default_rng(ctx + lanes)
     t0 = time.perf_counter()
-    ws.extend(kvs[:1], [0], rng.integers(0, geom["vocab"], (ctx, 1)))
+    pf = gphq.Prefill(lm, ctx)  # the batched pass fills lane 0's cache
+    pf.extend(kvs[0], 0, rng.integers(0, geom["vocab"], ctx), torch.empty(geom["hidden"], device="cuda"))
+    pf.check()
+    del pf
     for kv in kvs[1:]:
         kv.copy_from(kvs[0], ctx)
     torch.cuda.synchronize()
@@ -351,6 +355,48 @@ def decode_config(torch, gphq, lm, weight_bytes, geom, lanes, ctx, steps, warmup
     }
 
 
+def prefill_config(torch, gphq, lm, geom, tokens, reps, label):
+    """Config 4a: one `tokens`-token prompt evaluated by the batched pass
+    (gphq_prefill_extend, one pass of `tokens` rows) into a fresh prefix, timed
+    with HIP events on the launch stream over `reps` prefills after one
+    untimed prefill. FLOPs are algorithmic: 2 per weight per token for the
+    projections, 4 * head_dim per (query head, visible key) for attention."""
+    stream = torch.cuda.current_stream()
+    ws = gphq.Prefill(lm, tokens)
+    kv = gphq.Prefix(lm, tokens)
+    rng = np.random.default_rng(tokens)
+    ids = rng.integers(0, geom["vocab"], tokens)
+    hidden = torch.empty(geom["hidden"], device="cuda")
+    ws.extend(kv, 0, ids, hidden)
+    ws.check()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        ws.extend(kv, 0, ids, hidden)
+    e1.record(stream)
+    ws.check()
+    ms = e0.elapsed_time(e1) / reps
+    H, I, L = geom["hidden"], geom["intermediate"], geom["layers"]
+    qd, kvd = geom["heads"] * 128, geom["kv_heads"] * 128
+    weights = L * (H * (qd + 2 * kvd) + qd * H + H * 2 * I + I * H)
+    proj = 2.0 * weights * tokens
+    attn = 4.0 * 128 * geom["heads"] * L * tokens * (tokens + 1) / 2
+    tf = (proj + attn) / (ms / 1e3) / 1e12
+    return {
+        "workload": label,
+        "tokens": tokens,
+        "reps": reps,
+        "ms": round(ms, 3),
+        "tokens_per_s": round(tokens / (ms / 1e3), 1),
+        "tflops": round(tf, 1),
+        "fp16_mfma_frac": round(tf / FP16_PEAK_TFLOPS, 4),
+        "projection_tflop": round(proj / 1e12, 3),
+        "attention_tflop": round(attn / 1e12, 3),
+        "arithmetic": "FP16 weight/activation tiles, fp32 accumulate (the reference mm); FP16 attention tiles",
+        "finite": bool(torch.isfinite(hidden).all().item()),
+    }
+
+
 def decode_benchmarks(args, torch, gphq):
     fmt = {"q8b": gphq.FMT_Q8B, "q8b_f32": gphq.FMT_Q8B_F32, "q8": gphq.FMT_Q8, "q4": gphq.FMT_Q4}[args.decode_fmt]
     graph = not args.decode_eager
@@ -362,8 +408,11 @@ def decode_benchmarks(args, torch, gphq):
                                        "config 3: Qwen3-0.6B-shaped, batch 1, 1024-token K/V prefill, 256 greedy steps")
         del lm
         torch.cuda.empty_cache()
-    if want & {"4b1", "4b16"}:
+    if want & {"4a", "4b1", "4b16"}:
         lm, wb = decode_model(torch, gphq, QWEN3_8B, fmt, 4)
+        if "4a" in want:
+            res["config4a"] = prefill_config(torch, gphq, lm, QWEN3_8B, 4096, 3,
+                                             "config 4a: Qwen3-8B-shaped 4096-token prefill, one batched pass")
         if "4b1" in want:
             res["config4b_1"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 1, 4096, 64, 8, graph,
                                               "config 4b: Qwen3-8B-shaped decode at context 4096, 1 lane")
@@ -481,6 +530,7 @@ def main():
         "gemm_config2": gemm,
         "gptq_config5": gptq,
         "decode_ms_per_token": (decode or {}).get("config4b_1", {}).get("ms_per_step"),
+        "prefill_4096_ms": (decode or {}).get("config4a", {}).get("ms"),
         "decode": decode,
         "check": {"rel_l2_vs_float64": r["rel_l2"]},
     }

@@ -175,6 +175,10 @@ __device__ __forceinline__ void epilogue(const F16GemmArgs &a, const f32x4 &acc,
     for (int e = 0; e < 4; ++e) {
         const int row = row0 + e;
         float v = acc[e];
+        // The qwen3lm pass's row scale 2^-e (exact); rows past M read row 0.
+        if constexpr (EPI != EPI_PANELS) {
+            if (a.rowInv) v = __fmul_rn(v, a.rowInv[row < a.M ? row : 0]);
+        }
         if constexpr (EPI == EPI_SWIGLU) {
             if (a.colScale) v = __fmul_rn(v, cs);
             const float u = __shfl_xor(v, 1);
@@ -524,10 +528,13 @@ __device__ __forceinline__ void f16_row_scale(float m, float &scale, float &inv)
 // One block per row. mode 0: q8gemm Workspace.Pack (power-of-two row scale from
 // MaxAbs, then f16(x * scale)); mode 1: qwen3lm mm activations, half(x);
 // mode 2: PackRange with the row scales already on the device, converting only
-// columns [k0, k1) (and the K padding when k1 == K); mode 3: the qwen3lm
-// PRO_NORM prologue (gpu.metal:785-796, 825-826), half(x * f) with
-// f = 1/sqrt(sum(x^2)/K + eps). Writes the FP16 tile layout; modes 0, 1 and 3
-// convert whole rows and zero the K padding.
+// columns [k0, k1) (and the K padding when k1 == K); modes 3 and 4: the
+// qwen3lm batched pass's activations, half(x * f * 2^e) with f = 1 (mode 4) or
+// the PRO_NORM factor f = 1/sqrt(sum(x^2)/K + eps) (mode 3, gpu.metal:785-796,
+// 825-826), and e placing the row's max |x * f| in [2^14, 2^15) (the q8gemm
+// row scale rule, gemm.go:127-135); rowInv[row] = 2^-e scales the row's sums
+// back. Writes the FP16 tile layout; modes 0, 1, 3 and 4 convert whole rows
+// and zero the K padding.
 __global__ __launch_bounds__(256) void f16_act_pack_kernel(const float *__restrict__ x, long stride, int K, int kt,
                                                            int mode, int k0, int k1, float eps,
                                                            _Float16 *__restrict__ act, float *__restrict__ rowScale,
@@ -537,17 +544,26 @@ __global__ __launch_bounds__(256) void f16_act_pack_kernel(const float *__restri
     const int row = blockIdx.x;
     const float *xr = x + (size_t)row * stride;
     float scale = 1.0f, inv = 1.0f;
-    if (mode == 3) {
-        float ss = 0.0f;
+    if (mode == 3 || mode == 4) {
+        __shared__ float sss[4];
+        float ss = 0.0f, mx = 0.0f;
         for (int k = 4 * (int)threadIdx.x; k < K; k += 1024) {
             const float4 v = *(const float4 *)(xr + k);
             ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            mx = fmaxf(fmaxf(fmaxf(mx, fabsf(v.x)), fmaxf(fabsf(v.y), fabsf(v.z))), fabsf(v.w));
         }
         ss = wave_sum(ss);
-        if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = ss;
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        if ((threadIdx.x & 63) == 0) {
+            sss[threadIdx.x >> 6] = ss;
+            smax[threadIdx.x >> 6] = mx;
+        }
         __syncthreads();
-        const float t = (smax[0] + smax[1]) + (smax[2] + smax[3]);
-        scale = 1.0f / sqrtf(t / (float)K + eps);
+        const float f = mode == 3 ? 1.0f / sqrtf(((sss[0] + sss[1]) + (sss[2] + sss[3])) / (float)K + eps) : 1.0f;
+        float rs;
+        f16_row_scale(fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])) * f, rs, inv);
+        scale = f * rs;
+        if (threadIdx.x == 0) rowInv[row] = inv;
     } else if (mode == 0) {
         float m = 0.0f;
         int nan = 0;
@@ -621,24 +637,25 @@ int f16_act_pack(const float *x, long stride, int rows, int K, int kt, int mode,
     return launch_status();
 }
 
-// The qwen3lm batched pass's activation tiles: half(x) (norm false) or the
-// RMS-normalized half(x * f) (norm true). x rows are `stride` floats apart,
-// 16-byte aligned, K % 4 == 0.
-int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, _Float16 *act,
+// The qwen3lm batched pass's activation tiles, half(x * f * 2^e) with f the
+// RMSNorm factor (norm true) or 1, and rowInv[r] = 2^-e per row. x rows are
+// `stride` floats apart, 16-byte aligned, K % 4 == 0.
+int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, _Float16 *act, float *rowInv,
                 hipStream_t stream) {
     if (rows == 0) return GPHQ_OK;
     const int kt = (K + 63) / 64;
-    hipLaunchKernelGGL(f16_act_pack_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, norm ? 3 : 1, 0, K,
-                       eps, act, nullptr, nullptr);
+    hipLaunchKernelGGL(f16_act_pack_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, norm ? 3 : 4, 0, K,
+                       eps, act, nullptr, rowInv);
     return launch_status();
 }
 
 // One projection of the qwen3lm batched pass over M activation rows packed
-// by lm_act_pack: epi 0 stores y[M][N], 1 adds into y, 2 stores the SwiGLU of
-// interleaved gate/up columns into y[M][N/2]; y rows are y_stride floats
-// apart. fmt is a GPHQ_FMT_* layer format. Arguments were validated.
-int lm_mm_launch(int fmt, int epi, const void *codes, const void *scales, const _Float16 *act, float *y,
-                 long y_stride, int M, int K, int N, hipStream_t stream) {
+// by lm_act_pack (row sums scaled by rowInv): epi 0 stores y[M][N], 1 adds
+// into y, 2 stores the SwiGLU of interleaved gate/up columns into y[M][N/2];
+// y rows are y_stride floats apart. fmt is a GPHQ_FMT_* layer format.
+// Arguments were validated.
+int lm_mm_launch(int fmt, int epi, const void *codes, const void *scales, const _Float16 *act, const float *rowInv,
+                 float *y, long y_stride, int M, int K, int N, hipStream_t stream) {
     F16GemmArgs a{};
     int wf;
     switch (fmt) {
@@ -658,6 +675,7 @@ int lm_mm_launch(int fmt, int epi, const void *codes, const void *scales, const 
     a.B = codes;
     a.bScale = scales;
     a.colScale = q8 ? (const float *)scales : nullptr;
+    a.rowInv = rowInv;
     a.dst = y;
     a.stride = y_stride;
     a.M = M;

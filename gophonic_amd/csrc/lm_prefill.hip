@@ -32,10 +32,10 @@
 namespace gphq {
 int gemv_fused_launch(int fmt, int pro, int epi, const void *codes, const void *scales, const float *x, float *y,
                       int K, int N, float eps, hipStream_t stream);
-int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, _Float16 *act,
+int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, _Float16 *act, float *rowInv,
                 hipStream_t stream);
-int lm_mm_launch(int fmt, int epi, const void *codes, const void *scales, const _Float16 *act, float *y,
-                 long y_stride, int M, int K, int N, hipStream_t stream);
+int lm_mm_launch(int fmt, int epi, const void *codes, const void *scales, const _Float16 *act, const float *rowInv,
+                 float *y, long y_stride, int M, int K, int N, hipStream_t stream);
 }  // namespace gphq
 
 using namespace gphq;
@@ -45,6 +45,7 @@ struct gphq_prefill {
     int rows;  // tokens per pass, at most
     float *h, *qkv, *ctx, *act, *hn;
     _Float16 *a16;  // FP16 activation tiles [rows/16][K/64][64][16]
+    float *rinv;    // per-row 2^-e of the activation tiles
     int32_t *tok, *nonfinite;
     std::vector<void *> allocs;
 };
@@ -309,8 +310,9 @@ int project(gphq_prefill *ws, int R, int pro, int epi, const uint8_t *buf, int64
     const gphq_lm_config &c = ws->lm->cfg;
     const float eps = (float)c.eps;
     if (R == 1) return gemv_fused_launch(c.fmt, pro, epi, buf + codes, buf + scales, x, y, (int)K, (int)N, eps, st);
-    GPHQ_TRY(lm_act_pack(x, (long)K, R, (int)K, pro == PRO_NORM, eps, ws->a16, st));
-    return lm_mm_launch(c.fmt, epi, buf + codes, buf + scales, ws->a16, y, (long)ystride, R, (int)K, (int)N, st);
+    GPHQ_TRY(lm_act_pack(x, (long)K, R, (int)K, pro == PRO_NORM, eps, ws->a16, ws->rinv, st));
+    return lm_mm_launch(c.fmt, epi, buf + codes, buf + scales, ws->a16, ws->rinv, y, (long)ystride, R, (int)K, (int)N,
+                        st);
 }
 
 // One pass: rows tokens already in ws->tok, continuing kv at cache row base.
@@ -392,6 +394,7 @@ int gphq_prefill_new(const gphq_lm *lm, int64_t rows, gphq_prefill **out) {
         {(void **)&ws->ctx, (size_t)rows * lm->qd * 4}, {(void **)&ws->act, (size_t)rows * I * 4},
         {(void **)&ws->hn, (size_t)H * 4},            {(void **)&ws->a16, (size_t)rpad * kpad * 2},
         {(void **)&ws->tok, (size_t)rows * 4},        {(void **)&ws->nonfinite, 4},
+        {(void **)&ws->rinv, (size_t)rows * 4},
     };
     for (auto &b : bufs) {
         const hipError_t e = hipMalloc(b.dst, b.bytes);
