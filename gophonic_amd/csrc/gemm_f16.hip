@@ -13,7 +13,7 @@
 //  * the qwen3lm batched pass's projections (mm_qkv / mm_o / mm_gateup /
 //    mm_down, gpu.metal:994-1025): the same tiles with the residual-add and
 //    SwiGLU epilogues (gpu.metal:897-927), and Q8B with fp32 block scales
-//    (half(code * d), one rounding).
+//    (half(code) * half(d), as Q8B once the scale is rounded to FP16).
 //
 // Fragments: lane l of a 16x64 K step holds row (l % 16), columns
 // (l / 16) * 16 .. +16 of both operands (16 FP16 values = two 8-value MFMA
@@ -30,6 +30,7 @@ namespace gphq {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 enum WFmt {
     W_I8_TILE = 0,    // q8gemm int8 weights, tile layout (1 KiB groups)
@@ -61,15 +62,7 @@ struct F16GemmArgs {
 };
 
 __device__ __forceinline__ _Float16 i8h(uint32_t v, int i) { return (_Float16)(int)((int32_t)(v << (24 - 8 * i)) >> 24); }
-__device__ __forceinline__ float i8f(uint32_t v, int i) { return (float)((int32_t)(v << (24 - 8 * i)) >> 24); }
-// half of the fp32 value x. The asm barrier keeps a product feeding x a
-// separate fp32 multiply: without it the backend fuses multiply and convert
-// (v_fma_mix), which rounds the exact product to half once instead of the
-// fp32 product.
-__device__ __forceinline__ _Float16 f32_to_half(float x) {
-    asm volatile("" : "+v"(x));
-    return (_Float16)x;
-}
+
 
 // B fragment: 16 FP16 weights of row `n` (clamped in range), K step kt, lane
 // group g (values k = kt*64 + g*16 + 0..15), decoded per format.
@@ -108,16 +101,16 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
         }
     } else if constexpr (WF == W_Q8BF_ROW) {
         u32x4 w = u32x4{0, 0, 0, 0};
-        float d = 0.0f;
+        _Float16 d = (_Float16)0.0f;
         if (k < a.K) {
             w = __builtin_nontemporal_load((const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k));
-            d = ((const float *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
+            d = (_Float16)((const float *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
         }
         const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) lo[i] = f32_to_half(i8f(ww[i >> 2], i & 3) * d);
+        for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3) * d;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) hi[i] = f32_to_half(i8f(ww[2 + (i >> 2)], i & 3) * d);
+        for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3) * d;
     } else if constexpr (WF == W_Q4_ROW) {
         // Block (k / 32) is 16 bytes: value j in the low nibble of byte j,
         // value j + 16 in the high nibble; this lane needs half (k / 16) % 2.
@@ -319,69 +312,112 @@ __device__ __forceinline__ RawB load_raw(const F16GemmArgs &a, int n, int kt, in
     return r;
 }
 
+// Four int8 codes (one dword) as FP16 pairs (c0, c1), (c2, c3), exactly:
+// v_perm_b32 places each code + 128 (the xor) under the exponent byte 0x64,
+// giving 1024 + 128 + c, and one packed subtraction leaves c.
+__device__ __forceinline__ void i8x4_to_h(uint32_t w, f16x2 &p0, f16x2 &p1) {
+    const uint32_t u = w ^ 0x80808080u;
+    const f16x2 off = f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
+    p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - off;
+    p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - off;
+}
+// Four nibbles in the low halves of the bytes of w (w & 0x0F0F0F0F) as FP16
+// pairs (n - 8).
+__device__ __forceinline__ void n4x4_to_h(uint32_t w, f16x2 &p0, f16x2 &p1) {
+    const f16x2 off = f16x2{(_Float16)1032.0f, (_Float16)1032.0f};
+    p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) - off;
+    p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)) - off;
+}
+__device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
+    return __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // The same FP16 values as load_b: Q8 half(code); Q8B half(code) * d; Q8B
-// with fp32 scales half(code * d); Q4 (half(nib) - 8) * d; GPTQ
-// (half(nib) - half(z)) * s, each rounded to half.
+// with fp32 scales half(code) * half(d); Q4 (half(nib) - 8) * d; GPTQ
+// (half(nib) - half(z)) * s, each product rounded to half once (packed FP16
+// multiplies round like the scalar ones).
 template <int WF>
 __device__ __forceinline__ void dequant(const RawB &r, int g, f16x8 &lo, f16x8 &hi) {
-    const uint32_t ww[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
-    if constexpr (WF == W_Q8_ROW) {
+    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q8BF_ROW) {
+        f16x2 p[8];
+        i8x4_to_h(r.w.x, p[0], p[1]);
+        i8x4_to_h(r.w.y, p[2], p[3]);
+        i8x4_to_h(r.w.z, p[4], p[5]);
+        i8x4_to_h(r.w.w, p[6], p[7]);
+        if constexpr (WF != W_Q8_ROW) {
+            _Float16 d;
+            if constexpr (WF == W_Q8B_ROW)
+                d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
+            else
+                d = (_Float16)__builtin_bit_cast(float, r.sz);
+            const f16x2 dd = f16x2{d, d};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3);
-    } else if constexpr (WF == W_Q8B_ROW) {
-        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3) * d;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3) * d;
-    } else if constexpr (WF == W_Q8BF_ROW) {
-        const float d = __builtin_bit_cast(float, r.sz);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) lo[i] = f32_to_half(i8f(ww[i >> 2], i & 3) * d);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hi[i] = f32_to_half(i8f(ww[2 + (i >> 2)], i & 3) * d);
+            for (int i = 0; i < 8; ++i) p[i] = p[i] * dd;
+        }
+        lo = cat4(p[0], p[1], p[2], p[3]);
+        hi = cat4(p[4], p[5], p[6], p[7]);
     } else if constexpr (WF == W_Q4_ROW) {
         const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
+        const f16x2 dd = f16x2{d, d};
         const int sh = (g & 1) * 4;
+        f16x2 p[8];
+        n4x4_to_h((r.w.x >> sh) & 0x0F0F0F0Fu, p[0], p[1]);
+        n4x4_to_h((r.w.y >> sh) & 0x0F0F0F0Fu, p[2], p[3]);
+        n4x4_to_h((r.w.z >> sh) & 0x0F0F0F0Fu, p[4], p[5]);
+        n4x4_to_h((r.w.w >> sh) & 0x0F0F0F0Fu, p[6], p[7]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            lo[i] = ((_Float16)(int)((ww[i >> 2] >> (8 * (i & 3) + sh)) & 15) - (_Float16)8.0f) * d;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            hi[i] = ((_Float16)(int)((ww[2 + (i >> 2)] >> (8 * (i & 3) + sh)) & 15) - (_Float16)8.0f) * d;
+        for (int i = 0; i < 8; ++i) p[i] = p[i] * dd;
+        lo = cat4(p[0], p[1], p[2], p[3]);
+        hi = cat4(p[4], p[5], p[6], p[7]);
     } else {
         const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
         const _Float16 z = (_Float16)(int)(r.sz >> 16);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) lo[i] = ((_Float16)(int)((ww[0] >> (4 * i)) & 15) - z) * s;
+        for (int i = 0; i < 8; ++i) lo[i] = ((_Float16)(int)((r.w.x >> (4 * i)) & 15) - z) * s;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) hi[i] = ((_Float16)(int)((ww[1] >> (4 * i)) & 15) - z) * s;
+        for (int i = 0; i < 8; ++i) hi[i] = ((_Float16)(int)((r.w.y >> (4 * i)) & 15) - z) * s;
     }
 }
 
-// Block tile (32*WTM) x (32*WTN), four wavefronts as 2 x 2, each
-// (16*WTM) x (16*WTN) of the output. Per 64-deep K step the block's threads
-// dequantize the B tile once into LDS in MFMA fragment order (tile j, lane
-// slot g*16 + n%16, 16 values), double-buffered; the raw codes of step kt+1
-// are loaded before the MFMAs of step kt run and written to the other buffer
-// after them, with one barrier per step. A fragments come straight from the
-// FP16 tile layout (two 16-byte loads per lane and tile), one step ahead.
-template <int WF, int EPI, int WTM, int WTN>
-__global__ __launch_bounds__(256) void f16gemm_lds_kernel(const F16GemmArgs a) {
-    constexpr int BN16 = 2 * WTN;                      // 16-row B tiles per block
-    constexpr int PAIRS = BN16 * 64 / 256;             // (row, lane group) pairs per thread and step
+// Block b's output tile (bm, bn). Workgroups are dispatched to the 8 XCDs
+// round robin, so XCD x = b % 8 runs blocks x, x + 8, ...; those take one
+// contiguous range of the tile order, and the order walks groups of 8 M
+// blocks for each N block, so the blocks an XCD runs at once share their A
+// rows and B columns in that XCD's L2.
+__device__ __forceinline__ void tile_order(int b, int gridM, int gridN, int &bm, int &bn) {
+    constexpr int GM = 8;
+    const int G = gridM * gridN;
+    const int L = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+    const int span = GM * gridN;
+    const int grp = L / span, first = grp * GM;
+    const int gm = min(gridM - first, GM);
+    const int r = L - grp * span;
+    bm = first + r % gm;
+    bn = r / gm;
+}
+
+// Block tile (16*WTM*WGM) x (32*WTN): 2*WGM wavefronts, WGM along M and 2
+// along N, each (16*WTM) x (16*WTN) of the output. Per 64-deep K step the
+// block's threads dequantize the B tile once into LDS in MFMA fragment order
+// (tile j, lane slot g*16 + n%16, 16 values), double-buffered; the raw codes
+// of step kt+1 are loaded before the MFMAs of step kt run and written to the
+// other buffer after them, with one barrier per step. A fragments come
+// straight from the FP16 tile layout (two 16-byte loads per lane and tile),
+// one step ahead.
+template <int WF, int EPI, int WTM, int WTN, int WGM>
+__global__ __launch_bounds__(128 * WGM) void f16gemm_lds_kernel(const F16GemmArgs a) {
+    constexpr int NT = 128 * WGM;
+    constexpr int BN16 = 2 * WTN;           // 16-row B tiles per block
+    constexpr int PAIRS = BN16 * 64 / NT;   // (row, lane group) pairs per thread and step
+    static_assert(PAIRS >= 1 && PAIRS * NT == BN16 * 64, "B tile pairs divide over the block");
     __shared__ f16x8 bs[2][BN16][64][2];
-    const int G = a.gridM * a.gridN;
-    const int b = blockIdx.x;
-    int logical = b;
-    if (G % 8 == 0) logical = (b % 8) * (G / 8) + b / 8;  // blocks of one XCD take neighbouring tiles
-    const int bm = logical % a.gridM, bn = logical / a.gridM;
+    int bm, bn;
+    tile_order(blockIdx.x, a.gridM, a.gridN, bm, bn);
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int wm = wv >> 1, wn = wv & 1;
-    const int mt0 = (bm * 2 + wm) * WTM;
+    const int mt0 = (bm * WGM + wm) * WTM;
     const int nt0 = a.tileN0 + bn * BN16;
     const int MT = (a.M + 15) >> 4;
     const int KT = a.KT;
@@ -392,7 +428,7 @@ __global__ __launch_bounds__(256) void f16gemm_lds_kernel(const F16GemmArgs a) {
     int pn[PAIRS], pg[PAIRS], pt[PAIRS], ps[PAIRS];
 #pragma unroll
     for (int q = 0; q < PAIRS; ++q) {
-        const int p = threadIdx.x + 256 * q;
+        const int p = threadIdx.x + NT * q;
         pt[q] = p >> 6;
         ps[q] = p & 63;
         pg[q] = ps[q] >> 4;
@@ -452,13 +488,13 @@ __global__ __launch_bounds__(256) void f16gemm_lds_kernel(const F16GemmArgs a) {
             epilogue<EPI>(a, acc[i][j], (mt0 + i) * 16 + 4 * (lane >> 4), (nt0 + wn * WTN + j) * 16 + (lane & 15));
 }
 
-template <int WF, int EPI, int WTM, int WTN>
+template <int WF, int EPI, int WTM, int WTN, int WGM>
 static int launch_f16gemm_lds(F16GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
     a.gridN = (tiles + 2 * WTN - 1) / (2 * WTN);
-    a.gridM = (a.M + 32 * WTM - 1) / (32 * WTM);
-    hipLaunchKernelGGL((f16gemm_lds_kernel<WF, EPI, WTM, WTN>), dim3((unsigned)(a.gridM * a.gridN)), dim3(256), 0,
-                       stream, a);
+    a.gridM = (a.M + 16 * WTM * WGM - 1) / (16 * WTM * WGM);
+    hipLaunchKernelGGL((f16gemm_lds_kernel<WF, EPI, WTM, WTN, WGM>), dim3((unsigned)(a.gridM * a.gridN)),
+                       dim3(128 * WGM), 0, stream, a);
     return launch_status();
 }
 
@@ -472,15 +508,158 @@ static int launch_f16gemm(F16GemmArgs a, hipStream_t stream) {
     return launch_status();
 }
 
+// ---- 256 x 256 block tiles (qwen3lm row formats, large M) --------------------
+// Four wavefronts as 2 x 2, each 128 x 128 of the output as 4 x 4 tiles of
+// v_mfma_f32_32x32x16_f16. Per 64-deep K step both operands pass through LDS
+// (FP16, 128 bytes per row, 16-byte chunks swizzled by the row so the
+// fragment reads of 8 or 16 consecutive rows hit distinct banks), double
+// buffered: step kt+1's global loads (A: FP16 tiles, B: raw codes) are issued
+// one step ahead into registers, written (B dequantized) to the other buffer
+// after step kt's MFMAs, with one barrier per step.
+//
+// MFMA operands: lane l holds row l % 32 of its matrix (A row m, or weight row
+// n) and k values 8*(l/32) .. +7 of the 16-deep sub-step; the result lane l
+// holds column n = l % 32, rows 8*(i/4) + 4*(l/32) + i%4 of acc[i].
+constexpr int kBigBM = 256, kBigBN = 256;
+#ifndef GPHQ_BIG_WGM
+#define GPHQ_BIG_WGM 4
+#define GPHQ_BIG_WGN 2
+#endif
+
+__device__ __forceinline__ int big_swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
+
+template <int WF, int EPI_T, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16GemmArgs a) {
+    typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int TI = kBigBM / WGM / 32, TJ = kBigBN / WGN / 32;  // 32x32 tiles per wave
+    constexpr int AL = kBigBM * 8 / NT;   // 16-byte A units per thread and step
+    constexpr int BL = kBigBN * 4 / NT;   // (row, 16 K values) B pieces per thread and step
+    static_assert(AL >= 1 && BL >= 1 && NT % 128 == 0, "loader split");
+    __shared__ f16x8v As[2][kBigBM * 8];
+    __shared__ f16x8v Bs[2][kBigBN * 8];
+    int bm, bn;
+    tile_order(blockIdx.x, a.gridM, a.gridN, bm, bn);
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int wm = wv / WGN, wn = wv % WGN;
+    const int m0 = bm * kBigBM, n0 = a.tileN0 * 16 + bn * kBigBN;
+    const int MT = (a.M + 15) >> 4, KT = a.KT;
+
+    // A loader: 2 KB groups (16 rows x 64 K) of the FP16 tile layout; load i
+    // of thread t is 16-byte unit u = i*NT + t: group u/128 (rows
+    // 16*group ..), slot (t%128)/2 (row slot%16, K values 16*(slot/16) +
+    // 8*(t%2) ..), the same slot for every i.
+    const int aslot = (t & 127) >> 1, achunk = 2 * (aslot >> 4) + (t & 1);
+    const _Float16 *abase = a.A + (size_t)(t & 127) * 8;
+    const int mtb = (m0 >> 4) + (t >> 7);
+    // B loader: piece i of thread t is row (i*NT + t)/4 of the tile, 16 K
+    // values at 16*(t%4) of the step.
+    const int bc = t & 3;
+
+    f16x8v ar[AL];
+    RawB br[BL];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < AL; ++i)
+            ar[i] = *(const f16x8v *)(abase + ((size_t)min(mtb + i * (NT / 128), MT - 1) * KT + kt) * 1024);
+#pragma unroll
+        for (int i = 0; i < BL; ++i)
+            br[i] = load_raw<WF>(a, min(n0 + ((i * NT + t) >> 2), a.N - 1), kt, bc);
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < AL; ++i) {
+            const int r = 16 * (i * (NT / 128) + (t >> 7)) + (aslot & 15);
+            As[buf][r * 8 + big_swz(r, achunk)] = ar[i];
+        }
+#pragma unroll
+        for (int i = 0; i < BL; ++i) {
+            f16x8 lo, hi;
+            dequant<WF>(br[i], bc, lo, hi);
+            const int r = (i * NT + t) >> 2;
+            Bs[buf][r * 8 + big_swz(r, 2 * bc)] = lo;
+            Bs[buf][r * 8 + big_swz(r, 2 * bc + 1)] = hi;
+        }
+    };
+
+    f32x16 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x16{};
+
+    gload(0);
+    lstore(0);
+    if (KT > 1) gload(1);
+    __syncthreads();
+    const int fr = lane & 31, fh = lane >> 5;
+    auto frags = [&](int buf, int s, f16x8v (&fa)[TI], f16x8v (&fb)[TJ]) {
+        const int c = 2 * s + fh;
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int r = wm * (32 * TI) + 32 * i + fr;
+            fa[i] = As[buf][r * 8 + big_swz(r, c)];
+        }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int r = wn * (32 * TJ) + 32 * j + fr;
+            fb[j] = Bs[buf][r * 8 + big_swz(r, c)];
+        }
+    };
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        f16x8v fa[2][TI], fb[2][TJ];
+        frags(cur, 0, fa[0], fb[0]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (s < 3) frags(cur, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[s & 1][i], fb[s & 1][j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < KT) {
+            lstore(cur ^ 1);
+            if (kt + 2 < KT) gload(kt + 2);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                epilogue<EPI_T>(a, f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]},
+                                m0 + wm * (32 * TI) + 32 * i + 8 * q + 4 * fh, n0 + wn * (32 * TJ) + 32 * j + fr);
+}
+
+template <int WF, int EPI>
+static int launch_f16gemm_big(F16GemmArgs a, hipStream_t stream) {
+    a.gridN = (a.c1 - a.tileN0 * 16 + kBigBN - 1) / kBigBN;
+    a.gridM = (a.M + kBigBM - 1) / kBigBM;
+    hipLaunchKernelGGL((f16gemm_big_kernel<WF, EPI, GPHQ_BIG_WGM, GPHQ_BIG_WGN>), dim3((unsigned)(a.gridM * a.gridN)),
+                       dim3(64 * GPHQ_BIG_WGM * GPHQ_BIG_WGN), 0, stream, a);
+    return launch_status();
+}
+
 template <int WF, int EPI>
 static int launch_by_m(const F16GemmArgs &a, hipStream_t stream) {
     if (a.M <= 16) return launch_f16gemm<WF, EPI, 1, 2, 1, 2, 4, 2>(a, stream);
     if (a.M <= 64) return launch_f16gemm<WF, EPI, 4, 1, 1, 2, 4, 2>(a, stream);
+    if constexpr (WF != W_I8_TILE && WF != W_F16_TILE && WF != W_GPTQ_ROW) {
+        // 256 x 256 block tiles when they fill the chip.
+        const long big = (long)((a.M + kBigBM - 1) / kBigBM) * ((a.c1 - a.tileN0 * 16 + kBigBN - 1) / kBigBN);
+        if (a.M >= 512 && big >= 256) return launch_f16gemm_big<WF, EPI>(a, stream);
+    }
     if constexpr (WF != W_I8_TILE && WF != W_F16_TILE) {
-        // 128 x 128 block tiles when they fill the chip, else 128 x 64.
-        const long big = (long)((a.M + 127) / 128) * (((a.c1 + 15) / 16 - a.tileN0 + 7) / 8);
-        if (big >= 256) return launch_f16gemm_lds<WF, EPI, 4, 4>(a, stream);
-        return launch_f16gemm_lds<WF, EPI, 4, 2>(a, stream);
+        // 256 x 128 block tiles when they fill the chip, else 128 x 128 or 128 x 64.
+        const long ntiles = ((a.c1 + 15) / 16 - a.tileN0 + 7) / 8;
+        if ((long)((a.M + 255) / 256) * ntiles >= 256) return launch_f16gemm_lds<WF, EPI, 4, 4, 4>(a, stream);
+        if ((long)((a.M + 127) / 128) * ntiles >= 256) return launch_f16gemm_lds<WF, EPI, 4, 4, 2>(a, stream);
+        return launch_f16gemm_lds<WF, EPI, 4, 2, 2>(a, stream);
     }
     return launch_f16gemm<WF, EPI, 4, 2, 2, 2, 1, 1>(a, stream);
 }

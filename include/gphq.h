@@ -313,8 +313,8 @@ int gphq_q8gemm_mul_into(float *dst_dev, int64_t dst_len, const float *x_dev, in
  * each K step's weights dequantized to FP16 (Q8: half(code); Q8B:
  * half(code)*half(d); Q4: (half(nib)-8)*d, each rounded to half), activations
  * half(x), fp32 accumulation, and Q8 rows scaled by their fp32 scale after
- * the sum. fmt: GPHQ_FMT_Q8, GPHQ_FMT_Q8B, GPHQ_FMT_Q8B_F32 (half(code*d)
- * from the fp32 product), GPHQ_FMT_Q4, or
+ * the sum. fmt: GPHQ_FMT_Q8, GPHQ_FMT_Q8B, GPHQ_FMT_Q8B_F32 (half(code) *
+ * half(d): the Q8B tile once the scale is rounded to FP16), GPHQ_FMT_Q4, or
  * GPHQ_FMT_GPTQ4_G128: int32 codes [N][K/8] (nibble i of word j holds k = 8j+i,
  * unsigned 0..15), FP16 scales [N][K/128] and zero points zeros_dev
  * u8 [N][K/128] (low nibble), w = (q - z) * s -- the 4-bit group-128

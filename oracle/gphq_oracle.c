@@ -564,13 +564,13 @@ static float mm_weight(int fmt, const void *codes, const void *scales, const uin
         float c = (float)((const int8_t *)codes)[row * k + i];
         return orc_f16_to_f32(orc_f32_to_f16(c * d));
     }
-    if (fmt == 10) { /* Q8B with fp32 block scales: half(code * d), the fp32 product rounded once */
-        float d = ((const float *)scales)[row * (k / 32) + i / 32];
+    if (fmt == 10) { /* Q8B with fp32 block scales: half(code) * half(d), rounded to half */
+        float d = orc_f16_to_f32(orc_f32_to_f16(((const float *)scales)[row * (k / 32) + i / 32]));
         float c = (float)((const int8_t *)codes)[row * k + i];
         return orc_f16_to_f32(orc_f32_to_f16(c * d));
     }
-    if (fmt == 10) { /* Q8B with fp32 block scales: half(code * d), the fp32 product rounded once */
-        float d = ((const float *)scales)[row * (k / 32) + i / 32];
+    if (fmt == 10) { /* Q8B with fp32 block scales: half(code) * half(d), rounded to half */
+        float d = orc_f16_to_f32(orc_f32_to_f16(((const float *)scales)[row * (k / 32) + i / 32]));
         float c = (float)((const int8_t *)codes)[row * k + i];
         return orc_f16_to_f32(orc_f32_to_f16(c * d));
     }

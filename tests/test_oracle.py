@@ -361,7 +361,8 @@ def test_mm_f64_matches_numpy_fp16_tiles(fmt):
             scales = sc.view(np.uint16)
         else:
             scales = (np.abs(rng.standard_normal(n * k // 32)) * 0.02).astype(np.float32)
-            w = (c * np.repeat(scales.reshape(n, k // 32), 32, axis=1)).astype(np.float16)
+            hs = scales.astype(np.float16).astype(np.float32)
+            w = (c * np.repeat(hs.reshape(n, k // 32), 32, axis=1)).astype(np.float16)
     xh = x.astype(np.float16).astype(np.float64).reshape(m, k)
     want = xh @ w.astype(np.float64).T
     if fmt == orc.FMT_Q8:
