@@ -707,43 +707,18 @@ __device__ __forceinline__ void f16_row_scale(float m, float &scale, float &inv)
 // One block per row. mode 0: q8gemm Workspace.Pack (power-of-two row scale from
 // MaxAbs, then f16(x * scale)); mode 1: qwen3lm mm activations, half(x);
 // mode 2: PackRange with the row scales already on the device, converting only
-// columns [k0, k1) (and the K padding when k1 == K); modes 3 and 4: the
-// qwen3lm batched pass's activations, half(x * f * 2^e) with f = 1 (mode 4) or
-// the PRO_NORM factor f = 1/sqrt(sum(x^2)/K + eps) (mode 3, gpu.metal:785-796,
-// 825-826), and e placing the row's max |x * f| in [2^14, 2^15) (the q8gemm
-// row scale rule, gemm.go:127-135); rowInv[row] = 2^-e scales the row's sums
-// back. Writes the FP16 tile layout; modes 0, 1, 3 and 4 convert whole rows
-// and zero the K padding.
+// columns [k0, k1) (and the K padding when k1 == K). Writes the FP16 tile
+// layout; modes 0 and 1 convert whole rows and zero the K padding.
 __global__ __launch_bounds__(256) void f16_act_pack_kernel(const float *__restrict__ x, long stride, int K, int kt,
-                                                           int mode, int k0, int k1, float eps,
-                                                           _Float16 *__restrict__ act, float *__restrict__ rowScale,
+                                                           int mode, int k0, int k1, _Float16 *__restrict__ act,
+                                                           float *__restrict__ rowScale,
                                                            float *__restrict__ rowInv) {
     __shared__ float smax[4];
     __shared__ int snan[4];
     const int row = blockIdx.x;
     const float *xr = x + (size_t)row * stride;
     float scale = 1.0f, inv = 1.0f;
-    if (mode == 3 || mode == 4) {
-        __shared__ float sss[4];
-        float ss = 0.0f, mx = 0.0f;
-        for (int k = 4 * (int)threadIdx.x; k < K; k += 1024) {
-            const float4 v = *(const float4 *)(xr + k);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            mx = fmaxf(fmaxf(fmaxf(mx, fabsf(v.x)), fmaxf(fabsf(v.y), fabsf(v.z))), fabsf(v.w));
-        }
-        ss = wave_sum(ss);
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        if ((threadIdx.x & 63) == 0) {
-            sss[threadIdx.x >> 6] = ss;
-            smax[threadIdx.x >> 6] = mx;
-        }
-        __syncthreads();
-        const float f = mode == 3 ? 1.0f / sqrtf(((sss[0] + sss[1]) + (sss[2] + sss[3])) / (float)K + eps) : 1.0f;
-        float rs;
-        f16_row_scale(fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])) * f, rs, inv);
-        scale = f * rs;
-        if (threadIdx.x == 0) rowInv[row] = inv;
-    } else if (mode == 0) {
+    if (mode == 0) {
         float m = 0.0f;
         int nan = 0;
         constexpr int UNR = 8;
@@ -811,21 +786,107 @@ __global__ __launch_bounds__(256) void f16_act_pack_kernel(const float *__restri
 int f16_act_pack(const float *x, long stride, int rows, int K, int kt, int mode, int k0, int k1, _Float16 *act,
                  float *rowScale, float *rowInv, hipStream_t stream) {
     if (rows == 0) return GPHQ_OK;
-    hipLaunchKernelGGL(f16_act_pack_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, mode, k0, k1, 0.0f,
-                       act, rowScale, rowInv);
+    hipLaunchKernelGGL(f16_act_pack_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, mode, k0, k1, act,
+                       rowScale, rowInv);
+    return launch_status();
+}
+
+// Whole-row activation packing held in registers: one block of 256 threads
+// per row, thread t converting the 16-value chunks t, t + 256, ... (up to
+// CPT of them), each read as four 16-byte loads and written as one 32-byte
+// slot of the FP16 tile layout. MODE 0: half(x); 1: half(x * 2^e); 2:
+// half(x * f * 2^e) with the RMSNorm factor f, as f16_act_pack_kernel modes
+// 1, 4 and 3 (rowInv[row] = 2^-e for 1 and 2). K % 16 == 0, rows 16-byte
+// aligned; chunks past K (up to the 64-value tile) are zero.
+template <int MODE, int CPT>
+__global__ __launch_bounds__(256) void act_pack_rows_kernel(const float *__restrict__ x, long stride, int K, int kt,
+                                                            float eps, _Float16 *__restrict__ act,
+                                                            float *__restrict__ rowInv) {
+    __shared__ float sss[4], smx[4];
+    const int row = blockIdx.x;
+    const float *xr = x + (size_t)row * stride;
+    const int chunks = kt * 4;
+    float4 v[CPT][4];
+    float ss = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int k = 16 * ((int)threadIdx.x + 256 * c);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[c][q] = k < K ? *(const float4 *)(xr + k + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
+            ss += v[c][q].x * v[c][q].x + v[c][q].y * v[c][q].y + v[c][q].z * v[c][q].z + v[c][q].w * v[c][q].w;
+            mx = fmaxf(fmaxf(fmaxf(mx, fabsf(v[c][q].x)), fmaxf(fabsf(v[c][q].y), fabsf(v[c][q].z))), fabsf(v[c][q].w));
+        }
+    }
+    float scale = 1.0f;
+    if constexpr (MODE != 0) {
+        ss = wave_sum(ss);
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        if ((threadIdx.x & 63) == 0) {
+            sss[threadIdx.x >> 6] = ss;
+            smx[threadIdx.x >> 6] = mx;
+        }
+        __syncthreads();
+        const float f = MODE == 2 ? 1.0f / sqrtf(((sss[0] + sss[1]) + (sss[2] + sss[3])) / (float)K + eps) : 1.0f;
+        float rs, inv;
+        f16_row_scale(fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3])) * f, rs, inv);
+        scale = f * rs;
+        if (threadIdx.x == 0) rowInv[row] = inv;
+    }
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int ch = (int)threadIdx.x + 256 * c;
+        if (ch >= chunks) continue;
+        f16x8 h[2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            h[q >> 1][4 * (q & 1) + 0] = (_Float16)__fmul_rn(v[c][q].x, scale);
+            h[q >> 1][4 * (q & 1) + 1] = (_Float16)__fmul_rn(v[c][q].y, scale);
+            h[q >> 1][4 * (q & 1) + 2] = (_Float16)__fmul_rn(v[c][q].z, scale);
+            h[q >> 1][4 * (q & 1) + 3] = (_Float16)__fmul_rn(v[c][q].w, scale);
+        }
+        const size_t off = ((size_t)(row >> 4) * kt + (ch >> 2)) * 1024 + (size_t)((ch & 3) * 16 + (row & 15)) * 16;
+        *(f16x8 *)(act + off) = h[0];
+        *(f16x8 *)(act + off + 8) = h[1];
+    }
+}
+
+template <int MODE>
+static int launch_act_pack_rows(const float *x, long stride, int rows, int K, float eps, _Float16 *act,
+                                float *rowInv, hipStream_t stream) {
+    const int kt = (K + 63) / 64, chunks = kt * 4;
+    if (chunks <= 256)
+        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, 1>), dim3(rows), dim3(256), 0, stream, x, stride, K, kt, eps,
+                           act, rowInv);
+    else if (chunks <= 512)
+        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, 2>), dim3(rows), dim3(256), 0, stream, x, stride, K, kt, eps,
+                           act, rowInv);
+    else if (chunks <= 768)
+        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, 3>), dim3(rows), dim3(256), 0, stream, x, stride, K, kt, eps,
+                           act, rowInv);
+    else
+        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, 4>), dim3(rows), dim3(256), 0, stream, x, stride, K, kt, eps,
+                           act, rowInv);
     return launch_status();
 }
 
 // The qwen3lm batched pass's activation tiles, half(x * f * 2^e) with f the
 // RMSNorm factor (norm true) or 1, and rowInv[r] = 2^-e per row. x rows are
-// `stride` floats apart, 16-byte aligned, K % 4 == 0.
+// `stride` floats apart, 16-byte aligned, K % 16 == 0, K <= 16384.
 int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, _Float16 *act, float *rowInv,
                 hipStream_t stream) {
     if (rows == 0) return GPHQ_OK;
-    const int kt = (K + 63) / 64;
-    hipLaunchKernelGGL(f16_act_pack_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, norm ? 3 : 4, 0, K,
-                       eps, act, nullptr, rowInv);
-    return launch_status();
+    if (norm) return launch_act_pack_rows<2>(x, stride, rows, K, eps, act, rowInv, stream);
+    return launch_act_pack_rows<1>(x, stride, rows, K, eps, act, rowInv, stream);
+}
+
+// qwen3lm mm activations, half(x), through the register kernel when rows are
+// 16-byte aligned and K <= 16384, else the general one.
+int f16_act_pack_plain(const float *x, long stride, int rows, int K, _Float16 *act, hipStream_t stream) {
+    if (rows == 0) return GPHQ_OK;
+    if ((uintptr_t)x % 16 == 0 && stride % 4 == 0 && K % 16 == 0 && K <= 16384)
+        return launch_act_pack_rows<0>(x, stride, rows, K, 0.0f, act, nullptr, stream);
+    return f16_act_pack(x, stride, rows, K, (K + 63) / 64, 1, 0, K, act, nullptr, nullptr, stream);
 }
 
 // One projection of the qwen3lm batched pass over M activation rows packed

@@ -112,10 +112,11 @@ struct FlashArgs {
     int qkvw, qd, kvd, rows, base;
 };
 
-// Causal attention of pass rows m0 .. m0+31 (m0 = 32 * row block) for the
-// GROUP query heads of KV head g = blockIdx.y: wavefront w is query head
-// g*GROUP + w, and the block's waves share each 32-key tile of K and V,
-// staged through LDS as FP16. Row m attends cache rows 0 .. base + m.
+// Causal attention of pass rows m0 .. m0 + 32*RH - 1 (m0 = 32*RH * row block)
+// for the GROUP query heads of KV head g = blockIdx.y: wavefront w takes
+// query head g*GROUP + w % GROUP for rows m0 + 32*(w / GROUP) .. +31, and the
+// block's waves share each 32-key tile of K and V, staged through LDS as
+// FP16. Row m attends cache rows 0 .. base + m.
 //
 // Per tile, on v_mfma_f32_32x32x16_f16 with fp32 accumulation:
 //   S^T (32 keys x 32 queries) = K . Q^T, so lane l holds query l % 32 and 16
@@ -125,10 +126,12 @@ struct FlashArgs {
 //     S^T registers (the MFMA's K index runs over the lane's own keys; V^T is
 //     stored in LDS in the matching key order).
 // Queries enter as half(q * log2(e)) (q already carries 1/sqrt(head_dim)), so
-// the softmax is exp2(s - max); probabilities and values are FP16.
-template <int GROUP>
-__global__ __launch_bounds__(64 * GROUP) void lm_flash_kernel(const FlashArgs a) {
-    constexpr int NT = 64 * GROUP;
+// the softmax is exp2(s - max); probabilities and values are FP16. The
+// running output is rescaled only when some lane's maximum grew.
+template <int GROUP, int RH>
+__global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashArgs a) {
+    constexpr int NT = 64 * RH * GROUP;
+    constexpr int RB = 32 * RH;  // rows per block
     constexpr int KB = 32;             // keys per tile
     constexpr int KS = kHeadDim + 8;   // K tile row stride (halves): conflict-free 16-byte reads
     constexpr int VS = KB + 8;         // V^T row stride (halves)
@@ -136,23 +139,23 @@ __global__ __launch_bounds__(64 * GROUP) void lm_flash_kernel(const FlashArgs a)
     constexpr int VITEMS = (KB / 4 * kHeadDim + NT - 1) / NT;  // (dim, 4 keys) of V per thread
     __shared__ _Float16 Ks[KB * KS];
     __shared__ _Float16 Vt[kHeadDim * VS];
-    const int nmb = (a.rows + 31) >> 5;
+    const int nmb = (a.rows + RB - 1) / RB;
     const int mb = nmb - 1 - (int)blockIdx.x;  // longest rows first
     const int g = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int q = lane & 31, hi = lane >> 5;
-    const int head = g * GROUP + wave;
-    const int m0 = mb * 32;
+    const int head = g * GROUP + wave % GROUP;
+    const int m0 = mb * RB, mw = m0 + 32 * (wave / GROUP);
     const int kvEnd = a.base + a.rows;  // cache rows written by this pass's qk_rope
-    const int lastKey = a.base + min(m0 + 31, a.rows - 1);
-    const int tiles = lastKey / KB + 1;
-    const int myLast = a.base + m0 + q;  // this lane's query sees keys 0..myLast
+    const int tiles = (a.base + min(m0 + RB - 1, a.rows - 1)) / KB + 1;
+    const int myLast = a.base + mw + q;       // this lane's query sees keys 0..myLast
+    const int waveLast = a.base + mw + 31;    // no key past this is seen by the wave
     const float *kbase = a.kc + (size_t)g * kHeadDim;
     const float *vbase = a.vc + (size_t)g * kHeadDim;
 
     half8 qf[8];
     {
-        const float *qrow = a.qkv + (size_t)min(m0 + q, a.rows - 1) * a.qkvw + (size_t)head * kHeadDim + 8 * hi;
+        const float *qrow = a.qkv + (size_t)min(mw + q, a.rows - 1) * a.qkvw + (size_t)head * kHeadDim + 8 * hi;
         constexpr float kLog2e = 1.4426950408889634f;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -190,14 +193,13 @@ __global__ __launch_bounds__(64 * GROUP) void lm_flash_kernel(const FlashArgs a)
         }
     };
     auto store_tile = [&]() {
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 #pragma unroll
         for (int i = 0; i < KITEMS; ++i) {
             const int idx = tid + i * NT;
-            if (idx < KB * kHeadDim / 4) {
-                typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+            if (idx < KB * kHeadDim / 4)
                 *(half4 *)(Ks + (idx >> 5) * KS + 4 * (idx & 31)) =
                     half4{(_Float16)kr[i].x, (_Float16)kr[i].y, (_Float16)kr[i].z, (_Float16)kr[i].w};
-            }
         }
 #pragma unroll
         for (int i = 0; i < VITEMS; ++i) {
@@ -210,7 +212,6 @@ __global__ __launch_bounds__(64 * GROUP) void lm_flash_kernel(const FlashArgs a)
                 const int d = idx & (kHeadDim - 1), kg = idx >> 7;
                 const int r = kg & 3;
                 const int pg = (kg & ~3) + ((r == 1) ? 2 : (r == 2) ? 1 : r);
-                typedef _Float16 half4 __attribute__((ext_vector_type(4)));
                 *(half4 *)(Vt + d * VS + 4 * pg) =
                     half4{(_Float16)vr[i].x, (_Float16)vr[i].y, (_Float16)vr[i].z, (_Float16)vr[i].w};
             }
@@ -228,14 +229,15 @@ __global__ __launch_bounds__(64 * GROUP) void lm_flash_kernel(const FlashArgs a)
         store_tile();
         __syncthreads();
         if (t + 1 < tiles) load_tile(jb + KB);
+        if (jb > waveLast) continue;  // every key of the tile is past this wave's rows
         f32x16 s = f32x16{};
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const half8 kf = *(const half8 *)(Ks + q * KS + 16 * c + 8 * hi);
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], s, 0, 0, 0);
         }
-        // s[r] is key jb + 8*(r/4) + 4*hi + r%4 of query row m0 + q.
-        if (jb + KB - 1 > a.base + m0) {
+        // s[r] is key jb + 8*(r/4) + 4*hi + r%4 of query row mw + q.
+        if (jb + KB - 1 > a.base + mw) {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 if (jb + 8 * (r >> 2) + 4 * hi + (r & 3) > myLast) s[r] = -INFINITY;
@@ -246,12 +248,13 @@ __global__ __launch_bounds__(64 * GROUP) void lm_flash_kernel(const FlashArgs a)
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         // Tile 0 holds key 0, which every query sees, so mnew is finite.
         const float mnew = fmaxf(mrun, mx);
-        const float corr = exp2f(mrun - mnew);
+        const bool grew = mnew != mrun;
+        const float corr = __builtin_amdgcn_exp2f(mrun - mnew);
         mrun = mnew;
         float p[16], rs = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            p[r] = exp2f(s[r] - mnew);
+            p[r] = __builtin_amdgcn_exp2f(s[r] - mnew);
             rs += p[r];
         }
         rs += __shfl_xor(rs, 32);
@@ -262,15 +265,18 @@ __global__ __launch_bounds__(64 * GROUP) void lm_flash_kernel(const FlashArgs a)
             p0[i] = (_Float16)p[i];
             p1[i] = (_Float16)p[8 + i];
         }
+        if (__any(grew)) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[c] *= corr;
+        }
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            o[c] *= corr;
             const _Float16 *vrow = Vt + (32 * c + q) * VS + 8 * hi;
             o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)vrow, p0, o[c], 0, 0, 0);
             o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)(vrow + 16), p1, o[c], 0, 0, 0);
         }
     }
-    const int m = m0 + q;
+    const int m = mw + q;
     if (m >= a.rows) return;
     const float inv = 1.0f / lrun;
     float *out = a.ctx + (size_t)m * a.qd + (size_t)head * kHeadDim + 4 * hi;
@@ -282,10 +288,13 @@ __global__ __launch_bounds__(64 * GROUP) void lm_flash_kernel(const FlashArgs a)
                                                        o[c][4 * j + 2] * inv, o[c][4 * j + 3] * inv};
 }
 
+// Two 32-row halves per block up to four query heads per KV head (at most
+// 512 threads, so no wave is limited to 128 registers), one above.
 template <int G>
 int launch_flash_g(const FlashArgs &a, int kvh, hipStream_t st) {
-    hipLaunchKernelGGL((lm_flash_kernel<G>), dim3((unsigned)((a.rows + 31) / 32), (unsigned)kvh), dim3(64 * G), 0, st,
-                       a);
+    constexpr int RH = G <= 4 ? 2 : 1;
+    hipLaunchKernelGGL((lm_flash_kernel<G, RH>), dim3((unsigned)((a.rows + 32 * RH - 1) / (32 * RH)), (unsigned)kvh),
+                       dim3(64 * RH * G), 0, st, a);
     return launch_status();
 }
 

@@ -26,6 +26,7 @@ struct F16GemmArgs {
 int f16gemm_launch(int wf, int epi, F16GemmArgs a, hipStream_t stream);
 int gemv_gptq_launch(const void *codes, const void *scales, const uint8_t *zeros, const float *x, float *y, int K,
                      int N, hipStream_t stream);
+int f16_act_pack_plain(const float *x, long stride, int rows, int K, _Float16 *act, hipStream_t stream);
 int f16_act_pack(const float *x, long stride, int rows, int K, int kt, int mode, int k0, int k1, _Float16 *act,
                  float *rowScale, float *rowInv, hipStream_t stream);
 int f16_pack_tiles(const uint16_t *src, uint16_t *dst, int rows, int K, int row0, int kt, hipStream_t stream);
@@ -484,7 +485,7 @@ int gphq_mm(int fmt, const void *codes, const void *scales, const uint8_t *zeros
         if (st != GPHQ_ERR_UNSUPPORTED) return st;
     }
     const int64_t kt = ceil_div(k, 64);
-    GPHQ_TRY(f16_act_pack(x, (long)k, (int)m, (int)k, (int)kt, 1, 0, (int)k, (_Float16 *)work, nullptr, nullptr, s));
+    GPHQ_TRY(f16_act_pack_plain(x, (long)k, (int)m, (int)k, (_Float16 *)work, s));
     F16GemmArgs a{};
     a.A = (const _Float16 *)work;
     a.B = codes;

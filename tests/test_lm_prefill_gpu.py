@@ -152,6 +152,26 @@ def test_prefill_8b_widths(fmt):
     check_cache(cache, kv, g, len(tokens))
 
 
+@pytest.mark.parametrize("group", [1, 3, 5, 8])
+def test_prefill_query_groups(group):
+    # Query heads per KV head other than the 2 and 4 above: the attention
+    # kernel's block shape changes with the group (one or two 32-row halves).
+    geom = lo.Geometry(hidden=256, layers=1, heads=group, kv_heads=1, head_dim=128, inter=512, vocab=96,
+                       max_pos=320)
+    model, oracle, lm = setup(geom, lo.FMT_Q8B, seed=40 + group)
+    g = model["geom"]
+    rng = np.random.default_rng(36 + group)
+    tokens = list(rng.integers(0, g.vocab, 100))
+    ws = gphq.Prefill(lm, 128)
+    kv = gphq.Prefix(lm, 128)
+    got = run_prefill(ws, kv, 0, tokens, g)
+    cache = oracle.new_cache(128)
+    h = oracle.prefill(cache, 0, tokens)
+    want, _ = oracle.finish(h[-1])
+    assert cosine(want, got) >= COS
+    check_cache(cache, kv, g, len(tokens))
+
+
 def test_prefill_validation_errors():
     import torch
 
