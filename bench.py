@@ -216,7 +216,7 @@ def gptq_config5(args, torch, gphq, ms=(1, 256), steps=20):
         for m in ms:
             x = torch.randn((m, k), device="cuda", generator=g)
             y = torch.empty((m, n), device="cuda")
-            work = torch.empty(gphq.mm_workspace_bytes(m, k), dtype=torch.uint8, device="cuda")
+            work = torch.empty(gphq.mm_split_workspace_bytes(m, k, n), dtype=torch.uint8, device="cuda")
             for c, sc, z in sets:
                 gphq.mm(gphq.FMT_GPTQ4_G128, c, sc, x, y, m, k, n, work, zeros=z, stream=stream)
             torch.cuda.synchronize()

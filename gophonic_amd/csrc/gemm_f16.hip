@@ -24,6 +24,7 @@
 // layout: the int8 tile layout of gemm_i8.hip, an FP16 tile layout, or the
 // qwen3lm row-major code arrays.
 #include "common.h"
+#include "gemm_f16.h"
 
 namespace gphq {
 
@@ -31,35 +32,6 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-enum WFmt {
-    W_I8_TILE = 0,    // q8gemm int8 weights, tile layout (1 KiB groups)
-    W_F16_TILE = 1,   // q8gemm FP16 weights, tile layout (2 KiB groups)
-    W_Q8_ROW = 2,     // qwen3lm Q8 codes [N][K] (fp32 row scales in the epilogue)
-    W_Q8B_ROW = 3,    // qwen3lm Q8B codes [N][K], f16 scales [N][K/32]
-    W_Q4_ROW = 4,     // qwen3lm Q4 codes [N][K/2], f16 scales [N][K/32]
-    W_GPTQ_ROW = 5,   // int32 [N][K/8] (nibble i of word j = k 8j+i), f16 scales and u8 zeros [N][K/128]
-    W_Q8BF_ROW = 6,   // qwen3lm Q8B codes [N][K] with fp32 scales [N][K/32]
-};
-
-// EPI_ADD: dst += v (the residual stream). EPI_SWIGLU: columns 2i (gate) and
-// 2i+1 (up) give dst[row][i] = g / (1 + exp(-g)) * u. Both multiply by
-// colScale[col] first when it is set (Q8 row scales).
-enum Epi { EPI_PANELS = 0, EPI_PLAIN = 1, EPI_ROWSCALE = 2, EPI_ADD = 3, EPI_SWIGLU = 4 };
-
-struct F16GemmArgs {
-    const _Float16 *A;   // activations, FP16 tile layout, MT x KT groups
-    const void *B;       // weights (layout per WFmt)
-    const void *bScale;  // Q8B/Q4: f16 [N][K/32]; GPTQ: f16 [N][K/128]
-    const uint8_t *bZero;  // GPTQ: u8 [N][K/128]
-    const float *colScale;  // EPI_PANELS, EPI_ROWSCALE: fp32 [N]
-    const float *rowInv;    // EPI_PANELS: fp32 [M]
-    float *dst;
-    long stride;
-    int M, N, K, KT, NT;
-    int c0, c1, tileN0;
-    int gridM, gridN;
-};
 
 __device__ __forceinline__ _Float16 i8h(uint32_t v, int i) { return (_Float16)(int)((int32_t)(v << (24 - 8 * i)) >> 24); }
 
@@ -150,10 +122,10 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
     }
 }
 
-// Epilogue of one lane's part of a 16x16 accumulator tile: rows row0 ..
-// row0 + 3 of column col. Columns outside [c0, c1) and rows past M are not
-// written. Every lane of the wavefront calls it (EPI_SWIGLU exchanges the
-// gate and up values of neighbouring lanes).
+// Epilogue of one lane's part of a 16x16 accumulator tile (or of a 4-row
+// group of a 32x32 one): rows row0 .. row0 + 3 of column col. Columns outside
+// [c0, c1) and rows past M are not written. Every lane of the wavefront calls
+// it (EPI_SWIGLU exchanges the gate and up values of neighbouring lanes).
 template <int EPI>
 __device__ __forceinline__ void epilogue(const F16GemmArgs &a, const f32x4 &acc, int row0, int col) {
     const bool colOk = col >= a.c0 && col < a.c1;
@@ -174,17 +146,23 @@ __device__ __forceinline__ void epilogue(const F16GemmArgs &a, const f32x4 &acc,
         }
         if constexpr (EPI == EPI_SWIGLU) {
             if (a.colScale) v = __fmul_rn(v, cs);
-            const float u = __shfl_xor(v, 1);
+            // The up value of the neighbouring lane (DPP quad_perm [1,0,3,2]).
+            const float u = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF,
+                                                                               0xF, true));
             if (colOk && !(col & 1) && row < a.M) a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
         } else if (colOk && row < a.M) {
             float *p = a.dst + (size_t)row * a.stride + col;
             if constexpr (EPI == EPI_PANELS) v = __fmul_rn(__fmul_rn(v, cs), a.rowInv[row]);
             if constexpr (EPI == EPI_ROWSCALE) v = __fmul_rn(v, cs);
             if constexpr (EPI == EPI_ADD) {
+                // One fp32 add into the residual, done in L2 without a return
+                // (each element has one owner, so the sum is y + v exactly,
+                // and the wave does not wait for the old value).
                 if (a.colScale) v = __fmul_rn(v, cs);
-                v = *p + v;
+                __builtin_amdgcn_global_atomic_fadd_f32(p, v);
+            } else {
+                *p = v;
             }
-            *p = v;
         }
     }
 }
@@ -371,12 +349,27 @@ __device__ __forceinline__ void dequant(const RawB &r, int g, f16x8 &lo, f16x8 &
         lo = cat4(p[0], p[1], p[2], p[3]);
         hi = cat4(p[4], p[5], p[6], p[7]);
     } else {
-        const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
-        const _Float16 z = (_Float16)(int)(r.sz >> 16);
+        // GPTQ: nibble i of a word is value i. Even nibbles (w & 0x0F0F0F0F) and
+        // odd ones ((w >> 4) & 0x0F0F0F0F) are paired by v_perm_b32 into the low
+        // bytes of two halves, 0x6400 is or-ed in (1024 + n), and one packed
+        // subtraction of 1024 + z leaves n - z exactly.
+        const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
+        const _Float16 zb = (_Float16)(float)(1024 + (int)(r.sz >> 16));
+        const f16x2 off = f16x2{zb, zb}, ss = f16x2{sc, sc};
+        f16x2 p[8];
+        const uint32_t wds[2] = {r.w.x, r.w.y};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) lo[i] = ((_Float16)(int)((r.w.x >> (4 * i)) & 15) - z) * s;
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t x = wds[h] & 0x0F0F0F0Fu, y = (wds[h] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) hi[i] = ((_Float16)(int)((r.w.y >> (4 * i)) & 15) - z) * s;
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t sel = (uint32_t)q | (0x0Cu << 8) | ((uint32_t)(4 + q) << 16) | (0x0Cu << 24);
+                p[4 * h + q] =
+                    (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(y, x, sel) | 0x64006400u) - off) * ss;
+            }
+        }
+        lo = cat4(p[0], p[1], p[2], p[3]);
+        hi = cat4(p[4], p[5], p[6], p[7]);
     }
 }
 
@@ -508,9 +501,13 @@ static int launch_f16gemm(F16GemmArgs a, hipStream_t stream) {
     return launch_status();
 }
 
-// ---- 256 x 256 block tiles (qwen3lm row formats, large M) --------------------
-// Four wavefronts as 2 x 2, each 128 x 128 of the output as 4 x 4 tiles of
-// v_mfma_f32_32x32x16_f16. Per 64-deep K step both operands pass through LDS
+// ---- BM x BN block tiles (qwen3lm row formats, large M) -----------------------
+// WGM x WGN wavefronts, each (BM/WGM) x (BN/WGN) of the output as tiles of
+// v_mfma_f32_32x32x16_f16 (256 x 256 with 4 x 2 waves for long GEMMs,
+// 128 x 128 with 2 x 2 when fewer, larger-K blocks are wanted). With
+// a.splits > 1 block b takes K steps of split b / tiles and writes raw sums
+// to a.part; mm_finish_kernel adds the splits in order. Per 64-deep K step
+// both operands pass through LDS
 // (FP16, 128 bytes per row, 16-byte chunks swizzled by the row so the
 // fragment reads of 8 or 16 consecutive rows hit distinct banks), double
 // buffered: step kt+1's global loads (A: FP16 tiles, B: raw codes) are issued
@@ -520,31 +517,31 @@ static int launch_f16gemm(F16GemmArgs a, hipStream_t stream) {
 // MFMA operands: lane l holds row l % 32 of its matrix (A row m, or weight row
 // n) and k values 8*(l/32) .. +7 of the 16-deep sub-step; the result lane l
 // holds column n = l % 32, rows 8*(i/4) + 4*(l/32) + i%4 of acc[i].
-constexpr int kBigBM = 256, kBigBN = 256;
-#ifndef GPHQ_BIG_WGM
-#define GPHQ_BIG_WGM 4
-#define GPHQ_BIG_WGN 2
-#endif
+
 
 __device__ __forceinline__ int big_swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
 
-template <int WF, int EPI_T, int WGM, int WGN>
+template <int WF, int EPI_T, int BM, int BN, int WGM, int WGN, int PF>
 __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16GemmArgs a) {
     typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     constexpr int NT = 64 * WGM * WGN;
-    constexpr int TI = kBigBM / WGM / 32, TJ = kBigBN / WGN / 32;  // 32x32 tiles per wave
-    constexpr int AL = kBigBM * 8 / NT;   // 16-byte A units per thread and step
-    constexpr int BL = kBigBN * 4 / NT;   // (row, 16 K values) B pieces per thread and step
+    constexpr int TI = BM / WGM / 32, TJ = BN / WGN / 32;  // 32x32 tiles per wave
+    constexpr int AL = BM * 8 / NT;   // 16-byte A units per thread and step
+    constexpr int BL = BN * 4 / NT;   // (row, 16 K values) B pieces per thread and step
     static_assert(AL >= 1 && BL >= 1 && NT % 128 == 0, "loader split");
-    __shared__ f16x8v As[2][kBigBM * 8];
-    __shared__ f16x8v Bs[2][kBigBN * 8];
+    __shared__ f16x8v As[2][BM * 8];
+    __shared__ f16x8v Bs[2][BN * 8];
+    const int tiles = a.gridM * a.gridN;
+    const int sp = blockIdx.x / tiles;
     int bm, bn;
-    tile_order(blockIdx.x, a.gridM, a.gridN, bm, bn);
+    tile_order(blockIdx.x - sp * tiles, a.gridM, a.gridN, bm, bn);
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int wm = wv / WGN, wn = wv % WGN;
-    const int m0 = bm * kBigBM, n0 = a.tileN0 * 16 + bn * kBigBN;
+    const int m0 = bm * BM, n0 = a.tileN0 * 16 + bn * BN;
     const int MT = (a.M + 15) >> 4, KT = a.KT;
+    const int kper = (KT + a.splits - 1) / a.splits;
+    const int k0 = sp * kper, k1 = min(KT, k0 + kper);
 
     // A loader: 2 KB groups (16 rows x 64 K) of the FP16 tile layout; load i
     // of thread t is 16-byte unit u = i*NT + t: group u/128 (rows
@@ -557,26 +554,28 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
     // values at 16*(t%4) of the step.
     const int bc = t & 3;
 
-    f16x8v ar[AL];
-    RawB br[BL];
-    auto gload = [&](int kt) {
+    // PF register sets: step r's loads go to set r % PF, so loads run PF
+    // steps ahead of their LDS writes.
+    f16x8v ar[PF][AL];
+    RawB br[PF][BL];
+    auto gload = [&](int set, int kt) {
 #pragma unroll
         for (int i = 0; i < AL; ++i)
-            ar[i] = *(const f16x8v *)(abase + ((size_t)min(mtb + i * (NT / 128), MT - 1) * KT + kt) * 1024);
+            ar[set][i] = *(const f16x8v *)(abase + ((size_t)min(mtb + i * (NT / 128), MT - 1) * KT + kt) * 1024);
 #pragma unroll
         for (int i = 0; i < BL; ++i)
-            br[i] = load_raw<WF>(a, min(n0 + ((i * NT + t) >> 2), a.N - 1), kt, bc);
+            br[set][i] = load_raw<WF>(a, min(n0 + ((i * NT + t) >> 2), a.N - 1), kt, bc);
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int set, int buf) {
 #pragma unroll
         for (int i = 0; i < AL; ++i) {
             const int r = 16 * (i * (NT / 128) + (t >> 7)) + (aslot & 15);
-            As[buf][r * 8 + big_swz(r, achunk)] = ar[i];
+            As[buf][r * 8 + big_swz(r, achunk)] = ar[set][i];
         }
 #pragma unroll
         for (int i = 0; i < BL; ++i) {
             f16x8 lo, hi;
-            dequant<WF>(br[i], bc, lo, hi);
+            dequant<WF>(br[set][i], bc, lo, hi);
             const int r = (i * NT + t) >> 2;
             Bs[buf][r * 8 + big_swz(r, 2 * bc)] = lo;
             Bs[buf][r * 8 + big_swz(r, 2 * bc + 1)] = hi;
@@ -589,9 +588,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x16{};
 
-    gload(0);
-    lstore(0);
-    if (KT > 1) gload(1);
+    gload(0, k0);
+    lstore(0, 0);
+#pragma unroll
+    for (int r = 1; r <= PF; ++r)
+        if (k0 + r < k1) gload(r % PF, k0 + r);
     __syncthreads();
     const int fr = lane & 31, fh = lane >> 5;
     auto frags = [&](int buf, int s, f16x8v (&fa)[TI], f16x8v (&fb)[TJ]) {
@@ -607,8 +608,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
             fb[j] = Bs[buf][r * 8 + big_swz(r, c)];
         }
     };
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
+    // One K step: MFMAs on LDS buffer r & 1, then step r+1's tiles (register
+    // set `set` = (r+1) % PF) into the other buffer and step r+1+PF's loads.
+    auto step = [&](int r, int set) {
+        const int cur = r & 1, kt = k0 + r;
         f16x8v fa[2][TI], fb[2][TJ];
         frags(cur, 0, fa[0], fb[0]);
 #pragma unroll
@@ -620,11 +623,38 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
                 for (int j = 0; j < TJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[s & 1][i], fb[s & 1][j], acc[i][j], 0, 0, 0);
         }
-        if (kt + 1 < KT) {
-            lstore(cur ^ 1);
-            if (kt + 2 < KT) gload(kt + 2);
+        if (kt + 1 < k1) {
+            lstore(set, cur ^ 1);
+            if (kt + 1 + PF < k1) gload(set, kt + 1 + PF);
         }
         __syncthreads();
+    };
+    const int nsteps = k1 - k0;
+    if constexpr (PF == 1) {
+        for (int r = 0; r < nsteps; ++r) step(r, 0);
+    } else {
+        static_assert(PF == 2, "prefetch depth 1 or 2");
+        for (int r = 0; r < nsteps; r += 2) {
+            step(r, 1);
+            if (r + 1 < nsteps) step(r + 1, 0);
+        }
+    }
+    if (a.splits > 1) {
+        // Raw sums of this split: part[sp][row][col - c0].
+        const int ld = a.c1 - a.c0;
+        float *part = a.part + (size_t)sp * a.M * ld;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const int col = n0 + wn * (32 * TJ) + 32 * j + fr;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + wm * (32 * TI) + 32 * i + 8 * (e >> 2) + 4 * fh + (e & 3);
+                    if (row < a.M && col >= a.c0 && col < a.c1) part[(size_t)row * ld + (col - a.c0)] = acc[i][j][e];
+                }
+            }
+        return;
     }
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -636,23 +666,61 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
                                 m0 + wm * (32 * TI) + 32 * i + 8 * q + 4 * fh, n0 + wn * (32 * TJ) + 32 * j + fr);
 }
 
-template <int WF, int EPI>
+// Split-K finish (the reference's mm_finish, gpu.metal:953-982, for the store
+// epilogues): y[row][col] = sum over splits in order of part[s][row][col],
+// times the Q8 row scale for EPI_ROWSCALE. One thread per output.
+template <int EPI>
+__global__ __launch_bounds__(256) void mm_finish_kernel(const F16GemmArgs a) {
+    const int ld = a.c1 - a.c0;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)a.M * ld) return;
+    const int row = (int)(idx / ld), c = (int)(idx - (size_t)row * ld);
+    float v = a.part[idx];
+    for (int s = 1; s < a.splits; ++s) v += a.part[(size_t)s * a.M * ld + idx];
+    if constexpr (EPI == EPI_ROWSCALE) v = __fmul_rn(v, a.colScale[a.c0 + c]);
+    a.dst[(size_t)row * a.stride + a.c0 + c] = v;
+}
+
+template <int WF, int EPI, int BM, int BN, int WGM, int WGN, int PF>
 static int launch_f16gemm_big(F16GemmArgs a, hipStream_t stream) {
-    a.gridN = (a.c1 - a.tileN0 * 16 + kBigBN - 1) / kBigBN;
-    a.gridM = (a.M + kBigBM - 1) / kBigBM;
-    hipLaunchKernelGGL((f16gemm_big_kernel<WF, EPI, GPHQ_BIG_WGM, GPHQ_BIG_WGN>), dim3((unsigned)(a.gridM * a.gridN)),
-                       dim3(64 * GPHQ_BIG_WGM * GPHQ_BIG_WGN), 0, stream, a);
+    a.gridN = (a.c1 - a.tileN0 * 16 + BN - 1) / BN;
+    a.gridM = (a.M + BM - 1) / BM;
+    if (a.splits < 1) a.splits = 1;
+    hipLaunchKernelGGL((f16gemm_big_kernel<WF, EPI, BM, BN, WGM, WGN, PF>),
+                       dim3((unsigned)(a.gridM * a.gridN * a.splits)), dim3(64 * WGM * WGN), 0, stream, a);
+    GPHQ_TRY(launch_status());
+    if (a.splits == 1) return GPHQ_OK;
+    const size_t outs = (size_t)a.M * (a.c1 - a.c0);
+    hipLaunchKernelGGL((mm_finish_kernel<EPI>), dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, stream, a);
     return launch_status();
 }
 
+// K splits for a 128 x 128-tile GEMM whose grid has `tiles` blocks: doubled
+// while the grid is under 256 blocks, K divides, and each split keeps at
+// least 4 K steps (at most 16; mm_split_count must agree with the scratch
+// the caller sized).
+int mm_split_count(long tiles, int KT) {
+    int s = 1;
+    while (s < 16 && tiles * s < 256 && KT % (2 * s) == 0 && KT / (2 * s) >= 4) s *= 2;
+    return s;
+}
+
 template <int WF, int EPI>
-static int launch_by_m(const F16GemmArgs &a, hipStream_t stream) {
+static int launch_by_m(F16GemmArgs a, hipStream_t stream) {
     if (a.M <= 16) return launch_f16gemm<WF, EPI, 1, 2, 1, 2, 4, 2>(a, stream);
     if (a.M <= 64) return launch_f16gemm<WF, EPI, 4, 1, 1, 2, 4, 2>(a, stream);
-    if constexpr (WF != W_I8_TILE && WF != W_F16_TILE && WF != W_GPTQ_ROW) {
+    if constexpr (WF != W_I8_TILE && WF != W_F16_TILE) {
+        const long width = a.c1 - a.tileN0 * 16;
         // 256 x 256 block tiles when they fill the chip.
-        const long big = (long)((a.M + kBigBM - 1) / kBigBM) * ((a.c1 - a.tileN0 * 16 + kBigBN - 1) / kBigBN);
-        if (a.M >= 512 && big >= 256) return launch_f16gemm_big<WF, EPI>(a, stream);
+        const long big = (long)((a.M + 255) / 256) * ((width + 255) / 256);
+        if (a.M >= 512 && big >= 256) return launch_f16gemm_big<WF, EPI, 256, 256, 4, 2, 1>(a, stream);
+        // 128 x 128 tiles, with K split over extra blocks when the caller gave
+        // scratch for the partial sums (store epilogues only).
+        const long mid = (long)((a.M + 127) / 128) * ((width + 127) / 128);
+        a.splits = 1;
+        if constexpr (EPI == EPI_PLAIN || EPI == EPI_ROWSCALE)
+            if (a.part) a.splits = mm_split_count(mid, a.KT);
+        if (mid * a.splits >= 128) return launch_f16gemm_big<WF, EPI, 128, 128, 2, 2, 2>(a, stream);
     }
     if constexpr (WF != W_I8_TILE && WF != W_F16_TILE) {
         // 256 x 128 block tiles when they fill the chip, else 128 x 128 or 128 x 64.

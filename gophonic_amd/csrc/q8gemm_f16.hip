@@ -8,22 +8,9 @@
 #include <vector>
 
 #include "common.h"
+#include "gemm_f16.h"
 
 namespace gphq {
-struct F16GemmArgs {
-    const _Float16 *A;
-    const void *B;
-    const void *bScale;
-    const uint8_t *bZero;
-    const float *colScale;
-    const float *rowInv;
-    float *dst;
-    long stride;
-    int M, N, K, KT, NT;
-    int c0, c1, tileN0;
-    int gridM, gridN;
-};
-int f16gemm_launch(int wf, int epi, F16GemmArgs a, hipStream_t stream);
 int gemv_gptq_launch(const void *codes, const void *scales, const uint8_t *zeros, const float *x, float *y, int K,
                      int N, hipStream_t stream);
 int f16_act_pack_plain(const float *x, long stride, int rows, int K, _Float16 *act, hipStream_t stream);
@@ -41,8 +28,6 @@ using namespace gphq;
 static constexpr int64_t kOutputPanel = 64;  // q8gemm/packed.go:17
 static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-enum { W_I8_TILE = 0, W_F16_TILE = 1, W_Q8_ROW = 2, W_Q8B_ROW = 3, W_Q4_ROW = 4, W_GPTQ_ROW = 5, W_Q8BF_ROW = 6 };
-enum { EPI_PANELS = 0, EPI_PLAIN = 1, EPI_ROWSCALE = 2 };
 
 struct gphq_weights {
     int64_t k = 0, n = 0, kt = 0, nt = 0;
@@ -446,6 +431,16 @@ int64_t gphq_mm_workspace_bytes(int64_t m, int64_t k) {
     return ceil_div(m, 16) * ceil_div(k, 64) * 2048;
 }
 
+// Activation tiles, then (256-byte aligned) the split-K partial sums the
+// 128 x 128-tile GEMM uses for 64 < m with a grid under 256 blocks.
+int64_t gphq_mm_split_workspace_bytes(int64_t m, int64_t k, int64_t n) {
+    if (m < 0 || k < 0 || n < 0 || m > INT32_MAX || k > INT32_MAX || n > INT32_MAX) return GPHQ_ERR_DIMENSIONS;
+    const int64_t act = (gphq_mm_workspace_bytes(m, k) + 255) / 256 * 256;
+    if (m <= 64) return act;
+    const int splits = mm_split_count(ceil_div(m, 128) * ceil_div(n, 128), (int)ceil_div(k, 64));
+    return act + (splits > 1 ? (int64_t)splits * m * n * 4 : 0);
+}
+
 int gphq_mm(int fmt, const void *codes, const void *scales, const uint8_t *zeros, const float *x, float *y,
             int64_t m, int64_t k, int64_t n, void *work, int64_t work_bytes, void *stream) {
     int wf;
@@ -500,6 +495,8 @@ int gphq_mm(int fmt, const void *codes, const void *scales, const uint8_t *zeros
     a.KT = (int)kt;
     a.c0 = 0;
     a.c1 = (int)n;
+    const int64_t act = (gphq_mm_workspace_bytes(m, k) + 255) / 256 * 256;
+    if (m > 64 && work_bytes >= gphq_mm_split_workspace_bytes(m, k, n)) a.part = (float *)((char *)work + act);
     return f16gemm_launch(wf, epi, a, s);
 }
 

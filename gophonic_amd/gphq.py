@@ -121,6 +121,7 @@ SIGNATURES = {
     "gphq_decode_batch_set_graph": (ctypes.c_int, [_vp, ctypes.c_int]),
     "gphq_prepare_work_bytes": (_i64, [_i64, _i64]),
     "gphq_prepare_projection": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "gphq_mm_split_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "gphq_prefill_new": (ctypes.c_int, [_vp, _i64, _vpp]),
     "gphq_prefill_free": (None, [_vp]),
     "gphq_prefill_rows": (ctypes.c_int, [_vp]),
@@ -459,6 +460,10 @@ def mul_into(dst, x, rows, w, ws, stream=None):
 
 def mm_workspace_bytes(m, k):
     return load().gphq_mm_workspace_bytes(m, k)
+
+
+def mm_split_workspace_bytes(m, k, n):
+    return load().gphq_mm_split_workspace_bytes(m, k, n)
 
 
 def mm(fmt, codes, scales, x, y, m, k, n, work, zeros=None, stream=None):

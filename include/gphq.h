@@ -324,6 +324,11 @@ int gphq_q8gemm_mul_into(float *dst_dev, int64_t dst_len, const float *x_dev, in
  * (16-byte aligned) for the FP16 activations. */
 #define GPHQ_FMT_GPTQ4_G128 12
 int64_t gphq_mm_workspace_bytes(int64_t m, int64_t k);
+/* The workspace with room for split-K partial sums (gpu_darwin.go:1667-1699
+ * mmRun: small grids split K and mm_finish adds the splits in order): with at
+ * least this many bytes, a product whose grid of 128 x 128 tiles is under 256
+ * blocks splits K; the sums are then added split by split, deterministically. */
+int64_t gphq_mm_split_workspace_bytes(int64_t m, int64_t k, int64_t n);
 int gphq_mm(int fmt, const void *codes_dev, const void *scales_dev, const uint8_t *zeros_dev, const float *x_dev,
             float *y_dev, int64_t m, int64_t k, int64_t n, void *work_dev, int64_t work_bytes, void *stream);
 

@@ -31,10 +31,11 @@ def host(t):
     return t.cpu().numpy()
 
 
-def run_mm(fmt, codes, scales, x, m, k, n, zeros=None):
+def run_mm(fmt, codes, scales, x, m, k, n, zeros=None, split=False):
     import torch
 
-    work = torch.empty(max(1, gphq.mm_workspace_bytes(m, k)), dtype=torch.uint8, device="cuda")
+    nb = gphq.mm_split_workspace_bytes(m, k, n) if split else gphq.mm_workspace_bytes(m, k)
+    work = torch.empty(max(1, nb), dtype=torch.uint8, device="cuda")
     y = torch.full((m * n,), float("nan"), device="cuda")
     gphq.mm(fmt, dev(codes), dev(scales), dev(x), y, m, k, n, work, zeros=None if zeros is None else dev(zeros))
     return host(y).reshape(m, n)
@@ -74,16 +75,33 @@ def test_mm_matches_fp16_tile_oracle(fmt, m, k, n):
     assert np.all(np.abs(got - want) <= k * 2.0 ** -23 * absum + 1e-30)
 
 
-@pytest.mark.parametrize("m", [1, 256])
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("m,k,n", [(100, 640, 130), (65, 4096, 200), (256, 4096, 512), (128, 12288, 256),
+                                   (300, 1024, 1000)])
+def test_mm_split_k_matches_fp16_tile_oracle(fmt, m, k, n):
+    # With the split workspace, grids under 256 blocks split K; the splits are
+    # added in order by a second kernel, so the bound is the unsplit one.
+    rng = np.random.default_rng(fmt * 131 + m + k + n)
+    codes, scales, zeros = weights(fmt, rng, n, k)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    got = run_mm(fmt, codes, scales, x, m, k, n, zeros, split=True)
+    want, absum = orc.mm_f64(fmt, codes, scales, x, m, k, n, zeros=zeros)
+    assert np.isfinite(got).all()
+    assert np.all(np.abs(got - want) <= k * 2.0 ** -23 * absum + 1e-30)
+    again = run_mm(fmt, codes, scales, x, m, k, n, zeros, split=True)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))  # deterministic
+
+
+@pytest.mark.parametrize("m,split", [(1, False), (256, False), (256, True)])
 @pytest.mark.parametrize("k,n", [(4096, 12288), (12288, 4096)])
-def test_gptq_g128_config5_within_2e3(m, k, n):
+def test_gptq_g128_config5_within_2e3(m, split, k, n):
     # BASELINE config 5 shapes. The north-star tolerance (2e-3 relative) is
     # checked against float64 with un-rounded weights on a sample of columns;
     # the FP16-tile oracle bounds the same sample tightly.
     rng = np.random.default_rng(m + k)
     codes, scales, zeros = weights(orc.FMT_GPTQ4_G128, rng, n, k)
     x = rng.standard_normal(m * k).astype(np.float16).astype(np.float32)  # fp16 activations
-    got = run_mm(orc.FMT_GPTQ4_G128, codes, scales, x, m, k, n, zeros)
+    got = run_mm(orc.FMT_GPTQ4_G128, codes, scales, x, m, k, n, zeros, split=split)
     cols = np.sort(rng.choice(n, 48, replace=False))
     rows = np.arange(m) if m <= 8 else np.sort(rng.choice(m, 8, replace=False))
     sub_codes = codes.reshape(n, k // 8)[cols]
