@@ -83,4 +83,28 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// ---- GEMM tiling helpers ------------------------------------------------------
+
+// Block b's output tile (bm, bn). Workgroups are dispatched to the 8 XCDs
+// round robin, so XCD x = b % 8 runs blocks x, x + 8, ...; those take one
+// contiguous range of the tile order, and the order walks groups of 8 M
+// blocks for each N block, so the blocks an XCD runs at once share their A
+// rows and B columns in that XCD's L2.
+__device__ __forceinline__ void tile_order(int b, int gridM, int gridN, int &bm, int &bn) {
+    constexpr int GM = 8;
+    const int G = gridM * gridN;
+    const int L = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+    const int span = GM * gridN;
+    const int grp = L / span, first = grp * GM;
+    const int gm = min(gridM - first, GM);
+    const int r = L - grp * span;
+    bm = first + r % gm;
+    bn = r / gm;
+}
+
+// 16-byte chunk index within a 128-byte LDS row of a GEMM operand tile,
+// swizzled by the row: fragment reads of 8 or 16 consecutive rows at one
+// chunk hit distinct banks.
+__device__ __forceinline__ int big_swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
+
 }  // namespace gphq

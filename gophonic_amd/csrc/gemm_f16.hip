@@ -373,23 +373,6 @@ __device__ __forceinline__ void dequant(const RawB &r, int g, f16x8 &lo, f16x8 &
     }
 }
 
-// Block b's output tile (bm, bn). Workgroups are dispatched to the 8 XCDs
-// round robin, so XCD x = b % 8 runs blocks x, x + 8, ...; those take one
-// contiguous range of the tile order, and the order walks groups of 8 M
-// blocks for each N block, so the blocks an XCD runs at once share their A
-// rows and B columns in that XCD's L2.
-__device__ __forceinline__ void tile_order(int b, int gridM, int gridN, int &bm, int &bn) {
-    constexpr int GM = 8;
-    const int G = gridM * gridN;
-    const int L = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
-    const int span = GM * gridN;
-    const int grp = L / span, first = grp * GM;
-    const int gm = min(gridM - first, GM);
-    const int r = L - grp * span;
-    bm = first + r % gm;
-    bn = r / gm;
-}
-
 // Block tile (16*WTM*WGM) x (32*WTN): 2*WGM wavefronts, WGM along M and 2
 // along N, each (16*WTM) x (16*WTN) of the output. Per 64-deep K step the
 // block's threads dequantize the B tile once into LDS in MFMA fragment order
@@ -519,7 +502,6 @@ static int launch_f16gemm(F16GemmArgs a, hipStream_t stream) {
 // holds column n = l % 32, rows 8*(i/4) + 4*(l/32) + i%4 of acc[i].
 
 
-__device__ __forceinline__ int big_swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
 
 template <int WF, int EPI_T, int BM, int BN, int WGM, int WGN, int PF>
 __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16GemmArgs a) {

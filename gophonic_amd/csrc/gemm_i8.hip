@@ -399,6 +399,121 @@ __global__ __launch_bounds__(64 * WM * WN) void i8gemm_lds_kernel(const I8GemmAr
     }
 }
 
+// Large-M variant: BM x BN block tiles (WGM x WGN wavefronts, each a grid of
+// 32 x 32 v_mfma_i32_32x32x32_i8 tiles), 128-deep K steps (two tile-layout
+// groups) staged through LDS as 128-byte rows with the row-swizzled 16-byte
+// chunks of the FP16 big-tile GEMM, double-buffered with the next step's
+// global loads in flight; XCD-grouped tile order. Exact int32 sums, so the
+// bits equal the other kernels'.
+template <int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8GemmArgs a) {
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int TI = BM / WGM / 32, TJ = BN / WGN / 32;
+    constexpr int AL = BM * 8 / NT, BL = BN * 8 / NT;  // 16-byte units per thread and step
+    static_assert(AL >= 1 && BL >= 1, "loader split");
+    __shared__ i32x4 As[2][BM * 8];
+    __shared__ i32x4 Bs[2][BN * 8];
+    int bm, bn;
+    tile_order(blockIdx.x, a.gridM, a.gridN, bm, bn);
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int wm = wv / WGN, wn = wv % WGN;
+    const int rt0 = bm * (BM / 16), ct0 = a.tileN0 + bn * (BN / 16);
+    const int MT = (a.M + 15) >> 4, KT = a.KT;
+    const int steps = (KT + 1) / 2;
+    // Unit u = i*NT + t of a step: 16-row tile u/128, group (u/64)%2 of the
+    // step, lane slot u%64 (row slot%16, K bytes 16*(slot/16) of the group).
+    auto gload = [&](const int8_t *base, int tile0, int tiles, int u, int st) {
+        const int kt = 2 * st + ((u >> 6) & 1);
+        i32x4 v = i32x4{0, 0, 0, 0};
+        if (kt < KT)
+            v = *(const i32x4 *)(base + ((size_t)min(tile0 + (u >> 7), tiles - 1) * KT + kt) * 1024 +
+                                 (size_t)(u & 63) * 16);
+        return v;
+    };
+    auto lidx = [](int u) {
+        const int r = (u >> 7) * 16 + (u & 15);
+        return r * 8 + big_swz(r, ((u >> 6) & 1) * 4 + ((u & 63) >> 4));
+    };
+    i32x4 ar[AL], br[BL];
+    auto load = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < AL; ++i) ar[i] = gload(a.A, rt0, MT, i * NT + t, st);
+#pragma unroll
+        for (int i = 0; i < BL; ++i) br[i] = gload(a.B, ct0, a.NT, i * NT + t, st);
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < AL; ++i) As[buf][lidx(i * NT + t)] = ar[i];
+#pragma unroll
+        for (int i = 0; i < BL; ++i) Bs[buf][lidx(i * NT + t)] = br[i];
+    };
+    i32x16 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = i32x16{};
+    load(0);
+    store(0);
+    if (steps > 1) load(1);
+    __syncthreads();
+    const int fr = lane & 31, fh = lane >> 5;
+    for (int st = 0; st < steps; ++st) {
+        const int cur = st & 1;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int c = 2 * s + fh;
+            i32x4 fa[TI], fb[TJ];
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const int r = wm * (32 * TI) + 32 * i + fr;
+                fa[i] = As[cur][r * 8 + big_swz(r, c)];
+            }
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const int r = wn * (32 * TJ) + 32 * j + fr;
+                fb[j] = Bs[cur][r * 8 + big_swz(r, c)];
+            }
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+        if (st + 1 < steps) {
+            store(cur ^ 1);
+            if (st + 2 < steps) load(st + 2);
+        }
+        __syncthreads();
+    }
+    // Epilogue as MulPanelsI8: (float32(sum) * colScale) * rowScale.
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
+        if (col < a.c0 || col >= a.c1) continue;
+        const float cs = a.colScale[col];
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = (rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3);
+                if (row < a.M)
+                    a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row]);
+            }
+    }
+}
+
+template <int BM, int BN, int WGM, int WGN>
+static int launch_i8gemm_big(I8GemmArgs a, hipStream_t stream) {
+    const int tiles = (a.c1 + 15) / 16 - a.tileN0;
+    a.gridN = (tiles * 16 + BN - 1) / BN;
+    a.gridM = (a.M + BM - 1) / BM;
+    hipLaunchKernelGGL((i8gemm_big_kernel<BM, BN, WGM, WGN>), dim3((unsigned)(a.gridM * a.gridN)),
+                       dim3(64 * WGM * WGN), 0, stream, a);
+    return launch_status();
+}
+
 template <int BM, int BN, int WM, int WN, int BKT>
 static int launch_i8gemm_lds(I8GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
@@ -438,11 +553,14 @@ int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const
     a.c0 = c0;
     a.c1 = c1;
     a.tileN0 = c0 / 16;
-    // Shapes picked by measurement on MI355X at K = 4096, N = 12288.
+    // Shapes picked by measurement on MI355X at K = 4096, N = 12288 (M = 512:
+    // 78.5 us with 128 x 64 LDS tiles, 55.8 with 128 x 128 big tiles, 54.3
+    // with 256 x 128).
     if (M <= 16) return launch_i8gemm<1, 2, 1, 2, 4, 4>(a, stream);
     if (M <= 64) return launch_i8gemm<4, 1, 1, 2, 4, 4>(a, stream);
     if (M <= 192) return launch_i8gemm_lds<128, 64, 2, 2, 4>(a, stream);
-    return launch_i8gemm_lds<128, 64, 2, 2, 2>(a, stream);
+    if (M < 512) return launch_i8gemm_big<128, 128, 2, 2>(a, stream);
+    return launch_i8gemm_big<256, 128, 4, 2>(a, stream);
 }
 
 int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {
