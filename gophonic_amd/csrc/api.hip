@@ -75,6 +75,8 @@ const char *gphq_error_string(int status) {
         return "qwen3: token is outside vocabulary";
     case GPHQ_ERR_NON_FINITE_STATE:
         return "qwen3: non-finite hidden state";
+    case GPHQ_ERR_NOT_POSITIVE_DEFINITE:
+        return "qwen3: GPTQ Hessian is not positive definite";
     }
     return "gphq: unknown status";
 }

@@ -38,6 +38,7 @@ ERR_CONTEXT = -22
 ERR_DEST_WIDTH = -23
 ERR_TOKEN_VOCAB = -24
 ERR_NON_FINITE_STATE = -25
+ERR_NOT_POSITIVE_DEFINITE = -26
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
 
@@ -127,6 +128,10 @@ SIGNATURES = {
     "gphq_prefill_rows": (ctypes.c_int, [_vp]),
     "gphq_prefill_extend": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "gphq_prefill_check": (ctypes.c_int, [_vp, _vp]),
+    "gphq_gptq_work_bytes": (_i64, [_i64]),
+    "gphq_gptq_factor": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "gphq_gptq_round_work_bytes": (_i64, [_i64, _i64]),
+    "gphq_gptq_round": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, ctypes.c_int, _vp, _vp, _vp, _i64, _vp]),
 }
 
 FMT_GPTQ4_G128 = 12
@@ -872,3 +877,25 @@ def prepare_lm(geom_kwargs, fmt, tensors, device="cuda", prefix="model.", head_n
     lm.bind_head(head_buf, _bf16_host_f32(tensors[prefix + "norm.weight"]))
     torch.cuda.synchronize()
     return lm
+
+
+# ---- GPTQ producer (gphq_gptq_*) ----------------------------------------------
+
+
+def gptq_factor(x, rows, k, u, dead, stream=None):
+    """quantizeGroup's H = X^T X, damping and gptqInverseFactor: x [rows][k]
+    fp32, u [k][k] fp32 and dead [k] uint8 device tensors. Synchronizes."""
+    import torch
+
+    work = torch.empty(load().gphq_gptq_work_bytes(k), dtype=torch.uint8, device=x.device)
+    return check(load().gphq_gptq_factor(ptr(x), rows, k, ptr(u), ptr(dead), ptr(work), work.numel(),
+                                         stream_handle(stream)))
+
+
+def gptq_round(w, n, k, u, dead, bits, codes, scales, stream=None):
+    """gptqRound of w [n][k] (fp32 device tensor, rounded in place)."""
+    import torch
+
+    work = torch.empty(load().gphq_gptq_round_work_bytes(n, k), dtype=torch.uint8, device=w.device)
+    return check(load().gphq_gptq_round(ptr(w), n, k, ptr(u), ptr(dead), bits, ptr(codes), ptr(scales), ptr(work),
+                                        work.numel(), stream_handle(stream)))

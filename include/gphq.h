@@ -78,6 +78,8 @@ extern "C" {
 #define GPHQ_ERR_TOKEN_VOCAB (-24)
 /* gpu_darwin.go:1636-1638, 1649-1652 "qwen3: non-finite hidden state" */
 #define GPHQ_ERR_NON_FINITE_STATE (-25)
+/* gptq_linalg.go:81-83 "qwen3: GPTQ Hessian is not positive definite" */
+#define GPHQ_ERR_NOT_POSITIVE_DEFINITE (-26)
 
 /* The reference message for a status code ("" for GPHQ_OK). Static storage. */
 const char *gphq_error_string(int status);
@@ -521,6 +523,33 @@ int gphq_prefill_extend(gphq_prefill *ws, gphq_prefix *kv, int64_t keep, const i
 /* Waits for the stream; GPHQ_ERR_NON_FINITE_STATE if an extension since the
  * last check produced a non-finite hidden value. */
 int gphq_prefill_check(gphq_prefill *ws, void *stream);
+
+/* ---- GPTQ producer (cmd/qwen3-gptq) -------------------------------------------
+ * Replaces the core of qwen3lm quantizeGroup (gptq.go:604-666) for one group of
+ * projections that share their calibration inputs, on the device; the corpus,
+ * its tokenization and the model pass that collects the inputs, and the
+ * GPHQ0001 file writer, stay with the caller. fp32 products and storage as the
+ * reference's; the small substitutions sum in float64 as the reference's do;
+ * results agree with the reference to fp32 rounding, not bit for bit (its
+ * products sum in whispergemm's order). */
+/* Device scratch for gphq_gptq_factor: 4k^2 + 256k + 256 bytes. */
+int64_t gphq_gptq_work_bytes(int64_t k);
+/* H = X^T X of x_dev [rows][k] (fp32), dead channels (H[i][i] == 0 ->
+ * dead_dev[i] = 1, H[i][i] = 1), H += 0.01*mean(diag(H))*I, and
+ * u_dev [k][k] = U, upper triangular with H^-1 = U^T U (gptqInverseFactor,
+ * gptq_linalg.go:185-223). Synchronizes the stream; returns
+ * GPHQ_ERR_NOT_POSITIVE_DEFINITE where the reference returns its error. */
+int gphq_gptq_factor(const float *x_dev, int64_t rows, int64_t k, float *u_dev, uint8_t *dead_dev, void *work_dev,
+                     int64_t work_bytes, void *stream);
+/* Device scratch for gphq_gptq_round: 512n + 4n bytes. */
+int64_t gphq_gptq_round_work_bytes(int64_t n, int64_t k);
+/* gptqRound (gptq.go:671-796) of w_dev [n][k] (fp32, in place: dead columns
+ * zeroed, every value replaced by its rounded value) against U: bits 8 ->
+ * codes int8 [n][k] and fp32 row scales max|row|/127; bits 4 -> the GPU Q4
+ * bytes [n][k/2] (group of 32: value j low nibble of byte j, value j+16 high,
+ * stored + 8) and FP16 group scales (q4GroupScale) [n][k/32]. */
+int gphq_gptq_round(float *w_dev, int64_t n, int64_t k, const float *u_dev, const uint8_t *dead_dev, int bits,
+                    void *codes_dev, void *scales_dev, void *work_dev, int64_t work_bytes, void *stream);
 
 #ifdef __cplusplus
 }
