@@ -229,17 +229,22 @@ struct AttnArgs {
     int qkvw, qd, kvd, kvh, splits, sin_off;
 };
 
-// Merge factor of a softmax state with max m into one with max mn.
-__device__ __forceinline__ float rescale(float m, float mn) { return m == -INFINITY ? 0.0f : expf(m - mn); }
+// Merge factor of a base-2 softmax state with max m into one with max mn.
+__device__ __forceinline__ float rescale(float m, float mn) { return m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn); }
 
 // attend1 (gpu.metal:392-466) split over the context: grid (splits, kvh,
 // lanes), 4 wavefronts. Each of the block's 16 row groups of 16 lanes takes
 // one key at a time; lane li of a group holds dims 4li..4li+3 and
 // 64+4li..64+4li+3 of the key and value rows (two 16-byte loads, a group
-// reads one 512-byte row). The first keys' loads are issued before the
-// query/key norms are computed, so the two overlap.
+// reads one 512-byte row). Softmax in base 2 (log2(e) folded into the
+// queries). The loads for the norms are issued first, then the first keys',
+// so the norms are computed while the keys are in flight; each iteration
+// issues the next iteration's loads before its arithmetic. The new key
+// (position pos, the last one) is taken from LDS by the block that holds it,
+// after its cached keys.
 template <int GROUP, int KPI>
 __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
+    constexpr int NI = (GROUP + 4) / 4;  // norm items per wavefront, at most
     __shared__ float qs[GROUP][kHeadDim];
     __shared__ float knew[kHeadDim], vnew[kHeadDim];
     __shared__ float wm[4][GROUP], wl[4][GROUP];
@@ -252,66 +257,86 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     const int used = (n + chunk - 1) / chunk;
     if (sp >= used) return;
     const int j0 = sp * chunk, j1 = min(n, j0 + chunk);
+    const bool owner = j1 == n;          // this block holds the new key
+    const int jc = owner ? j1 - 1 : j1;  // cached keys [j0, jc)
     const float *qkv = a.qkv + (size_t)lid * a.qkvw;
     float *kc = a.kc[lid] + g * kHeadDim;
     float *vc = a.vc[lid] + g * kHeadDim;
     const int sub = lane >> 4, li = lane & 15;
     const int rowgroup = wave * 4 + sub;  // 0..15
     const int d0 = li * 4, d1 = 64 + li * 4;
-    const int iters = (j1 - j0 + 16 * KPI - 1) / (16 * KPI);
+    const int iters = (jc - j0 + 16 * KPI - 1) / (16 * KPI);
+
+    // Norm inputs: item GROUP is the new key, the others the query heads.
+    const float rc = a.rope[(size_t)pos * 64 + lane], rs = a.rope[a.sin_off + (size_t)pos * 64 + lane];
+    float x0[NI], x1[NI], w0[NI], w1[NI];
+    float nv0 = 0.0f, nv1 = 0.0f;
+#pragma unroll
+    for (int ii = 0; ii < NI; ++ii) {
+        const int item = wave + 4 * ii;
+        x0[ii] = x1[ii] = w0[ii] = w1[ii] = 0.0f;
+        if (item <= GROUP) {
+            const bool isKey = item == GROUP;
+            const float *src = isKey ? qkv + a.qd + g * kHeadDim : qkv + (size_t)(g * GROUP + item) * kHeadDim;
+            const float *w = isKey ? a.kn : a.qn;
+            x0[ii] = src[lane];
+            x1[ii] = src[lane + 64];
+            w0[ii] = w[lane];
+            w1[ii] = w[lane + 64];
+            if (isKey) {
+                nv0 = qkv[a.qd + a.kvd + g * kHeadDim + lane];
+                nv1 = qkv[a.qd + a.kvd + g * kHeadDim + lane + 64];
+            }
+        }
+    }
 
     float kr[KPI][8], vr[KPI][8];
     bool valid[KPI];
-    auto load_keys = [&](int it) {
+    auto load_keys = [&](int it, float (&kd)[KPI][8], float (&vd)[KPI][8], bool (&ok)[KPI]) {
 #pragma unroll
         for (int u = 0; u < KPI; ++u) {
             const int j = j0 + (it * KPI + u) * 16 + rowgroup;
-            valid[u] = j < j1;
-            const int jj = valid[u] ? j : j0;
+            ok[u] = j < jc;
+            const int jj = ok[u] ? j : j0;
             const float4 k0 = *(const float4 *)(kc + (size_t)jj * a.kvd + d0);
             const float4 k1 = *(const float4 *)(kc + (size_t)jj * a.kvd + d1);
             const float4 v0 = *(const float4 *)(vc + (size_t)jj * a.kvd + d0);
             const float4 v1 = *(const float4 *)(vc + (size_t)jj * a.kvd + d1);
-            kr[u][0] = k0.x, kr[u][1] = k0.y, kr[u][2] = k0.z, kr[u][3] = k0.w;
-            kr[u][4] = k1.x, kr[u][5] = k1.y, kr[u][6] = k1.z, kr[u][7] = k1.w;
-            vr[u][0] = v0.x, vr[u][1] = v0.y, vr[u][2] = v0.z, vr[u][3] = v0.w;
-            vr[u][4] = v1.x, vr[u][5] = v1.y, vr[u][6] = v1.z, vr[u][7] = v1.w;
+            kd[u][0] = k0.x, kd[u][1] = k0.y, kd[u][2] = k0.z, kd[u][3] = k0.w;
+            kd[u][4] = k1.x, kd[u][5] = k1.y, kd[u][6] = k1.z, kd[u][7] = k1.w;
+            vd[u][0] = v0.x, vd[u][1] = v0.y, vd[u][2] = v0.z, vd[u][3] = v0.w;
+            vd[u][4] = v1.x, vd[u][5] = v1.y, vd[u][6] = v1.z, vd[u][7] = v1.w;
         }
     };
-    if (iters > 0) load_keys(0);
+    if (iters > 0) load_keys(0, kr, vr, valid);
 
-    // Head RMSNorm and RoPE of the new key and of the GROUP query heads
-    // (gpu.metal:380-388 normRopeAt). Lane l holds the rotary pair (l, l+64).
-    {
-        const float c = a.rope[(size_t)pos * 64 + lane], s = a.rope[a.sin_off + (size_t)pos * 64 + lane];
-        for (int item = wave; item <= GROUP; item += 4) {
-            const bool isKey = item == GROUP;
-            const float *src = isKey ? qkv + a.qd + g * kHeadDim : qkv + (size_t)(g * GROUP + item) * kHeadDim;
-            const float *w = isKey ? a.kn : a.qn;
-            float x0 = src[lane], x1 = src[lane + 64];
-            const float ss = wave_sum(x0 * x0 + x1 * x1);
-            const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
-            x0 = x0 * (inv * w[lane]);
-            x1 = x1 * (inv * w[lane + 64]);
-            const float y0 = x0 * c - x1 * s, y1 = x1 * c + x0 * s;
-            if (isKey) {
-                const float v0 = qkv[a.qd + a.kvd + g * kHeadDim + lane];
-                const float v1 = qkv[a.qd + a.kvd + g * kHeadDim + lane + 64];
-                knew[lane] = y0;
-                knew[lane + 64] = y1;
-                vnew[lane] = v0;
-                vnew[lane + 64] = v1;
-                if (j0 <= pos && pos < j1) {  // this block appends the token's K/V row
-                    float *kd = kc + (size_t)pos * a.kvd, *vd = vc + (size_t)pos * a.kvd;
-                    kd[lane] = y0;
-                    kd[lane + 64] = y1;
-                    vd[lane] = v0;
-                    vd[lane + 64] = v1;
-                }
-            } else {
-                qs[item][lane] = y0 * a.scale;
-                qs[item][lane + 64] = y1 * a.scale;
+    // Head RMSNorm and RoPE (gpu.metal:380-388 normRopeAt). Lane l holds the
+    // rotary pair (l, l+64).
+#pragma unroll
+    for (int ii = 0; ii < NI; ++ii) {
+        const int item = wave + 4 * ii;
+        if (item > GROUP) continue;
+        const bool isKey = item == GROUP;
+        const float ss = wave_sum(x0[ii] * x0[ii] + x1[ii] * x1[ii]);
+        const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + a.eps);
+        const float y0n = x0[ii] * (inv * w0[ii]), y1n = x1[ii] * (inv * w1[ii]);
+        const float y0 = y0n * rc - y1n * rs, y1 = y1n * rc + y0n * rs;
+        if (isKey) {
+            knew[lane] = y0;
+            knew[lane + 64] = y1;
+            vnew[lane] = nv0;
+            vnew[lane + 64] = nv1;
+            if (owner) {  // this block appends the token's K/V row
+                float *kd = kc + (size_t)pos * a.kvd, *vd = vc + (size_t)pos * a.kvd;
+                kd[lane] = y0;
+                kd[lane + 64] = y1;
+                vd[lane] = nv0;
+                vd[lane + 64] = nv1;
             }
+        } else {
+            const float qscale = a.scale * 1.4426950408889634f;
+            qs[item][lane] = y0 * qscale;
+            qs[item][lane + 64] = y1 * qscale;
         }
     }
     __syncthreads();
@@ -333,18 +358,8 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[hh][i] = 0.0f;
     }
-    for (int it = 0; it < iters; ++it) {
-        if (it > 0) load_keys(it);
-#pragma unroll
-        for (int u = 0; u < KPI; ++u) {
-            if (j0 + (it * KPI + u) * 16 + rowgroup == pos) {  // the new row, from this block's LDS
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    kr[u][i] = knew[d0 + i], kr[u][4 + i] = knew[d1 + i];
-                    vr[u][i] = vnew[d0 + i], vr[u][4 + i] = vnew[d1 + i];
-                }
-            }
-        }
+    // One softmax step over KPI keys held by this row group.
+    auto step = [&](const float (&kd)[KPI][8], const float (&vd)[KPI][8], const bool (&ok)[KPI]) {
 #pragma unroll
         for (int hh = 0; hh < GROUP; ++hh) {
             float s[KPI];
@@ -353,26 +368,51 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
             for (int u = 0; u < KPI; ++u) {
                 float p = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) p = fmaf(q[hh][i], kr[u][i], p);
+                for (int i = 0; i < 8; ++i) p = fmaf(q[hh][i], kd[u][i], p);
                 p = row16_sum(p);
-                s[u] = valid[u] ? p : -INFINITY;
+                s[u] = ok[u] ? p : -INFINITY;
                 bm = fmaxf(bm, s[u]);
             }
             const float mn = fmaxf(m[hh], bm);
-            if (mn == -INFINITY) continue;
             const float c = rescale(m[hh], mn);
             l[hh] *= c;
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[hh][i] *= c;
 #pragma unroll
             for (int u = 0; u < KPI; ++u) {
-                const float p = valid[u] ? expf(s[u] - mn) : 0.0f;
+                const float p = ok[u] ? __builtin_amdgcn_exp2f(s[u] - mn) : 0.0f;
                 l[hh] += p;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[hh][i] = fmaf(p, vr[u][i], acc[hh][i]);
+                for (int i = 0; i < 8; ++i) acc[hh][i] = fmaf(p, vd[u][i], acc[hh][i]);
             }
             m[hh] = mn;
         }
+    };
+    for (int it = 0; it < iters; ++it) {
+        float kn2[KPI][8], vn2[KPI][8];
+        bool ok2[KPI];
+        if (it + 1 < iters) load_keys(it + 1, kn2, vn2, ok2);
+        step(kr, vr, valid);
+        if (it + 1 < iters) {
+#pragma unroll
+            for (int u = 0; u < KPI; ++u) {
+                valid[u] = ok2[u];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) kr[u][i] = kn2[u][i], vr[u][i] = vn2[u][i];
+            }
+        }
+    }
+    if (owner) {  // the new key, on row group 0
+#pragma unroll
+        for (int u = 0; u < KPI; ++u) {
+            valid[u] = u == 0 && rowgroup == 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kr[u][i] = knew[d0 + i], kr[u][4 + i] = knew[d1 + i];
+                vr[u][i] = vnew[d0 + i], vr[u][4 + i] = vnew[d1 + i];
+            }
+        }
+        step(kr, vr, valid);
     }
     // Merge the wave's four row groups (lanes l, l^16, l^32, l^48 hold the
     // same dims): xor 16, then xor 32.
@@ -427,7 +467,7 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
 }
 
 // The merge of attention's split partials (grid: q_heads, lanes; 128
-// threads, thread d owns dim d): weights exp(m_s - max) per split, then
+// threads, thread d owns dim d): weights 2^(m_s - max) per split, then
 // ctx = sum_s w_s A_s / sum_s w_s l_s, splits in order. Every load is issued
 // up front (thread d reads dim d of each used split, 64 threads read the
 // maxima and sums), so the kernel waits for memory once.
@@ -542,7 +582,7 @@ __global__ __launch_bounds__(1024) void lm_argmax_kernel(const ArgmaxArgs a) {
 
 template <int G>
 int launch_attend_g(const AttnArgs &a, int lanes, hipStream_t st) {
-    constexpr int KPI = G <= 4 ? 4 : 2;
+    constexpr int KPI = G <= 4 ? 2 : 1;
     hipLaunchKernelGGL((lm_attend_kernel<G, KPI>), dim3(a.splits, a.kvh, lanes), dim3(256), 0, st, a);
     return launch_status();
 }

@@ -148,6 +148,35 @@ def test_decode_06b_widths_long_context(fmt):
             pos[i] += 1
 
 
+@pytest.mark.parametrize("group", [1, 3, 5, 8])
+def test_decode_query_groups(group):
+    # Query heads per KV head other than 2 and 4: the attention kernel's
+    # per-lane query registers and keys per step change with the group. Two
+    # lanes at ragged contexts of 150 and 37 keys (several splits, a partial
+    # last step, the new key in the last block).
+    import torch
+
+    geom = lo.Geometry(hidden=256, layers=2, heads=group, kv_heads=1, head_dim=128, inter=512, vocab=96,
+                       max_pos=320)
+    model, oracle, lm = setup(geom, lo.FMT_Q8B, seed=50 + group)
+    g = model["geom"]
+    rng = np.random.default_rng(60 + group)
+    ws = gphq.DecodeBatch(lm, 2)
+    kvs = [gphq.Prefix(lm, 200), gphq.Prefix(lm, 64)]
+    prompts = [list(rng.integers(0, g.vocab, 150)), list(rng.integers(0, g.vocab, 37))]
+    caches, pos = prefill(oracle, ws, kvs, prompts)
+    tokens = list(rng.integers(0, g.vocab, 2))
+    hidden = torch.empty((2, g.hidden), device="cuda")
+    logits = torch.empty((2, g.vocab), device="cuda")
+    ws.into(kvs, pos, tokens, hidden, logits)
+    hid, lg = hidden.cpu().numpy(), logits.cpu().numpy()
+    for i in range(2):
+        wh, wl, _ = oracle.step(caches[i], pos[i], tokens[i])
+        rh, _ = err(wh, hid[i])
+        rl, _ = err(wl, lg[i])
+        assert rh <= REL and rl <= REL, (group, i, rh, rl)
+
+
 @pytest.mark.parametrize("lanes", [1, 2, 5])
 def test_greedy_into_and_run_match_oracle(lanes):
     import torch
