@@ -125,6 +125,7 @@ struct Vec2Args {
     long ystride;
     int V, K, N, KB;
     float eps;
+    float *part;  // K-split stationary path: [parts][V][N] partial sums
 };
 
 // Multi-vector GEMV over prepared A fragments: each wavefront applies its A
@@ -348,7 +349,7 @@ __global__ __launch_bounds__(256) void vech_prep_kernel(const float *__restrict_
     }
 }
 
-template <int FMT, int SK, int EPI, bool NORM>
+template <int FMT, int SK, int EPI, bool NORM, bool SPLIT>
 __global__ __launch_bounds__(64 * SK) void vech_kernel(const Vec2Args a, int iters) {
     constexpr int NB = kVechNB, STEPS = NB / 4;
     // Scale bytes per row and slice in 16-byte loads (Q8's row scale is applied at the end).
@@ -359,7 +360,8 @@ __global__ __launch_bounds__(64 * SK) void vech_kernel(const Vec2Args a, int ite
     const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, m = lane & 15;
     const int KB = a.KB;
-    const int kb0 = ks * NB;
+    // SPLIT: blockIdx.y picks which SK slices of K this block holds.
+    const int kb0 = ((SPLIT ? (int)blockIdx.y * SK : 0) + ks) * NB;
     const int tiles = (a.N + 15) / 16;
     u32x4 *st = stage[ks];
     u32x4 R[STEPS][2];
@@ -447,6 +449,14 @@ __global__ __launch_bounds__(64 * SK) void vech_kernel(const Vec2Args a, int ite
         }
         // Lane (g, m) holds vectors 4g..4g+3 of row tt*16 + m.
         const int col = tt * 16 + m;
+        if constexpr (SPLIT) {  // this part's sums; vech_finish_kernel applies the rest
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int v = 4 * g + i;
+                if (v < a.V && col < a.N) a.part[((size_t)blockIdx.y * a.V + v) * a.N + col] = acc[i];
+            }
+            continue;
+        }
         float rs = 1.0f;
         if constexpr (FMT == GPHQ_FMT_Q8) rs = ((const float *)a.scales)[min(col, a.N - 1)];
 #pragma unroll
@@ -470,10 +480,52 @@ __global__ __launch_bounds__(64 * SK) void vech_kernel(const Vec2Args a, int ite
     }
 }
 
+// The K-split stationary path's finish: thread (v, row) sums the parts in
+// order, then applies the vector's scale, the norm, the Q8 row scale and the
+// epilogue as vech_kernel does (SwiGLU: one thread per row pair).
+template <int FMT, int EPI, bool NORM>
+__global__ __launch_bounds__(256) void vech_finish_kernel(const Vec2Args a, int parts) {
+    const int per = EPI == VEC_SWIGLU ? a.N / 2 : a.N;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= a.V * per) return;
+    const int v = idx / per, r = idx - v * per;
+    auto row_value = [&](int col) {
+        float sum = 0.0f;
+        for (int p = 0; p < parts; ++p) sum += a.part[((size_t)p * a.V + v) * a.N + col];
+        float val = sum * a.inv[v];
+        if constexpr (NORM) val *= 1.0f / sqrtf(a.ssq[v] / (float)a.K + a.eps);
+        if constexpr (FMT == GPHQ_FMT_Q8) val *= ((const float *)a.scales)[col];
+        return val;
+    };
+    if constexpr (EPI == VEC_SWIGLU) {
+        const float gate = row_value(2 * r), up = row_value(2 * r + 1);
+        a.y[(size_t)v * a.ystride + r] = gate / (1.0f + expf(-gate)) * up;
+    } else if constexpr (EPI == VEC_ADD) {
+        a.y[(size_t)v * a.ystride + r] += row_value(r);
+    } else {
+        a.y[(size_t)v * a.ystride + r] = row_value(r);
+    }
+}
+
 // Whether the stationary-activation kernel takes this GEMV.
 static bool vech_takes(int fmt, int V, int K) {
     return fmt != GPHQ_FMT_Q4 && V >= 1 && V <= 16 && K % (32 * kVechNB) == 0 &&
            K / (32 * kVechNB) <= kVechMaxSlices;
+}
+
+// K parts of the split stationary path (K above one block's kVechMaxSlices
+// slices, split evenly), or 0 when it does not apply.
+static int vech_split_parts(int fmt, int V, int K) {
+    if (fmt == GPHQ_FMT_Q4 || V < 1 || V > 16 || K % (32 * kVechNB)) return 0;
+    const int slices = K / (32 * kVechNB);
+    if (slices <= kVechMaxSlices) return 0;
+    const int parts = (slices + kVechMaxSlices - 1) / kVechMaxSlices;
+    return slices % parts == 0 && parts <= 8 ? parts : 0;
+}
+
+size_t gemv_vec_split_bytes(int V, int K, int N) {
+    const int parts = vech_split_parts(GPHQ_FMT_Q8B, V, K);
+    return parts ? (size_t)parts * V * N * 4 : 0;
 }
 
 static int vech_cus() {
@@ -494,8 +546,36 @@ static int go_vech(const Vec2Args &a, hipStream_t stream) {
     const int perCu = std::max(1, 8 / SK);  // about 8 wavefronts per CU
     const int blocks = std::max(1, std::min(tiles, vech_cus() * perCu));
     const int iters = (tiles + blocks - 1) / blocks;
-    hipLaunchKernelGGL((vech_kernel<FMT, SK, EPI, NORM>), dim3((unsigned)blocks), dim3(64 * SK), 0, stream, a, iters);
+    hipLaunchKernelGGL((vech_kernel<FMT, SK, EPI, NORM, false>), dim3((unsigned)blocks), dim3(64 * SK), 0, stream, a,
+                       iters);
     return launch_status();
+}
+
+// K-split stationary path: blocks of kVechMaxSlices slices, one grid row per
+// K part (about 8 wavefronts per CU in all), then the ordered finish.
+template <int FMT, int EPI, bool NORM>
+static int go_vech_split(const Vec2Args &a, int parts, hipStream_t stream) {
+    constexpr int SK = kVechMaxSlices;
+    const int tiles = (a.N + 15) / 16;
+    const int blocks = std::max(1, std::min(tiles, vech_cus() / parts));
+    const int iters = (tiles + blocks - 1) / blocks;
+    hipLaunchKernelGGL((vech_kernel<FMT, SK, VEC_STORE, false, true>), dim3((unsigned)blocks, (unsigned)parts),
+                       dim3(64 * SK), 0, stream, a, iters);
+    GPHQ_TRY(launch_status());
+    const int per = EPI == VEC_SWIGLU ? a.N / 2 : a.N;
+    hipLaunchKernelGGL((vech_finish_kernel<FMT, EPI, NORM>), dim3((unsigned)((a.V * per + 255) / 256)), dim3(256), 0,
+                       stream, a, parts);
+    return launch_status();
+}
+
+template <int EPI, bool NORM>
+static int launch_vech_split(int fmt, const Vec2Args &a, int parts, hipStream_t stream) {
+    switch (fmt) {
+    case GPHQ_FMT_Q8: return go_vech_split<GPHQ_FMT_Q8, EPI, NORM>(a, parts, stream);
+    case GPHQ_FMT_Q8B: return go_vech_split<GPHQ_FMT_Q8B, EPI, NORM>(a, parts, stream);
+    case GPHQ_FMT_Q8B_F32: return go_vech_split<GPHQ_FMT_Q8B_F32, EPI, NORM>(a, parts, stream);
+    }
+    return GPHQ_ERR_UNSUPPORTED;
 }
 
 template <int FMT, int EPI, bool NORM>
@@ -572,9 +652,25 @@ static int launch_vec2_fmt(int fmt, const Vec2Args &a, hipStream_t stream) {
 // aligned; work holds gemv_vec_workspace_bytes(V, K). Validated by the caller.
 int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const void *scales, const float *x,
                           long xstride, float *y, long ystride, int V, int K, int N, float eps, void *work,
-                          hipStream_t stream) {
+                          hipStream_t stream, float *split, size_t split_bytes) {
     if (N == 0 || V == 0) return GPHQ_OK;
     const int KB = K / 32;
+    const int parts = vech_split_parts(fmt, V, K);
+    if (parts && split && split_bytes >= (size_t)parts * V * N * 4 && (epi != VEC_SWIGLU || N % 2 == 0)) {
+        _Float16 *A = (_Float16 *)work;
+        float *inv = (float *)((char *)work + (size_t)2 * KB * 1024);
+        float *ssq = inv + V;
+        hipLaunchKernelGGL(vech_prep_kernel, dim3(16), dim3(256), 0, stream, x, xstride, V, K, A, inv, ssq);
+        GPHQ_TRY(launch_status());
+        Vec2Args a{codes, scales, A, inv, ssq, y, ystride, V, K, N, KB, eps};
+        a.part = split;
+        if (epi == VEC_ADD) return norm ? launch_vech_split<VEC_ADD, true>(fmt, a, parts, stream)
+                                        : launch_vech_split<VEC_ADD, false>(fmt, a, parts, stream);
+        if (epi == VEC_SWIGLU) return norm ? launch_vech_split<VEC_SWIGLU, true>(fmt, a, parts, stream)
+                                           : launch_vech_split<VEC_SWIGLU, false>(fmt, a, parts, stream);
+        return norm ? launch_vech_split<VEC_STORE, true>(fmt, a, parts, stream)
+                    : launch_vech_split<VEC_STORE, false>(fmt, a, parts, stream);
+    }
     if (vech_takes(fmt, V, K)) {
         _Float16 *A = (_Float16 *)work;
         float *inv = (float *)((char *)work + (size_t)2 * KB * 1024);
@@ -611,7 +707,7 @@ int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const v
 int gemv_vec_launch(int fmt, const void *codes, const void *scales, const float *x, long xstride, float *y,
                     long ystride, int V, int K, int N, void *work, hipStream_t stream) {
     return gemv_vec_fused_launch(fmt, 0, VEC_STORE, codes, scales, x, xstride, y, ystride, V, K, N, 0.0f, work,
-                                 stream);
+                                 stream, nullptr, 0);
 }
 
 }  // namespace gphq

@@ -41,7 +41,8 @@ int gemv_fused_launch(int fmt, int pro, int epi, const void *codes, const void *
                       int K, int N, float eps, hipStream_t stream);
 int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const void *scales, const float *x,
                           long xstride, float *y, long ystride, int V, int K, int N, float eps, void *work,
-                          hipStream_t stream);
+                          hipStream_t stream, float *split, size_t split_bytes);
+size_t gemv_vec_split_bytes(int V, int K, int N);
 size_t gemv_vec_workspace_bytes(int V, int K);
 }  // namespace gphq
 
@@ -91,6 +92,8 @@ struct gphq_decode_batch {
     int32_t *tok, *pos, *start, *nonfinite;
     void *vec_work;
     size_t vec_bytes;
+    float *vec_split;  // partial sums of the K-split multi-vector GEMV
+    size_t vec_split_bytes;
     int vec_min_lanes = 2;  // lane count from which GEMVs use the MFMA multi-vector kernel
     std::vector<void *> allocs;
     // One captured greedy step (gphq_decode_greedy_run), valid for the lane
@@ -204,16 +207,14 @@ __global__ __launch_bounds__(1024) void lm_final_kernel(const float *__restrict_
     if (threadIdx.x == 0 && bad) nonfinite[lane] = 1;
 }
 
-// Keys per attention block for a context of n keys: n spread over at most
-// `splits` blocks, at least kMinChunk each, a multiple of 16. The blocks in
-// use, ceil(n / chunk), are never empty.
-__device__ __forceinline__ int attn_chunk(int n, int splits) {
-    const int chunk = (n + splits - 1) / splits;
-    return max(kMinChunk, (chunk + 15) & ~15);
-}
-__device__ __forceinline__ int attn_used_splits(int n, int splits) {
-    const int chunk = attn_chunk(n, splits);
-    return (n + chunk - 1) / chunk;
+// Keys per attention block of a prefix with `capacity` rows: the capacity
+// spread over at most `splits` blocks, at least kMinChunk each, a multiple of
+// 16. Fixed per prefix, so a block knows its key range before it has read the
+// lane's position; at a context of n keys the blocks in use, ceil(n / chunk),
+// are never empty.
+static int attn_chunk(int64_t capacity, int splits) {
+    const int64_t chunk = (capacity + splits - 1) / splits;
+    return (int)std::max<int64_t>(kMinChunk, (chunk + 15) & ~15);
 }
 
 struct AttnArgs {
@@ -225,6 +226,8 @@ struct AttnArgs {
     const int32_t *pos;    // [lanes]
     float *ctx;            // [lanes][qd]
     float *part;           // [lanes][kvh][splits][GROUP][kPart]
+    int chunk[kMaxLanes];  // keys per block (attn_chunk of the lane's prefix)
+    int cap[kMaxLanes];    // the lane's prefix capacity
     float eps, scale;
     int qkvw, qd, kvd, kvh, splits, sin_off;
 };
@@ -251,24 +254,18 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     __shared__ float wacc[4][GROUP][kHeadDim];
     const int lid = blockIdx.z, g = blockIdx.y, sp = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int chunk = a.chunk[lid], cap = a.cap[lid];
+    const int j0 = sp * chunk;
+    if (j0 >= cap) return;
     const int pos = a.pos[lid];
-    const int n = pos + 1;
-    const int chunk = attn_chunk(n, a.splits);
-    const int used = (n + chunk - 1) / chunk;
-    if (sp >= used) return;
-    const int j0 = sp * chunk, j1 = min(n, j0 + chunk);
-    const bool owner = j1 == n;          // this block holds the new key
-    const int jc = owner ? j1 - 1 : j1;  // cached keys [j0, jc)
     const float *qkv = a.qkv + (size_t)lid * a.qkvw;
     float *kc = a.kc[lid] + g * kHeadDim;
     float *vc = a.vc[lid] + g * kHeadDim;
     const int sub = lane >> 4, li = lane & 15;
     const int rowgroup = wave * 4 + sub;  // 0..15
     const int d0 = li * 4, d1 = 64 + li * 4;
-    const int iters = (jc - j0 + 16 * KPI - 1) / (16 * KPI);
 
     // Norm inputs: item GROUP is the new key, the others the query heads.
-    const float rc = a.rope[(size_t)pos * 64 + lane], rs = a.rope[a.sin_off + (size_t)pos * 64 + lane];
     float x0[NI], x1[NI], w0[NI], w1[NI];
     float nv0 = 0.0f, nv1 = 0.0f;
 #pragma unroll
@@ -290,14 +287,18 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
         }
     }
 
+    // Keys of step `it`: rows past the block's cached keys (jc, once the
+    // position is known) load row j0 instead, or, for step 0, whose loads are
+    // issued before the position arrives, the row clamped to the capacity.
     float kr[KPI][8], vr[KPI][8];
     bool valid[KPI];
+    int jc = cap;
     auto load_keys = [&](int it, float (&kd)[KPI][8], float (&vd)[KPI][8], bool (&ok)[KPI]) {
 #pragma unroll
         for (int u = 0; u < KPI; ++u) {
             const int j = j0 + (it * KPI + u) * 16 + rowgroup;
             ok[u] = j < jc;
-            const int jj = ok[u] ? j : j0;
+            const int jj = ok[u] ? j : (it == 0 ? cap - 1 : j0);
             const float4 k0 = *(const float4 *)(kc + (size_t)jj * a.kvd + d0);
             const float4 k1 = *(const float4 *)(kc + (size_t)jj * a.kvd + d1);
             const float4 v0 = *(const float4 *)(vc + (size_t)jj * a.kvd + d0);
@@ -308,7 +309,25 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
             vd[u][4] = v1.x, vd[u][5] = v1.y, vd[u][6] = v1.z, vd[u][7] = v1.w;
         }
     };
-    if (iters > 0) load_keys(0, kr, vr, valid);
+    load_keys(0, kr, vr, valid);
+    const int n = pos + 1;
+    if (j0 >= n) return;  // no keys of this lane's context
+    const int j1 = min(n, j0 + chunk);
+    const bool owner = j1 == n;  // this block holds the new key
+    jc = owner ? j1 - 1 : j1;    // cached keys [j0, jc)
+    const int iters = (jc - j0 + 16 * KPI - 1) / (16 * KPI);
+    // Step 0's rows past jc (loaded speculatively) are zeroed, so masked keys
+    // never multiply stale cache contents.
+#pragma unroll
+    for (int u = 0; u < KPI; ++u) {
+        valid[u] = j0 + u * 16 + rowgroup < jc;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            kr[u][i] = valid[u] ? kr[u][i] : 0.0f;
+            vr[u][i] = valid[u] ? vr[u][i] : 0.0f;
+        }
+    }
+    const float rc = a.rope[(size_t)pos * 64 + lane], rs = a.rope[a.sin_off + (size_t)pos * 64 + lane];
 
     // Head RMSNorm and RoPE (gpu.metal:380-388 normRopeAt). Lane l holds the
     // rotary pair (l, l+64).
@@ -476,18 +495,29 @@ __global__ __launch_bounds__(128) void lm_attn_merge_kernel(const AttnArgs a, in
     __shared__ float linv;
     const int h = blockIdx.x, lid = blockIdx.y;
     const int g = h / group, hh = h - g * group;
-    const int used = attn_used_splits(a.pos[lid] + 1, a.splits);
+    const int pos = a.pos[lid];
     const float *lp = a.part + (((size_t)lid * a.kvh + g) * a.splits * group + hh) * kPart;
     const size_t stride = (size_t)group * kPart;
     const int d = threadIdx.x;
+    // Every split's partial is loaded with the position; the splits in use
+    // are selected once it has arrived (the others hold stale values).
     float v[kMaxSplits];
 #pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) v[s] = s < used ? lp[(size_t)s * stride + 2 + d] : 0.0f;
+    for (int s = 0; s < kMaxSplits; ++s) v[s] = s < a.splits ? lp[(size_t)s * stride + 2 + d] : 0.0f;
+    float ms = -INFINITY, ls = 0.0f;
+    if (threadIdx.x < 64 && threadIdx.x < a.splits) {
+        ms = lp[threadIdx.x * stride];
+        ls = lp[threadIdx.x * stride + 1];
+    }
+    const int chunk = a.chunk[lid];
+    const int used = (pos + 1 + chunk - 1) / chunk;
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) v[s] = s < used ? v[s] : 0.0f;
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
         const bool has = lane < used;
-        const float ms = has ? lp[lane * stride] : -INFINITY;
-        const float ls = has ? lp[lane * stride + 1] : 0.0f;
+        ms = has ? ms : -INFINITY;
+        ls = has ? ls : 0.0f;
         float M = ms;
         for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
         const float c = has ? rescale(ms, M) : 0.0f;
@@ -620,7 +650,7 @@ int gemv(gphq_decode_batch *ws, int lanes, int fmt, int pro, int epi, const uint
         return GPHQ_OK;
     }
     return gemv_vec_fused_launch(fmt, pro == PRO_NORM, epi, buf + codes, buf + scales, x, (long)xs, y, (long)ys, lanes,
-                                 (int)K, (int)N, eps, ws->vec_work, st);
+                                 (int)K, (int)N, eps, ws->vec_work, st, ws->vec_split, ws->vec_split_bytes);
 }
 
 // Enqueues one decode step for `lanes` lanes whose tokens and positions are
@@ -658,6 +688,8 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool 
             const size_t off = (size_t)layer * kvs[l]->capacity * lm->kvd;
             aa.kc[l] = kvs[l]->kc + off;
             aa.vc[l] = kvs[l]->vc + off;
+            aa.chunk[l] = attn_chunk(kvs[l]->capacity, aa.splits);
+            aa.cap[l] = (int)kvs[l]->capacity;
         }
         aa.qn = lm->norms + (size_t)layer * 2 * kHeadDim;
         aa.kn = aa.qn + kHeadDim;
@@ -1041,6 +1073,8 @@ int gphq_decode_batch_new(const gphq_lm *lm, int64_t capacity, gphq_decode_batch
     const int64_t H = c.hidden, I = c.intermediate, qkvw = lm->qd + 2 * lm->kvd;
     const int64_t kmax = std::max({H, lm->qd, I});
     ws->vec_bytes = gemv_vec_workspace_bytes((int)capacity, (int)kmax);
+    // Partial sums of the K-split multi-vector path (down: K = intermediate).
+    ws->vec_split_bytes = std::max<size_t>(256, gemv_vec_split_bytes((int)std::min<int64_t>(capacity, 16), (int)I, (int)H));
     const size_t partFloats = (size_t)capacity * c.kv_heads * kMaxSplits * lm->group * kPart;
     struct {
         void **dst;
@@ -1059,6 +1093,7 @@ int gphq_decode_batch_new(const gphq_lm *lm, int64_t capacity, gphq_decode_batch
         {(void **)&ws->start, (size_t)capacity * 4},
         {(void **)&ws->nonfinite, (size_t)capacity * 4},
         {(void **)&ws->vec_work, ws->vec_bytes},
+        {(void **)&ws->vec_split, ws->vec_split_bytes},
     };
     for (auto &b : bufs) {
         hipError_t e = hipMalloc(b.dst, b.bytes);

@@ -358,3 +358,27 @@ def test_decode_8b_widths(fmt):
             assert rh <= REL and rl <= REL, (lanes, i, rh, rl)
             assert ah <= 10 * REL and al <= 10 * REL, (lanes, i, ah, al)
             pos[i] += 1
+
+
+def test_decode_8b_widths_16_lanes():
+    # 16 lanes through the stationary-activation multi-vector GEMVs at Qwen3-8B
+    # widths, the down projection (K = 12288) on its K-split path.
+    import torch
+
+    model, oracle, lm = setup(QWEN3_8B_LAYER, lo.FMT_Q8B_F32, seed=23)
+    g = model["geom"]
+    rng = np.random.default_rng(9)
+    lanes = 16
+    ws = gphq.DecodeBatch(lm, lanes)
+    kvs = [gphq.Prefix(lm, 16) for _ in range(lanes)]
+    caches, pos = prefill(oracle, ws, kvs, [list(rng.integers(0, g.vocab, 1 + i % 5)) for i in range(lanes)])
+    tokens = list(rng.integers(0, g.vocab, lanes))
+    hidden = torch.empty((lanes, g.hidden), device="cuda")
+    logits = torch.empty((lanes, g.vocab), device="cuda")
+    ws.into(kvs, pos, tokens, hidden, logits)
+    hid, lg = hidden.cpu().numpy(), logits.cpu().numpy()
+    for i in range(lanes):
+        wh, wl, _ = oracle.step(caches[i], pos[i], tokens[i])
+        rh, _ = err(wh, hid[i])
+        rl, _ = err(wl, lg[i])
+        assert rh <= REL and rl <= REL, (i, rh, rl)
