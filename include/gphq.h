@@ -137,14 +137,6 @@ int gphq_q8gemv_mul_into(const float *x_dev, int64_t x_len, const int8_t *q_dev,
 int gphq_gemv(int fmt, const void *codes_dev, const void *scales_dev, const float *x_dev,
               float *y_dev, int64_t k, int64_t n, void *stream);
 
-/* Up to GPHQ_GEMV_MAX_BATCH independent GEMVs of one format and one shape in
- * a single launch: y_dev[i] = dequant(codes_dev[i], scales_dev[i]) . x_dev[i].
- * The four arrays are host arrays of device pointers, count entries each.
- * Same arithmetic per GEMV as gphq_gemv. This is the device form of the
- * reference's projection stream, several gemv dispatches encoded into one
- * command buffer (qwen3lm/gpu_projection_stream_darwin_test.go:75-90); one
- * launch amortizes the fixed launch cost over all of them. Q8 here needs
- * k % 16 == 0. Outputs must not overlap each other or any input. */
 /* Multi-vector GEMV: `lanes` input vectors share one read of the weights,
  * y_dev[v*y_stride + j] = sum_k dequant(W)[j,k] * x_dev[v*x_stride + k].
  * Replaces gemvQ8BVector<V> (qwen3lm/gpu.metal:239-314) with its host side
@@ -164,6 +156,14 @@ int gphq_gemv_vec(int fmt, const void *codes_dev, const void *scales_dev, const 
                   float *y_dev, int64_t y_stride, int64_t lanes, int64_t k, int64_t n, void *work_dev,
                   int64_t work_bytes, void *stream);
 
+/* Up to GPHQ_GEMV_MAX_BATCH independent GEMVs of one format and one shape in
+ * a single launch: y_dev[i] = dequant(codes_dev[i], scales_dev[i]) . x_dev[i].
+ * The four arrays are host arrays of device pointers, count entries each.
+ * Same arithmetic per GEMV as gphq_gemv. This is the device form of the
+ * reference's projection stream, several gemv dispatches encoded into one
+ * command buffer (qwen3lm/gpu_projection_stream_darwin_test.go:75-90); one
+ * launch amortizes the fixed launch cost over all of them. Q8 here needs
+ * k % 16 == 0. Outputs must not overlap each other or any input. */
 #define GPHQ_GEMV_MAX_BATCH 32
 int gphq_gemv_batch(int fmt, const void *const *codes_dev, const void *const *scales_dev,
                     const float *const *x_dev, float *const *y_dev, int count, int64_t k, int64_t n,
