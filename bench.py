@@ -194,6 +194,74 @@ def gemm_config2(args, torch, gphq, ms=(1, 16, 128, 512), rotations=6, steps=20)
     return out
 
 
+def gemm_config2_block32(args, torch, gphq, ms=(1, 16, 128, 512), steps=20):
+    """Config 2 with BASELINE's per-32-block weight scales: int8 codes [12288, 4096]
+    U[-127,127] with one fp32 scale per 32-value block |N(0,1)|*0.01 (GPHQ_FMT_Q8B_F32),
+    x fp32 [M, 4096] N(0,1). The reference has no block-scaled int8 x int8 GEMM (its
+    q8gemm int8 path scales per row, gemm_config2); block-scaled weights go through
+    qwen3lm's kernels as the reference runs them: one row through the GEMV
+    (gphq_gemv, fp32), up to 16 rows through the multi-vector GEMV (gphq_gemv_vec, as
+    decode lanes), more through mm (gphq_mm: FP16 tiles, fp32 sums). Rotates > 256 MB
+    of weights."""
+    K, N = 4096, 12288
+    per = N * K + N * (K // 32) * 4
+    rotations = (300 << 20) // per + 1
+    g = torch.Generator(device="cuda")
+    g.manual_seed(22)
+    sets = []
+    for _ in range(rotations):
+        codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+        scales = torch.randn((N, K // 32), device="cuda", generator=g).abs() * 0.01
+        sets.append((codes, scales))
+    stream = torch.cuda.current_stream()
+    out = {}
+    for m in ms:
+        x = torch.randn((m, K), device="cuda", generator=g)
+        y = torch.empty((m, N), device="cuda")
+        if m == 1:
+            path = "gphq_gemv"
+            run = lambda c, sc, st: gphq.gemv(gphq.FMT_Q8B_F32, c, sc, x, y, K, N, stream=st)
+        elif m <= 16:
+            path = "gphq_gemv_vec"
+            work = torch.empty(gphq.gemv_vec_workspace_bytes(m, K), dtype=torch.uint8, device="cuda")
+            run = lambda c, sc, st: gphq.gemv_vec(gphq.FMT_Q8B_F32, c, sc, x, y, m, K, N, work, stream=st)
+        else:
+            path = "gphq_mm"
+            work = torch.empty(gphq.mm_split_workspace_bytes(m, K, N), dtype=torch.uint8, device="cuda")
+            run = lambda c, sc, st: gphq.mm(gphq.FMT_Q8B_F32, c, sc, x, y, m, K, N, work, stream=st)
+        for c, sc in sets:
+            run(c, sc, stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            cs = torch.cuda.current_stream()
+            for c, sc in sets:
+                run(c, sc, cs)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (steps * rotations)
+        nbytes = per + 4 * m * K + 4 * m * N
+        flops = 2.0 * m * N * K
+        out[f"M{m}"] = {
+            "us": round(us, 3),
+            "gbs": round(nbytes / us / 1e3, 1),
+            "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "tflops": round(flops / us / 1e6, 2),
+            "fp16_frac": round(flops / us / 1e6 / FP16_PEAK_TFLOPS, 4),
+            "rotations": rotations,
+            "path": path,
+        }
+    del sets
+    torch.cuda.empty_cache()
+    return out
+
+
 def gptq_config5(args, torch, gphq, ms=(1, 256), steps=20):
     """Config 5: GPTQ int4 dequant-matmul at the Qwen3-8B shapes K=4096 -> N=12288 and
     K=12288 -> N=4096 (gphq_mm, GPHQ_FMT_GPTQ4_G128: nibbles U[0,15] 8 per int32 along K,
@@ -480,6 +548,7 @@ def main():
     single = gemv_config1(args, torch, gphq, "graph") if args.mode == "batch" else None
     value = r["value_gbs"]
     gemm = None if args.no_gemm else gemm_config2(args, torch, gphq)
+    gemm_b32 = None if args.no_gemm else gemm_config2_block32(args, torch, gphq)
     gptq = None if args.no_gptq else gptq_config5(args, torch, gphq)
     decode = None if args.no_decode else decode_benchmarks(args, torch, gphq)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -528,6 +597,7 @@ def main():
             "mode": "one gphq_gemv launch per 4096x4096 GEMV, HIP graph of 32 launches",
         },
         "gemm_config2": gemm,
+        "gemm_config2_block32": gemm_b32,
         "gptq_config5": gptq,
         "decode_ms_per_token": (decode or {}).get("config4b_1", {}).get("ms_per_step"),
         "prefill_4096_ms": (decode or {}).get("config4a", {}).get("ms"),
