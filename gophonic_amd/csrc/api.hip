@@ -77,6 +77,10 @@ const char *gphq_error_string(int status) {
         return "qwen3: non-finite hidden state";
     case GPHQ_ERR_NOT_POSITIVE_DEFINITE:
         return "qwen3: GPTQ Hessian is not positive definite";
+    case GPHQ_ERR_SEQUENCE_COUNT:
+        return "qwen3: destinations do not match sequences";
+    case GPHQ_ERR_PASS_ROWS:
+        return "qwen3: sequence exceeds the GPU context";
     }
     return "gphq: unknown status";
 }

@@ -47,6 +47,8 @@ struct gphq_prefill {
     _Float16 *a16;  // FP16 activation tiles [rows/16][K/64][64][16]
     float *rinv;    // per-row 2^-e of the activation tiles
     int32_t *tok, *nonfinite;
+    int32_t *rowpos, *rowstart;  // packed passes: each row's position and its sequence's first row
+    float *okc = nullptr, *ovc = nullptr;  // packed passes' own K/V [layers][rows][kv_dim], on first use
     std::vector<void *> allocs;
 };
 
@@ -62,6 +64,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 struct RopeArgs {
     float *qkv;             // [rows][qkvw]
     float *kc, *vc;         // this layer's cache [capacity][kvd]
+    const int32_t *rowpos;  // packed pass: row m's position, K/V at cache row m
     const float *qn, *kn;   // head norm weights [128]
     const float *rope;      // cos [positions][64], sin at +sin_off
     float eps, qscale;
@@ -71,12 +74,14 @@ struct RopeArgs {
 // qkRope (gpu.metal:1027-1056) for row m = blockIdx.y, head item blockIdx.x
 // (query heads, then key heads, then value heads); one wavefront, lane l
 // holding the rotary pair (l, l + 64). The same norm and rotation arithmetic
-// as the decode step's attention kernel.
+// as the decode step's attention kernel. Row m sits at position base + m and
+// cache row base + m, or, in a packed pass, at position rowpos[m] and cache
+// row m.
 __global__ __launch_bounds__(64) void lm_qk_rope_kernel(const RopeArgs a) {
     const int h = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
     float *row = a.qkv + (size_t)m * a.qkvw;
-    const int pos = a.base + m;
-    const size_t slot = (size_t)pos * a.kvd;
+    const int pos = a.rowpos ? a.rowpos[m] : a.base + m;
+    const size_t slot = (size_t)(a.rowpos ? m : pos) * a.kvd;
     if (h < a.heads + a.kvh) {
         const bool isQ = h < a.heads;
         float *src = row + (size_t)h * kHeadDim;  // key head h - heads starts at qd + (h - heads) * 128
@@ -107,16 +112,21 @@ __global__ __launch_bounds__(64) void lm_qk_rope_kernel(const RopeArgs a) {
 
 struct FlashArgs {
     const float *qkv;        // [rows][qkvw], queries prepared by lm_qk_rope_kernel
-    const float *kc, *vc;    // this layer's cache [capacity][kvd]
+    const float *kc, *vc;    // this layer's cache [capacity][kvd] holding the pass's rows
+    const float *pkc, *pvc;  // a shared prefix's cache rows [0, plen), seen by every row
+    const int32_t *rowstart; // packed pass: the cache row where row m's sequence starts
     float *ctx;              // [rows][qd]
-    int qkvw, qd, kvd, rows, base;
+    int qkvw, qd, kvd, rows, base, plen;
 };
 
 // Causal attention of pass rows m0 .. m0 + 32*RH - 1 (m0 = 32*RH * row block)
 // for the GROUP query heads of KV head g = blockIdx.y: wavefront w takes
 // query head g*GROUP + w % GROUP for rows m0 + 32*(w / GROUP) .. +31, and the
 // block's waves share each 32-key tile of K and V, staged through LDS as
-// FP16. Row m attends cache rows 0 .. base + m.
+// FP16. Keys come in two segments: the shared prefix's rows 0 .. plen-1,
+// which every row sees, then the pass's cache, where row m sees rows
+// 0 .. base + m or, in a packed pass (attention items of batchPacked,
+// gpu_darwin.go:1445-1500), rows rowstart[m] .. m of its own sequence.
 //
 // Per tile, on v_mfma_f32_32x32x16_f16 with fp32 accumulation:
 //   S^T (32 keys x 32 queries) = K . Q^T, so lane l holds query l % 32 and 16
@@ -146,12 +156,24 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
     const int q = lane & 31, hi = lane >> 5;
     const int head = g * GROUP + wave % GROUP;
     const int m0 = mb * RB, mw = m0 + 32 * (wave / GROUP);
-    const int kvEnd = a.base + a.rows;  // cache rows written by this pass's qk_rope
-    const int tiles = (a.base + min(m0 + RB - 1, a.rows - 1)) / KB + 1;
-    const int myLast = a.base + mw + q;       // this lane's query sees keys 0..myLast
-    const int waveLast = a.base + mw + 31;    // no key past this is seen by the wave
+    const bool packed = a.rowstart != nullptr;
+    const int off = packed ? 0 : a.base;  // cache row of pass row 0
+    const int kvEnd = off + a.rows;       // cache rows written by this pass's qk_rope
+    // Tiles: tA of the prefix, then the pass cache's from the block's first
+    // visible row (rowstart never decreases along the pass) to its last row.
+    const int tA = (a.plen + KB - 1) / KB;
+    const int tb0 = (packed ? a.rowstart[m0] : 0) / KB;
+    const int tiles = tA + (off + min(m0 + RB - 1, a.rows - 1)) / KB + 1 - tb0;
+    const int myLast = off + mw + q;  // this lane's query sees pass-cache keys myFirst..myLast
+    const int myFirst = packed ? a.rowstart[min(mw + q, a.rows - 1)] : 0;
+    const int waveLast = off + mw + 31;  // no key past this is seen by the wave
+    const int waveFirst = packed ? a.rowstart[min(mw, a.rows - 1)] : 0;
+    const int waveFirstMax = packed ? a.rowstart[min(mw + 31, a.rows - 1)] : 0;
     const float *kbase = a.kc + (size_t)g * kHeadDim;
     const float *vbase = a.vc + (size_t)g * kHeadDim;
+    const float *pkbase = a.pkc ? a.pkc + (size_t)g * kHeadDim : nullptr;
+    const float *pvbase = a.pvc ? a.pvc + (size_t)g * kHeadDim : nullptr;
+    auto tile_key = [&](int t) { return t < tA ? t * KB : (tb0 + t - tA) * KB; };
 
     half8 qf[8];
     {
@@ -168,14 +190,16 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
 
     float4 kr[KITEMS];
     float4 vr[VITEMS];
-    auto load_tile = [&](int jb) {
+    auto load_tile = [&](int t) {
+        const bool inA = t < tA;
+        const int jb = tile_key(t), end = inA ? a.plen : kvEnd;
+        const float *kb = inA ? pkbase : kbase, *vb = inA ? pvbase : vbase;
 #pragma unroll
         for (int i = 0; i < KITEMS; ++i) {
             const int idx = tid + i * NT;
             const int j = jb + (idx >> 5);
-            kr[i] = (idx < KB * kHeadDim / 4 && j < kvEnd)
-                        ? *(const float4 *)(kbase + (size_t)j * a.kvd + 4 * (idx & 31))
-                        : float4{0.f, 0.f, 0.f, 0.f};
+            kr[i] = (idx < KB * kHeadDim / 4 && j < end) ? *(const float4 *)(kb + (size_t)j * a.kvd + 4 * (idx & 31))
+                                                         : float4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
         for (int i = 0; i < VITEMS; ++i) {
@@ -183,11 +207,11 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
             const int d = idx & (kHeadDim - 1), j = jb + 4 * (idx >> 7);
             float4 v{0.f, 0.f, 0.f, 0.f};
             if (idx < KB / 4 * kHeadDim) {
-                const float *p = vbase + (size_t)j * a.kvd + d;
-                if (j < kvEnd) v.x = p[0];
-                if (j + 1 < kvEnd) v.y = p[a.kvd];
-                if (j + 2 < kvEnd) v.z = p[2 * (size_t)a.kvd];
-                if (j + 3 < kvEnd) v.w = p[3 * (size_t)a.kvd];
+                const float *p = vb + (size_t)j * a.kvd + d;
+                if (j < end) v.x = p[0];
+                if (j + 1 < end) v.y = p[a.kvd];
+                if (j + 2 < end) v.z = p[2 * (size_t)a.kvd];
+                if (j + 3 < end) v.w = p[3 * (size_t)a.kvd];
             }
             vr[i] = v;
         }
@@ -224,12 +248,14 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
     float mrun = -INFINITY, lrun = 0.0f;
     load_tile(0);
     for (int t = 0; t < tiles; ++t) {
-        const int jb = t * KB;
+        const bool inA = t < tA;
+        const int jb = tile_key(t);
         __syncthreads();  // the previous tile's LDS reads are done
         store_tile();
         __syncthreads();
-        if (t + 1 < tiles) load_tile(jb + KB);
-        if (jb > waveLast) continue;  // every key of the tile is past this wave's rows
+        if (t + 1 < tiles) load_tile(t + 1);
+        // Every key of the tile is outside this wave's rows' ranges.
+        if (!inA && (jb > waveLast || jb + KB - 1 < waveFirst)) continue;
         f32x16 s = f32x16{};
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -237,24 +263,34 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
             s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], s, 0, 0, 0);
         }
         // s[r] is key jb + 8*(r/4) + 4*hi + r%4 of query row mw + q.
-        if (jb + KB - 1 > a.base + mw) {
+        if (inA) {
+            if (jb + KB > a.plen) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (jb + 8 * (r >> 2) + 4 * hi + (r & 3) > myLast) s[r] = -INFINITY;
+                for (int r = 0; r < 16; ++r)
+                    if (jb + 8 * (r >> 2) + 4 * hi + (r & 3) >= a.plen) s[r] = -INFINITY;
+            }
+        } else if (jb + KB - 1 > off + mw || jb < waveFirstMax) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = jb + 8 * (r >> 2) + 4 * hi + (r & 3);
+                if (key > myLast || key < myFirst) s[r] = -INFINITY;
+            }
         }
         float mx = s[0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        // Tile 0 holds key 0, which every query sees, so mnew is finite.
+        // A query with no visible key yet (packed passes) keeps mnew = -inf;
+        // its exponentials are taken against 0 so they stay 0, not NaN.
         const float mnew = fmaxf(mrun, mx);
+        const float msafe = mnew == -INFINITY ? 0.0f : mnew;
         const bool grew = mnew != mrun;
-        const float corr = __builtin_amdgcn_exp2f(mrun - mnew);
+        const float corr = __builtin_amdgcn_exp2f(mrun - msafe);
         mrun = mnew;
         float p[16], rs = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            p[r] = __builtin_amdgcn_exp2f(s[r] - mnew);
+            p[r] = __builtin_amdgcn_exp2f(s[r] - msafe);
             rs += p[r];
         }
         rs += __shfl_xor(rs, 32);
@@ -324,8 +360,19 @@ int project(gphq_prefill *ws, int R, int pro, int epi, const uint8_t *buf, int64
                         st);
 }
 
-// One pass: rows tokens already in ws->tok, continuing kv at cache row base.
-int encode_pass(gphq_prefill *ws, gphq_prefix *kv, int base, int R, hipStream_t st) {
+// Where a pass's keys and values live (layer 0; each layer is cap rows further).
+struct PassKV {
+    float *kc, *vc;          // the cache receiving the pass's rows
+    int64_t cap;
+    const float *pkc, *pvc;  // a shared, read-only prefix (or null)
+    int64_t pcap;
+    int plen;
+    const int32_t *rowpos, *rowstart;  // packed pass: per-row position and sequence start (device)
+};
+
+// One pass: R tokens already in ws->tok, at cache rows base.. of kv.kc (or,
+// packed, at rows 0..R-1 with per-row positions).
+int encode_pass(gphq_prefill *ws, const PassKV &kv, int base, int R, hipStream_t st) {
     const gphq_lm *lm = ws->lm;
     const gphq_lm_config &c = lm->cfg;
     const int64_t H = c.hidden, I = c.intermediate, qd = lm->qd, kvd = lm->kvd, qkvw = qd + 2 * kvd;
@@ -342,6 +389,7 @@ int encode_pass(gphq_prefill *ws, gphq_prefix *kv, int base, int R, hipStream_t 
     ra.kvh = (int)c.kv_heads;
     ra.base = base;
     ra.sin_off = (int)(lm->positions * 64);
+    ra.rowpos = kv.rowpos;
     FlashArgs fa{};
     fa.qkv = ws->qkv;
     fa.ctx = ws->ctx;
@@ -350,13 +398,19 @@ int encode_pass(gphq_prefill *ws, gphq_prefix *kv, int base, int R, hipStream_t 
     fa.kvd = (int)kvd;
     fa.rows = R;
     fa.base = base;
+    fa.plen = kv.plen;
+    fa.rowstart = kv.rowstart;
     for (int layer = 0; layer < c.layers; ++layer) {
         const gphq_lm_layer &L = lm->layers[layer];
         const uint8_t *buf = (const uint8_t *)L.buf_dev;
         GPHQ_TRY(project(ws, R, PRO_NORM, EPI_STORE, buf, L.qkv, L.qkv_scale, ws->h, H, ws->qkv, qkvw, qkvw, st));
-        const size_t off = (size_t)layer * kv->capacity * kvd;
-        ra.kc = kv->kc + off;
-        ra.vc = kv->vc + off;
+        const size_t off = (size_t)layer * kv.cap * kvd;
+        ra.kc = kv.kc + off;
+        ra.vc = kv.vc + off;
+        if (kv.plen > 0) {
+            fa.pkc = kv.pkc + (size_t)layer * kv.pcap * kvd;
+            fa.pvc = kv.pvc + (size_t)layer * kv.pcap * kvd;
+        }
         ra.qn = lm->norms + (size_t)layer * 2 * kHeadDim;
         ra.kn = ra.qn + kHeadDim;
         hipLaunchKernelGGL(lm_qk_rope_kernel, dim3((unsigned)(c.heads + 2 * c.kv_heads), (unsigned)R), dim3(64), 0,
@@ -403,7 +457,8 @@ int gphq_prefill_new(const gphq_lm *lm, int64_t rows, gphq_prefill **out) {
         {(void **)&ws->ctx, (size_t)rows * lm->qd * 4}, {(void **)&ws->act, (size_t)rows * I * 4},
         {(void **)&ws->hn, (size_t)H * 4},            {(void **)&ws->a16, (size_t)rpad * kpad * 2},
         {(void **)&ws->tok, (size_t)rows * 4},        {(void **)&ws->nonfinite, 4},
-        {(void **)&ws->rinv, (size_t)rows * 4},
+        {(void **)&ws->rinv, (size_t)rows * 4},       {(void **)&ws->rowpos, (size_t)rows * 4},
+        {(void **)&ws->rowstart, (size_t)rows * 4},
     };
     for (auto &b : bufs) {
         const hipError_t e = hipMalloc(b.dst, b.bytes);
@@ -450,10 +505,92 @@ int gphq_prefill_extend(gphq_prefill *ws, gphq_prefix *kv, int64_t keep, const i
         const int R = (int)std::min<int64_t>(ws->rows, n - off);
         GPHQ_TRY(hip_status(
             hipMemcpyAsync(ws->tok, tokens + off, (size_t)R * sizeof(int32_t), hipMemcpyHostToDevice, st)));
-        GPHQ_TRY(encode_pass(ws, kv, (int)(keep + off), R, st));
+        const PassKV pk{kv->kc, kv->vc, kv->capacity, nullptr, nullptr, 0, 0, nullptr, nullptr};
+        GPHQ_TRY(encode_pass(ws, pk, (int)(keep + off), R, st));
         last = R;
     }
     return lm_final_launch(lm, ws->h + (size_t)(last - 1) * H, 1, hidden_dev, ws->hn, ws->nonfinite, st);
+}
+
+int gphq_prefill_batch(gphq_prefill *ws, const gphq_prefix *shared, int64_t past, const int32_t *tokens,
+                       const int64_t *lens, int64_t count, float *hidden_dev, int64_t hidden_len, void *stream) {
+    if (!ws || !ws->lm) return GPHQ_ERR_WORKSPACE;
+    const gphq_lm *lm = ws->lm;
+    const gphq_lm_config &c = lm->cfg;
+    // HiddenLastSharedInto (evaluator.go:413-419): the prefix is the caller's
+    // and `past` is its token count.
+    if (shared && (shared->lm != lm || !shared->kc)) return GPHQ_ERR_FOREIGN_PREFIX;
+    if (past < 0 || past > (shared ? shared->capacity : 0)) return GPHQ_ERR_KEEP_RANGE;
+    // HiddenLastBatchInto (evaluator.go:539-561), sequence by sequence.
+    if (count < 1 || !lens) return GPHQ_ERR_SEQUENCE_COUNT;
+    const int64_t H = c.hidden;
+    int64_t total = 0;
+    for (int64_t q = 0; q < count; ++q) {
+        const int64_t n = lens[q];
+        if (n < 1 || !tokens) return GPHQ_ERR_EMPTY_SEQUENCE;
+        if (past + n > c.max_positions || past + n > lm->positions) return GPHQ_ERR_CONTEXT;
+        if (!hidden_dev || hidden_len != count * H) return GPHQ_ERR_DEST_WIDTH;
+        for (int64_t i = 0; i < n; ++i)
+            if (tokens[total + i] < 0 || tokens[total + i] >= c.vocab) return GPHQ_ERR_TOKEN_VOCAB;
+        total += n;
+    }
+    // batchPacked (gpu_darwin.go:1488-1496): a sequence must fit one pass.
+    for (int64_t q = 0; q < count; ++q)
+        if (lens[q] > ws->rows) return GPHQ_ERR_PASS_ROWS;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t kvd = lm->kvd;
+    if (!ws->okc) {
+        const size_t bytes = (size_t)c.layers * ws->rows * kvd * 4;
+        float *k = nullptr, *v = nullptr;
+        hipError_t e = hipMalloc(&k, bytes);
+        if (e == hipSuccess) {
+            e = hipMalloc(&v, bytes);
+            if (e != hipSuccess) (void)hipFree(k);
+        }
+        if (e != hipSuccess) return hip_status(e);
+        ws->okc = k;
+        ws->ovc = v;
+        ws->allocs.push_back(k);
+        ws->allocs.push_back(v);
+    }
+    const PassKV pk{ws->okc,
+                    ws->ovc,
+                    ws->rows,
+                    shared ? shared->kc : nullptr,
+                    shared ? shared->vc : nullptr,
+                    shared ? shared->capacity : 0,
+                    (int)past,
+                    ws->rowpos,
+                    ws->rowstart};
+    std::vector<int32_t> tok, pos, start;
+    int64_t q0 = 0, t0 = 0;
+    while (q0 < count) {
+        // Sequences in order until the next would overflow the pass.
+        int64_t q1 = q0, R = 0;
+        while (q1 < count && R + lens[q1] <= ws->rows) R += lens[q1++];
+        tok.assign(tokens + t0, tokens + t0 + R);
+        pos.resize(R);
+        start.resize(R);
+        for (int64_t q = q0, r = 0; q < q1; ++q)
+            for (int64_t i = 0; i < lens[q]; ++i, ++r) {
+                pos[r] = (int32_t)(past + i);
+                start[r] = (int32_t)(r - i);
+            }
+        GPHQ_TRY(hip_status(hipMemcpyAsync(ws->tok, tok.data(), R * 4, hipMemcpyHostToDevice, st)));
+        GPHQ_TRY(hip_status(hipMemcpyAsync(ws->rowpos, pos.data(), R * 4, hipMemcpyHostToDevice, st)));
+        GPHQ_TRY(hip_status(hipMemcpyAsync(ws->rowstart, start.data(), R * 4, hipMemcpyHostToDevice, st)));
+        GPHQ_TRY(encode_pass(ws, pk, 0, (int)R, st));
+        for (int64_t q = q0, r = 0; q < q1; ++q) {
+            r += lens[q];
+            GPHQ_TRY(lm_final_launch(lm, ws->h + (size_t)(r - 1) * H, 1, hidden_dev + q * H, ws->hn, ws->nonfinite,
+                                     st));
+        }
+        // The host arrays are read before the next pass rewrites them.
+        GPHQ_TRY(hip_status(hipStreamSynchronize(st)));
+        t0 += R;
+        q0 = q1;
+    }
+    return GPHQ_OK;
 }
 
 int gphq_prefill_check(gphq_prefill *ws, void *stream) {

@@ -39,6 +39,8 @@ ERR_DEST_WIDTH = -23
 ERR_TOKEN_VOCAB = -24
 ERR_NON_FINITE_STATE = -25
 ERR_NOT_POSITIVE_DEFINITE = -26
+ERR_SEQUENCE_COUNT = -27
+ERR_PASS_ROWS = -28
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
 
@@ -127,6 +129,7 @@ SIGNATURES = {
     "gphq_prefill_free": (None, [_vp]),
     "gphq_prefill_rows": (ctypes.c_int, [_vp]),
     "gphq_prefill_extend": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "gphq_prefill_batch": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp]),
     "gphq_prefill_check": (ctypes.c_int, [_vp, _vp]),
     "gphq_gptq_work_bytes": (_i64, [_i64]),
     "gphq_gptq_factor": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
@@ -715,6 +718,21 @@ class Prefill:
         tok = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
         check(load().gphq_prefill_extend(self.h, kv.h if kv is not None else None, keep, tok.ctypes.data, tok.size,
                                          ptr(hidden), 0 if hidden is None else hidden.numel(), stream_handle(stream)))
+
+    def batch(self, seqs, hidden, shared=None, past=0, stream=None):
+        """HiddenLastBatchInto (evaluator.go:531), or HiddenLastSharedInto
+        (evaluator.go:413) with `shared` (a Prefix holding `past` tokens, only
+        read): seqs is a list of host token lists; hidden [len(seqs), hidden]
+        device tensor receives each sequence's last-token state."""
+        import numpy as np
+
+        lens = np.array([len(q) for q in seqs], dtype=np.int64)
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(q, dtype=np.int64) for q in seqs])
+                                    if len(seqs) else np.zeros(0), dtype=np.int32)
+        check(load().gphq_prefill_batch(self.h, shared.h if shared is not None else None, past,
+                                        flat.ctypes.data if flat.size else None, lens.ctypes.data if lens.size else None,
+                                        len(seqs), ptr(hidden), 0 if hidden is None else hidden.numel(),
+                                        stream_handle(stream)))
 
     def check(self, stream=None):
         return check(load().gphq_prefill_check(self.h, stream_handle(stream)))

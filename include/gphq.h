@@ -80,6 +80,11 @@ extern "C" {
 #define GPHQ_ERR_NON_FINITE_STATE (-25)
 /* gptq_linalg.go:81-83 "qwen3: GPTQ Hessian is not positive definite" */
 #define GPHQ_ERR_NOT_POSITIVE_DEFINITE (-26)
+/* evaluator.go:539-541 "qwen3: destinations do not match sequences" */
+#define GPHQ_ERR_SEQUENCE_COUNT (-27)
+/* gpu_darwin.go:1494-1496 "qwen3: sequence exceeds the GPU context" (a
+ * packed batch's sequence longer than one pass) */
+#define GPHQ_ERR_PASS_ROWS (-28)
 
 /* The reference message for a status code ("" for GPHQ_OK). Static storage. */
 const char *gphq_error_string(int status);
@@ -520,6 +525,20 @@ int gphq_prefill_rows(const gphq_prefill *ws);
  * hidden state. */
 int gphq_prefill_extend(gphq_prefill *ws, gphq_prefix *kv, int64_t keep, const int32_t *tokens, int64_t n,
                         float *hidden_dev, int64_t hidden_len, void *stream);
+/* HiddenLastBatchInto (evaluator.go:525-575) and, with a shared prefix,
+ * HiddenLastSharedInto (evaluator.go:408-425): `count` independent sequences,
+ * their tokens concatenated in `tokens` (host) with lengths lens[count], packed
+ * into shared passes of at most the workspace's rows (batchPacked,
+ * gpu_darwin.go:1445-1500). Each sequence attends to its own earlier tokens
+ * and, when shared is not NULL, to the first `past` rows of shared, which is
+ * only read; positions start at `past` (0 without a prefix). The new rows' K/V
+ * live in the workspace's own cache (allocated on first use: layers x rows x
+ * kv_dim x 8 bytes). hidden_dev receives count x hidden floats, row s the
+ * post-final-norm state of sequence s's last token. Validation follows
+ * HiddenLastSharedInto, then HiddenLastBatchInto's checks per sequence in
+ * order, before any device work. */
+int gphq_prefill_batch(gphq_prefill *ws, const gphq_prefix *shared, int64_t past, const int32_t *tokens,
+                       const int64_t *lens, int64_t count, float *hidden_dev, int64_t hidden_len, void *stream);
 /* Waits for the stream; GPHQ_ERR_NON_FINITE_STATE if an extension since the
  * last check produced a non-finite hidden value. */
 int gphq_prefill_check(gphq_prefill *ws, void *stream);

@@ -206,3 +206,108 @@ def test_prefill_validation_errors():
     assert status(lambda: gphq.Prefill(lm, 0)) == gphq.ERR_DIMENSIONS
     bare = gphq.Lm(gphq.lm_config(fmt=lo.FMT_Q8B, **geom_kwargs(g)))
     assert status(lambda: gphq.Prefill(bare, 4)) == gphq.ERR_MODEL_INCOMPLETE
+
+
+def oracle_last(oracle, prefix, seq, capacity=128):
+    """The oracle's last-token state of seq evaluated after `prefix` tokens."""
+    cache = oracle.new_cache(capacity)
+    if prefix:
+        oracle.prefill(cache, 0, prefix)
+    h = oracle.prefill(cache, len(prefix), seq)
+    want, _ = oracle.finish(h[-1])
+    return want
+
+
+def run_batch(ws, seqs, g, shared=None, past=0):
+    import torch
+
+    hidden = torch.full((len(seqs), g.hidden), -7.0, device="cuda")
+    print(f"batch lens={[len(q) for q in seqs]} past={past} rows={ws.rows}", flush=True)
+    ws.batch(seqs, hidden, shared=shared, past=past)
+    ws.check()
+    return hidden.cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt", [lo.FMT_Q8B, lo.FMT_Q4])
+def test_batch_matches_separate_sequences(fmt):
+    # HiddenLastBatchInto: four sequences packed into passes of 24 rows
+    # (5 + 17 + 1, then 9), and a batch of one single-token sequence (the GEMV
+    # path); each result against the oracle's separate evaluation.
+    model, oracle, lm = setup(lc.GPU_SHAPE, fmt, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(41)
+    seqs = [list(rng.integers(0, g.vocab, n)) for n in (5, 17, 1, 9)]
+    ws = gphq.Prefill(lm, 24)
+    got = run_batch(ws, seqs, g)
+    for i, q in enumerate(seqs):
+        assert cosine(oracle_last(oracle, [], q), got[i]) >= COS, i
+    one = [[int(rng.integers(0, g.vocab))]]
+    got = run_batch(ws, one, g)
+    assert cosine(oracle_last(oracle, [], one[0]), got[0]) >= COS
+
+
+def test_batch_shared_prefix_is_read_only():
+    # HiddenLastSharedInto: three continuations of a 12-token prefix, packed
+    # in one pass; the prefix's cache rows are unchanged afterwards.
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(42)
+    prefix = list(rng.integers(0, g.vocab, 12))
+    ws = gphq.Prefill(lm, 32)
+    kv = gphq.Prefix(lm, 40)
+    run_prefill(ws, kv, 0, prefix, g)
+    kc, vc, cap = kv.kv()
+    before = [_read_dev_floats(base, g.layers * cap * g.kvd) for base in (kc, vc)]
+    seqs = [list(rng.integers(0, g.vocab, n)) for n in (7, 1, 20)]
+    got = run_batch(ws, seqs, g, shared=kv, past=12)
+    for i, q in enumerate(seqs):
+        assert cosine(oracle_last(oracle, prefix, q), got[i]) >= COS, i
+    after = [_read_dev_floats(base, g.layers * cap * g.kvd) for base in (kc, vc)]
+    assert all(np.array_equal(a, b) for a, b in zip(before, after))
+    # The prefix still serves a plain extension afterwards.
+    more = list(rng.integers(0, g.vocab, 3))
+    assert cosine(oracle_last(oracle, prefix, more), run_prefill(ws, kv, 12, more, g)) >= COS
+
+
+@pytest.mark.parametrize("group", [3, 8])
+def test_batch_query_groups(group):
+    # Packed rows at other query groups (one 32-row half per block above 4).
+    geom = lo.Geometry(hidden=256, layers=1, heads=group, kv_heads=1, head_dim=128, inter=512, vocab=96,
+                       max_pos=320)
+    model, oracle, lm = setup(geom, lo.FMT_Q8B, seed=40 + group)
+    g = model["geom"]
+    rng = np.random.default_rng(46 + group)
+    seqs = [list(rng.integers(0, g.vocab, n)) for n in (40, 3, 70, 33)]
+    ws = gphq.Prefill(lm, 160)
+    got = run_batch(ws, seqs, g)
+    for i, q in enumerate(seqs):
+        assert cosine(oracle_last(oracle, [], q, 160), got[i]) >= COS, i
+
+
+def test_batch_validation_errors():
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    ws = gphq.Prefill(lm, 8)
+    kv = gphq.Prefix(lm, 8)
+    other = gphq.lm_from_stored(geom_kwargs(g), lo.FMT_Q8B, model["layers"], model["embed"], model["final_norm"],
+                                model["head"])
+    hid = torch.empty((2, g.hidden), device="cuda")
+
+    def status(f):
+        try:
+            f()
+        except gphq.GphqError as e:
+            return e.status
+        return gphq.OK
+
+    assert status(lambda: ws.batch([[1], [2]], hid, shared=gphq.Prefix(other, 8), past=0)) == gphq.ERR_FOREIGN_PREFIX
+    assert status(lambda: ws.batch([[1], [2]], hid, shared=kv, past=9)) == gphq.ERR_KEEP_RANGE
+    assert status(lambda: ws.batch([[1], [2]], hid, past=1)) == gphq.ERR_KEEP_RANGE
+    assert status(lambda: ws.batch([], hid)) == gphq.ERR_SEQUENCE_COUNT
+    assert status(lambda: ws.batch([[1], []], hid)) == gphq.ERR_EMPTY_SEQUENCE
+    assert status(lambda: ws.batch([[1], [2] * (g.max_pos + 1)], hid)) == gphq.ERR_CONTEXT
+    assert status(lambda: ws.batch([[1]], hid)) == gphq.ERR_DEST_WIDTH
+    assert status(lambda: ws.batch([[1], [g.vocab]], hid)) == gphq.ERR_TOKEN_VOCAB
+    assert status(lambda: ws.batch([[1], [2] * 9], hid)) == gphq.ERR_PASS_ROWS
