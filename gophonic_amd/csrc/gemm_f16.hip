@@ -590,10 +590,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
             fb[j] = Bs[buf][r * 8 + big_swz(r, c)];
         }
     };
-    // One K step: MFMAs on LDS buffer r & 1, then step r+1's tiles (register
+    // One K step: MFMAs on LDS buffer r & 1, and step r+1's tiles (register
     // set `set` = (r+1) % PF) into the other buffer and step r+1+PF's loads.
+    // With two wavefronts per SIMD (8 per block), the second wavefront of each
+    // SIMD writes the next tiles before its MFMAs and the first after them, so
+    // one of the two keeps the SIMD's MFMA pipe busy while the other
+    // dequantizes (measured: 2% on the 4096-row pass).
+    const bool early = NT >= 512 && wv >= NT / 128;
     auto step = [&](int r, int set) {
         const int cur = r & 1, kt = k0 + r;
+        if (early && kt + 1 < k1) {
+            lstore(set, cur ^ 1);
+            if (kt + 1 + PF < k1) gload(set, kt + 1 + PF);
+        }
         f16x8v fa[2][TI], fb[2][TJ];
         frags(cur, 0, fa[0], fb[0]);
 #pragma unroll
@@ -605,7 +614,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
                 for (int j = 0; j < TJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[s & 1][i], fb[s & 1][j], acc[i][j], 0, 0, 0);
         }
-        if (kt + 1 < k1) {
+        if (!early && kt + 1 < k1) {
             lstore(set, cur ^ 1);
             if (kt + 1 + PF < k1) gload(set, kt + 1 + PF);
         }
