@@ -459,8 +459,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
     if (steps > 1) load(1);
     __syncthreads();
     const int fr = lane & 31, fh = lane >> 5;
+    // With two wavefronts per SIMD (8 per block), the second wavefront of each
+    // SIMD stores the next step's tiles before its MFMAs and the first after
+    // them, so the SIMD's MFMA pipe is fed by one while the other stores
+    // (measured: M = 512, 54 -> 52 us).
+    const bool early = NT >= 512 && wv >= NT / 128;
     for (int st = 0; st < steps; ++st) {
         const int cur = st & 1;
+        if (early && st + 1 < steps) {
+            store(cur ^ 1);
+            if (st + 2 < steps) load(st + 2);
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int c = 2 * s + fh;
@@ -481,7 +490,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
                 for (int j = 0; j < TJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
-        if (st + 1 < steps) {
+        if (!early && st + 1 < steps) {
             store(cur ^ 1);
             if (st + 2 < steps) load(st + 2);
         }
