@@ -136,8 +136,9 @@ struct FlashArgs {
 //     S^T registers (the MFMA's K index runs over the lane's own keys; V^T is
 //     stored in LDS in the matching key order).
 // Queries enter as half(q * log2(e)) (q already carries 1/sqrt(head_dim)), so
-// the softmax is exp2(s - max); probabilities and values are FP16. The
-// running output is rescaled only when some lane's maximum grew.
+// the softmax is exp2(s - m) against a reference maximum m that moves only
+// when a score exceeds it by more than 8; probabilities and values are FP16.
+// The running output is rescaled only when some lane's reference moved.
 template <int GROUP, int RH>
 __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashArgs a) {
     constexpr int NT = 64 * RH * GROUP;
@@ -280,11 +281,14 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
 #pragma unroll
         for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        // A query with no visible key yet (packed passes) keeps mnew = -inf;
-        // its exponentials are taken against 0 so they stay 0, not NaN.
-        const float mnew = fmaxf(mrun, mx);
+        // The reference maximum moves only when a score passes it by more
+        // than 8 (probabilities stay below 2^8, well inside FP16), so most
+        // tiles skip the rescale. A query with no visible key yet (packed
+        // passes) keeps mrun = -inf and takes its exponentials against 0, so
+        // they stay 0, not NaN.
+        const bool grew = mx > mrun + 8.0f;
+        const float mnew = grew ? mx : mrun;
         const float msafe = mnew == -INFINITY ? 0.0f : mnew;
-        const bool grew = mnew != mrun;
         const float corr = __builtin_amdgcn_exp2f(mrun - msafe);
         mrun = mnew;
         float p[16], rs = 0.0f;
