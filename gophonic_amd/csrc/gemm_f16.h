@@ -39,6 +39,6 @@ struct F16GemmArgs {
 // Dispatch over weight format and epilogue; arguments were validated.
 int f16gemm_launch(int wf, int epi, F16GemmArgs a, hipStream_t stream);
 // K splits of a 128 x 128-tile GEMM whose grid has `tiles` blocks (1: none).
-int mm_split_count(long tiles, int KT);
+int mm_split_count(long tiles, int KT, long outs);
 
 }  // namespace gphq

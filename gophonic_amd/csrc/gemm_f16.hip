@@ -686,13 +686,18 @@ static int launch_f16gemm_big(F16GemmArgs a, hipStream_t stream) {
     return launch_status();
 }
 
-// K splits for a 128 x 128-tile GEMM whose grid has `tiles` blocks: doubled
-// while the grid is under 256 blocks, K divides, and each split keeps at
-// least 4 K steps (at most 16; mm_split_count must agree with the scratch
-// the caller sized).
-int mm_split_count(long tiles, int KT) {
+// K splits for a 128 x 128-tile GEMM whose grid has `tiles` blocks and
+// `outs` outputs: doubled while the grid is under 512 blocks, the doubled
+// count's partial sums stay within 32 MiB (the finish kernel reads them all),
+// K divides, and each split keeps at least 4 K steps (at most 16;
+// mm_split_count must agree with the scratch the caller sized). Measured on
+// the GPTQ shapes at M = 256: K = 12288 -> N = 4096 takes 8 splits (98.7 ->
+// 77 us), K = 4096 -> N = 12288 stays at 2.
+int mm_split_count(long tiles, int KT, long outs) {
     int s = 1;
-    while (s < 16 && tiles * s < 256 && KT % (2 * s) == 0 && KT / (2 * s) >= 4) s *= 2;
+    while (s < 16 && tiles * s < 512 && (long)(2 * s) * outs * 4 <= (32L << 20) && KT % (2 * s) == 0 &&
+           KT / (2 * s) >= 4)
+        s *= 2;
     return s;
 }
 
@@ -710,7 +715,7 @@ static int launch_by_m(F16GemmArgs a, hipStream_t stream) {
         const long mid = (long)((a.M + 127) / 128) * ((width + 127) / 128);
         a.splits = 1;
         if constexpr (EPI == EPI_PLAIN || EPI == EPI_ROWSCALE)
-            if (a.part) a.splits = mm_split_count(mid, a.KT);
+            if (a.part) a.splits = mm_split_count(mid, a.KT, (long)a.M * (a.c1 - a.c0));
         if (mid * a.splits >= 128) return launch_f16gemm_big<WF, EPI, 128, 128, 2, 2, 2>(a, stream);
     }
     if constexpr (WF != W_I8_TILE && WF != W_F16_TILE) {

@@ -432,12 +432,12 @@ int64_t gphq_mm_workspace_bytes(int64_t m, int64_t k) {
 }
 
 // Activation tiles, then (256-byte aligned) the split-K partial sums the
-// 128 x 128-tile GEMM uses for 64 < m with a grid under 256 blocks.
+// 128 x 128-tile GEMM uses for 64 < m with a grid under 512 blocks.
 int64_t gphq_mm_split_workspace_bytes(int64_t m, int64_t k, int64_t n) {
     if (m < 0 || k < 0 || n < 0 || m > INT32_MAX || k > INT32_MAX || n > INT32_MAX) return GPHQ_ERR_DIMENSIONS;
     const int64_t act = (gphq_mm_workspace_bytes(m, k) + 255) / 256 * 256;
     if (m <= 64) return act;
-    const int splits = mm_split_count(ceil_div(m, 128) * ceil_div(n, 128), (int)ceil_div(k, 64));
+    const int splits = mm_split_count(ceil_div(m, 128) * ceil_div(n, 128), (int)ceil_div(k, 64), m * n);
     return act + (splits > 1 ? (int64_t)splits * m * n * 4 : 0);
 }
 

@@ -333,8 +333,9 @@ int gphq_q8gemm_mul_into(float *dst_dev, int64_t dst_len, const float *x_dev, in
 int64_t gphq_mm_workspace_bytes(int64_t m, int64_t k);
 /* The workspace with room for split-K partial sums (gpu_darwin.go:1667-1699
  * mmRun: small grids split K and mm_finish adds the splits in order): with at
- * least this many bytes, a product whose grid of 128 x 128 tiles is under 256
- * blocks splits K; the sums are then added split by split, deterministically. */
+ * least this many bytes, a product whose grid of 128 x 128 tiles is under 512
+ * blocks splits K (while the partial sums stay within 32 MiB); the sums are
+ * then added split by split, deterministically. */
 int64_t gphq_mm_split_workspace_bytes(int64_t m, int64_t k, int64_t n);
 int gphq_mm(int fmt, const void *codes_dev, const void *scales_dev, const uint8_t *zeros_dev, const float *x_dev,
             float *y_dev, int64_t m, int64_t k, int64_t n, void *work_dev, int64_t work_bytes, void *stream);
