@@ -262,6 +262,75 @@ def gemm_config2_block32(args, torch, gphq, ms=(1, 16, 128, 512), steps=20):
     return out
 
 
+def gemm_config2_block32_int8(args, torch, gphq, ms=(1, 16, 128, 512), steps=20):
+    """Config 2 as BASELINE words it, exactly: x fp32 [M, 4096] N(0,1) quantized to
+    int8 per 32-value block (WorkspaceI8's rule per block) and int8 weights [12288, 4096]
+    U[-127,127] with fp32 block scales |N(0,1)|*0.01; exact int32 per block, then the
+    block-ordered fp32 scale-accumulate (gphq_q8b_quantize + gphq_q8b_gemm; no
+    counterpart in the reference). Rotates > 256 MB of weights; times the GEMM and,
+    separately, the activation quantizer."""
+    K, N = 4096, 12288
+    per = N * K + N * (K // 32) * 4
+    rotations = (300 << 20) // per + 1
+    g = torch.Generator(device="cuda")
+    g.manual_seed(23)
+    sets = []
+    for _ in range(rotations):
+        codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+        scales = torch.randn((N, K // 32), device="cuda", generator=g).abs() * 0.01
+        sets.append((codes, scales))
+    stream = torch.cuda.current_stream()
+    out = {}
+    for m in ms:
+        x = torch.randn((m, K), device="cuda", generator=g)
+        q = torch.empty((m, K), dtype=torch.int8, device="cuda")
+        d = torch.empty((m, K // 32), device="cuda")
+        y = torch.empty((m, N), device="cuda")
+        gphq.q8b_quantize(x, m, K, q, d, stream=stream)
+        for c, sc in sets:
+            gphq.q8b_gemm(q, d, c, sc, y, m, K, N, stream=stream)
+        torch.cuda.synchronize()
+        g_gemm, g_quant = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_gemm):
+            cs = torch.cuda.current_stream()
+            for c, sc in sets:
+                gphq.q8b_gemm(q, d, c, sc, y, m, K, N, stream=cs)
+        with torch.cuda.graph(g_quant):
+            cs = torch.cuda.current_stream()
+            for _ in range(rotations):
+                gphq.q8b_quantize(x, m, K, q, d, stream=cs)
+        g_gemm.replay()
+        g_quant.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            g_gemm.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (steps * rotations)
+        e0.record(stream)
+        for _ in range(steps):
+            g_quant.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        q_us = e0.elapsed_time(e1) * 1e3 / (steps * rotations)
+        nbytes = per + m * K + m * (K // 32) * 4 + 4 * m * N
+        ops = 2.0 * m * N * K
+        out[f"M{m}"] = {
+            "gemm_us": round(us, 3),
+            "gemm_gbs": round(nbytes / us / 1e3, 1),
+            "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "tops": round(ops / us / 1e6, 1),
+            "int8_frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
+            "quantize_us": round(q_us, 3),
+            "rotations": rotations,
+        }
+    del sets
+    torch.cuda.empty_cache()
+    return out
+
+
 def gptq_config5(args, torch, gphq, ms=(1, 256), steps=20):
     """Config 5: GPTQ int4 dequant-matmul at the Qwen3-8B shapes K=4096 -> N=12288 and
     K=12288 -> N=4096 (gphq_mm, GPHQ_FMT_GPTQ4_G128: nibbles U[0,15] 8 per int32 along K,
@@ -549,6 +618,7 @@ def main():
     value = r["value_gbs"]
     gemm = None if args.no_gemm else gemm_config2(args, torch, gphq)
     gemm_b32 = None if args.no_gemm else gemm_config2_block32(args, torch, gphq)
+    gemm_b32i8 = None if args.no_gemm else gemm_config2_block32_int8(args, torch, gphq)
     gptq = None if args.no_gptq else gptq_config5(args, torch, gphq)
     decode = None if args.no_decode else decode_benchmarks(args, torch, gphq)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -598,6 +668,7 @@ def main():
         },
         "gemm_config2": gemm,
         "gemm_config2_block32": gemm_b32,
+        "gemm_config2_block32_int8": gemm_b32i8,
         "gptq_config5": gptq,
         "decode_ms_per_token": (decode or {}).get("config4b_1", {}).get("ms_per_step"),
         "prefill_4096_ms": (decode or {}).get("config4a", {}).get("ms"),

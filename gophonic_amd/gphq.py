@@ -130,6 +130,8 @@ SIGNATURES = {
     "gphq_prefill_rows": (ctypes.c_int, [_vp]),
     "gphq_prefill_extend": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "gphq_prefill_batch": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "gphq_q8b_quantize": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "gphq_q8b_gemm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "gphq_prefill_check": (ctypes.c_int, [_vp, _vp]),
     "gphq_gptq_work_bytes": (_i64, [_i64]),
     "gphq_gptq_factor": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
@@ -898,6 +900,18 @@ def prepare_lm(geom_kwargs, fmt, tensors, device="cuda", prefix="model.", head_n
 
 
 # ---- GPTQ producer (gphq_gptq_*) ----------------------------------------------
+
+
+def q8b_quantize(x, rows, k, q, d, x_stride=None, stream=None):
+    """Block-32 int8 activations (gphq_q8b_quantize): x [rows][k] fp32 device tensor ->
+    q [rows][k] int8 and d [rows][k/32] fp32."""
+    return check(load().gphq_q8b_quantize(ptr(x), rows, k, k if x_stride is None else x_stride, ptr(q), ptr(d),
+                                          stream_handle(stream)))
+
+
+def q8b_gemm(qa, da, qw, dw, y, m, k, n, stream=None):
+    """Block-32 int8 GEMM (gphq_q8b_gemm): y [m][n] from codes and block scales."""
+    return check(load().gphq_q8b_gemm(ptr(qa), ptr(da), ptr(qw), ptr(dw), ptr(y), m, k, n, stream_handle(stream)))
 
 
 def gptq_factor(x, rows, k, u, dead, stream=None):

@@ -544,6 +544,23 @@ int gphq_prefill_batch(gphq_prefill *ws, const gphq_prefix *shared, int64_t past
  * last check produced a non-finite hidden value. */
 int gphq_prefill_check(gphq_prefill *ws, void *stream);
 
+/* ---- Block-32 int8 GEMM (BASELINE configuration 2 as worded there) -----------
+ * No counterpart in the reference, whose q8gemm int8 path scales per row
+ * (gphq_q8gemm_* above). Activations and weights carry one fp32 scale per
+ * 32-value block; each block is quantized with WorkspaceI8's per-row rule
+ * (int8.go:106-168: scale max/127, inverse 127/max, both 0 unless
+ * 0 < max < inf; codes RNE(x * inverse) saturated, NaN -> 0).
+ * gphq_q8b_quantize: x [rows][x_stride] fp32 -> q [rows][k] int8 and
+ * d [rows][k/32] fp32; k % 32 == 0, x_stride a multiple of 4 and >= k, x 16-byte
+ * aligned. gphq_q8b_gemm: y [m][n] fp32 = for each output, over the blocks b
+ * in order, acc = fmaf(float(dot_b), da[r][b] * dw[c][b], acc) from +0, dot_b
+ * the exact int32 product of the block's codes; weights qw [n][k] int8
+ * row-major (the Q8B_F32 code layout) with dw [n][k/32]. Bit-exact. */
+int gphq_q8b_quantize(const float *x_dev, int64_t rows, int64_t k, int64_t x_stride, int8_t *q_dev, float *d_dev,
+                      void *stream);
+int gphq_q8b_gemm(const int8_t *qa_dev, const float *da_dev, const int8_t *qw_dev, const float *dw_dev, float *y_dev,
+                  int64_t m, int64_t k, int64_t n, void *stream);
+
 /* ---- GPTQ producer (cmd/qwen3-gptq) -------------------------------------------
  * Replaces the core of qwen3lm quantizeGroup (gptq.go:604-666) for one group of
  * projections that share their calibration inputs, on the device; the corpus,

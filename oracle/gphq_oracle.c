@@ -482,6 +482,45 @@ void orc_i8_mul_panels(float *dst, int64_t stride, const int8_t *act, const floa
     }
 }
 
+/* Block-32 int8 variant (BASELINE configuration 2's wording; the reference's
+ * q8gemm int8 path scales per row): every 32-value block of a row takes the
+ * per-row rule of WorkspaceI8 (int8.go:106-119: scale max/127, inverse 127/max,
+ * both 0 unless 0 < max < inf) and quantize's codes (int8.go:163-168). q is
+ * [rows][k], d is [rows][k/32]. No counterpart function in the reference. */
+void orc_q8b_quantize(const float *x, int64_t rows, int64_t k, int64_t stride, int8_t *q, float *d) {
+    const int64_t kb = k / 32;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t b = 0; b < kb; b++) {
+            float s, inv;
+            const float *xb = x + r * stride + b * 32;
+            orc_i8_row_scale(orc_max_abs(xb, 32), &s, &inv);
+            d[r * kb + b] = s;
+            for (int i = 0; i < 32; i++) q[r * k + b * 32 + i] = orc_i8_quantize(xb[i] * inv);
+        }
+}
+
+/* Block-32 int8 GEMM: for each output, over the 32-value blocks b in
+ * increasing order, acc = fmaf((float)dot_b, da[r][b] * dw[c][b], acc) with
+ * dot_b the exact int32 block product and acc starting at +0.0f. Activations
+ * qa [m][k] with scales da [m][k/32]; weights qw [n][k] (row-major, as the
+ * GPU formats) with scales dw [n][k/32]; y [m][n]. */
+void orc_q8b_gemm(const int8_t *qa, const float *da, const int8_t *qw, const float *dw, float *y, int64_t m,
+                  int64_t k, int64_t n) {
+    const int64_t kb = k / 32;
+    for (int64_t r = 0; r < m; r++)
+        for (int64_t c = 0; c < n; c++) {
+            float acc = 0.0f;
+            for (int64_t b = 0; b < kb; b++) {
+                int32_t dot = 0;
+                for (int i = 0; i < 32; i++)
+                    dot += (int32_t)qa[r * k + b * 32 + i] * (int32_t)qw[c * k + b * 32 + i];
+                const float s = da[r * kb + b] * dw[c * kb + b];
+                acc = fmaf((float)dot, s, acc);
+            }
+            y[r * n + c] = acc;
+        }
+}
+
 /* Multi-threaded restatement of the same oracle for the CPU baseline: the
  * reference splits 64-column panels across its worker pool
  * (qwen3lm/ops.go:153-214); the arithmetic per output is identical. */

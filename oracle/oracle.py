@@ -56,6 +56,8 @@ def _load():
         "orc_i8_row_scale": (None, [ctypes.c_float, _f32p, _f32p]),
         "orc_i8_quantize": (ctypes.c_int8, [ctypes.c_float]),
         "orc_i8_pack_rows": (None, [_f32p, _i64, _i64, _i64, _i8p, _f32p, _f32p]),
+        "orc_q8b_quantize": (None, [_f32p, _i64, _i64, _i64, _i8p, _f32p]),
+        "orc_q8b_gemm": (None, [_i8p, _f32p, _i8p, _f32p, _f32p, _i64, _i64, _i64]),
         "orc_i8_mul_panels": (None, [_f32p, _i64, _i8p, _f32p, _i64, _i8p, _f32p, _i64, _i64, _i64, _i64]),
         "orc_i8_mul_panels_mt": (None, [_f32p, _i64, _i8p, _f32p, _i64, _i8p, _f32p, _i64, _i64, ctypes.c_int]),
         "orc_pack_panels_i8_quads": (None, [_i8p, _i64, _i64, _i8p]),
@@ -265,6 +267,25 @@ def i8_pack_rows(x, rows, k, stride=None):
     inv = np.zeros(rows, dtype=np.float32)
     lib().orc_i8_pack_rows(_p(x, _f32p), rows, k, stride, _p(out, _i8p), _p(s, _f32p), _p(inv, _f32p))
     return out, s, inv
+
+
+def q8b_quantize(x, rows, k, stride=None):
+    """Block-32 variant of the int8 activation quantizer: each 32-value block
+    takes WorkspaceI8's per-row rule (int8.go:106-168) -> (q [rows,k], d [rows,k/32])."""
+    stride = k if stride is None else stride
+    x = _c(x, np.float32)
+    q = np.zeros((rows, k), dtype=np.int8)
+    d = np.zeros((rows, k // 32), dtype=np.float32)
+    lib().orc_q8b_quantize(_p(x, _f32p), rows, k, stride, _p(q, _i8p), _p(d, _f32p))
+    return q, d
+
+
+def q8b_gemm(qa, da, qw, dw, m, k, n):
+    """Block-32 int8 GEMM: exact int32 per block, then acc = fmaf(dot, da*dw, acc) in block order."""
+    y = np.zeros((m, n), dtype=np.float32)
+    lib().orc_q8b_gemm(_p(_c(qa, np.int8), _i8p), _p(_c(da, np.float32), _f32p), _p(_c(qw, np.int8), _i8p),
+                       _p(_c(dw, np.float32), _f32p), _p(y, _f32p), m, k, n)
+    return y
 
 
 def i8_mul_panels(act, row_scale, w, scales, k, n, p0=0, p1=None, stride=None, dst=None, threads=0):
