@@ -81,6 +81,8 @@ const char *gphq_error_string(int status) {
         return "qwen3: destinations do not match sequences";
     case GPHQ_ERR_PASS_ROWS:
         return "qwen3: sequence exceeds the GPU context";
+    case GPHQ_ERR_LOGITS_SHAPE:
+        return "qwen3: logits of the given values do not fill whole states and vocabulary rows";
     }
     return "gphq: unknown status";
 }

@@ -1186,6 +1186,36 @@ int gphq_decode_extend(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t l
     return GPHQ_OK;
 }
 
+int gphq_decode_batch_logits(gphq_decode_batch *ws, const float *hidden_dev, int64_t hidden_len, float *logits_dev,
+                             int64_t logits_len, void *stream) {
+    if (!ws || !ws->lm) return GPHQ_ERR_FOREIGN_WORKSPACE;
+    const gphq_lm *lm = ws->lm;
+    const int64_t H = lm->cfg.hidden, V = lm->cfg.vocab;
+    const int64_t k = hidden_len / H;
+    // evaluator.go:325-327: whole states in, whole logit rows out, at most maxTail rows.
+    if (k == 0 || hidden_len != k * H || logits_len != k * V || k > GPHQ_LOGITS_MAX_ROWS)
+        return GPHQ_ERR_LOGITS_SHAPE;
+    if (!hidden_dev || !logits_dev) return GPHQ_ERR_LOGITS_SHAPE;
+    if (overlaps(hidden_dev, hidden_len * 4, logits_dev, logits_len * 4)) return GPHQ_ERR_OVERLAP;
+    hipStream_t st = (hipStream_t)stream;
+    for (int64_t r0 = 0; r0 < k; r0 += ws->capacity) {
+        const int lanes = (int)std::min<int64_t>(ws->capacity, k - r0);
+        // gpu_darwin.go:1517-1520: hidden.apply to each state, then the head
+        // GEMV over the rotated rows (gpu_darwin.go:1530-1532).
+        GPHQ_TRY(hip_status(hipMemcpyAsync(ws->hn, hidden_dev + r0 * H, (size_t)lanes * H * 4,
+                                           hipMemcpyDeviceToDevice, st)));
+        hipLaunchKernelGGL(lm_rotate_kernel, dim3((unsigned)(H / lm->hblock), lanes), dim3(256),
+                           lm->hblock * sizeof(float), st, ws->hn, (int)H, lm->hsigns, (int)lm->hblock);
+        GPHQ_TRY(launch_status());
+        GPHQ_TRY(gemv(ws, lanes, GPHQ_FMT_Q8B, PRO_PLAIN, EPI_STORE, lm->head, 0, lm->head_scale, ws->hn, H,
+                      ws->logits, lm->head_rows, H, lm->head_rows, st));
+        GPHQ_TRY(hip_status(hipMemcpy2DAsync(logits_dev + r0 * V, (size_t)V * 4, ws->logits,
+                                             (size_t)lm->head_rows * 4, (size_t)V * 4, (size_t)lanes,
+                                             hipMemcpyDeviceToDevice, st)));
+    }
+    return GPHQ_OK;
+}
+
 int gphq_decode_batch_check(gphq_decode_batch *ws, void *stream) {
     if (!ws) return GPHQ_ERR_FOREIGN_WORKSPACE;
     int32_t flags[kMaxLanes];

@@ -41,6 +41,7 @@ ERR_NON_FINITE_STATE = -25
 ERR_NOT_POSITIVE_DEFINITE = -26
 ERR_SEQUENCE_COUNT = -27
 ERR_PASS_ROWS = -28
+ERR_LOGITS_SHAPE = -29
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
 
@@ -121,6 +122,7 @@ SIGNATURES = {
     "gphq_decode_greedy_run": (ctypes.c_int, [_vp, _vpp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "gphq_decode_extend": (ctypes.c_int, [_vp, _vpp, _i64, _vp, _vp, _i64, _vp]),
     "gphq_decode_batch_check": (ctypes.c_int, [_vp, _vp]),
+    "gphq_decode_batch_logits": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _vp]),
     "gphq_decode_batch_set_graph": (ctypes.c_int, [_vp, ctypes.c_int]),
     "gphq_prepare_work_bytes": (_i64, [_i64, _i64]),
     "gphq_prepare_projection": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
@@ -686,6 +688,12 @@ class DecodeBatch:
         tok = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1, len(kvs))
         check(load().gphq_decode_extend(self.h, _prefix_array(kvs), len(kvs), pp, tok.ctypes.data, tok.shape[0],
                                         stream_handle(stream)))
+
+    def logits(self, hidden, logits, stream=None):
+        """LogitsRowsInto: hidden [k][hidden] post-final-norm states, logits [k][vocab] device tensors."""
+        check(load().gphq_decode_batch_logits(self.h, ptr(hidden), 0 if hidden is None else hidden.numel(),
+                                              ptr(logits), 0 if logits is None else logits.numel(),
+                                              stream_handle(stream)))
 
     def check(self, stream=None):
         return check(load().gphq_decode_batch_check(self.h, stream_handle(stream)))

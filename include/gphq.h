@@ -85,6 +85,9 @@ extern "C" {
 /* gpu_darwin.go:1494-1496 "qwen3: sequence exceeds the GPU context" (a
  * packed batch's sequence longer than one pass) */
 #define GPHQ_ERR_PASS_ROWS (-28)
+/* evaluator.go:325-327 "qwen3: logits of %d values into %d, want whole
+ * states of %d and %d" */
+#define GPHQ_ERR_LOGITS_SHAPE (-29)
 
 /* The reference message for a status code ("" for GPHQ_OK). Static storage. */
 const char *gphq_error_string(int status);
@@ -452,6 +455,19 @@ int gphq_decode_batch_set_graph(gphq_decode_batch *ws, int on);
  * appends K/V rows; no head. */
 int gphq_decode_extend(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
                        const int32_t *tokens, int64_t steps, void *stream);
+/* Evaluator.LogitsRowsInto / LogitsInto on the GPU (evaluator.go:313-370;
+ * gpuWorkspace.logitsRowsInto / logitsInto, gpu_darwin.go:1510-1572): the
+ * head's logits of k = hidden_len / hidden post-final-norm states (device
+ * [k][hidden], e.g. earlier hidden_dev results) into logits_dev [k][vocab].
+ * Each state is rotated into the head's basis (hidden.apply) and multiplied by
+ * the Q8B head; a chunk of L <= capacity rows takes the same GEMV a decode step
+ * of L lanes takes, so the logits of a step's hidden states equal that step's
+ * logits bit for bit. GPHQ_ERR_LOGITS_SHAPE unless 1 <= k <=
+ * GPHQ_LOGITS_MAX_ROWS (the reference's maxTail) with whole rows on both
+ * sides. Stream-ordered; the workspace's scratch is reused. */
+#define GPHQ_LOGITS_MAX_ROWS 256
+int gphq_decode_batch_logits(gphq_decode_batch *ws, const float *hidden_dev, int64_t hidden_len, float *logits_dev,
+                             int64_t logits_len, void *stream);
 /* Waits for the stream and reports GPHQ_ERR_NON_FINITE_HIDDEN if a step since
  * the last check produced a non-finite hidden value (the reference's error,
  * gpu_darwin.go:1245-1249, which it raises before returning). */

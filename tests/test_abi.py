@@ -123,6 +123,7 @@ def test_decode_entry_points_reject_null_workspace():
     p = ctypes.c_void_p(256)
     assert lib.gphq_decode_batch_into(None, None, 1, p, p, p, 1, p, 1, None) == gphq.ERR_FOREIGN_WORKSPACE
     assert lib.gphq_decode_batch_new(None, 1, ctypes.byref(ctypes.c_void_p())) == gphq.ERR_FOREIGN_WORKSPACE
+    assert lib.gphq_decode_batch_logits(None, p, 1, p, 1, None) == gphq.ERR_FOREIGN_WORKSPACE
     assert gphq.error_string(gphq.ERR_PREFIX_FULL) == "qwen3: decode prefix has no room for another token"
 
 

@@ -382,3 +382,89 @@ def test_decode_8b_widths_16_lanes():
         rh, _ = err(wh, hid[i])
         rl, _ = err(wl, lg[i])
         assert rh <= REL and rl <= REL, (i, rh, rl)
+
+
+def head_oracle(oracle, hidden):
+    """LogitsInto on float64: the head times R applied to each post-final-norm state."""
+    h = np.asarray(hidden, np.float64)
+    return np.stack([oracle.head @ lo.rot_apply(row, oracle.hrot) for row in h])
+
+
+@pytest.mark.parametrize("lanes", [1, 3])
+def test_logits_of_step_hidden_equal_step_logits(lanes):
+    """The head over a step's hidden states reproduces that step's logits bit
+    for bit (same rotation and the same GEMV for the same row count)."""
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(40 + lanes)
+    ws = gphq.DecodeBatch(lm, 4)
+    kvs = [gphq.Prefix(lm, 32) for _ in range(lanes)]
+    prompts = [list(rng.integers(0, g.vocab, n)) for n in (4, 9, 2)[:lanes]]
+    _, pos = prefill(oracle, ws, kvs, prompts)
+    hidden = torch.empty((lanes, g.hidden), device="cuda")
+    logits = torch.empty((lanes, g.vocab), device="cuda")
+    ws.into(kvs, pos, list(rng.integers(0, g.vocab, lanes)), hidden, logits)
+    again = torch.full((lanes, g.vocab), -7.0, device="cuda")
+    ws.logits(hidden, again)
+    torch.cuda.synchronize()
+    assert torch.equal(again, logits)
+    rl, al = err(head_oracle(oracle, hidden.cpu().numpy()), again.cpu().numpy())
+    assert rl <= REL and al <= 10 * REL, (rl, al)
+
+
+@pytest.mark.parametrize("rows,capacity", [(1, 1), (2, 4), (11, 4), (256, 32)])
+def test_logits_rows_match_oracle(rows, capacity):
+    """LogitsRowsInto over row counts that span several workspace chunks
+    (11 rows through 4 lanes: 4 + 4 + 3) up to the reference's maxTail (256)."""
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(rows)
+    hid = (rng.standard_normal((rows, g.hidden)) * 2).astype(np.float32)
+    ws = gphq.DecodeBatch(lm, capacity)
+    out = torch.full((rows, g.vocab), -7.0, device="cuda")
+    ws.logits(torch.from_numpy(hid).cuda(), out)
+    got = out.cpu().numpy()
+    want = head_oracle(oracle, hid)
+    for r in range(rows):
+        rl, al = err(want[r], got[r])
+        assert rl <= REL and al <= 10 * REL, (r, rl, al)
+    # A row's logits do not depend on the rows beside it beyond the GEMV
+    # variant: one row alone agrees to the same bound.
+    one = torch.empty((1, g.vocab), device="cuda")
+    ws.logits(torch.from_numpy(hid[-1:]).cuda(), one)
+    rl, _ = err(want[-1], one.cpu().numpy()[0])
+    assert rl <= REL
+
+
+def test_logits_validation_errors():
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    ws = gphq.DecodeBatch(lm, 2)
+
+    def status(fn):
+        try:
+            fn()
+        except gphq.GphqError as e:
+            return e.status
+        return gphq.OK
+
+    hid = torch.zeros((3, g.hidden), device="cuda")
+    out = torch.full((3, g.vocab), -7.0, device="cuda")
+    assert status(lambda: ws.logits(hid[:0], out[:0])) == gphq.ERR_LOGITS_SHAPE
+    assert status(lambda: ws.logits(hid.view(-1)[: g.hidden + 1], out[:1])) == gphq.ERR_LOGITS_SHAPE
+    assert status(lambda: ws.logits(hid, out[:2])) == gphq.ERR_LOGITS_SHAPE
+    assert status(lambda: ws.logits(hid, out.view(-1)[: 3 * g.vocab - 1])) == gphq.ERR_LOGITS_SHAPE
+    big = torch.zeros((257, g.hidden), device="cuda")
+    assert status(lambda: ws.logits(big, torch.empty((257, g.vocab), device="cuda"))) == gphq.ERR_LOGITS_SHAPE
+    both = torch.zeros(4 * g.hidden, device="cuda")
+    assert status(lambda: ws.logits(both[: g.hidden], both[g.hidden - 4: g.hidden - 4 + g.vocab])) == \
+        gphq.ERR_OVERLAP
+    torch.cuda.synchronize()
+    assert (out == -7.0).all()
+    assert gphq.error_string(gphq.ERR_LOGITS_SHAPE).startswith("qwen3: logits")
