@@ -31,6 +31,7 @@ namespace gphq {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ _Float16 i8h(uint32_t v, int i) { return (_Float16)(int)((int32_t)(v << (24 - 8 * i)) >> 24); }
@@ -56,7 +57,7 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
         hi = __builtin_nontemporal_load(p + 1);
     } else if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW) {
         u32x4 w = u32x4{0, 0, 0, 0};
-        if (k < a.K) w = __builtin_nontemporal_load((const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k));
+        if (k < a.K) w = *(const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k);
         const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
         if constexpr (WF == W_Q8_ROW) {
 #pragma unroll
@@ -75,7 +76,7 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
         u32x4 w = u32x4{0, 0, 0, 0};
         _Float16 d = (_Float16)0.0f;
         if (k < a.K) {
-            w = __builtin_nontemporal_load((const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k));
+            w = *(const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k);
             d = (_Float16)((const float *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
         }
         const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
@@ -89,7 +90,7 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
         u32x4 w = u32x4{0, 0, 0, 0};
         _Float16 d = (_Float16)0.0f;
         if (k < a.K) {
-            w = __builtin_nontemporal_load((const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16));
+            w = *(const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16);
             d = __builtin_bit_cast(_Float16, ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)]);
         }
         const int sh = (g & 1) * 4;
@@ -108,9 +109,9 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
         uint32_t w0 = 0, w1 = 0;
         _Float16 s = (_Float16)0.0f, z = (_Float16)0.0f;
         if (k < a.K) {
-            const uint32_t *p = (const uint32_t *)a.B + (size_t)n * (a.K >> 3) + (k >> 3);
-            w0 = __builtin_nontemporal_load(p);
-            w1 = __builtin_nontemporal_load(p + 1);
+            const u32x2 w2 = *(const u32x2 *)((const uint32_t *)a.B + (size_t)n * (a.K >> 3) + (k >> 3));
+            w0 = w2.x;
+            w1 = w2.y;
             const size_t gi = (size_t)n * (a.K >> 7) + (k >> 7);
             s = __builtin_bit_cast(_Float16, ((const uint16_t *)a.bScale)[gi]);
             z = (_Float16)(int)(a.bZero[gi] & 15);
@@ -262,7 +263,11 @@ __global__ __launch_bounds__(64 * WM * WN * SK) void f16gemm_kernel(const F16Gem
 // ---- LDS-shared B tiles (qwen3lm row formats, M > 64) -------------------------
 // Raw codes of one B fragment (16 values of row n at k = kt*64 + g*16): the
 // code bytes (GPTQ: two words), and the scale bits (FP16 in the low half, or
-// all 32 bits of an fp32 scale) and GPTQ zero point (bits 16..23).
+// all 32 bits of an fp32 scale) and GPTQ zero point (bits 16..23). The codes
+// are read with ordinary (cached) loads: one K step takes 16-64 bytes of a
+// row, so each 128-byte line serves two (Q8) to four (GPTQ) consecutive
+// steps, and nontemporal loads re-fetched it for each (measured on MI355X:
+// GPTQ M = 256, K = 4096 -> N = 12288, 81 -> 67 us; Q8B M = 512, 106 -> 96 us).
 struct RawB {
     u32x4 w;
     uint32_t sz;
@@ -274,16 +279,16 @@ __device__ __forceinline__ RawB load_raw(const F16GemmArgs &a, int n, int kt, in
     RawB r{u32x4{0, 0, 0, 0}, 0};
     if (k >= a.K) return r;
     if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q8BF_ROW) {
-        r.w = __builtin_nontemporal_load((const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k));
+        r.w = *(const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k);
         if constexpr (WF == W_Q8B_ROW) r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
         if constexpr (WF == W_Q8BF_ROW) r.sz = ((const uint32_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
     } else if constexpr (WF == W_Q4_ROW) {
-        r.w = __builtin_nontemporal_load((const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16));
+        r.w = *(const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16);
         r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
     } else {  // W_GPTQ_ROW
-        const uint32_t *p = (const uint32_t *)a.B + (size_t)n * (a.K >> 3) + (k >> 3);
-        r.w.x = __builtin_nontemporal_load(p);
-        r.w.y = __builtin_nontemporal_load(p + 1);
+        const u32x2 w2 = *(const u32x2 *)((const uint32_t *)a.B + (size_t)n * (a.K >> 3) + (k >> 3));
+        r.w.x = w2.x;
+        r.w.y = w2.y;
         const size_t gi = (size_t)n * (a.K >> 7) + (k >> 7);
         r.sz = ((const uint16_t *)a.bScale)[gi] | ((uint32_t)(a.bZero[gi] & 15) << 16);
     }
