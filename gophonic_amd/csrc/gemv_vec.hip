@@ -285,8 +285,9 @@ __global__ __launch_bounds__(64 * SK) void gemv_vec2_kernel(const Vec2Args a) {
 // ---- stationary activations: up to 16 vectors, 8-bit formats -------------------
 // For V <= 16 vectors and K a multiple of 512 up to 4096 the activations stay
 // in registers and the weights are transposed through LDS:
-//   * vech_prep_kernel (one block per A row, 16 blocks) scales each vector by
-//     one power of two 2^e (its max into [2^14, 2^15)) and splits it into
+//   * vech_prep_kernel (one block per A row, 16 blocks, x read once) scales
+//     each vector by one power of two 2^e (its max into [2^14, 2^15)) and
+//     splits it into
 //     FP16 hi + lo, as two 16-row A tiles (tile 0 hi, tile 1 lo; row v =
 //     vector v, rows past V zero). Against the per-block split above, values
 //     smaller than 2^-17 of the vector's maximum lose relative precision, but
@@ -307,45 +308,66 @@ __global__ __launch_bounds__(64 * SK) void gemv_vec2_kernel(const Vec2Args a) {
 constexpr int kVechNB = 16;        // K blocks of 32 values per wavefront slice
 constexpr int kVechMaxSlices = 8;  // 512 threads; the kernel holds ~230 VGPRs
 
-__global__ __launch_bounds__(256) void vech_prep_kernel(const float *__restrict__ x, long stride, int V, int K,
-                                                        _Float16 *__restrict__ A, float *__restrict__ inv,
-                                                        float *__restrict__ ssq) {
-    __shared__ float red[2][4];
+// One block of 1024 threads per vector; thread t holds float4 units t, t +
+// 1024, .. of the vector (K <= 4 * 1024 * kPrepUnits), so the vector is read
+// once: the maximum and the sum of squares come from registers, and the same
+// registers are split into hi and lo.
+constexpr int kPrepUnits = 8;
+__global__ __launch_bounds__(1024) void vech_prep_kernel(const float *__restrict__ x, long stride, int V, int K,
+                                                         _Float16 *__restrict__ A, float *__restrict__ inv,
+                                                         float *__restrict__ ssq) {
+    typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
+    __shared__ float red[2][16];
     const int v = blockIdx.x;  // 16 blocks; rows v >= V are written as zero
     const bool live = v < V;
     const float *xv = x + (size_t)min(v, V - 1) * stride;
+    const int U = K / 4;
+    float4 q[kPrepUnits];
+#pragma unroll
+    for (int j = 0; j < kPrepUnits; ++j) {
+        const int u = threadIdx.x + j * 1024;
+        q[j] = (live && u < U) ? *(const float4 *)(xv + 4 * u) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     float mx = 0.0f, ss = 0.0f;
-    for (int i = threadIdx.x * 4; live && i < K; i += 1024) {
-        const float4 q = *(const float4 *)(xv + i);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
-        ss += q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w;
+#pragma unroll
+    for (int j = 0; j < kPrepUnits; ++j) {
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(q[j].x), fabsf(q[j].y)), fmaxf(fabsf(q[j].z), fabsf(q[j].w))));
+        ss += q[j].x * q[j].x + q[j].y * q[j].y + q[j].z * q[j].z + q[j].w * q[j].w;
     }
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     ss = wave_sum(ss);
     if ((threadIdx.x & 63) == 0) red[0][threadIdx.x >> 6] = mx, red[1][threadIdx.x >> 6] = ss;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    mx = red[0][0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) mx = fmaxf(mx, red[0][w]);
     const int e = pow2_exponent(mx);
     const float sc = live ? pow2f(e) : 0.0f;
     const int KB = K / 32;
-    for (int idx = threadIdx.x; idx < KB * 4; idx += blockDim.x) {
-        const int kb = idx >> 2, gq = idx & 3;
-        const float4 q0 = *(const float4 *)(xv + kb * 32 + gq * 8), q1 = *(const float4 *)(xv + kb * 32 + gq * 8 + 4);
-        const float xs[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        f16x8 hi, lo;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+    for (int j = 0; j < kPrepUnits; ++j) {
+        const int u = threadIdx.x + j * 1024;
+        if (u >= U) break;
+        // Unit u: block u / 8, 8-value group (u % 8) / 2, half u % 2.
+        const int kb = u >> 3, gq = (u >> 1) & 3, half = u & 1;
+        const float xs[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+        f16x4v hi, lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
             const float y = xs[i] * sc;  // exact: a power-of-two scaling (or zero)
             const _Float16 h = (_Float16)y;
             hi[i] = h;
             lo[i] = (_Float16)(y - (float)h);
         }
-        *(f16x8 *)(A + vec_a_offset(0, kb, KB, gq * 16 + v)) = hi;
-        *(f16x8 *)(A + vec_a_offset(1, kb, KB, gq * 16 + v)) = lo;
+        *(f16x4v *)(A + vec_a_offset(0, kb, KB, gq * 16 + v) + half * 4) = hi;
+        *(f16x4v *)(A + vec_a_offset(1, kb, KB, gq * 16 + v) + half * 4) = lo;
     }
     if (threadIdx.x == 0 && live) {
         inv[v] = pow2f(-e);
-        ssq[v] = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+        float t = red[1][0];
+#pragma unroll
+        for (int w = 1; w < 16; ++w) t += red[1][w];
+        ssq[v] = t;
     }
 }
 
@@ -520,7 +542,7 @@ static int vech_split_parts(int fmt, int V, int K) {
     const int slices = K / (32 * kVechNB);
     if (slices <= kVechMaxSlices) return 0;
     const int parts = (slices + kVechMaxSlices - 1) / kVechMaxSlices;
-    return slices % parts == 0 && parts <= 8 ? parts : 0;
+    return slices % parts == 0 && parts <= 8 && K <= 4 * 1024 * kPrepUnits ? parts : 0;
 }
 
 size_t gemv_vec_split_bytes(int V, int K, int N) {
@@ -660,7 +682,7 @@ int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const v
         _Float16 *A = (_Float16 *)work;
         float *inv = (float *)((char *)work + (size_t)2 * KB * 1024);
         float *ssq = inv + V;
-        hipLaunchKernelGGL(vech_prep_kernel, dim3(16), dim3(256), 0, stream, x, xstride, V, K, A, inv, ssq);
+        hipLaunchKernelGGL(vech_prep_kernel, dim3(16), dim3(1024), 0, stream, x, xstride, V, K, A, inv, ssq);
         GPHQ_TRY(launch_status());
         Vec2Args a{codes, scales, A, inv, ssq, y, ystride, V, K, N, KB, eps};
         a.part = split;
@@ -675,7 +697,7 @@ int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const v
         _Float16 *A = (_Float16 *)work;
         float *inv = (float *)((char *)work + (size_t)2 * KB * 1024);
         float *ssq = inv + V;
-        hipLaunchKernelGGL(vech_prep_kernel, dim3(16), dim3(256), 0, stream, x, xstride, V, K, A, inv, ssq);
+        hipLaunchKernelGGL(vech_prep_kernel, dim3(16), dim3(1024), 0, stream, x, xstride, V, K, A, inv, ssq);
         GPHQ_TRY(launch_status());
         const Vec2Args a{codes, scales, A, inv, ssq, y, ystride, V, K, N, KB, eps};
         if (epi == VEC_ADD) return norm ? launch_vech<VEC_ADD, true>(fmt, a, stream)
