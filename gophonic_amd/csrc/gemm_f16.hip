@@ -37,12 +37,128 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ _Float16 i8h(uint32_t v, int i) { return (_Float16)(int)((int32_t)(v << (24 - 8 * i)) >> 24); }
 
 
+// Raw codes of one B fragment (16 values of row n at k = kt*64 + g*16): the
+// code bytes (GPTQ: two words), and the scale bits (FP16 in the low half, or
+// all 32 bits of an fp32 scale) and GPTQ zero point (bits 16..23). The codes
+// are read with ordinary (cached) loads: one K step takes 16-64 bytes of a
+// row, so each 128-byte line serves two (Q8) to four (GPTQ) consecutive
+// steps, and nontemporal loads re-fetched it for each (measured on MI355X:
+// GPTQ M = 256, K = 4096 -> N = 12288, 81 -> 67 us; Q8B M = 512, 106 -> 96 us).
+struct RawB {
+    u32x4 w;
+    uint32_t sz;
+};
+
+template <int WF>
+__device__ __forceinline__ RawB load_raw(const F16GemmArgs &a, int n, int kt, int g) {
+    const int k = kt * 64 + g * 16;
+    RawB r{u32x4{0, 0, 0, 0}, 0};
+    if (k >= a.K) return r;
+    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q8BF_ROW) {
+        r.w = *(const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k);
+        if constexpr (WF == W_Q8B_ROW) r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
+        if constexpr (WF == W_Q8BF_ROW) r.sz = ((const uint32_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
+    } else if constexpr (WF == W_Q4_ROW) {
+        r.w = *(const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16);
+        r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
+    } else {  // W_GPTQ_ROW
+        const u32x2 w2 = *(const u32x2 *)((const uint32_t *)a.B + (size_t)n * (a.K >> 3) + (k >> 3));
+        r.w.x = w2.x;
+        r.w.y = w2.y;
+        const size_t gi = (size_t)n * (a.K >> 7) + (k >> 7);
+        r.sz = ((const uint16_t *)a.bScale)[gi] | ((uint32_t)(a.bZero[gi] & 15) << 16);
+    }
+    return r;
+}
+
+// Four int8 codes (one dword) as FP16 pairs (c0, c1), (c2, c3), exactly:
+// v_perm_b32 places each code + 128 (the xor) under the exponent byte 0x64,
+// giving 1024 + 128 + c, and one packed subtraction leaves c.
+__device__ __forceinline__ void i8x4_to_h(uint32_t w, f16x2 &p0, f16x2 &p1) {
+    const uint32_t u = w ^ 0x80808080u;
+    const f16x2 off = f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
+    p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - off;
+    p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - off;
+}
+// Four nibbles in the low halves of the bytes of w (w & 0x0F0F0F0F) as FP16
+// pairs (n - 8).
+__device__ __forceinline__ void n4x4_to_h(uint32_t w, f16x2 &p0, f16x2 &p1) {
+    const f16x2 off = f16x2{(_Float16)1032.0f, (_Float16)1032.0f};
+    p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) - off;
+    p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)) - off;
+}
+__device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
+    return __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// The same FP16 values as load_b: Q8 half(code); Q8B half(code) * d; Q8B
+// with fp32 scales half(code) * half(d); Q4 (half(nib) - 8) * d; GPTQ
+// (half(nib) - half(z)) * s, each product rounded to half once (packed FP16
+// multiplies round like the scalar ones).
+template <int WF>
+__device__ __forceinline__ void dequant(const RawB &r, int g, f16x8 &lo, f16x8 &hi) {
+    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q8BF_ROW) {
+        f16x2 p[8];
+        i8x4_to_h(r.w.x, p[0], p[1]);
+        i8x4_to_h(r.w.y, p[2], p[3]);
+        i8x4_to_h(r.w.z, p[4], p[5]);
+        i8x4_to_h(r.w.w, p[6], p[7]);
+        if constexpr (WF != W_Q8_ROW) {
+            _Float16 d;
+            if constexpr (WF == W_Q8B_ROW)
+                d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
+            else
+                d = (_Float16)__builtin_bit_cast(float, r.sz);
+            const f16x2 dd = f16x2{d, d};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) p[i] = p[i] * dd;
+        }
+        lo = cat4(p[0], p[1], p[2], p[3]);
+        hi = cat4(p[4], p[5], p[6], p[7]);
+    } else if constexpr (WF == W_Q4_ROW) {
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
+        const f16x2 dd = f16x2{d, d};
+        const int sh = (g & 1) * 4;
+        f16x2 p[8];
+        n4x4_to_h((r.w.x >> sh) & 0x0F0F0F0Fu, p[0], p[1]);
+        n4x4_to_h((r.w.y >> sh) & 0x0F0F0F0Fu, p[2], p[3]);
+        n4x4_to_h((r.w.z >> sh) & 0x0F0F0F0Fu, p[4], p[5]);
+        n4x4_to_h((r.w.w >> sh) & 0x0F0F0F0Fu, p[6], p[7]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = p[i] * dd;
+        lo = cat4(p[0], p[1], p[2], p[3]);
+        hi = cat4(p[4], p[5], p[6], p[7]);
+    } else {
+        // GPTQ: nibble i of a word is value i. Even nibbles (w & 0x0F0F0F0F) and
+        // odd ones ((w >> 4) & 0x0F0F0F0F) are paired by v_perm_b32 into the low
+        // bytes of two halves, 0x6400 is or-ed in (1024 + n), and one packed
+        // subtraction of 1024 + z leaves n - z exactly.
+        const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
+        const _Float16 zb = (_Float16)(float)(1024 + (int)(r.sz >> 16));
+        const f16x2 off = f16x2{zb, zb}, ss = f16x2{sc, sc};
+        f16x2 p[8];
+        const uint32_t wds[2] = {r.w.x, r.w.y};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t x = wds[h] & 0x0F0F0F0Fu, y = (wds[h] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t sel = (uint32_t)q | (0x0Cu << 8) | ((uint32_t)(4 + q) << 16) | (0x0Cu << 24);
+                p[4 * h + q] =
+                    (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(y, x, sel) | 0x64006400u) - off) * ss;
+            }
+        }
+        lo = cat4(p[0], p[1], p[2], p[3]);
+        hi = cat4(p[4], p[5], p[6], p[7]);
+    }
+}
+
 // B fragment: 16 FP16 weights of row `n` (clamped in range), K step kt, lane
 // group g (values k = kt*64 + g*16 + 0..15), decoded per format.
 template <int WF>
 __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int lane, f16x8 &lo, f16x8 &hi) {
     const int g = lane >> 4;
-    const int k = kt * 64 + g * 16;
     if constexpr (WF == W_I8_TILE) {
         const u32x4 w = __builtin_nontemporal_load(
             (const u32x4 *)((const int8_t *)a.B + ((size_t)(n >> 4) * a.KT + kt) * 1024 + (size_t)lane * 16));
@@ -55,71 +171,8 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
         const f16x8 *p = (const f16x8 *)((const _Float16 *)a.B + ((size_t)(n >> 4) * a.KT + kt) * 1024 + (size_t)lane * 16);
         lo = __builtin_nontemporal_load(p);
         hi = __builtin_nontemporal_load(p + 1);
-    } else if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW) {
-        u32x4 w = u32x4{0, 0, 0, 0};
-        if (k < a.K) w = *(const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k);
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-        if constexpr (WF == W_Q8_ROW) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3);
-        } else {
-            _Float16 d = (_Float16)0.0f;
-            if (k < a.K) d = __builtin_bit_cast(_Float16, ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)]);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3) * d;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3) * d;
-        }
-    } else if constexpr (WF == W_Q8BF_ROW) {
-        u32x4 w = u32x4{0, 0, 0, 0};
-        _Float16 d = (_Float16)0.0f;
-        if (k < a.K) {
-            w = *(const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k);
-            d = (_Float16)((const float *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
-        }
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) lo[i] = i8h(ww[i >> 2], i & 3) * d;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hi[i] = i8h(ww[2 + (i >> 2)], i & 3) * d;
-    } else if constexpr (WF == W_Q4_ROW) {
-        // Block (k / 32) is 16 bytes: value j in the low nibble of byte j,
-        // value j + 16 in the high nibble; this lane needs half (k / 16) % 2.
-        u32x4 w = u32x4{0, 0, 0, 0};
-        _Float16 d = (_Float16)0.0f;
-        if (k < a.K) {
-            w = *(const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16);
-            d = __builtin_bit_cast(_Float16, ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)]);
-        }
-        const int sh = (g & 1) * 4;
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            lo[i] = ((_Float16)(int)((ww[i >> 2] >> (8 * (i & 3) + sh)) & 15) - (_Float16)8.0f) * d;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            hi[i] = ((_Float16)(int)((ww[2 + (i >> 2)] >> (8 * (i & 3) + sh)) & 15) - (_Float16)8.0f) * d;
-        if (k >= a.K) {
-            lo = f16x8{};
-            hi = f16x8{};
-        }
-    } else {  // W_GPTQ_ROW
-        uint32_t w0 = 0, w1 = 0;
-        _Float16 s = (_Float16)0.0f, z = (_Float16)0.0f;
-        if (k < a.K) {
-            const u32x2 w2 = *(const u32x2 *)((const uint32_t *)a.B + (size_t)n * (a.K >> 3) + (k >> 3));
-            w0 = w2.x;
-            w1 = w2.y;
-            const size_t gi = (size_t)n * (a.K >> 7) + (k >> 7);
-            s = __builtin_bit_cast(_Float16, ((const uint16_t *)a.bScale)[gi]);
-            z = (_Float16)(int)(a.bZero[gi] & 15);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) lo[i] = ((_Float16)(int)((w0 >> (4 * i)) & 15) - z) * s;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hi[i] = ((_Float16)(int)((w1 >> (4 * i)) & 15) - z) * s;
+    } else {  // row formats: the same codes and FP16 products as the LDS-tiled kernels
+        dequant<WF>(load_raw<WF>(a, n, kt, g), g, lo, hi);
     }
 }
 
@@ -261,123 +314,6 @@ __global__ __launch_bounds__(64 * WM * WN * SK) void f16gemm_kernel(const F16Gem
 }
 
 // ---- LDS-shared B tiles (qwen3lm row formats, M > 64) -------------------------
-// Raw codes of one B fragment (16 values of row n at k = kt*64 + g*16): the
-// code bytes (GPTQ: two words), and the scale bits (FP16 in the low half, or
-// all 32 bits of an fp32 scale) and GPTQ zero point (bits 16..23). The codes
-// are read with ordinary (cached) loads: one K step takes 16-64 bytes of a
-// row, so each 128-byte line serves two (Q8) to four (GPTQ) consecutive
-// steps, and nontemporal loads re-fetched it for each (measured on MI355X:
-// GPTQ M = 256, K = 4096 -> N = 12288, 81 -> 67 us; Q8B M = 512, 106 -> 96 us).
-struct RawB {
-    u32x4 w;
-    uint32_t sz;
-};
-
-template <int WF>
-__device__ __forceinline__ RawB load_raw(const F16GemmArgs &a, int n, int kt, int g) {
-    const int k = kt * 64 + g * 16;
-    RawB r{u32x4{0, 0, 0, 0}, 0};
-    if (k >= a.K) return r;
-    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q8BF_ROW) {
-        r.w = *(const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k);
-        if constexpr (WF == W_Q8B_ROW) r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
-        if constexpr (WF == W_Q8BF_ROW) r.sz = ((const uint32_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
-    } else if constexpr (WF == W_Q4_ROW) {
-        r.w = *(const u32x4 *)((const uint8_t *)a.B + (size_t)n * (a.K >> 1) + (k >> 5) * 16);
-        r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
-    } else {  // W_GPTQ_ROW
-        const u32x2 w2 = *(const u32x2 *)((const uint32_t *)a.B + (size_t)n * (a.K >> 3) + (k >> 3));
-        r.w.x = w2.x;
-        r.w.y = w2.y;
-        const size_t gi = (size_t)n * (a.K >> 7) + (k >> 7);
-        r.sz = ((const uint16_t *)a.bScale)[gi] | ((uint32_t)(a.bZero[gi] & 15) << 16);
-    }
-    return r;
-}
-
-// Four int8 codes (one dword) as FP16 pairs (c0, c1), (c2, c3), exactly:
-// v_perm_b32 places each code + 128 (the xor) under the exponent byte 0x64,
-// giving 1024 + 128 + c, and one packed subtraction leaves c.
-__device__ __forceinline__ void i8x4_to_h(uint32_t w, f16x2 &p0, f16x2 &p1) {
-    const uint32_t u = w ^ 0x80808080u;
-    const f16x2 off = f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
-    p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - off;
-    p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - off;
-}
-// Four nibbles in the low halves of the bytes of w (w & 0x0F0F0F0F) as FP16
-// pairs (n - 8).
-__device__ __forceinline__ void n4x4_to_h(uint32_t w, f16x2 &p0, f16x2 &p1) {
-    const f16x2 off = f16x2{(_Float16)1032.0f, (_Float16)1032.0f};
-    p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) - off;
-    p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)) - off;
-}
-__device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
-    return __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3),
-                                   0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-// The same FP16 values as load_b: Q8 half(code); Q8B half(code) * d; Q8B
-// with fp32 scales half(code) * half(d); Q4 (half(nib) - 8) * d; GPTQ
-// (half(nib) - half(z)) * s, each product rounded to half once (packed FP16
-// multiplies round like the scalar ones).
-template <int WF>
-__device__ __forceinline__ void dequant(const RawB &r, int g, f16x8 &lo, f16x8 &hi) {
-    if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q8BF_ROW) {
-        f16x2 p[8];
-        i8x4_to_h(r.w.x, p[0], p[1]);
-        i8x4_to_h(r.w.y, p[2], p[3]);
-        i8x4_to_h(r.w.z, p[4], p[5]);
-        i8x4_to_h(r.w.w, p[6], p[7]);
-        if constexpr (WF != W_Q8_ROW) {
-            _Float16 d;
-            if constexpr (WF == W_Q8B_ROW)
-                d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
-            else
-                d = (_Float16)__builtin_bit_cast(float, r.sz);
-            const f16x2 dd = f16x2{d, d};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) p[i] = p[i] * dd;
-        }
-        lo = cat4(p[0], p[1], p[2], p[3]);
-        hi = cat4(p[4], p[5], p[6], p[7]);
-    } else if constexpr (WF == W_Q4_ROW) {
-        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
-        const f16x2 dd = f16x2{d, d};
-        const int sh = (g & 1) * 4;
-        f16x2 p[8];
-        n4x4_to_h((r.w.x >> sh) & 0x0F0F0F0Fu, p[0], p[1]);
-        n4x4_to_h((r.w.y >> sh) & 0x0F0F0F0Fu, p[2], p[3]);
-        n4x4_to_h((r.w.z >> sh) & 0x0F0F0F0Fu, p[4], p[5]);
-        n4x4_to_h((r.w.w >> sh) & 0x0F0F0F0Fu, p[6], p[7]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) p[i] = p[i] * dd;
-        lo = cat4(p[0], p[1], p[2], p[3]);
-        hi = cat4(p[4], p[5], p[6], p[7]);
-    } else {
-        // GPTQ: nibble i of a word is value i. Even nibbles (w & 0x0F0F0F0F) and
-        // odd ones ((w >> 4) & 0x0F0F0F0F) are paired by v_perm_b32 into the low
-        // bytes of two halves, 0x6400 is or-ed in (1024 + n), and one packed
-        // subtraction of 1024 + z leaves n - z exactly.
-        const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)r.sz);
-        const _Float16 zb = (_Float16)(float)(1024 + (int)(r.sz >> 16));
-        const f16x2 off = f16x2{zb, zb}, ss = f16x2{sc, sc};
-        f16x2 p[8];
-        const uint32_t wds[2] = {r.w.x, r.w.y};
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t x = wds[h] & 0x0F0F0F0Fu, y = (wds[h] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t sel = (uint32_t)q | (0x0Cu << 8) | ((uint32_t)(4 + q) << 16) | (0x0Cu << 24);
-                p[4 * h + q] =
-                    (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(y, x, sel) | 0x64006400u) - off) * ss;
-            }
-        }
-        lo = cat4(p[0], p[1], p[2], p[3]);
-        hi = cat4(p[4], p[5], p[6], p[7]);
-    }
-}
-
 // Block tile (16*WTM*WGM) x (32*WTN): 2*WGM wavefronts, WGM along M and 2
 // along N, each (16*WTM) x (16*WTN) of the output. Per 64-deep K step the
 // block's threads dequantize the B tile once into LDS in MFMA fragment order
@@ -708,8 +644,10 @@ int mm_split_count(long tiles, int KT, long outs) {
 
 template <int WF, int EPI>
 static int launch_by_m(F16GemmArgs a, hipStream_t stream) {
-    if (a.M <= 16) return launch_f16gemm<WF, EPI, 1, 2, 1, 2, 4, 2>(a, stream);
-    if (a.M <= 64) return launch_f16gemm<WF, EPI, 4, 1, 1, 2, 4, 2>(a, stream);
+    // Measured on MI355X at K = 4096, N = 12288 (Q8B): M <= 16 in 32-row
+    // blocks with K split 8 ways, 26.7 us; M = 32 / 64 36.9 / 41.5 us.
+    if (a.M <= 16) return launch_f16gemm<WF, EPI, 1, 2, 1, 1, 8, 2>(a, stream);
+    if (a.M <= 64) return launch_f16gemm<WF, EPI, 4, 2, 1, 2, 4, 2>(a, stream);
     if constexpr (WF != W_I8_TILE && WF != W_F16_TILE) {
         const long width = a.c1 - a.tileN0 * 16;
         // 256 x 256 block tiles when they fill the chip.
