@@ -233,6 +233,63 @@ __global__ __launch_bounds__(64 * WGM * WGN) void q8b_gemm_kernel(const Q8bArgs 
         }
 }
 
+// M <= 2 (K a multiple of 1024): one wavefront per group of kRowsRW weight
+// rows, so the grid is N / 4 blocks wide instead of N / 128. Lane l takes
+// 16-byte chunk l of each 1 KiB K step of its rows and of every activation
+// row; v_dot4_i32_i8 gives exact int32 partial dots, lanes l and l ^ 1 add
+// their halves into the 32-value block's dot (exact), which is staged in LDS
+// with both scale vectors. Lane (r, i) then runs output (i, row r)'s chain
+// acc = fmaf(float(dot_b), da[i][b] * dw[r][b], acc) in block order: the
+// operations of the tiled kernel and of the oracle, so the result is the same
+// bit for bit.
+constexpr int kRowsRW = 4;
+// Each activation row adds a pass over the lane's K chunks and a chain per
+// output: measured at K = 4096, N = 12288, M = 1 takes 23 us (the tiled
+// kernel 47 us) and M = 16 192 us, so the kernel stops at two rows.
+constexpr int kRowsMaxM = 2;
+__global__ __launch_bounds__(64) void q8b_rows_kernel(const Q8bArgs a) {
+    extern __shared__ float sm[];
+    const int KB = a.k >> 5, m = a.m, lane = threadIdx.x;
+    float *dots = sm;                     // [kRowsRW][m][KB]
+    float *sw = dots + kRowsRW * m * KB;  // [kRowsRW][KB] weight block scales
+    float *sa = sw + kRowsRW * KB;        // [m][KB] activation block scales
+    const int n0 = blockIdx.x * kRowsRW;
+    for (int i = lane; i < kRowsRW * KB; i += 64) {
+        const int r = i / KB, b = i - r * KB;
+        sw[i] = a.dw[(size_t)min(n0 + r, a.n - 1) * KB + b];
+    }
+    for (int i = lane; i < m * KB; i += 64) sa[i] = a.da[i];
+    const int steps = a.k >> 10;
+    for (int s = 0; s < steps; ++s) {
+        const size_t kb = (size_t)s * 1024 + (size_t)lane * 16;
+        i32x4 w[kRowsRW];
+#pragma unroll
+        for (int r = 0; r < kRowsRW; ++r) w[r] = *(const i32x4 *)(a.qw + (size_t)min(n0 + r, a.n - 1) * a.k + kb);
+        for (int i = 0; i < m; ++i) {
+            const i32x4 x = *(const i32x4 *)(a.qa + (size_t)i * a.k + kb);
+#pragma unroll
+            for (int r = 0; r < kRowsRW; ++r) {
+                int d = __builtin_amdgcn_sdot4(x.x, w[r].x, 0, false);
+                d = __builtin_amdgcn_sdot4(x.y, w[r].y, d, false);
+                d = __builtin_amdgcn_sdot4(x.z, w[r].z, d, false);
+                d = __builtin_amdgcn_sdot4(x.w, w[r].w, d, false);
+                d += __shfl_xor(d, 1);
+                if (!(lane & 1)) dots[(r * m + i) * KB + s * 32 + (lane >> 1)] = (float)d;
+            }
+        }
+    }
+    __syncthreads();
+    if (lane < kRowsRW * m) {
+        const int r = lane / m, i = lane - r * m;
+        const float *dr = dots + (r * m + i) * KB, *wr = sw + r * KB, *ar = sa + i * KB;
+        float acc = 0.0f;
+        for (int b = 0; b < KB; ++b) acc = fmaf(dr[b], ar[b] * wr[b], acc);
+        if (n0 + r < a.n) a.y[(size_t)i * a.n + n0 + r] = acc;
+    }
+}
+
+size_t rows_lds_bytes(int m, int k) { return (size_t)(kRowsRW * m + kRowsRW + m) * (k / 32) * 4; }
+
 template <int BM, int BN, int WGM, int WGN>
 int launch_q8b(Q8bArgs a, hipStream_t st) {
     a.gridM = (a.m + BM - 1) / BM;
@@ -267,8 +324,14 @@ int gphq_q8b_gemm(const int8_t *qa_dev, const float *da_dev, const int8_t *qw_de
     if (k == 0) return hip_status(hipMemsetAsync(y_dev, 0, (size_t)m * n * 4, (hipStream_t)stream));
     Q8bArgs a{qa_dev, da_dev, qw_dev, dw_dev, y_dev, (int)m, (int)k, (int)n, 0, 0};
     hipStream_t st = (hipStream_t)stream;
-    // 128 x 128 tiles from M = 256; below, 32-row tiles keep the grid wide.
+    // 128 x 128 tiles from M = 256; below, 32-row tiles keep the grid wide;
+    // up to 2 rows, the dot-product kernel.
     if (m >= 256) return launch_q8b<128, 128, 2, 2>(a, st);
+    if (m <= kRowsMaxM && k % 1024 == 0 && rows_lds_bytes((int)m, (int)k) <= 65536) {
+        hipLaunchKernelGGL(q8b_rows_kernel, dim3((unsigned)((n + kRowsRW - 1) / kRowsRW)), dim3(64),
+                           rows_lds_bytes((int)m, (int)k), st, a);
+        return launch_status();
+    }
     return launch_q8b<32, 128, 1, 4>(a, st);
 }
 

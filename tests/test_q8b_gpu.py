@@ -42,7 +42,8 @@ def test_quantize_bit_exact_with_special_blocks():
     assert np.array_equal(d.cpu().numpy().view(np.uint32), wd.view(np.uint32))
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 64, 96), (5, 4096, 200), (37, 160, 130), (128, 4096, 384), (300, 1024, 257)])
+@pytest.mark.parametrize("m,k,n", [(1, 64, 96), (5, 4096, 200), (37, 160, 130), (128, 4096, 384), (300, 1024, 257),
+                                   (1, 4096, 1001), (16, 2048, 301), (3, 8192, 77), (2, 1024, 3), (17, 1024, 64)])
 def test_gemm_bit_exact(m, k, n):
     import torch
 
