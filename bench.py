@@ -100,11 +100,13 @@ def gemv_config1(args, torch, gphq, mode):
     gemvs_per_launch = R / per_launch
     unit_bytes = N * K + N * (K // 32) * 4 + K * 4 + N * 4  # 18,907,136 per GEMV
     launch_s = ms / 1e3 / launches
-    # Spot-check the last rotation against a float64 product on the device.
-    deq = codes[R - 1].double() * scales[R - 1].double().repeat_interleave(32, dim=1)
-    ref = deq @ x.double()
-    rel = float(((y[R - 1].double() - ref).norm() / ref.norm()).item())
-    del deq, ref
+    # Every rotation's output against a float64 product on the device.
+    rel = 0.0
+    for r in range(R):
+        deq = codes[r].double() * scales[r].double().repeat_interleave(32, dim=1)
+        ref = deq @ x.double()
+        rel = max(rel, float(((y[r].double() - ref).norm() / ref.norm()).item()))
+        del deq, ref
     if not rel <= 1e-5:
         raise SystemExit(f"bench: GEMV result check failed (relative L2 {rel:.3g})")
     return {
@@ -394,49 +396,10 @@ QWEN3_8B = dict(hidden=4096, layers=36, heads=32, kv_heads=8, head_dim=128, inte
 
 def decode_model(torch, gphq, geom, fmt, seed):
     """A random-init Qwen3-shaped model in the qwen3lm GPU layout, generated on
-    the device: int8 codes U[-127,127] (Q4: bytes U[0,255]), scales |N(0,1)|*0.02,
-    norms 1 + N(0,0.02), BF16 embeddings N(0,1), a Q8B head padded to 16 rows.
-    Returns (lm, algorithmic weight bytes read per step)."""
-    cfg = gphq.lm_config(fmt=fmt, **geom)
-    desc, nbytes = gphq.lm_layer_layout(cfg)
-    lm = gphq.Lm(cfg)
-    gen = torch.Generator(device="cuda").manual_seed(seed)
-    rng = np.random.default_rng(seed)
-    H, I = geom["hidden"], geom["intermediate"]
-    qd, kvd = geom["heads"] * 128, geom["kv_heads"] * 128
-    regions = [(desc.qkv, desc.qkv_scale, qd + 2 * kvd, H), (desc.o, desc.o_scale, H, qd),
-               (desc.gu, desc.gu_scale, 2 * I, H), (desc.d, desc.d_scale, H, I)]
-
-    def fill(buf, w, s, rows, k, f):
-        if f == gphq.FMT_Q4:
-            nc = rows * k // 2
-            buf[w:w + nc].copy_(torch.randint(0, 256, (nc,), dtype=torch.uint8, device="cuda", generator=gen))
-        else:
-            nc = rows * k
-            buf[w:w + nc].view(torch.int8).copy_(
-                torch.randint(-127, 128, (nc,), dtype=torch.int8, device="cuda", generator=gen))
-        ns = rows if f == gphq.FMT_Q8 else rows * k // 32
-        sc = torch.randn(ns, device="cuda", generator=gen).abs() * 0.02
-        if f in (gphq.FMT_Q8, gphq.FMT_Q8B_F32):
-            buf[s:s + 4 * ns].view(torch.float32).copy_(sc)
-            return nc + 4 * ns
-        buf[s:s + 2 * ns].view(torch.float16).copy_(sc.half())
-        return nc + 2 * ns
-
-    weight_bytes = 0
-    for layer in range(geom["layers"]):
-        buf = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
-        for w, s_, rows, k in regions:
-            weight_bytes += fill(buf, w, s_, rows, k, fmt)
-        lm.bind_layer(layer, buf, desc, (1 + 0.02 * rng.standard_normal(128)).astype(np.float32),
-                      (1 + 0.02 * rng.standard_normal(128)).astype(np.float32))
-    emb = torch.randn((geom["vocab"], H), device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
-    lm.bind_embed(emb)
-    rows, so, hb = gphq.lm_head_layout(cfg)
-    head = torch.zeros(hb, dtype=torch.uint8, device="cuda")
-    weight_bytes += fill(head, 0, so, geom["vocab"], H, gphq.FMT_Q8B)  # rows past vocab stay zero
-    lm.bind_head(head, (1 + 0.02 * rng.standard_normal(H)).astype(np.float32))
-    torch.cuda.synchronize()
+    the device (gphq.lm_random): int8 codes U[-127,127] (Q4: bytes U[0,255]),
+    scales |N(0,1)|*0.02, norms 1 + N(0,0.02), BF16 embeddings N(0,1), a Q8B
+    head padded to 16 rows. Returns (lm, algorithmic weight bytes read per step)."""
+    lm, weight_bytes, _ = gphq.lm_random(geom, fmt, seed)
     return lm, weight_bytes
 
 

@@ -23,6 +23,10 @@ inline int hip_status(hipError_t e) {
 // Checks the launch that was just enqueued.
 inline int launch_status() { return hip_status(hipGetLastError()); }
 
+// n floats of dst set to v by a fill kernel (util.hip); never hipMemsetAsync,
+// so the fill may be captured in a HIP graph.
+int fill_f32(float *dst, size_t n, float v, hipStream_t stream);
+
 #define GPHQ_TRY(expr)                      \
     do {                                    \
         int _st = (expr);                   \

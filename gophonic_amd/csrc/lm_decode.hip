@@ -102,6 +102,8 @@ struct gphq_decode_batch {
     hipStream_t capture = nullptr;
     hipGraphExec_t step_exec = nullptr;
     std::vector<gphq_prefix *> graph_kvs;
+    std::vector<uint64_t> graph_kv_gens;  // the prefixes' generations at capture
+    uint64_t graph_lm_gen = 0;            // the model's binding generation at capture
     float *graph_hidden = nullptr;
     int32_t *graph_out = nullptr;
     int graph_vec_min = 0;
@@ -778,6 +780,7 @@ void drop_graph(gphq_decode_batch *ws) {
     if (ws->step_exec) (void)hipGraphExecDestroy(ws->step_exec);
     ws->step_exec = nullptr;
     ws->graph_kvs.clear();
+    ws->graph_kv_gens.clear();
 }
 
 void free_batch(gphq_decode_batch *ws) {
@@ -790,10 +793,22 @@ void free_batch(gphq_decode_batch *ws) {
 // Captures one chained greedy step (embed .. argmax) on the workspace's own
 // stream into an executable graph, unless the cached one matches. Capture
 // records the launches without running them.
+// The cache key is the model's binding generation and each lane's prefix
+// generation (a freed prefix's host address may come back from
+// gphq_prefix_new with other K/V buffers; its generation does not), plus the
+// output pointers and the GEMV mode.
+bool graph_matches(const gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, const float *hidden,
+                   const int32_t *out) {
+    if (!ws->step_exec || (int)ws->graph_kvs.size() != lanes || ws->graph_hidden != hidden || ws->graph_out != out ||
+        ws->graph_vec_min != ws->vec_min_lanes || ws->graph_lm_gen != ws->lm->gen)
+        return false;
+    for (int l = 0; l < lanes; ++l)
+        if (ws->graph_kvs[(size_t)l] != kvs[l] || ws->graph_kv_gens[(size_t)l] != kvs[l]->gen) return false;
+    return true;
+}
+
 int step_graph(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, float *hidden, int32_t *out) {
-    if (ws->step_exec && (int)ws->graph_kvs.size() == lanes && ws->graph_hidden == hidden && ws->graph_out == out &&
-        ws->graph_vec_min == ws->vec_min_lanes && std::equal(kvs, kvs + lanes, ws->graph_kvs.begin()))
-        return GPHQ_OK;
+    if (graph_matches(ws, kvs, lanes, hidden, out)) return GPHQ_OK;
     drop_graph(ws);
     if (!ws->capture) GPHQ_TRY(hip_status(hipStreamCreateWithFlags(&ws->capture, hipStreamNonBlocking)));
     GPHQ_TRY(hip_status(hipStreamBeginCapture(ws->capture, hipStreamCaptureModeRelaxed)));
@@ -811,6 +826,9 @@ int step_graph(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, float 
         return hip_status(ie);
     }
     ws->graph_kvs.assign(kvs, kvs + lanes);
+    ws->graph_kv_gens.resize((size_t)lanes);
+    for (int l = 0; l < lanes; ++l) ws->graph_kv_gens[(size_t)l] = kvs[l]->gen;
+    ws->graph_lm_gen = ws->lm->gen;
     ws->graph_hidden = hidden;
     ws->graph_out = out;
     ws->graph_vec_min = ws->vec_min_lanes;
@@ -988,12 +1006,14 @@ int gphq_lm_bind_layer(gphq_lm *lm, int64_t layer, const gphq_lm_layer *desc) {
     lm->layers[layer].q_norm_host = nullptr;
     lm->layers[layer].k_norm_host = nullptr;
     lm->bound[layer] = 1;
+    lm->gen = next_generation();
     return GPHQ_OK;
 }
 
 int gphq_lm_bind_embed(gphq_lm *lm, const uint16_t *embed_dev, int64_t len) {
     if (!lm || !embed_dev || len != lm->cfg.vocab * lm->cfg.hidden) return GPHQ_ERR_DIMENSIONS;
     lm->embed = embed_dev;
+    lm->gen = next_generation();
     return GPHQ_OK;
 }
 
@@ -1008,6 +1028,7 @@ int gphq_lm_bind_head(gphq_lm *lm, const void *head_dev, int64_t bytes, const fl
     lm->head = (const uint8_t *)head_dev;
     lm->head_rows = rows;
     lm->head_scale = so;
+    lm->gen = next_generation();
     return GPHQ_OK;
 }
 
@@ -1017,6 +1038,7 @@ int gphq_prefix_new(const gphq_lm *lm, int64_t capacity, gphq_prefix **out) {
     gphq_prefix *p = new gphq_prefix();
     p->lm = lm;
     p->capacity = capacity;
+    p->gen = next_generation();
     const size_t n = (size_t)lm->cfg.layers * capacity * lm->kvd * sizeof(float);
     hipError_t e = hipMalloc(&p->kc, n);
     if (e == hipSuccess) e = hipMalloc(&p->vc, n);

@@ -1,6 +1,7 @@
 // The qwen3lm model and prefix objects shared by the decode provider
 // (lm_decode.hip) and the batched pass (lm_prefill.hip).
 #pragma once
+#include <atomic>
 #include <vector>
 
 #include "common.h"
@@ -18,17 +19,30 @@ struct gphq_lm {
     const uint16_t *embed = nullptr;
     const uint8_t *head = nullptr;
     int64_t head_scale = 0, head_rows = 0;
+    // New value on every bind (layer, embedding, head): a captured step graph
+    // holds the bound addresses, so it is valid only for the generation it
+    // was captured under.
+    uint64_t gen = 0;
 };
 
 struct gphq_prefix {
     const gphq_lm *lm;
     float *kc = nullptr, *vc = nullptr;  // [layers][capacity][kvd]
     int64_t capacity = 0;
+    // Unique per prefix object for the life of the process (host addresses
+    // of freed prefixes are reused; generations are not).
+    uint64_t gen = 0;
 };
 
 namespace gphq {
 
 constexpr int kLmHeadDim = 128;
+
+// Process-wide source of model-binding and prefix generations (never 0).
+inline uint64_t next_generation() {
+    static std::atomic<uint64_t> counter{0};
+    return counter.fetch_add(1, std::memory_order_relaxed) + 1;
+}
 
 // Whether the embedding, head, final norm and every layer are bound.
 bool lm_model_ready(const gphq_lm *lm);

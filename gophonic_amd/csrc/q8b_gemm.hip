@@ -321,7 +321,7 @@ int gphq_q8b_gemm(const int8_t *qa_dev, const float *da_dev, const int8_t *qw_de
         return GPHQ_ERR_DIMENSIONS;
     if (m == 0 || n == 0) return GPHQ_OK;
     if (!qa_dev || !da_dev || !qw_dev || !dw_dev || !y_dev) return GPHQ_ERR_DIMENSIONS;
-    if (k == 0) return hip_status(hipMemsetAsync(y_dev, 0, (size_t)m * n * 4, (hipStream_t)stream));
+    if (k == 0) return fill_f32(y_dev, (size_t)m * n, 0.0f, (hipStream_t)stream);
     Q8bArgs a{qa_dev, da_dev, qw_dev, dw_dev, y_dev, (int)m, (int)k, (int)n, 0, 0};
     hipStream_t st = (hipStream_t)stream;
     // 128 x 128 tiles from M = 256; below, 32-row tiles keep the grid wide;

@@ -40,7 +40,11 @@ struct gphq_workspace_i8 {
     float *rowScale = nullptr;  // [rowcap]
     float *rowInv = nullptr;    // [rowcap]
     std::vector<float> hScale, hInv;
-    bool dirty = false;  // host scales newer than the device copy
+    // Rows whose host scales are newer than the device copy. The fused Pack
+    // computes every row's scales on the device, so it leaves all rows clean;
+    // PackRange uploads only the rows SetRowScale or Prepare touched since.
+    std::vector<uint8_t> rowDirty;
+    bool dirty = false;  // some rowDirty entry is set
 };
 
 static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -142,6 +146,7 @@ int gphq_q8gemm_new_workspace_i8(int64_t k, int64_t max_rows, gphq_workspace_i8 
     ws->rowcap = max_rows;
     ws->hScale.assign((size_t)max_rows, 0.0f);
     ws->hInv.assign((size_t)max_rows, 0.0f);
+    ws->rowDirty.assign((size_t)max_rows, 0);
     const size_t abytes = (size_t)ceil_div(max_rows, 16) * ceil_div(k, 64) * 1024;
     int st = GPHQ_OK;
     if (abytes) {
@@ -181,6 +186,7 @@ int gphq_q8gemm_workspace_i8_prepare(gphq_workspace_i8 *ws, int64_t rows, int64_
     ws->kt = ceil_div(k, 64);
     std::fill(ws->hScale.begin(), ws->hScale.end(), 0.0f);
     std::fill(ws->hInv.begin(), ws->hInv.end(), 0.0f);
+    std::fill(ws->rowDirty.begin(), ws->rowDirty.begin() + rows, (uint8_t)1);
     ws->dirty = true;
     return GPHQ_OK;
 }
@@ -195,6 +201,7 @@ int gphq_q8gemm_workspace_i8_set_row_scale(gphq_workspace_i8 *ws, int64_t row, f
         ws->hScale[(size_t)row] = 0.0f;
         ws->hInv[(size_t)row] = 0.0f;
     }
+    ws->rowDirty[(size_t)row] = 1;
     ws->dirty = true;
     return GPHQ_OK;
 }
@@ -208,10 +215,21 @@ int gphq_q8gemm_workspace_i8_pack_range(gphq_workspace_i8 *ws, const float *x, i
     if (ws->rows == 0) return GPHQ_OK;
     hipStream_t s = (hipStream_t)stream;
     if (ws->dirty) {
-        GPHQ_TRY(hip_status(hipMemcpyAsync(ws->rowScale, ws->hScale.data(), (size_t)ws->rows * sizeof(float),
-                                           hipMemcpyHostToDevice, s)));
-        GPHQ_TRY(hip_status(hipMemcpyAsync(ws->rowInv, ws->hInv.data(), (size_t)ws->rows * sizeof(float),
-                                           hipMemcpyHostToDevice, s)));
+        // Upload each run of consecutive dirty rows; rows whose scales the
+        // device computed (the fused Pack) keep them.
+        for (int64_t r = 0; r < ws->rows;) {
+            if (!ws->rowDirty[(size_t)r]) {
+                ++r;
+                continue;
+            }
+            int64_t e = r;
+            while (e < ws->rows && ws->rowDirty[(size_t)e]) ws->rowDirty[(size_t)e++] = 0;
+            GPHQ_TRY(hip_status(hipMemcpyAsync(ws->rowScale + r, ws->hScale.data() + r, (size_t)(e - r) * sizeof(float),
+                                               hipMemcpyHostToDevice, s)));
+            GPHQ_TRY(hip_status(hipMemcpyAsync(ws->rowInv + r, ws->hInv.data() + r, (size_t)(e - r) * sizeof(float),
+                                               hipMemcpyHostToDevice, s)));
+            r = e;
+        }
         // The host arrays may change right after this call returns.
         GPHQ_TRY(hip_status(hipStreamSynchronize(s)));
         ws->dirty = false;
@@ -228,6 +246,7 @@ int gphq_q8gemm_workspace_i8_pack(gphq_workspace_i8 *ws, const float *x, int64_t
     // PackRange(x, stride, 0, k) (int8_test.go:32-43) -- fused on the device.
     GPHQ_TRY(gphq_q8gemm_workspace_i8_prepare(ws, rows, k));
     if (stride < k || (rows > 0 && x_len < (rows - 1) * stride + k)) return GPHQ_ERR_DIMENSIONS;
+    std::fill(ws->rowDirty.begin(), ws->rowDirty.end(), (uint8_t)0);
     ws->dirty = false;
     if (rows == 0) return GPHQ_OK;
     if (k > 0 && !x) return GPHQ_ERR_DIMENSIONS;

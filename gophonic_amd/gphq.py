@@ -782,6 +782,91 @@ def lm_from_stored(geom_kwargs, fmt, layers, embed_bf16, final_norm, head, devic
     return lm
 
 
+def lm_random(geom_kwargs, fmt, seed, device="cuda", host=False):
+    """A random-init Qwen3-shaped model in the qwen3lm GPU layout, generated on
+    the device with a seeded torch generator (lmtest's distributions,
+    lmtest/lmtest.go:34-80): int8 codes U[-127,127] (Q4: bytes U[0,255]),
+    scales |N(0,1)|*0.02, norms 1 + N(0,0.02), BF16 embeddings N(0,1), and a
+    Q8B head padded to 16 rows with zeros.
+
+    Returns (lm, weight_bytes, stored): weight_bytes are the layer and head
+    codes and scales one decode step reads; stored is None, or with host=True
+    a dict of host copies (layers: list of dicts qkv/o/gu/down = (codes,
+    scales) and q_norm/k_norm; embed (uint16 BF16 bits); final_norm; head =
+    (codes, scales)) for a CPU check of the same model."""
+    import numpy as np
+    import torch
+
+    cfg = lm_config(fmt=fmt, **geom_kwargs)
+    desc, nbytes = lm_layer_layout(cfg)
+    lm = Lm(cfg)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    H, I, hd = cfg.hidden, cfg.intermediate, cfg.head_dim
+    qd, kvd = cfg.heads * hd, cfg.kv_heads * hd
+    regions = [("qkv", desc.qkv, desc.qkv_scale, qd + 2 * kvd, H), ("o", desc.o, desc.o_scale, H, qd),
+               ("gu", desc.gu, desc.gu_scale, 2 * I, H), ("down", desc.d, desc.d_scale, H, I)]
+
+    def fill(buf, w, s, rows, k, f, pad_rows=0):
+        """Random codes and scales of `rows` rows (then `pad_rows` zero rows) at
+        byte offsets w and s of buf; returns (bytes, host codes, host scales)."""
+        rk = rows * k
+        if f == FMT_Q4:
+            nc = rk // 2
+            buf[w:w + nc].copy_(torch.randint(0, 256, (nc,), dtype=torch.uint8, device=device, generator=gen))
+            codes = buf[w:w + nc]
+        else:
+            nc = rk
+            codes = buf[w:w + nc].view(torch.int8)
+            codes.copy_(torch.randint(-127, 128, (nc,), dtype=torch.int8, device=device, generator=gen))
+        ns = rows if f == FMT_Q8 else rk // 32
+        sc = torch.randn(ns, device=device, generator=gen).abs() * 0.02
+        if f in (FMT_Q8, FMT_Q8B_F32):
+            scales = buf[s:s + 4 * ns].view(torch.float32)
+            scales.copy_(sc)
+            sb = 4 * ns
+        else:
+            scales = buf[s:s + 2 * ns].view(torch.float16)
+            scales.copy_(sc.half())
+            sb = 2 * ns
+        hc = hs = None
+        if host:
+            cpad = (rows + pad_rows) * k // (2 if f == FMT_Q4 else 1)
+            spad = (rows + pad_rows) * (1 if f == FMT_Q8 else k // 32) * (sb // ns)
+            hc = buf[w:w + cpad].cpu().numpy()
+            hs = buf[s:s + spad].cpu().numpy()
+            hc = hc.view(np.int8) if f != FMT_Q4 else hc
+            hs = hs.view(np.float32) if f in (FMT_Q8, FMT_Q8B_F32) else hs.view(np.uint16)
+        return nc + sb, hc, hs
+
+    weight_bytes = 0
+    stored = dict(layers=[]) if host else None
+    for layer in range(cfg.layers):
+        buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        mats = {}
+        for name, w, s_, rows, k in regions:
+            b, hc, hs = fill(buf, w, s_, rows, k, fmt)
+            weight_bytes += b
+            mats[name] = (hc, hs)
+        qn = (1 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+        kn = (1 + 0.02 * rng.standard_normal(hd)).astype(np.float32)
+        lm.bind_layer(layer, buf, desc, qn, kn)
+        if host:
+            stored["layers"].append(dict(mats, q_norm=qn, k_norm=kn))
+    emb = torch.randn((cfg.vocab, H), device=device, generator=gen).to(torch.bfloat16).view(torch.int16)
+    lm.bind_embed(emb)
+    rows, so, hb = lm_head_layout(cfg)
+    head = torch.zeros(hb, dtype=torch.uint8, device=device)
+    b, hc, hs = fill(head, 0, so, cfg.vocab, H, FMT_Q8B, pad_rows=rows - cfg.vocab)  # padding rows stay zero
+    weight_bytes += b
+    final_norm = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    lm.bind_head(head, final_norm)
+    if host:
+        stored.update(embed=emb.cpu().numpy().view(np.uint16), final_norm=final_norm, head=(hc, hs))
+    torch.cuda.synchronize()
+    return lm, weight_bytes, stored
+
+
 # ---- weight preparation (gphq_prepare_projection) ----------------------------
 
 

@@ -179,9 +179,37 @@ class DecodeOracle:
                 qn=np.asarray(L.q_norm, np.float32).astype(np.float64),
                 kn=np.asarray(L.k_norm, np.float32).astype(np.float64),
             ))
-        self.head = dequant(FMT_Q8B, *head, g.head_rows, g.hidden)[: g.vocab]
+        self._head_codes = np.asarray(head[0], np.int8).reshape(g.head_rows, g.hidden)[: g.vocab]
+        self._head_scales = np.asarray(head[1], np.uint16).reshape(g.head_rows, g.hidden // 32)[: g.vocab]
+        self._head = None
         cos, sin = rope_table(g, g.max_pos)
         self.cos, self.sin = cos.astype(np.float64), sin.astype(np.float64)
+
+    @property
+    def head(self):
+        """float64 [vocab][hidden] of the Q8B head (dequantized on first use)."""
+        if self._head is None:
+            self._head = dequant(FMT_Q8B, self._head_codes, self._head_scales, self.g.vocab, self.g.hidden)
+        return self._head
+
+    HEAD_CHUNK = 8192  # rows per dequantized chunk
+    DENSE_HEAD_MAX = 1 << 26  # head values kept dense in float64 (512 MiB)
+
+    def head_rows(self, x):
+        """head @ x_r for each row of x [rows][hidden] -> [rows][vocab]. A
+        full-size head (151,936 x 4096 is 5 GB in float64) is dequantized in
+        row chunks instead of being kept; each logit is the same float64 dot
+        product either way."""
+        g = self.g
+        x = np.atleast_2d(np.asarray(x, np.float64))
+        if self._head is not None or g.vocab * g.hidden <= self.DENSE_HEAD_MAX:
+            return x @ self.head.T
+        out = np.empty((x.shape[0], g.vocab))
+        for r in range(0, g.vocab, self.HEAD_CHUNK):
+            e = min(g.vocab, r + self.HEAD_CHUNK)
+            w = dequant(FMT_Q8B, self._head_codes[r:e], self._head_scales[r:e], e - r, g.hidden)
+            out[:, r:e] = x @ w.T
+        return out
 
     def new_cache(self, capacity):
         g = self.g
@@ -243,35 +271,44 @@ class DecodeOracle:
         a, b = v[:, :half], v[:, half:]
         return np.concatenate([a * c - b * s, b * c + a * s], axis=1)
 
-    def prefill(self, cache, base, tokens):
+    def prefill(self, cache, base, tokens, last_only=False):
         """All rows of tokens at positions base.. at once (the batched pass,
         gpu_darwin.go:1703-1764: each row attends cache rows 0..its own
         position): appends K/V and returns the residual rows [T][hidden]. The
-        same float64 math as stepping layers() token by token."""
+        same float64 math as stepping layers() token by token.
+
+        last_only: the last layer still appends every row's K/V but finishes
+        only the final row (the only row HiddenLastExtendInto returns), and
+        the result is that row's residual [1][hidden]. For a one-layer model
+        this skips all but one row's attention and MLP."""
         g = self.g
         T = len(tokens)
         hd = g.head_dim
         grp = g.heads // g.kv_heads
         scale = 1.0 / np.sqrt(hd)
         pos = base + np.arange(T)
-        h = np.stack([self.embed_row(t) for t in tokens])
+        h = rot_apply(bf16_to_f64(self.embed[np.asarray(tokens, np.int64)]), self.hrot).reshape(T, g.hidden)
         mask = np.arange(base + T)[None, :] <= pos[:, None]
         for li, W in enumerate(self.W):
-            qkv = self._norm_rows(h) @ W["qkv"].T
+            rows = slice(T - 1, T) if last_only and li == len(self.W) - 1 else slice(0, T)
+            hn = self._norm_rows(h)
+            kv = hn @ W["qkv"][g.qd:].T
+            qs = hn[rows] @ W["qkv"][: g.qd].T
             kc, vc = cache[li]
             for kh in range(g.kv_heads):
-                k = qkv[:, g.qd + kh * hd: g.qd + (kh + 1) * hd]
-                v = qkv[:, g.qd + g.kvd + kh * hd: g.qd + g.kvd + (kh + 1) * hd]
+                k = kv[:, kh * hd:(kh + 1) * hd]
+                v = kv[:, g.kvd + kh * hd: g.kvd + (kh + 1) * hd]
                 kc[pos, kh * hd:(kh + 1) * hd] = self._rope_rows(self._norm_rows(k, W["kn"]), pos)
                 vc[pos, kh * hd:(kh + 1) * hd] = v
-            ctx = np.empty((T, g.qd))
+            prow = pos[rows]
+            ctx = np.empty((len(prow), g.qd))
             for qh in range(g.heads):
                 kh = qh // grp
-                q = self._rope_rows(self._norm_rows(qkv[:, qh * hd:(qh + 1) * hd], W["qn"]), pos) * scale
-                s = np.where(mask, q @ kc[: base + T, kh * hd:(kh + 1) * hd].T, -np.inf)
+                q = self._rope_rows(self._norm_rows(qs[:, qh * hd:(qh + 1) * hd], W["qn"]), prow) * scale
+                s = np.where(mask[rows], q @ kc[: base + T, kh * hd:(kh + 1) * hd].T, -np.inf)
                 p = np.exp(s - s.max(axis=1, keepdims=True))
                 ctx[:, qh * hd:(qh + 1) * hd] = (p / p.sum(axis=1, keepdims=True)) @ vc[: base + T, kh * hd:(kh + 1) * hd]
-            h = h + ctx @ W["o"].T
+            h = h[rows] + ctx @ W["o"].T
             gu = self._norm_rows(h) @ W["gu"].T
             gate, up = gu[:, 0::2], gu[:, 1::2]
             with np.errstate(over="ignore"):
@@ -283,9 +320,16 @@ class DecodeOracle:
 
     def finish(self, h):
         """(hidden, logits): R^T, final RMSNorm, R, head (first vocab rows)."""
-        hu = rot_unapply(h, self.hrot)
-        hidden = self._norm(hu, self.final_norm)
-        logits = self.head @ rot_apply(hidden, self.hrot)
+        hidden, logits = self.finish_rows(np.asarray(h, np.float64)[None, :])
+        return hidden[0], logits[0]
+
+    def finish_rows(self, h):
+        """finish() of each residual row of h [rows][hidden], with one pass
+        over the head for all rows: (hidden [rows][hidden], logits [rows][vocab])."""
+        h = np.atleast_2d(np.asarray(h, np.float64))
+        hu = rot_unapply(h, self.hrot).reshape(h.shape)
+        hidden = self._norm_rows(hu, self.final_norm)
+        logits = self.head_rows(rot_apply(hidden, self.hrot).reshape(h.shape))
         return hidden, logits
 
     def step(self, cache, pos, token):

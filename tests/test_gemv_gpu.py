@@ -235,6 +235,36 @@ def test_gemv_batch_bit_identical_to_single(fmt, count):
         assert rel_l2(host(ys[i]), y64) <= 1e-5
 
 
+@pytest.mark.parametrize("fmt", [orc.FMT_Q8B_F32, orc.FMT_Q8B])
+def test_gemv_batch_config1_every_set(fmt):
+    # The benchmark's timed launch: gphq_gemv_batch at K = N = 4096 with 32
+    # sets (the persistent batch shape: two K slices merged in LDS, each wave
+    # group switching sets inside its run of row groups). Every set has its
+    # own x, and every output of every set is checked: relative L2 <= 1e-5
+    # against the float64 product, each value within the fp32 accumulation
+    # bound K * 2^-23 * sum|w x|, and the bits of a single-GEMV launch.
+    import torch
+
+    K = N = 4096
+    count = 32
+    rng = np.random.default_rng(0x5147 + fmt)
+    sets = [make_block_weights(fmt, rng, N, K) for _ in range(count)]
+    xs_h = [rng.standard_normal(K).astype(np.float32) for _ in range(count)]
+    codes = [dev(c) for c, _ in sets]
+    scales = [dev(s) for _, s in sets]
+    xs = [dev(x) for x in xs_h]
+    ys = [empty_f32(N) for _ in range(count)]
+    gphq.gemv_batch(fmt, codes, scales, xs, ys, K, N)
+    for i in range(count):
+        got = host(ys[i])
+        y64, a = orc.gemv_f64(fmt, sets[i][0], sets[i][1], xs_h[i], K, N)
+        assert rel_l2(got, y64) <= 1e-5, i
+        assert np.all(np.abs(got - y64) <= K * 2.0 ** -23 * a), i
+        single = empty_f32(N)
+        gphq.gemv(fmt, codes[i], scales[i], xs[i], single, K, N)
+        assert np.array_equal(host(single).view(np.uint32), got.view(np.uint32)), i
+
+
 def test_gemv_batch_rejects_bad_counts():
     import torch
 

@@ -328,6 +328,61 @@ def test_run_graph_replays_match_eager_launches():
         torch.cuda.synchronize()
 
 
+def test_run_graph_recaptured_after_prefix_free_and_rebind():
+    # The captured step holds the lanes' K/V addresses and the bound weight
+    # addresses. A prefix freed and replaced by a new one (whose host object
+    # may reuse the freed one's address, with other K/V buffers and another
+    # capacity), or a layer rebound to other weights, must not replay the
+    # stale graph: each chained run equals the eager launches.
+    import torch
+
+    model = lc.random_model(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    lm = device_model(model)  # rebound below: not the shared cached model
+    g = model["geom"]
+    rng = np.random.default_rng(12)
+    lanes, steps = 2, 5
+    ws = gphq.DecodeBatch(lm, 2)
+    base = [gphq.Prefix(lm, 40) for _ in range(lanes)]
+    prompts = [list(rng.integers(0, g.vocab, 6 + i)) for i in range(lanes)]
+    _, pos = prefill(lc.oracle_for(model), ws, base, prompts)
+    first = list(rng.integers(0, g.vocab, lanes))
+
+    def run(graph, kvs):
+        for a, b in zip(kvs, base):
+            a.copy_from(b, max(pos))
+        ws.set_graph(graph)
+        out = torch.full((steps, lanes), -1, dtype=torch.int32, device="cuda")
+        hid = torch.empty((lanes, g.hidden), device="cuda")
+        ws.greedy_run(kvs, pos, first, steps, out, hid)
+        torch.cuda.synchronize()
+        return out.cpu().numpy(), hid.cpu().numpy()
+
+    kv1 = [gphq.Prefix(lm, 40) for _ in range(lanes)]
+    run(True, kv1)  # captures a graph over kv1
+    addrs = [p.h.value for p in kv1]
+    for p in kv1:
+        p.close()
+    kv2 = [gphq.Prefix(lm, 24 + 8 * i) for i in range(lanes)]
+    reused = sum(p.h.value in addrs for p in kv2)
+    got_t, got_h = run(True, kv2)
+    want_t, want_h = run(False, kv2)
+    np.testing.assert_array_equal(got_t, want_t)
+    np.testing.assert_array_equal(got_h, want_h)
+    print(f"prefix host addresses reused: {reused} of {lanes}")
+    # Rebind layer 0 to another model's weights after a capture.
+    run(True, kv2)
+    other_model = lc.random_model(lc.GPU_SHAPE, lo.FMT_Q8B, seed=6)
+    other = device_model(other_model)
+    desc, _ = gphq.lm_layer_layout(lm.cfg)
+    L0 = other_model["layers"][0]
+    lm.bind_layer(0, other._keep[0], desc, L0.q_norm, L0.k_norm)
+    got_t, got_h = run(True, kv2)
+    want2_t, want2_h = run(False, kv2)
+    np.testing.assert_array_equal(got_t, want2_t)
+    np.testing.assert_array_equal(got_h, want2_h)
+    assert not np.array_equal(want2_h, want_h)  # the rebind changed the model
+
+
 # One layer at Qwen3-8B widths: the GEMVs take the K = 4096 shapes with two
 # and four K slices (the norm prologue's cross-slice sum included) and
 # down's K = 12288 in six slices.

@@ -1,0 +1,334 @@
+"""Workload-size parity of the decode provider and the batched pass, through
+the C ABI: BASELINE configurations 3, 4a and 4b at their real widths, context
+lengths and vocabulary.
+
+* One layer at Qwen3-8B widths with the real 151,936-row head, against the
+  float64 oracle (oracle/lm_oracle.py): a 4096-token batched pass (the
+  HiddenLastExtendInto path of config 4a: 4096 query rows of flash attention,
+  the skipped-rescale softmax over 4096 keys) and decode steps at context
+  4096 for 1 lane (32 attention splits per KV head) and 16 lanes (the
+  multi-vector GEMVs, the K-split down projection), then chained greedy
+  steps. The decode oracle starts from the K/V rows the device wrote, so
+  each step is held to the reference's GPU decode bound
+  (gpu_decode_batch_darwin_test.go:121-131, relative 1e-5) on its own.
+* Full depth (Qwen3-8B's 36 layers, Qwen3-0.6B's 28) with the real head at a
+  1024-token context, by properties the reference's tests use: graph replays
+  equal eager launches (the chained run, gpu_darwin.go:1913-2006), lanes
+  decoded together equal lanes decoded alone
+  (gpu_vector_batch_darwin_test.go:217-220), the batched pass equals
+  token-by-token decoding by the cosine of gpu_official_darwin_test.go:63-87
+  (at a depth-aware bound, COS_FULL_DEPTH), and LogitsInto of a step's hidden
+  states equals that step's logits bit for bit.
+
+Weights are random-init Q8B (the reference's gpu-q8 decode format) with the
+benchmark's distributions, generated on the device by gphq.lm_random.
+"""
+import numpy as np
+import pytest
+
+from gophonic_amd import gphq
+from oracle import lm_oracle as lo
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 151936
+CTX = 4096
+REL = 1e-5
+COS = 0.99999  # gpu_official_darwin_test.go:86 (batched pass vs token by token)
+# The same comparison at full depth on random-init weights. The batched pass
+# multiplies FP16 weight and activation tiles as the reference's mm does
+# (gpu.metal:836-861), about 1e-3 relative error per layer (one layer: cosine
+# 0.9999994 against float64), and random-init layers amplify it with depth:
+# measured 0.9999914 at 28 layers (Qwen3-0.6B widths) and 0.9999874 at 36
+# (Qwen3-8B widths). The reference states its bound for a real checkpoint.
+COS_FULL_DEPTH = 0.99995
+
+QWEN3_8B = dict(hidden=4096, layers=36, heads=32, kv_heads=8, head_dim=128, intermediate=12288, vocab=VOCAB,
+                max_positions=8192)
+QWEN3_06B = dict(hidden=1024, layers=28, heads=16, kv_heads=8, head_dim=128, intermediate=3072, vocab=VOCAB,
+                 max_positions=8192)
+
+
+def rel_l2(want, got):
+    want, got = np.asarray(want, np.float64), np.asarray(got, np.float64)
+    assert np.isfinite(got).all()
+    return float(np.linalg.norm(want - got) / np.linalg.norm(want))
+
+
+def cosine(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def read_cache(kv, rows, layer=0):
+    """Rows [0, rows) of one layer's K and V cache of a prefix, as float64
+    host arrays [rows][kv_dim]."""
+    import ctypes
+
+    import torch
+
+    kc, vc, cap = kv.kv()
+    kvd = kv.lm.cfg.kv_heads * kv.lm.cfg.head_dim
+    out = []
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    torch.cuda.synchronize()
+    for base in (kc, vc):
+        t = torch.empty((rows, kvd), dtype=torch.float32, device="cuda")
+        assert hip.hipMemcpy(t.data_ptr(), base + layer * cap * kvd * 4, rows * kvd * 4, 3) == 0
+        out.append(t.cpu().numpy().astype(np.float64))
+    return out
+
+
+_ONE = {}
+
+
+def one_layer():
+    """(lm, oracle) of a one-layer Qwen3-8B-width Q8B model with the full head
+    (built once per session; the oracle keeps the head as codes)."""
+    if not _ONE:
+        lm, _, st = gphq.lm_random(dict(QWEN3_8B, layers=1), gphq.FMT_Q8B, seed=81, host=True)
+        g = lo.Geometry(hidden=4096, layers=1, heads=32, kv_heads=8, head_dim=128, inter=12288, vocab=VOCAB,
+                        max_pos=8192)
+        layers = [lo.Layer(qkv=L["qkv"], o=L["o"], gu=L["gu"], down=L["down"], q_norm=L["q_norm"],
+                           k_norm=L["k_norm"]) for L in st["layers"]]
+        _ONE.update(lm=lm, orc=lo.DecodeOracle(g, lo.FMT_Q8B, layers, st["embed"], st["final_norm"], st["head"]))
+    return _ONE["lm"], _ONE["orc"]
+
+
+def test_prefill_4096_tokens_one_layer_8b():
+    # Config 4a's pass at one layer: 4096 rows in one batched pass into a
+    # fresh prefix. The last row's post-final-norm state and sampled K/V rows
+    # against the float64 batched pass.
+    import torch
+
+    lm, orc = one_layer()
+    g = orc.g
+    rng = np.random.default_rng(4096)
+    toks = rng.integers(0, g.vocab, CTX)
+    pf = gphq.Prefill(lm, CTX)
+    kv = gphq.Prefix(lm, CTX + 8)
+    hidden = torch.empty(g.hidden, device="cuda")
+    pf.extend(kv, 0, toks, hidden)
+    pf.check()
+    got_k, got_v = read_cache(kv, CTX)
+    cache = orc.new_cache(CTX + 8)
+    h = orc.prefill(cache, 0, toks, last_only=True)
+    want_hidden, _ = orc.finish_rows(h)
+    got = hidden.cpu().numpy()
+    c = cosine(want_hidden[0], got)
+    print(f"4096-row pass: last-row cosine {c:.8f}, relative L2 {rel_l2(want_hidden[0], got):.3g}")
+    assert c >= COS, c
+    rows = sorted({0, 1, 31, 32, 2047, 2048, CTX - 2, CTX - 1} | set(rng.integers(0, CTX, 56).tolist()))
+    want_k, want_v = cache[0][0][:CTX], cache[0][1][:CTX]
+    for r in rows:
+        for name, want, gotr in (("k", want_k, got_k), ("v", want_v, got_v)):
+            for kh in range(g.kv_heads):  # each KV head's row separately
+                sl = slice(kh * g.head_dim, (kh + 1) * g.head_dim)
+                c = cosine(want[r, sl], gotr[r, sl])
+                assert c >= COS, (name, r, kh, c)
+    # Untouched capacity rows stay zero.
+    tail_k, _ = read_cache(kv, CTX + 8)
+    assert not tail_k[CTX:].any()
+
+
+@pytest.mark.parametrize("lanes", [1, 16])
+def test_decode_at_context_4096_one_layer_8b(lanes):
+    # Config 4b's step at one layer: lanes at contexts 4096 (lane 0) down to
+    # 4096 - 37*(lanes-1), caches filled by the batched pass over random ids.
+    # The oracle starts from the rows the device wrote: hidden states and
+    # logits of every lane within relative 1e-5, the appended K/V rows too;
+    # then two chained greedy steps whose tokens are the oracle's argmax
+    # (teacher-forced with the device's choices; near ties within the bound
+    # may go either way).
+    import torch
+
+    lm, orc = one_layer()
+    g = orc.g
+    rng = np.random.default_rng(100 + lanes)
+    ctxs = [CTX - 37 * i for i in range(lanes)]
+    cap = CTX + 8
+    kvs = [gphq.Prefix(lm, cap) for _ in range(lanes)]
+    pf = gphq.Prefill(lm, CTX)
+    scratch = torch.empty(g.hidden, device="cuda")
+    for kv, n in zip(kvs, ctxs):
+        pf.extend(kv, 0, rng.integers(0, g.vocab, n), scratch)
+    pf.check()
+    del pf
+    caches = []
+    for kv, n in zip(kvs, ctxs):
+        k, v = read_cache(kv, n)
+        c = orc.new_cache(cap)
+        c[0][0][:n], c[0][1][:n] = k, v
+        caches.append(c)
+    ws = gphq.DecodeBatch(lm, lanes)
+    tokens = rng.integers(0, g.vocab, lanes)
+    hidden = torch.empty((lanes, g.hidden), device="cuda")
+    logits = torch.empty((lanes, g.vocab), device="cuda")
+    ws.into(kvs, ctxs, tokens, hidden, logits)
+    ws.check()
+    hs = np.stack([orc.layers(caches[i], ctxs[i], orc.embed_row(int(tokens[i]))) for i in range(lanes)])
+    want_h, want_l = orc.finish_rows(hs)
+    got_h, got_l = hidden.cpu().numpy(), logits.cpu().numpy()
+    for i in range(lanes):
+        rh, rl = rel_l2(want_h[i], got_h[i]), rel_l2(want_l[i], got_l[i])
+        assert rh <= REL and rl <= REL, (i, rh, rl)
+        k, v = read_cache(kvs[i], ctxs[i] + 1)
+        assert rel_l2(caches[i][0][0][ctxs[i]], k[-1]) <= REL, i
+        assert rel_l2(caches[i][0][1][ctxs[i]], v[-1]) <= REL, i
+    # Chained greedy steps from the step's argmax.
+    first = [lo.greedy_argmax_np(got_l[i]) for i in range(lanes)]
+    steps = 2
+    out = torch.full((steps, lanes), -1, dtype=torch.int32, device="cuda")
+    ws.greedy_run(kvs, [c + 1 for c in ctxs], first, steps, out)
+    ws.check()
+    seq = out.cpu().numpy()
+    toks = list(first)
+    for s in range(steps):
+        hs = np.stack([orc.layers(caches[i], ctxs[i] + 1 + s, orc.embed_row(int(toks[i]))) for i in range(lanes)])
+        _, wl = orc.finish_rows(hs)
+        for i in range(lanes):
+            got, want = int(seq[s, i]), lo.greedy_argmax_np(wl[i])
+            assert got == want or wl[i][want] - wl[i][got] <= 1e-4 * np.abs(wl[i]).max(), (s, i, got, want)
+        toks = seq[s].tolist()
+
+
+# ---- full depth: property checks ---------------------------------------------
+
+_FULL = {}
+
+
+def full_model(name):
+    """A full-depth random Q8B model with the real head (one kept at a time)."""
+    if name not in _FULL:
+        _FULL.clear()
+        import torch
+
+        torch.cuda.empty_cache()
+        geom = {"qwen3_8b": QWEN3_8B, "qwen3_06b": QWEN3_06B}[name]
+        lm, _, _ = gphq.lm_random(geom, gphq.FMT_Q8B, seed=4 if name == "qwen3_8b" else 3)
+        _FULL[name] = (lm, geom)
+    return _FULL[name]
+
+
+def prefilled(lm, geom, ctxs, cap, seed):
+    """Prefixes holding random prompts of the given lengths (the batched pass)."""
+    import torch
+
+    rng = np.random.default_rng(seed)
+    kvs = [gphq.Prefix(lm, cap) for _ in ctxs]
+    pf = gphq.Prefill(lm, max(ctxs))
+    scratch = torch.empty(geom["hidden"], device="cuda")
+    for kv, n in zip(kvs, ctxs):
+        pf.extend(kv, 0, rng.integers(0, geom["vocab"], n), scratch)
+    pf.check()
+    return kvs
+
+
+MODELS = ["qwen3_8b", "qwen3_06b"]
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_full_depth_graph_replay_equals_eager(name):
+    import torch
+
+    lm, geom = full_model(name)
+    lanes, steps, ctx = 2, 6, 1024
+    base = prefilled(lm, geom, [ctx, ctx - 9], ctx + 16, seed=1)
+    ws = gphq.DecodeBatch(lm, lanes)
+    first = [11, 70001]
+    pos = [ctx, ctx - 9]
+
+    def run(graph):
+        kvs = [gphq.Prefix(lm, ctx + 16) for _ in range(lanes)]
+        for a, b in zip(kvs, base):
+            a.copy_from(b, ctx)
+        ws.set_graph(graph)
+        out = torch.full((steps, lanes), -1, dtype=torch.int32, device="cuda")
+        hid = torch.empty((lanes, geom["hidden"]), device="cuda")
+        ws.greedy_run(kvs, pos, first, steps, out, hid)
+        torch.cuda.synchronize()
+        ws.check()
+        return out.cpu().numpy(), hid.cpu().numpy()
+
+    want_t, want_h = run(False)
+    assert np.isfinite(want_h).all()
+    for _ in range(2):  # a capture, then a replay of the cached graph
+        got_t, got_h = run(True)
+        np.testing.assert_array_equal(got_t, want_t)
+        np.testing.assert_array_equal(got_h, want_h)
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_full_depth_lanes_together_equal_alone(name):
+    import torch
+
+    lm, geom = full_model(name)
+    ctxs = [1024, 1000, 977, 1011]
+    lanes = len(ctxs)
+    kv_a = prefilled(lm, geom, ctxs, 1040, seed=2)
+    kv_b = [gphq.Prefix(lm, 1040) for _ in range(lanes)]
+    for a, b in zip(kv_b, kv_a):
+        a.copy_from(b, max(ctxs))
+    ws = gphq.DecodeBatch(lm, lanes)
+    tokens = [5, 151935, 1000, 42]
+    hid = torch.empty((lanes, geom["hidden"]), device="cuda")
+    lg = torch.empty((lanes, geom["vocab"]), device="cuda")
+    ws.into(kv_a, ctxs, tokens, hid, lg)
+    ws.check()
+    worst = 0.0
+    for i in range(lanes):
+        h1 = torch.empty((1, geom["hidden"]), device="cuda")
+        l1 = torch.empty((1, geom["vocab"]), device="cuda")
+        ws.into([kv_b[i]], [ctxs[i]], [tokens[i]], h1, l1)
+        rh = rel_l2(h1.cpu().numpy()[0], hid.cpu().numpy()[i])
+        rl = rel_l2(l1.cpu().numpy()[0], lg.cpu().numpy()[i])
+        worst = max(worst, rh, rl)
+        assert rh <= REL and rl <= REL, (i, rh, rl)
+    print(f"{name}: lanes together vs alone, worst relative L2 {worst:.3g}")
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_full_depth_prefill_equals_stepped_decode(name):
+    # HiddenLastExtendInto by one batched pass against the same prompt
+    # decoded token by token (gpu_official_darwin_test.go:63-87, cosine of
+    # the final hidden state), at the full-depth bound above.
+    import torch
+
+    lm, geom = full_model(name)
+    n = 1024
+    rng = np.random.default_rng(7)
+    toks = rng.integers(0, geom["vocab"], n)
+    kv_p = gphq.Prefix(lm, n + 8)
+    pf = gphq.Prefill(lm, n)
+    hp = torch.empty(geom["hidden"], device="cuda")
+    pf.extend(kv_p, 0, toks, hp)
+    pf.check()
+    kv_d = gphq.Prefix(lm, n + 8)
+    ws = gphq.DecodeBatch(lm, 1)
+    ws.extend([kv_d], [0], toks[: n - 1].reshape(-1, 1))
+    hd = torch.empty((1, geom["hidden"]), device="cuda")
+    lg = torch.empty((1, geom["vocab"]), device="cuda")
+    ws.into([kv_d], [n - 1], [int(toks[-1])], hd, lg)
+    ws.check()
+    c = cosine(hp.cpu().numpy(), hd.cpu().numpy()[0])
+    print(f"{name}: batched pass vs token by token over {n} tokens, cosine {c:.8f}")
+    assert c >= COS_FULL_DEPTH, c
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_full_depth_logits_of_hidden_equal_step_logits(name):
+    import torch
+
+    lm, geom = full_model(name)
+    ctxs = [1024, 513, 77]
+    kvs = prefilled(lm, geom, ctxs, 1032, seed=4)
+    ws = gphq.DecodeBatch(lm, len(ctxs))
+    hid = torch.empty((len(ctxs), geom["hidden"]), device="cuda")
+    lg = torch.empty((len(ctxs), geom["vocab"]), device="cuda")
+    ws.into(kvs, ctxs, [1, 2, 3], hid, lg)
+    again = torch.full_like(lg, -7.0)
+    ws.logits(hid, again)
+    torch.cuda.synchronize()
+    assert torch.isfinite(lg).all()
+    assert torch.equal(again, lg)

@@ -181,6 +181,47 @@ def test_batched_prefill_oracle_matches_stepping_and_transformers(fmt):
         assert np.linalg.norm(hidden - hid[pos]) / np.linalg.norm(hid[pos]) < 2e-5, pos
 
 
+@pytest.mark.parametrize("layers", [1, 2])
+def test_prefill_last_only_equals_full_pass(layers):
+    """prefill(last_only=True), used at workload size, against the pinned full
+    pass: the final row's residual and every appended K/V row agree."""
+    g = lo.Geometry(hidden=256, layers=layers, heads=4, kv_heads=2, head_dim=128, inter=512, vocab=96, max_pos=64)
+    model = lc.random_model(g, lo.FMT_Q8B, seed=70 + layers)
+    orc_ = lc.oracle_for(model)
+    rng = np.random.default_rng(layers)
+    tokens = list(rng.integers(0, g.vocab, 23))
+    c_full, c_last = orc_.new_cache(40), orc_.new_cache(40)
+    orc_.prefill(c_full, 0, tokens[:5])
+    orc_.prefill(c_last, 0, tokens[:5])
+    full = orc_.prefill(c_full, 5, tokens[5:])
+    last = orc_.prefill(c_last, 5, tokens[5:], last_only=True)
+    assert last.shape == (1, g.hidden)
+    assert np.abs(last[0] - full[-1]).max() <= 1e-12 * np.abs(full[-1]).max()
+    for (k1, v1), (k2, v2) in zip(c_full, c_last):
+        assert np.abs(k1 - k2).max() <= 1e-12 * np.abs(k1).max()
+        assert np.abs(v1 - v2).max() <= 1e-12 * np.abs(v1).max()
+
+
+def test_chunked_head_equals_dense_head():
+    """head_rows over row chunks (the path a 151,936-row head takes) gives the
+    dense head's logits; the chunk boundary falls inside the vocabulary."""
+    g = lo.Geometry(hidden=256, layers=1, heads=2, kv_heads=1, head_dim=128, inter=512, vocab=1000, max_pos=8)
+    model = lc.random_model(g, lo.FMT_Q8B, seed=3)
+    orc_ = lc.oracle_for(model)
+    x = np.random.default_rng(0).standard_normal((3, g.hidden))
+    dense = x @ orc_.head.T
+    chunked = lc.oracle_for(model)
+    chunked.HEAD_CHUNK, chunked.DENSE_HEAD_MAX = 384, 0  # force the chunked path
+    got = chunked.head_rows(x)
+    assert chunked._head is None
+    np.testing.assert_allclose(got, dense, rtol=1e-13, atol=1e-13 * np.abs(dense).max())
+    hid, lg = orc_.finish_rows(x)
+    for i in range(3):
+        h1, l1 = orc_.finish(x[i])
+        np.testing.assert_allclose(h1, hid[i], rtol=1e-13)
+        np.testing.assert_allclose(l1, lg[i], rtol=1e-12, atol=1e-12 * np.abs(l1).max())
+
+
 def test_rope_table_matches_transformers():
     torch = pytest.importorskip("torch")
     tr = pytest.importorskip("transformers")

@@ -192,6 +192,34 @@ def test_pack_range_with_host_row_scales_matches_fused_pack():
     assert np.array_equal(host(a).view(np.uint32), host(b).view(np.uint32))
 
 
+def test_set_row_scale_after_fused_pack_keeps_other_rows():
+    # After a fused Pack (scales computed on the device), SetRowScale on one
+    # row and a PackRange re-quantize that row only: the other rows keep the
+    # scales Pack gave them (WorkspaceI8 keeps per-row state, int8.go:106-163).
+    rows, k, n = 5, 256, 80
+    w, q, scales = int8_fixture(k, n, 12)
+    x = activations(rows, k, 6)
+    dx = dev(x)
+    ws = gphq.WorkspaceI8(k, rows)
+    ws.pack(dx, rows, k)
+    a = fill(rows * n)
+    gphq.mul_panels_i8(a, n, ws, w, 0, w.panels())
+    ws.set_row_scale(2, 2 * orc.max_abs(x[2 * k:3 * k]))
+    ws.pack_range(dx, k, 0, k)
+    b = fill(rows * n, -1.0)
+    gphq.mul_panels_i8(b, n, ws, w, 0, w.panels())
+    ha, hb = host(a).reshape(rows, n), host(b).reshape(rows, n)
+    for r in (0, 1, 3, 4):
+        assert np.array_equal(ha[r].view(np.uint32), hb[r].view(np.uint32)), r
+    # Row 2 now uses the doubled scale: bit-equal to the oracle's quantizer
+    # and product with that scale (int8.go:106-119, 163-168, 200-211).
+    s2, inv2 = orc.i8_row_scale(np.float32(2 * orc.max_abs(x[2 * k:3 * k])))
+    q2 = np.array([orc.i8_quantize(np.float32(v) * inv2) for v in x[2 * k:3 * k]], dtype=np.int8)
+    want = orc.i8_mul_panels(q2.reshape(1, k), np.array([s2], np.float32), q, scales, k, n)
+    assert np.array_equal(hb[2].view(np.uint32), want.view(np.uint32))
+    assert not np.array_equal(hb[2], ha[2])
+
+
 def test_non_finite_rows_and_extremes():
     # NaN / Inf rows get scale 0 (int8.go:106-112); tiny and huge rows keep exact semantics.
     k, n = 96, 40
