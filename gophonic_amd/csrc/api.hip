@@ -83,6 +83,8 @@ const char *gphq_error_string(int status) {
         return "qwen3: sequence exceeds the GPU context";
     case GPHQ_ERR_LOGITS_SHAPE:
         return "qwen3: logits of the given values do not fill whole states and vocabulary rows";
+    case GPHQ_ERR_SCRATCH_LIMIT:
+        return "gphq: the call needs more scratch than the library's static array holds";
     }
     return "gphq: unknown status";
 }

@@ -42,6 +42,7 @@ ERR_NOT_POSITIVE_DEFINITE = -26
 ERR_SEQUENCE_COUNT = -27
 ERR_PASS_ROWS = -28
 ERR_LOGITS_SHAPE = -29
+ERR_SCRATCH_LIMIT = -30
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
 
@@ -60,6 +61,7 @@ SIGNATURES = {
     "gphq_gemv_batch": (ctypes.c_int, [ctypes.c_int, _vpp, _vpp, _vpp, _vpp, ctypes.c_int, _i64, _i64, _vp]),
     "gphq_gemv_vec_workspace_bytes": (_i64, [_i64, _i64]),
     "gphq_gemv_vec": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "gphq_gemv_vec_noalloc": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp]),
     "gphq_q8gemm_new_weights_i8": (ctypes.c_int, [_i64, _i64, _vpp]),
     "gphq_q8gemm_weights_i8_free": (None, [_vp]),
     "gphq_q8gemm_weights_i8_pack": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64]),
@@ -500,6 +502,19 @@ def gemv_vec(fmt, codes, scales, x, y, lanes, k, n, work, x_stride=None, y_strid
     return check(
         load().gphq_gemv_vec(fmt, ptr(codes), ptr(scales), ptr(x), x_stride, ptr(y), y_stride, lanes, k, n, ptr(work),
                              work.numel() * work.element_size(), stream_handle(stream))
+    )
+
+
+GEMV_VEC_NOALLOC_BYTES = 4 << 20
+
+
+def gemv_vec_noalloc(fmt, codes, scales, x, y, lanes, k, n, x_stride=None, y_stride=None, stream=None):
+    """gemv_vec with the library's static scratch (gphq_gemv_vec_noalloc): allocates nothing."""
+    x_stride = k if x_stride is None else x_stride
+    y_stride = n if y_stride is None else y_stride
+    return check(
+        load().gphq_gemv_vec_noalloc(fmt, ptr(codes), ptr(scales), ptr(x), x_stride, ptr(y), y_stride, lanes, k, n,
+                                     stream_handle(stream))
     )
 
 

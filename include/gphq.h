@@ -88,6 +88,9 @@ extern "C" {
 /* evaluator.go:325-327 "qwen3: logits of %d values into %d, want whole
  * states of %d and %d" */
 #define GPHQ_ERR_LOGITS_SHAPE (-29)
+/* No reference counterpart: a no-allocation entry point was asked for more
+ * scratch than the library's static array holds (gphq_gemv_vec_noalloc). */
+#define GPHQ_ERR_SCRATCH_LIMIT (-30)
 
 /* The reference message for a status code ("" for GPHQ_OK). Static storage. */
 const char *gphq_error_string(int status);
@@ -163,6 +166,22 @@ int64_t gphq_gemv_vec_workspace_bytes(int64_t lanes, int64_t k);
 int gphq_gemv_vec(int fmt, const void *codes_dev, const void *scales_dev, const float *x_dev, int64_t x_stride,
                   float *y_dev, int64_t y_stride, int64_t lanes, int64_t k, int64_t n, void *work_dev,
                   int64_t work_bytes, void *stream);
+
+/* gphq_gemv_vec without a workspace argument, allocating nothing. No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid
+ * allocation). Same checks (the workspace ones aside), kernels and results as
+ * gphq_gemv_vec, bit for bit; the scratch is a library-owned device array of
+ * GPHQ_GEMV_VEC_NOALLOC_BYTES per GPU, held until the process ends, so
+ * gphq_gemv_vec_workspace_bytes(lanes, k) must fit it (else
+ * GPHQ_ERR_SCRATCH_LIMIT; 32 lanes fit up to k = 16384). The stream must
+ * belong to the current device. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (streams not ordered with each other)
+ * race. */
+#define GPHQ_GEMV_VEC_NOALLOC_BYTES (4 << 20)
+int gphq_gemv_vec_noalloc(int fmt, const void *codes_dev, const void *scales_dev, const float *x_dev,
+                          int64_t x_stride, float *y_dev, int64_t y_stride, int64_t lanes, int64_t k, int64_t n,
+                          void *stream);
 
 /* Up to GPHQ_GEMV_MAX_BATCH independent GEMVs of one format and one shape in
  * a single launch: y_dev[i] = dequant(codes_dev[i], scales_dev[i]) . x_dev[i].
