@@ -85,6 +85,12 @@ const char *gphq_error_string(int status) {
         return "qwen3: logits of the given values do not fill whole states and vocabulary rows";
     case GPHQ_ERR_SCRATCH_LIMIT:
         return "gphq: the call needs more scratch than the library's static array holds";
+    case GPHQ_ERR_TAIL_SHAPE:
+        return "qwen3: tail values do not fill whole states, or exceed the tokens or maxTail";
+    case GPHQ_ERR_REUSE:
+        return "qwen3: cannot reuse the rows at this anchor";
+    case GPHQ_ERR_EMBED_ROWS:
+        return "qwen3: embedding values do not fill one row per placeholder";
     }
     return "gphq: unknown status";
 }

@@ -143,16 +143,24 @@ __global__ void lm_seed_kernel(const SeedArgs a) {
 
 // One block per lane: h = R . float32(bf16 embedding row of the lane's token)
 // (weights.go:614-619 embedRow, then rotation.apply, gpu_darwin.go:1172-1174).
+// With a splice table, a negative token -1-j takes row j of it (an Embeds
+// row: fp32, unrotated, evaluator.go:155-163) in place of an embedding row.
 __global__ __launch_bounds__(1024) void lm_embed_kernel(const uint16_t *__restrict__ embed,
                                                         const int32_t *__restrict__ tok, int vocab, int H,
                                                         const float *__restrict__ signs, int block,
-                                                        float *__restrict__ h) {
+                                                        float *__restrict__ h, const float *__restrict__ splice) {
     extern __shared__ float v[];
     const int lane = blockIdx.x;
-    const int t = min(max(tok[lane], 0), vocab - 1);
-    const uint16_t *row = embed + (size_t)t * H;
-    for (int i = threadIdx.x; i < H; i += blockDim.x)
-        v[i] = __builtin_bit_cast(float, (uint32_t)row[i] << 16) * signs[i];
+    const int id = tok[lane];
+    if (splice && id < 0) {
+        const float *row = splice + (size_t)(-1 - id) * H;
+        for (int i = threadIdx.x; i < H; i += blockDim.x) v[i] = row[i] * signs[i];
+    } else {
+        const int t = min(max(id, 0), vocab - 1);
+        const uint16_t *row = embed + (size_t)t * H;
+        for (int i = threadIdx.x; i < H; i += blockDim.x)
+            v[i] = __builtin_bit_cast(float, (uint32_t)row[i] << 16) * signs[i];
+    }
     __syncthreads();
     lds_fwht(v, H, block);
     for (int i = threadIdx.x; i < H; i += blockDim.x) h[(size_t)lane * H + i] = v[i];
@@ -173,12 +181,14 @@ __global__ __launch_bounds__(256) void lm_rotate_kernel(float *__restrict__ x, i
 
 // One block per lane (gpu_darwin.go:1241-1252): u = R^T h; hidden = u *
 // float32(1/sqrt(mean(u^2) + eps)) * w (ops.go:251-254, mean and root in
-// float64); hn = R hidden for the head. Flags a non-finite hidden value.
+// float64); hn = R hidden for the head (skipped when hn is null). Flags a
+// non-finite hidden value in nonfinite[lane], or in nonfinite[0] for every
+// lane when one_flag is set.
 __global__ __launch_bounds__(1024) void lm_final_kernel(const float *__restrict__ h, int H,
                                                         const float *__restrict__ signs, int block,
                                                         const float *__restrict__ w, float eps,
                                                         float *__restrict__ hidden, float *__restrict__ hn,
-                                                        int32_t *__restrict__ nonfinite) {
+                                                        int32_t *__restrict__ nonfinite, int one_flag) {
     extern __shared__ float v[];
     __shared__ float red[16];
     __shared__ int bad;
@@ -204,9 +214,11 @@ __global__ __launch_bounds__(1024) void lm_final_kernel(const float *__restrict_
     }
     if (any) bad = 1;
     __syncthreads();
-    lds_fwht(v, H, block);
-    for (int i = threadIdx.x; i < H; i += blockDim.x) hn[(size_t)lane * H + i] = v[i];
-    if (threadIdx.x == 0 && bad) nonfinite[lane] = 1;
+    if (hn) {
+        lds_fwht(v, H, block);
+        for (int i = threadIdx.x; i < H; i += blockDim.x) hn[(size_t)lane * H + i] = v[i];
+    }
+    if (threadIdx.x == 0 && bad) nonfinite[one_flag ? 0 : lane] = 1;
 }
 
 // Keys per attention block of a prefix with `capacity` rows: the capacity
@@ -665,7 +677,7 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool 
     const int64_t H = c.hidden, I = c.intermediate, qkvw = lm->qd + 2 * lm->kvd;
     const int fmt = c.fmt;
     hipLaunchKernelGGL(lm_embed_kernel, dim3(lanes), dim3(1024), H * sizeof(float), st, lm->embed, ws->tok,
-                       (int)c.vocab, (int)H, lm->hsigns, (int)lm->hblock, ws->h);
+                       (int)c.vocab, (int)H, lm->hsigns, (int)lm->hblock, ws->h, (const float *)nullptr);
     GPHQ_TRY(launch_status());
     AttnArgs aa{};
     aa.qkv = ws->qkv;
@@ -712,7 +724,7 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool 
     }
     if (!head) return GPHQ_OK;
     hipLaunchKernelGGL(lm_final_kernel, dim3(lanes), dim3(1024), H * sizeof(float), st, ws->h, (int)H, lm->hsigns,
-                       (int)lm->hblock, lm->final_norm, (float)c.eps, hidden_out, ws->hn, ws->nonfinite);
+                       (int)lm->hblock, lm->final_norm, (float)c.eps, hidden_out, ws->hn, ws->nonfinite, 0);
     GPHQ_TRY(launch_status());
     GPHQ_TRY(gemv(ws, lanes, GPHQ_FMT_Q8B, PRO_PLAIN, EPI_STORE, lm->head, 0, lm->head_scale, ws->hn, H, ws->logits,
                   lm->head_rows, H, lm->head_rows, st));
@@ -841,10 +853,10 @@ namespace gphq {
 
 bool lm_model_ready(const gphq_lm *lm) { return model_ready(lm); }
 
-int lm_embed_launch(const gphq_lm *lm, const int32_t *tok, int rows, float *h, hipStream_t st) {
+int lm_embed_launch(const gphq_lm *lm, const int32_t *tok, int rows, float *h, hipStream_t st, const float *splice) {
     const int H = (int)lm->cfg.hidden;
     hipLaunchKernelGGL(lm_embed_kernel, dim3(rows), dim3(1024), H * sizeof(float), st, lm->embed, tok,
-                       (int)lm->cfg.vocab, H, lm->hsigns, (int)lm->hblock, h);
+                       (int)lm->cfg.vocab, H, lm->hsigns, (int)lm->hblock, h, splice);
     return launch_status();
 }
 
@@ -856,10 +868,10 @@ int lm_rotate_launch(const gphq_lm *lm, float *act, int rows, long stride, hipSt
 }
 
 int lm_final_launch(const gphq_lm *lm, const float *h, int rows, float *hidden, float *hn, int32_t *nonfinite,
-                    hipStream_t st) {
+                    hipStream_t st, bool one_flag) {
     const int H = (int)lm->cfg.hidden;
     hipLaunchKernelGGL(lm_final_kernel, dim3(rows), dim3(1024), H * sizeof(float), st, h, H, lm->hsigns,
-                       (int)lm->hblock, lm->final_norm, (float)lm->cfg.eps, hidden, hn, nonfinite);
+                       (int)lm->hblock, lm->final_norm, (float)lm->cfg.eps, hidden, hn, nonfinite, one_flag ? 1 : 0);
     return launch_status();
 }
 

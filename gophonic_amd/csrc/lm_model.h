@@ -47,15 +47,17 @@ inline uint64_t next_generation() {
 // Whether the embedding, head, final norm and every layer are bound.
 bool lm_model_ready(const gphq_lm *lm);
 // h[r] = R . float32(bf16 embedding row of tok[r]) for r < rows (tok on the
-// device, clamped into the vocabulary).
-int lm_embed_launch(const gphq_lm *lm, const int32_t *tok, int rows, float *h, hipStream_t st);
+// device, clamped into the vocabulary); with a splice table, a token -1-j
+// takes R . splice[j] (an fp32 Embeds row) instead.
+int lm_embed_launch(const gphq_lm *lm, const int32_t *tok, int rows, float *h, hipStream_t st,
+                    const float *splice = nullptr);
 // The down input's online Hadamard over `rows` rows of the intermediate
 // width, rows `stride` floats apart.
 int lm_rotate_launch(const gphq_lm *lm, float *act, int rows, long stride, hipStream_t st);
 // Final norm of `rows` residual rows: hidden[r] (post-final-norm state),
-// hn[r] = R hidden[r] (the head's input); sets nonfinite[r] on a non-finite
-// hidden value.
+// hn[r] = R hidden[r] (the head's input; skipped for a null hn); sets
+// nonfinite[r] (nonfinite[0] with one_flag) on a non-finite hidden value.
 int lm_final_launch(const gphq_lm *lm, const float *h, int rows, float *hidden, float *hn, int32_t *nonfinite,
-                    hipStream_t st);
+                    hipStream_t st, bool one_flag = false);
 
 }  // namespace gphq

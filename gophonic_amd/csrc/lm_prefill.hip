@@ -376,11 +376,11 @@ struct PassKV {
 
 // One pass: R tokens already in ws->tok, at cache rows base.. of kv.kc (or,
 // packed, at rows 0..R-1 with per-row positions).
-int encode_pass(gphq_prefill *ws, const PassKV &kv, int base, int R, hipStream_t st) {
+int encode_pass(gphq_prefill *ws, const PassKV &kv, int base, int R, hipStream_t st, const float *splice = nullptr) {
     const gphq_lm *lm = ws->lm;
     const gphq_lm_config &c = lm->cfg;
     const int64_t H = c.hidden, I = c.intermediate, qd = lm->qd, kvd = lm->kvd, qkvw = qd + 2 * kvd;
-    GPHQ_TRY(lm_embed_launch(lm, ws->tok, R, ws->h, st));
+    GPHQ_TRY(lm_embed_launch(lm, ws->tok, R, ws->h, st, splice));
     RopeArgs ra{};
     ra.qkv = ws->qkv;
     ra.rope = lm->rope;
@@ -514,6 +514,67 @@ int gphq_prefill_extend(gphq_prefill *ws, gphq_prefix *kv, int64_t keep, const i
         last = R;
     }
     return lm_final_launch(lm, ws->h + (size_t)(last - 1) * H, 1, hidden_dev, ws->hn, ws->nonfinite, st);
+}
+
+int gphq_prefill_extend_embed(gphq_prefill *ws, gphq_prefix *kv, int64_t stored, int64_t keep, int64_t reuse,
+                              const int32_t *tokens, int64_t n, const gphq_embeds *embeds, float *tail_dev,
+                              int64_t tail_len, void *stream) {
+    // HiddenTailContinueEmbedInto (evaluator.go:293-310): the tail shape
+    // first (a one-row tail is HiddenLast*, whose empty sequence is reported
+    // by the batch checks below).
+    if (!ws || !ws->lm) return GPHQ_ERR_WORKSPACE;
+    const gphq_lm *lm = ws->lm;
+    const gphq_lm_config &c = lm->cfg;
+    const int64_t H = c.hidden;
+    const int64_t k = tail_len / H;
+    if (k == 0 || tail_len != k * H || k > GPHQ_TAIL_MAX_ROWS || (k > 1 && k > n)) return GPHQ_ERR_TAIL_SHAPE;
+    // hiddenLastContinueEmbedInto (evaluator.go:182-213), in order.
+    if (!kv || kv->lm != lm || !kv->kc) return GPHQ_ERR_FOREIGN_PREFIX;
+    if (stored < 0 || stored > kv->capacity || keep < 0 || keep > stored) return GPHQ_ERR_KEEP_RANGE;
+    if (n < 0 || keep + n > kv->capacity) return GPHQ_ERR_PREFIX_CAPACITY;
+    if (reuse < 0 || reuse > stored - keep || reuse > n) return GPHQ_ERR_REUSE;
+    // The GPU path recomputes every row (evaluator.go:197-199): a valid reuse
+    // changes nothing.
+    const bool splicing = embeds && embeds->rows_len != 0;
+    if (splicing) {
+        int64_t placeholders = 0;
+        for (int64_t i = 0; i < n; ++i) placeholders += tokens && tokens[i] == embeds->token;
+        if (embeds->rows_len != placeholders * H || !embeds->rows_dev) return GPHQ_ERR_EMBED_ROWS;
+    }
+    // HiddenLastBatchInto (evaluator.go:540-560) for the one sequence.
+    if (n == 0 || !tokens) return GPHQ_ERR_EMPTY_SEQUENCE;
+    if (keep + n > c.max_positions || keep + n > lm->positions) return GPHQ_ERR_CONTEXT;
+    if (!tail_dev) return GPHQ_ERR_DEST_WIDTH;
+    for (int64_t i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= c.vocab) return GPHQ_ERR_TOKEN_VOCAB;
+    // The last pass holds the whole tail (gpu_darwin.go:1473-1479), so a
+    // pass must have room for it.
+    if (k > ws->rows) return GPHQ_ERR_PASS_ROWS;
+    hipStream_t st = (hipStream_t)stream;
+    // Placeholders become -1-j (row j of the splice table) in the device ids.
+    std::vector<int32_t> ids(tokens, tokens + n);
+    if (splicing) {
+        int32_t j = 0;
+        for (int32_t &t : ids)
+            if (t == embeds->token) t = -1 - j++;
+    }
+    int last = 0;
+    for (int64_t off = 0; off < n;) {
+        int64_t R = std::min<int64_t>(ws->rows, n - off);
+        const int64_t rest = n - off - R;
+        if (rest > 0 && rest < k) R = n - off - k;
+        GPHQ_TRY(hip_status(
+            hipMemcpyAsync(ws->tok, ids.data() + off, (size_t)R * sizeof(int32_t), hipMemcpyHostToDevice, st)));
+        const PassKV pk{kv->kc, kv->vc, kv->capacity, nullptr, nullptr, 0, 0, nullptr, nullptr};
+        GPHQ_TRY(encode_pass(ws, pk, (int)(keep + off), (int)R, st, splicing ? embeds->rows_dev : nullptr));
+        // The host ids are read before the next pass rewrites the device copy.
+        if (off + R < n) GPHQ_TRY(hip_status(hipStreamSynchronize(st)));
+        last = (int)R;
+        off += R;
+    }
+    GPHQ_TRY(lm_final_launch(lm, ws->h + (size_t)(last - k) * H, (int)k, tail_dev, nullptr, ws->nonfinite, st, true));
+    // `ids` is freed on return: wait for the last upload to have read it.
+    return hip_status(hipStreamSynchronize(st));
 }
 
 int gphq_prefill_batch(gphq_prefill *ws, const gphq_prefix *shared, int64_t past, const int32_t *tokens,

@@ -43,6 +43,10 @@ ERR_SEQUENCE_COUNT = -27
 ERR_PASS_ROWS = -28
 ERR_LOGITS_SHAPE = -29
 ERR_SCRATCH_LIMIT = -30
+ERR_TAIL_SHAPE = -31
+ERR_REUSE = -32
+ERR_EMBED_ROWS = -33
+TAIL_MAX_ROWS = 256
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
 
@@ -133,6 +137,7 @@ SIGNATURES = {
     "gphq_prefill_free": (None, [_vp]),
     "gphq_prefill_rows": (ctypes.c_int, [_vp]),
     "gphq_prefill_extend": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "gphq_prefill_extend_embed": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp]),
     "gphq_prefill_batch": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp]),
     "gphq_q8b_quantize": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
     "gphq_q8b_gemm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
@@ -714,6 +719,13 @@ class DecodeBatch:
         return check(load().gphq_decode_batch_check(self.h, stream_handle(stream)))
 
 
+class Embeds(ctypes.Structure):
+    """gphq_embeds: placeholder token and its replacement rows (evaluator.go:155-163)."""
+
+    _fields_ = [("token", ctypes.c_int32), ("reserved", ctypes.c_int32), ("rows_dev", ctypes.c_void_p),
+                ("rows_len", ctypes.c_int64)]
+
+
 class Prefill:
     """gphq_prefill: the batched pass's scratch for up to `rows` tokens per pass
     (gpuWorkspace, gpu_darwin.go:895-960)."""
@@ -743,6 +755,24 @@ class Prefill:
         tok = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
         check(load().gphq_prefill_extend(self.h, kv.h if kv is not None else None, keep, tok.ctypes.data, tok.size,
                                          ptr(hidden), 0 if hidden is None else hidden.numel(), stream_handle(stream)))
+
+    def extend_embed(self, kv, stored, keep, tokens, tail, embeds_token=0, embeds_rows=None, reuse=0, stream=None):
+        """HiddenTailContinueEmbedInto (evaluator.go:293-310): tokens (host
+        ints) continue the first `keep` of the `stored` tokens of kv;
+        placeholders equal to embeds_token take the rows of embeds_rows (a
+        float32 device tensor [occurrences][hidden]) when given; tail (a
+        float32 device tensor [k][hidden], or [hidden] for k = 1) receives the
+        post-final-norm states of the last k positions."""
+        import numpy as np
+
+        tok = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+        emb = None
+        if embeds_rows is not None:
+            emb = Embeds(int(embeds_token), 0, ptr(embeds_rows), embeds_rows.numel())
+        check(load().gphq_prefill_extend_embed(self.h, kv.h if kv is not None else None, stored, keep, reuse,
+                                               tok.ctypes.data if tok.size else None, tok.size,
+                                               None if emb is None else ctypes.byref(emb), ptr(tail),
+                                               0 if tail is None else tail.numel(), stream_handle(stream)))
 
     def batch(self, seqs, hidden, shared=None, past=0, stream=None):
         """HiddenLastBatchInto (evaluator.go:531), or HiddenLastSharedInto

@@ -91,6 +91,12 @@ extern "C" {
 /* No reference counterpart: a no-allocation entry point was asked for more
  * scratch than the library's static array holds (gphq_gemv_vec_noalloc). */
 #define GPHQ_ERR_SCRATCH_LIMIT (-30)
+/* evaluator.go:298-301 "qwen3: %d tail values for %d tokens of width %d" */
+#define GPHQ_ERR_TAIL_SHAPE (-31)
+/* evaluator.go:194-196 "qwen3: cannot reuse %d rows at anchor %d" */
+#define GPHQ_ERR_REUSE (-32)
+/* evaluator.go:208-210 "qwen3: %d embedding values for %d placeholders of width %d" */
+#define GPHQ_ERR_EMBED_ROWS (-33)
 
 /* The reference message for a status code ("" for GPHQ_OK). Static storage. */
 const char *gphq_error_string(int status);
@@ -561,6 +567,38 @@ int gphq_prefill_rows(const gphq_prefill *ws);
  * hidden state. */
 int gphq_prefill_extend(gphq_prefill *ws, gphq_prefix *kv, int64_t keep, const int32_t *tokens, int64_t n,
                         float *hidden_dev, int64_t hidden_len, void *stream);
+/* Embeds (evaluator.go:150-163): the i-th occurrence of `token` among a
+ * call's tokens takes row i of rows_dev (device, rows_len = occurrences x
+ * hidden fp32 values, unrotated like an embedding-table row) instead of the
+ * embedding row. rows_len == 0 replaces nothing. */
+typedef struct gphq_embeds {
+    int32_t token;
+    int32_t reserved;
+    const float *rows_dev;
+    int64_t rows_len;
+} gphq_embeds;
+/* evaluator.go:283-285 maxTail: states one tail call returns, at most. */
+#define GPHQ_TAIL_MAX_ROWS 256
+/* HiddenTailContinueEmbedInto (evaluator.go:293-310) and, with a one-row
+ * tail, HiddenLastContinueEmbedInto / HiddenLastExtendEmbedInto
+ * (evaluator.go:164-262); the provider seam is gpuWorkspace.batch with
+ * Embeds (gpu_darwin.go:1412-1480, pass 1574-1657). tokens[0..n) (host)
+ * continue the first `keep` of the `stored` tokens the caller records for
+ * kv (PrefixKV.tokens stays on the caller's side); placeholder tokens of
+ * `embeds` (may be NULL) take its rows. tail_dev receives the
+ * post-final-norm states of the last tail_len / hidden positions, in order
+ * (1 <= that count <= GPHQ_TAIL_MAX_ROWS and <= n); passes hold at most the
+ * workspace's rows and the last pass holds the whole tail. `reuse` leading
+ * rows may be declared unchanged (the reuse contract, checked as the
+ * reference checks it); like the reference's GPU path every row is
+ * recomputed, so the result does not depend on it. Afterwards the caller
+ * records tokens[:keep] followed by the ids, each placeholder as -1.
+ * Validation (evaluator.go:295-301, 182-213, 540-560) in order, before any
+ * device work; returns once the host arrays are consumed (the stream is
+ * synchronized). gphq_prefill_check reports a non-finite tail state. */
+int gphq_prefill_extend_embed(gphq_prefill *ws, gphq_prefix *kv, int64_t stored, int64_t keep, int64_t reuse,
+                              const int32_t *tokens, int64_t n, const gphq_embeds *embeds, float *tail_dev,
+                              int64_t tail_len, void *stream);
 /* HiddenLastBatchInto (evaluator.go:525-575) and, with a shared prefix,
  * HiddenLastSharedInto (evaluator.go:408-425): `count` independent sequences,
  * their tokens concatenated in `tokens` (host) with lengths lens[count], packed

@@ -271,26 +271,40 @@ class DecodeOracle:
         a, b = v[:, :half], v[:, half:]
         return np.concatenate([a * c - b * s, b * c + a * s], axis=1)
 
-    def prefill(self, cache, base, tokens, last_only=False):
+    def prefill(self, cache, base, tokens, last_only=False, embeds=None, tail=None):
         """All rows of tokens at positions base.. at once (the batched pass,
         gpu_darwin.go:1703-1764: each row attends cache rows 0..its own
         position): appends K/V and returns the residual rows [T][hidden]. The
         same float64 math as stepping layers() token by token.
 
-        last_only: the last layer still appends every row's K/V but finishes
-        only the final row (the only row HiddenLastExtendInto returns), and
-        the result is that row's residual [1][hidden]. For a one-layer model
-        this skips all but one row's attention and MLP."""
+        tail: the last layer still appends every row's K/V but finishes only
+        the final `tail` rows (the rows HiddenTail*/HiddenLast* return), and
+        the result is those rows' residuals [tail][hidden]; last_only is
+        tail=1. For a one-layer model this skips the other rows' attention
+        and MLP.
+
+        embeds: (token, rows [occurrences][hidden]) -- Embeds
+        (evaluator.go:150-163, gpu_darwin.go:1582-1590): the i-th occurrence
+        of token takes row i (float32, unrotated like an embedding row)
+        instead of the embedding table's row."""
         g = self.g
         T = len(tokens)
         hd = g.head_dim
         grp = g.heads // g.kv_heads
         scale = 1.0 / np.sqrt(hd)
         pos = base + np.arange(T)
-        h = rot_apply(bf16_to_f64(self.embed[np.asarray(tokens, np.int64)]), self.hrot).reshape(T, g.hidden)
+        ids = np.asarray(tokens, np.int64)
+        raw = bf16_to_f64(self.embed[ids]).reshape(T, g.hidden)
+        if embeds is not None:
+            at = np.nonzero(ids == embeds[0])[0]
+            rows_in = np.asarray(embeds[1], np.float32).reshape(-1, g.hidden)
+            assert len(rows_in) == len(at), "one Embeds row per placeholder"
+            raw[at] = rows_in.astype(np.float64)
+        h = rot_apply(raw, self.hrot).reshape(T, g.hidden)
         mask = np.arange(base + T)[None, :] <= pos[:, None]
+        tail = 1 if last_only and tail is None else tail
         for li, W in enumerate(self.W):
-            rows = slice(T - 1, T) if last_only and li == len(self.W) - 1 else slice(0, T)
+            rows = slice(T - tail, T) if tail is not None and li == len(self.W) - 1 else slice(0, T)
             hn = self._norm_rows(h)
             kv = hn @ W["qkv"][g.qd:].T
             qs = hn[rows] @ W["qkv"][: g.qd].T

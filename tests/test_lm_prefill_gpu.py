@@ -311,3 +311,136 @@ def test_batch_validation_errors():
     assert status(lambda: ws.batch([[1]], hid)) == gphq.ERR_DEST_WIDTH
     assert status(lambda: ws.batch([[1], [g.vocab]], hid)) == gphq.ERR_TOKEN_VOCAB
     assert status(lambda: ws.batch([[1], [2] * 9], hid)) == gphq.ERR_PASS_ROWS
+
+
+# ---- Embeds, tail states and the reuse contract (gphq_prefill_extend_embed) ----
+
+def run_embed(ws, kv, stored, keep, tokens, k, g, ph=0, rows=None, reuse=0):
+    import torch
+
+    tail = torch.full((k, g.hidden), -7.0, device="cuda")
+    dev_rows = None if rows is None else torch.from_numpy(np.ascontiguousarray(rows, np.float32)).cuda()
+    print(f"extend_embed stored={stored} keep={keep} n={len(tokens)} k={k} rows={ws.rows}", flush=True)
+    ws.extend_embed(kv, stored, keep, tokens, tail, embeds_token=ph, embeds_rows=dev_rows, reuse=reuse)
+    ws.check()
+    return tail.cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt", [lo.FMT_Q8B, lo.FMT_Q4])
+def test_embeds_splice_and_tail_match_oracle(fmt):
+    # qwen3asr's splice (transcriber.go:481-551): audio rows at the
+    # placeholder positions, spread over two passes, and the last 12 states
+    # (HiddenTailExtendEmbedInto). 25 tokens in passes of 16 would leave 9 of
+    # the 12 tail rows for the second pass, so the passes are 13 + 12
+    # (gpu_darwin.go:1473-1479: the last pass holds the whole tail).
+    model, oracle, lm = setup(lc.GPU_SHAPE, fmt, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(51)
+    ph = 77
+    tokens = [int(t) if t != ph else 3 for t in rng.integers(0, g.vocab, 25)]
+    for i in (0, 4, 5, 6, 12, 13, 18, 24):
+        tokens[i] = ph
+    occ = tokens.count(ph)
+    rows = rng.standard_normal((occ, g.hidden)).astype(np.float32)
+    ws = gphq.Prefill(lm, 16)
+    kv = gphq.Prefix(lm, 48)
+    k = 12
+    got = run_embed(ws, kv, 0, 0, tokens, k, g, ph, rows)
+    cache = oracle.new_cache(48)
+    h = oracle.prefill(cache, 0, tokens, embeds=(ph, rows), tail=k)
+    want, _ = oracle.finish_rows(h)
+    for i in range(k):
+        assert cosine(want[i], got[i]) >= COS, i
+    check_cache(cache, kv, g, len(tokens))
+
+
+def test_embeds_of_table_rows_equal_plain_tokens_bitwise():
+    # Splice rows that are the embedding table's own rows (as float32) give
+    # the bits of the unspliced pass: the splice changes only the source row.
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(52)
+    tokens = [int(t) for t in rng.integers(0, g.vocab, 23)]
+    ph = tokens[3]
+    occ = tokens.count(ph)
+    table = lo.bf16_to_f64(model["embed"][ph]).astype(np.float32)
+    ws = gphq.Prefill(lm, 32)
+    a = run_embed(ws, gphq.Prefix(lm, 32), 0, 0, tokens, 5, g, ph, np.tile(table, (occ, 1)))
+    b = run_embed(ws, gphq.Prefix(lm, 32), 0, 0, tokens, 5, g)
+    np.testing.assert_array_equal(a, b)
+    # The tail's last row is HiddenLastExtendInto's state.
+    last = run_prefill(ws, gphq.Prefix(lm, 32), 0, tokens, g)
+    np.testing.assert_array_equal(b[-1], last)
+
+
+def test_continue_with_reuse_recomputes_every_row():
+    # HiddenLastContinueEmbedInto: a declared reuse passes the reference's
+    # checks and changes nothing (the GPU path recomputes every row,
+    # evaluator.go:197-199), including at a kept anchor inside the cache.
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B_F32, seed=5)
+    g = model["geom"]
+    rng = np.random.default_rng(53)
+    first = [int(t) for t in rng.integers(0, g.vocab, 20)]
+    ws = gphq.Prefill(lm, 32)
+    kv = gphq.Prefix(lm, 48)
+    run_embed(ws, kv, 0, 0, first, 1, g)
+    ids = first[6:] + [int(t) for t in rng.integers(0, g.vocab, 4)]
+    a = run_embed(ws, kv, 20, 6, ids, 3, g, reuse=14)
+    kv2 = gphq.Prefix(lm, 48)
+    run_embed(ws, kv2, 0, 0, first, 1, g)
+    b = run_embed(ws, kv2, 20, 6, ids, 3, g, reuse=0)
+    np.testing.assert_array_equal(a, b)
+    cache = oracle.new_cache(48)
+    oracle.prefill(cache, 0, first[:6])
+    h = oracle.prefill(cache, 6, ids, tail=3)
+    want, _ = oracle.finish_rows(h)
+    for i in range(3):
+        assert cosine(want[i], a[i]) >= COS, i
+
+
+def test_embed_extend_validation_errors():
+    import torch
+
+    model, oracle, lm = setup(lc.GPU_SHAPE, lo.FMT_Q8B, seed=5)
+    g = model["geom"]
+    ws = gphq.Prefill(lm, 8)
+    kv = gphq.Prefix(lm, 16)
+    rows = torch.zeros((2, g.hidden), device="cuda")
+
+    def status(fn):
+        try:
+            fn()
+        except gphq.GphqError as e:
+            return e.status
+        return gphq.OK
+
+    t1 = torch.full((1, g.hidden), -7.0, device="cuda")
+    t3 = torch.full((3, g.hidden), -7.0, device="cuda")
+    ok = [1, 2, 3, 4]
+    # Tail shape (evaluator.go:298-301): empty, ragged, more rows than tokens, beyond maxTail.
+    assert status(lambda: ws.extend_embed(kv, 0, 0, ok, t1.view(-1)[:0])) == gphq.ERR_TAIL_SHAPE
+    assert status(lambda: ws.extend_embed(kv, 0, 0, ok, t3.view(-1)[: g.hidden + 5])) == gphq.ERR_TAIL_SHAPE
+    assert status(lambda: ws.extend_embed(kv, 0, 0, [1, 2], t3)) == gphq.ERR_TAIL_SHAPE
+    big = torch.zeros((257, g.hidden), device="cuda")
+    assert status(lambda: ws.extend_embed(kv, 0, 0, list(range(300)), big)) == gphq.ERR_TAIL_SHAPE
+    # Prefix and anchor (evaluator.go:182-196).
+    other = gphq.lm_from_stored(geom_kwargs(g), lo.FMT_Q8B, model["layers"], model["embed"], model["final_norm"],
+                                model["head"])
+    assert status(lambda: ws.extend_embed(gphq.Prefix(other, 16), 0, 0, ok, t1)) == gphq.ERR_FOREIGN_PREFIX
+    assert status(lambda: ws.extend_embed(kv, 2, 3, ok, t1)) == gphq.ERR_KEEP_RANGE
+    assert status(lambda: ws.extend_embed(kv, 14, 14, ok, t1)) == gphq.ERR_PREFIX_CAPACITY
+    assert status(lambda: ws.extend_embed(kv, 6, 2, ok, t1, reuse=5)) == gphq.ERR_REUSE
+    assert status(lambda: ws.extend_embed(kv, 9, 2, ok, t1, reuse=5)) == gphq.ERR_REUSE
+    # One row per placeholder (evaluator.go:200-211).
+    assert status(lambda: ws.extend_embed(kv, 0, 0, [1, 5, 5, 5], t1, embeds_token=5, embeds_rows=rows)) == \
+        gphq.ERR_EMBED_ROWS
+    # The batch checks (evaluator.go:540-560).
+    assert status(lambda: ws.extend_embed(kv, 0, 0, [], t1)) == gphq.ERR_EMPTY_SEQUENCE
+    assert status(lambda: ws.extend_embed(kv, 0, 0, [1, g.vocab], t1)) == gphq.ERR_TOKEN_VOCAB
+    # A tail taller than one pass.
+    t9 = torch.zeros((9, g.hidden), device="cuda")
+    assert status(lambda: ws.extend_embed(kv, 0, 0, list(range(12)), t9)) == gphq.ERR_PASS_ROWS
+    torch.cuda.synchronize()
+    assert (t1 == -7.0).all() and (t3 == -7.0).all()
+    kc, _, cap = kv.kv()
+    assert not _read_dev_floats(kc, g.kvd * cap).any()

@@ -202,6 +202,50 @@ def test_prefill_last_only_equals_full_pass(layers):
         assert np.abs(v1 - v2).max() <= 1e-12 * np.abs(v1).max()
 
 
+def test_prefill_embeds_and_tail():
+    """Embeds rows that equal the embedding table's rows (as float32) give the
+    plain pass exactly; the tail rows equal the full pass's last rows."""
+    g = lo.Geometry(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=128, inter=512, vocab=96, max_pos=64)
+    model = lc.random_model(g, lo.FMT_Q8B, seed=81)
+    orc_ = lc.oracle_for(model)
+    tokens = [5, 90, 7, 90, 90, 3, 11, 90, 1]
+    ph = 90
+    rows = lo.bf16_to_f64(model["embed"][ph]).astype(np.float32)
+    occ = tokens.count(ph)
+    c1, c2, c3 = orc_.new_cache(16), orc_.new_cache(16), orc_.new_cache(16)
+    plain = orc_.prefill(c1, 0, tokens)
+    spliced = orc_.prefill(c2, 0, tokens, embeds=(ph, np.tile(rows, (occ, 1))))
+    np.testing.assert_array_equal(spliced, plain)
+    tail = orc_.prefill(c3, 0, tokens, tail=4)
+    assert tail.shape == (4, g.hidden)
+    assert np.abs(tail - plain[-4:]).max() <= 1e-12 * np.abs(plain).max()
+    for (k1, v1), (k3, v3) in zip(c1, c3):
+        assert np.abs(k1 - k3).max() <= 1e-12 * np.abs(k1).max()
+
+
+@pytest.mark.parametrize("fmt", [lo.FMT_Q8B, lo.FMT_Q8])
+def test_prefill_embeds_match_transformers_inputs_embeds(fmt):
+    """The spliced pass against transformers' Qwen3 fed inputs_embeds with the
+    same rows at the placeholders (and embedding rows elsewhere)."""
+    torch = pytest.importorskip("torch")
+    model = lc.random_model(lc.GPU_SHAPE, fmt, seed=31 + fmt)
+    g = model["geom"]
+    orc_ = lc.oracle_for(model)
+    tokens = [4, 60, 60, 9, 60, 22, 7]
+    ph = 60
+    rng = np.random.default_rng(8)
+    rows = rng.standard_normal((tokens.count(ph), g.hidden)).astype(np.float32)
+    h = orc_.prefill(orc_.new_cache(16), 0, tokens, embeds=(ph, rows))
+    emb = lo.bf16_to_f64(model["embed"]).reshape(g.vocab, g.hidden)[tokens]
+    emb[np.array(tokens) == ph] = rows.astype(np.float64)
+    hf = _hf_model(model)
+    with torch.no_grad():
+        hid = hf.model(inputs_embeds=torch.from_numpy(emb)[None]).last_hidden_state[0].numpy()
+    for pos in range(len(tokens)):
+        hidden, _ = orc_.finish(h[pos])
+        assert np.linalg.norm(hidden - hid[pos]) / np.linalg.norm(hid[pos]) < 2e-5, pos
+
+
 def test_chunked_head_equals_dense_head():
     """head_rows over row chunks (the path a 151,936-row head takes) gives the
     dense head's logits; the chunk boundary falls inside the vocabulary."""
