@@ -1007,6 +1007,36 @@ __global__ void f16_pack_tiles_kernel(const uint16_t *__restrict__ src, uint16_t
     }
 }
 
+// The reference's FP16 panel layout [panel = row/64][K/2][64][2]
+// (q8gemm/packed.go:233-239 at()) -> this library's tile layout, rows past n
+// and K values past K zero. One thread per tile-layout lane (16 values).
+__global__ void f16_ref_panels_to_tiles_kernel(const uint16_t *__restrict__ ref, uint16_t *__restrict__ dst, int n,
+                                               int K, long pairs, int nt, int kt) {
+    const size_t chunk = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)nt * kt * 64;
+    if (chunk >= total) return;
+    const int lane = (int)(chunk & 63);
+    const size_t g = chunk >> 6;
+    const int ktile = (int)(g % kt), rtile = (int)(g / kt);
+    const int r = rtile * 16 + (lane & 15);
+    const int kbase = ktile * 64 + (lane >> 4) * 16;
+    uint16_t *d = dst + g * 1024 + (size_t)lane * 16;
+    const uint16_t *panel = ref + (size_t)(r / 64) * pairs * 128 + (size_t)(r % 64) * 2;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int k = kbase + i;
+        d[i] = (r < n && k < K) ? panel[(size_t)(k >> 1) * 128 + (k & 1)] : (uint16_t)0;
+    }
+}
+
+int f16_ref_panels_to_tiles(const uint16_t *ref, uint16_t *dst, int n, int K, int nt, int kt, hipStream_t stream) {
+    const size_t chunks = (size_t)nt * kt * 64;
+    if (chunks == 0) return GPHQ_OK;
+    hipLaunchKernelGGL(f16_ref_panels_to_tiles_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream,
+                       ref, dst, n, K, (long)((K + 1) / 2), nt, kt);
+    return launch_status();
+}
+
 int f16_pack_tiles(const uint16_t *src, uint16_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {
     if (rows == 0) return GPHQ_OK;
     const int rowTiles = ((row0 + rows + 15) >> 4) - (row0 >> 4);

@@ -327,4 +327,123 @@ int gphq_prepare_projection(const gphq_prepare_job *j, void *work_dev, int64_t w
     return hip_status(hipStreamSynchronize(st));
 }
 
+int gphq_prepare_layer_jobs(const gphq_lm_config *cfg, const float *input_norm_host, const float *post_norm_host,
+                            void *dst_dev, int64_t dst_bytes, gphq_prepare_job *jobs) {
+    // prepareGPU's dense-layer jobs (gpu_darwin.go:400-415), in its order.
+    if (!cfg || !jobs || !input_norm_host || !post_norm_host) return GPHQ_ERR_DIMENSIONS;
+    gphq_lm_layer L{};
+    int64_t bytes = 0;
+    GPHQ_TRY(gphq_lm_layer_layout(cfg, &L, &bytes));
+    const int64_t h = cfg->hidden, hd = cfg->head_dim, qd = cfg->heads * hd, kv = cfg->kv_heads * hd,
+                  inter = cfg->intermediate;
+    const int fmt = cfg->fmt;
+    const gphq_rotation_spec none{0, 0}, hidden{h, 0}, head{0, hd};
+    // Q8B skips the down projection's input rotation (gpu_darwin.go:209-215).
+    const gphq_rotation_spec down_in = fmt == GPHQ_FMT_Q8B ? none : gphq_rotation_spec{inter, 0};
+    struct {
+        int64_t n, k;
+        const float *norm;
+        gphq_rotation_spec in, out;
+        int64_t base, sc, step, row0;
+    } spec[GPHQ_LAYER_PROJECTIONS] = {
+        {qd, h, input_norm_host, hidden, none, L.qkv, L.qkv_scale, 1, 0},          // q_proj
+        {kv, h, input_norm_host, hidden, none, L.qkv, L.qkv_scale, 1, qd},         // k_proj
+        {kv, h, input_norm_host, hidden, head, L.qkv, L.qkv_scale, 1, qd + kv},    // v_proj
+        {h, qd, nullptr, head, hidden, L.o, L.o_scale, 1, 0},                      // o_proj
+        {inter, h, post_norm_host, hidden, none, L.gu, L.gu_scale, 2, 0},          // gate_proj
+        {inter, h, post_norm_host, hidden, none, L.gu, L.gu_scale, 2, 1},          // up_proj
+        {h, inter, nullptr, down_in, hidden, L.d, L.d_scale, 1, 0},                // down_proj
+    };
+    for (int i = 0; i < GPHQ_LAYER_PROJECTIONS; ++i) {
+        gphq_prepare_job &j = jobs[i];
+        j = gphq_prepare_job{};
+        j.n = spec[i].n;
+        j.k = spec[i].k;
+        j.norm_host = spec[i].norm;
+        j.in_rot = spec[i].in;
+        j.out_rot = spec[i].out;
+        j.fmt = fmt;
+        j.dst_dev = dst_dev;
+        j.dst_bytes = dst_bytes;
+        j.base = spec[i].base;
+        j.sc = spec[i].sc;
+        j.step = spec[i].step;
+        j.row0 = spec[i].row0;
+        j.scale_mul = 1.0f;
+    }
+    return GPHQ_OK;
+}
+
+int64_t gphq_prepare_head_chunk_rows(const gphq_lm_config *cfg) {
+    // gpu_darwin.go:432-436: the head is read in chunks of max(inter, 4096) rows.
+    if (!cfg || cfg->intermediate <= 0) return GPHQ_ERR_DIMENSIONS;
+    return std::max<int64_t>(cfg->intermediate, 4096);
+}
+
+int gphq_prepare_head_job(const gphq_lm_config *cfg, int64_t row0, void *dst_dev, int64_t dst_bytes,
+                          gphq_prepare_job *job) {
+    // One head chunk (gpu_darwin.go:435): vocabulary rows row0.. of at most
+    // one chunk over hidden-rotated rows, Q8B whatever the layers' format.
+    if (!cfg || !job || row0 < 0 || row0 >= cfg->vocab) return GPHQ_ERR_DIMENSIONS;
+    int64_t rows = 0, sc = 0, bytes = 0;
+    GPHQ_TRY(gphq_lm_head_layout(cfg, &rows, &sc, &bytes));
+    const int64_t chunk = gphq_prepare_head_chunk_rows(cfg);
+    *job = gphq_prepare_job{};
+    job->n = std::min(chunk, cfg->vocab - row0);
+    job->k = cfg->hidden;
+    job->in_rot = gphq_rotation_spec{cfg->hidden, 0};
+    job->fmt = GPHQ_FMT_Q8B;
+    job->dst_dev = dst_dev;
+    job->dst_bytes = dst_bytes;
+    job->base = 0;
+    job->sc = sc;
+    job->step = 1;
+    job->row0 = row0;
+    job->scale_mul = 1.0f;
+    return GPHQ_OK;
+}
+
+int64_t gphq_prepare_lm_work_bytes(const gphq_lm_config *cfg) {
+    if (!cfg) return GPHQ_ERR_DIMENSIONS;
+    gphq_prepare_job jobs[GPHQ_LAYER_PROJECTIONS];
+    static const float one = 1.0f;  // placeholders: only the shapes are read
+    GPHQ_TRY(gphq_prepare_layer_jobs(cfg, &one, &one, nullptr, 0, jobs));
+    int64_t most = 0;
+    for (const gphq_prepare_job &j : jobs) {
+        const int64_t b = gphq_prepare_work_bytes(j.n, j.k);
+        if (b < 0) return b;
+        most = std::max(most, b);
+    }
+    const int64_t head = gphq_prepare_work_bytes(std::min(gphq_prepare_head_chunk_rows(cfg), cfg->vocab), cfg->hidden);
+    if (head < 0) return head;
+    return std::max(most, head);
+}
+
+int gphq_prepare_layer(const gphq_lm_config *cfg, const uint16_t *const *src_bf16_dev, const float *input_norm_host,
+                       const float *post_norm_host, void *dst_dev, int64_t dst_bytes, void *work_dev,
+                       int64_t work_bytes, void *stream) {
+    if (!src_bf16_dev) return GPHQ_ERR_DIMENSIONS;
+    gphq_prepare_job jobs[GPHQ_LAYER_PROJECTIONS];
+    GPHQ_TRY(gphq_prepare_layer_jobs(cfg, input_norm_host, post_norm_host, dst_dev, dst_bytes, jobs));
+    for (int i = 0; i < GPHQ_LAYER_PROJECTIONS; ++i) {
+        jobs[i].src_bf16_dev = src_bf16_dev[i];
+        GPHQ_TRY(gphq_prepare_projection(&jobs[i], work_dev, work_bytes, stream));
+    }
+    return GPHQ_OK;
+}
+
+int gphq_prepare_head(const gphq_lm_config *cfg, const uint16_t *src_bf16_dev, void *dst_dev, int64_t dst_bytes,
+                      void *work_dev, int64_t work_bytes, void *stream) {
+    if (!cfg || !src_bf16_dev) return GPHQ_ERR_DIMENSIONS;
+    const int64_t chunk = gphq_prepare_head_chunk_rows(cfg);
+    if (chunk < 0) return (int)chunk;
+    for (int64_t r = 0; r < cfg->vocab; r += chunk) {
+        gphq_prepare_job j;
+        GPHQ_TRY(gphq_prepare_head_job(cfg, r, dst_dev, dst_bytes, &j));
+        j.src_bf16_dev = src_bf16_dev + r * cfg->hidden;
+        GPHQ_TRY(gphq_prepare_projection(&j, work_dev, work_bytes, stream));
+    }
+    return GPHQ_OK;
+}
+
 }  // extern "C"

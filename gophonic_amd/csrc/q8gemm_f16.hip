@@ -17,6 +17,7 @@ int f16_act_pack_plain(const float *x, long stride, int rows, int K, _Float16 *a
 int f16_act_pack(const float *x, long stride, int rows, int K, int kt, int mode, int k0, int k1, _Float16 *act,
                  float *rowScale, float *rowInv, hipStream_t stream);
 int f16_pack_tiles(const uint16_t *src, uint16_t *dst, int rows, int K, int row0, int kt, hipStream_t stream);
+int f16_ref_panels_to_tiles(const uint16_t *ref, uint16_t *dst, int n, int K, int nt, int kt, hipStream_t stream);
 int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int kt, hipStream_t stream);
 int fill_zero_columns(float *dst, long stride, int rows, int c0, int c1, hipStream_t stream);
 int bf16_rows_to_f16(const uint16_t *src, int rows, int K, uint16_t *dst, float *rowScale, unsigned long long *rounded,
@@ -129,6 +130,43 @@ int gphq_q8gemm_new_weights_f16_buffer(int64_t k, int64_t n, void *data_dev, int
     w->scales = (float *)((char *)data_dev + w->code_bytes());
     *out = w;
     return GPHQ_OK;
+}
+
+int64_t gphq_q8gemm_reference_f16_bytes(int64_t k, int64_t n) {
+    // packed.go:78-93 WeightsF16Bytes: the reference's own layout, FP16
+    // panels [ceil(n/64)][ceil(k/2)][64][2] followed by n fp32 row scales.
+    if (k < 0 || n < 0 || k > INT32_MAX - 64 || n > INT32_MAX - 64) return GPHQ_ERR_DIMENSIONS;
+    return ceil_div(n, kOutputPanel) * ((k + 1) / 2) * 4 * kOutputPanel + n * 4;
+}
+
+int gphq_q8gemm_weights_f16_load_reference(gphq_weights *w, const void *ref_host, int64_t ref_len) {
+    // The bytes a reference NewWeightsF16Buffer + PackBF16 leave in the
+    // caller's storage (a wcache mapping, qwen3lm/weights.go:362-370; packed.go
+    // 95-175), copied from host memory and repacked on the device.
+    if (!w || !w->f16) return GPHQ_ERR_DIMENSIONS;
+    const int64_t size = gphq_q8gemm_reference_f16_bytes(w->k, w->n);
+    if (size < 0 || ref_len < size) return GPHQ_ERR_DIMENSIONS;
+    if (size == 0) return GPHQ_OK;
+    if (!ref_host) return GPHQ_ERR_DIMENSIONS;
+    const int64_t code_bytes = size - 4 * w->n;
+    const float *scales = (const float *)((const char *)ref_host + code_bytes);
+    for (int64_t r = 0; r < w->n; ++r) {
+        float s;
+        std::memcpy(&s, scales + r, 4);
+        if (!std::isfinite(s)) return GPHQ_ERR_NON_FINITE;
+    }
+    void *staging = nullptr;
+    GPHQ_TRY(hip_status(hipMalloc(&staging, (size_t)size)));
+    int st = hip_status(hipMemcpy(staging, ref_host, (size_t)size, hipMemcpyHostToDevice));
+    if (st == GPHQ_OK && code_bytes)
+        st = f16_ref_panels_to_tiles((const uint16_t *)staging, (uint16_t *)w->codes, (int)w->n, (int)w->k,
+                                     (int)w->nt, (int)w->kt, nullptr);
+    if (st == GPHQ_OK && w->n)
+        st = hip_status(hipMemcpyAsync(w->scales, (const char *)staging + code_bytes, (size_t)w->n * 4,
+                                       hipMemcpyDeviceToDevice, nullptr));
+    if (st == GPHQ_OK) st = hip_status(hipStreamSynchronize(nullptr));
+    (void)hipFree(staging);
+    return st;
 }
 
 void gphq_q8gemm_weights_free(gphq_weights *w) {

@@ -88,6 +88,8 @@ SIGNATURES = {
     "gphq_q8gemm_weights_f16_bytes": (_i64, [_i64, _i64]),
     "gphq_q8gemm_new_weights_f16_buffer": (ctypes.c_int, [_i64, _i64, _vp, _i64, _vpp]),
     "gphq_q8gemm_weights_free": (None, [_vp]),
+    "gphq_q8gemm_reference_f16_bytes": (_i64, [_i64, _i64]),
+    "gphq_q8gemm_weights_f16_load_reference": (ctypes.c_int, [_vp, _vp, _i64]),
     "gphq_q8gemm_weights_pack": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64]),
     "gphq_q8gemm_weights_pack_bf16": (ctypes.c_int, [_vp, _vp, _i64, _i64p]),
     "gphq_q8gemm_weights_pack_bf16_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64p]),
@@ -132,6 +134,12 @@ SIGNATURES = {
     "gphq_decode_batch_set_graph": (ctypes.c_int, [_vp, ctypes.c_int]),
     "gphq_prepare_work_bytes": (_i64, [_i64, _i64]),
     "gphq_prepare_projection": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "gphq_prepare_layer_jobs": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _vp]),
+    "gphq_prepare_head_chunk_rows": (_i64, [_vp]),
+    "gphq_prepare_head_job": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp]),
+    "gphq_prepare_lm_work_bytes": (_i64, [_vp]),
+    "gphq_prepare_layer": (ctypes.c_int, [_vp, _vpp, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "gphq_prepare_head": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "gphq_mm_split_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "gphq_prefill_new": (ctypes.c_int, [_vp, _i64, _vpp]),
     "gphq_prefill_free": (None, [_vp]),
@@ -392,6 +400,14 @@ class Weights:
         r = ctypes.c_int64()
         check(load().gphq_q8gemm_weights_pack_bf16(self.h, bp, b.size, ctypes.byref(r)))
         return r.value
+
+    def load_reference(self, ref_bytes):
+        """Loads FP16 weights from the reference's own packed buffer bytes
+        (panels [n/64][k/2][64][2] then n fp32 scales; a numpy uint8 array)."""
+        import numpy as np
+
+        b, bp = _host(np.asarray(ref_bytes).view(np.uint8).reshape(-1), np.uint8)
+        return check(load().gphq_q8gemm_weights_f16_load_reference(self.h, bp, b.size))
 
     def pack_bf16_rows(self, bf16, row0):
         import numpy as np
@@ -969,69 +985,61 @@ def _bf16_host_f32(bits):
     return (np.asarray(bits).view(np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(-1)
 
 
-def prepare_lm(geom_kwargs, fmt, tensors, device="cuda", prefix="model.", head_name="lm_head.weight"):
+LAYER_PROJECTIONS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                     "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+def prepare_layer_jobs(cfg, input_norm, post_norm, dst=None):
+    """gphq_prepare_layer_jobs: the seven PrepareJob of one layer (src unset)."""
+    import numpy as np
+
+    an, ap = _host(input_norm, np.float32)
+    mn, mp = _host(post_norm, np.float32)
+    jobs = (PrepareJob * 7)()
+    check(load().gphq_prepare_layer_jobs(ctypes.byref(cfg), ap, mp, None if dst is None else dst.data_ptr(),
+                                         0 if dst is None else dst.numel() * dst.element_size(), jobs))
+    return list(jobs), (an, mn)
+
+
+def prepare_lm(geom_kwargs, fmt, tensors, device="cuda", prefix="model.", head_name="lm_head.weight", stream=None):
     """prepareGPU (gpu_darwin.go:392-567) for a dense Qwen3 checkpoint, on the
-    device: every projection of every layer quantized into its layer buffer
-    (the placement of gphq_lm_layer_layout), the head into its own buffer
-    (Q8B, in chunks of max(inter, 4096) rows), and the model bound.
+    device, through the library's job list (gphq_prepare_layer /
+    gphq_prepare_head): every projection of every layer quantized into its
+    layer buffer (the placement of gphq_lm_layer_layout), the head into its
+    own buffer (Q8B, in chunks of max(inter, 4096) rows), and the model bound.
 
     tensors maps checkpoint names (model.layers.N.self_attn.q_proj.weight, ...,
     model.embed_tokens.weight, model.norm.weight, lm_head.weight) to BF16 bits:
     numpy uint16/int16 arrays or device int16 tensors. Returns an Lm.
-
-    The job list is the reference's: q/k/v over the input-normalized,
-    hidden-rotated rows (v's rows also rotated per head), o with the per-head
-    input rotation and the hidden output rotation, gate/up over the
-    post-attention-normalized rows interleaved with step 2, down with the
-    intermediate input rotation (none for Q8B) and the hidden output rotation,
-    and the head over hidden-rotated rows.
     """
     import torch
 
     cfg = lm_config(fmt=fmt, **geom_kwargs)
     desc, nbytes = lm_layer_layout(cfg)
-    h, qd, inter, hd = cfg.hidden, cfg.heads * cfg.head_dim, cfg.intermediate, cfg.head_dim
-    kv = cfg.kv_heads * hd
-    hidden_rot, head_rot = (h, 0), (0, hd)
-    down_in = (0, 0) if fmt == FMT_Q8B else (inter, 0)
+    h = cfg.hidden
     lm = Lm(cfg)
-    jobs_per_layer = []
+    work = torch.empty(load().gphq_prepare_lm_work_bytes(ctypes.byref(cfg)), dtype=torch.uint8, device=device)
     for i in range(cfg.layers):
         p = f"{prefix}layers.{i}."
         an = _bf16_host_f32(tensors[p + "input_layernorm.weight"])
         mn = _bf16_host_f32(tensors[p + "post_attention_layernorm.weight"])
-        jobs_per_layer.append([
-            # name, n, k, norm, in, out, base, sc, step, row0
-            (p + "self_attn.q_proj.weight", qd, h, an, hidden_rot, (0, 0), desc.qkv, desc.qkv_scale, 1, 0),
-            (p + "self_attn.k_proj.weight", kv, h, an, hidden_rot, (0, 0), desc.qkv, desc.qkv_scale, 1, qd),
-            (p + "self_attn.v_proj.weight", kv, h, an, hidden_rot, head_rot, desc.qkv, desc.qkv_scale, 1, qd + kv),
-            (p + "self_attn.o_proj.weight", h, qd, None, head_rot, hidden_rot, desc.o, desc.o_scale, 1, 0),
-            (p + "mlp.gate_proj.weight", inter, h, mn, hidden_rot, (0, 0), desc.gu, desc.gu_scale, 2, 0),
-            (p + "mlp.up_proj.weight", inter, h, mn, hidden_rot, (0, 0), desc.gu, desc.gu_scale, 2, 1),
-            (p + "mlp.down_proj.weight", h, inter, None, down_in, hidden_rot, desc.d, desc.d_scale, 1, 0),
-        ])
-    rows, head_sc, head_bytes = lm_head_layout(cfg)
-    chunk = max(inter, 4096)
-    wmax = max([prepare_work_bytes(j[1], j[2]) for js in jobs_per_layer for j in js] +
-               [prepare_work_bytes(min(chunk, cfg.vocab), h)])
-    work = torch.empty(wmax, dtype=torch.uint8, device=device)
-    for i, js in enumerate(jobs_per_layer):
+        jobs, (an, mn) = prepare_layer_jobs(cfg, an, mn)
+        srcs = [_bf16_device(tensors[p + name + ".weight"], (j.n, j.k), device)
+                for name, j in zip(LAYER_PROJECTIONS, jobs)]
+        arr = (ctypes.c_void_p * 7)(*[t.data_ptr() for t in srcs])
         buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        for name, n, k, norm, rin, rout, base, sc, step, row0 in js:
-            src = _bf16_device(tensors[name], (n, k), device)
-            prepare_projection(src, n, k, fmt, buf, base, sc, norm=norm, in_rot=rin, out_rot=rout, step=step,
-                               row0=row0, work=work)
-            del src
-        p = f"{prefix}layers.{i}."
+        check(load().gphq_prepare_layer(ctypes.byref(cfg), arr, an.ctypes.data, mn.ctypes.data, buf.data_ptr(),
+                                        nbytes, work.data_ptr(), work.numel(), stream_handle(stream)))
+        del srcs
         lm.bind_layer(i, buf, desc, _bf16_host_f32(tensors[p + "self_attn.q_norm.weight"]),
                       _bf16_host_f32(tensors[p + "self_attn.k_norm.weight"]))
     lm.bind_embed(_bf16_device(tensors[prefix + "embed_tokens.weight"], (cfg.vocab, h), device))
+    rows, head_sc, head_bytes = lm_head_layout(cfg)
     head_buf = torch.zeros(head_bytes, dtype=torch.uint8, device=device)
-    head_src = tensors[head_name]
-    for r in range(0, cfg.vocab, chunk):
-        n = min(r + chunk, cfg.vocab) - r
-        src = _bf16_device(head_src.reshape(cfg.vocab, h)[r:r + n], (n, h), device)
-        prepare_projection(src, n, h, FMT_Q8B, head_buf, 0, head_sc, in_rot=hidden_rot, row0=r, work=work)
+    head_src = _bf16_device(tensors[head_name], (cfg.vocab, h), device)
+    check(load().gphq_prepare_head(ctypes.byref(cfg), head_src.data_ptr(), head_buf.data_ptr(), head_bytes,
+                                   work.data_ptr(), work.numel(), stream_handle(stream)))
+    del head_src
     lm.bind_head(head_buf, _bf16_host_f32(tensors[prefix + "norm.weight"]))
     torch.cuda.synchronize()
     return lm

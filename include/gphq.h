@@ -293,6 +293,18 @@ int64_t gphq_q8gemm_weights_f16_bytes(int64_t k, int64_t n);
 /* NewWeightsF16Buffer (packed.go:95-121): binds caller-owned zeroed device
  * storage (4-byte aligned, at least weights_f16_bytes). */
 int gphq_q8gemm_new_weights_f16_buffer(int64_t k, int64_t n, void *data_dev, int64_t data_len, gphq_weights **out);
+/* packed.go:78-93 WeightsF16Bytes as the reference computes it: the size of
+ * the reference's own FP16 layout, panels [ceil(n/64)][ceil(k/2)][64][2] then
+ * n fp32 row scales (K = 3, N = 65: 1284 bytes). */
+int64_t gphq_q8gemm_reference_f16_bytes(int64_t k, int64_t n);
+/* Loads FP16 weights from a buffer in the reference's layout -- the bytes a
+ * reference NewWeightsF16Buffer + PackBF16[Rows] leave in caller storage,
+ * such as a wcache mapping (qwen3lm/weights.go:362-370, packed.go:95-175) --
+ * from host memory (ref_len >= gphq_q8gemm_reference_f16_bytes(k, n)) into F16
+ * weights w of the same k and n: one upload, then a device repack into this
+ * library's tile layout. A non-finite row scale gives GPHQ_ERR_NON_FINITE.
+ * One-time setup; synchronizes. */
+int gphq_q8gemm_weights_f16_load_reference(gphq_weights *w, const void *ref_host, int64_t ref_len);
 void gphq_q8gemm_weights_free(gphq_weights *w);
 /* (*Weights).Pack (packed.go:181-204): int8 row-major [n][k] + fp32 scales. */
 int gphq_q8gemm_weights_pack(gphq_weights *w, const int8_t *q_host, int64_t q_len, const float *scales_host,
@@ -535,6 +547,37 @@ typedef struct gphq_prepare_job {
 /* Scratch for gphq_prepare_projection: float32 rows plus tables (n*k*4 + ...). */
 int64_t gphq_prepare_work_bytes(int64_t n, int64_t k);
 int gphq_prepare_projection(const gphq_prepare_job *job, void *work_dev, int64_t work_bytes, void *stream);
+
+/* prepareGPU's job list for a dense Qwen3 model (gpu_darwin.go:392-437), so a
+ * loader (loadGPU, gpu_darwin.go:161-338) need not restate it. A layer's jobs,
+ * in the reference's order: q, k, v (input norm folded, hidden input
+ * rotation, v's rows also per-head rotated), o (per-head input, hidden output
+ * rotation), gate, up (post-attention norm folded, interleaved rows: step 2,
+ * row0 0 / 1), down (the intermediate input rotation except for Q8B, hidden
+ * output rotation), at the offsets of gphq_lm_layer_layout in one layer
+ * buffer, in cfg->fmt. gphq_prepare_layer_jobs fills jobs[7] (src_bf16_dev
+ * left NULL; the norms are float32 host arrays of hidden values, the
+ * checkpoint's BF16 widened); gphq_prepare_layer runs them from the seven
+ * BF16 projections src_bf16_dev[7] (device, [n][k] each: q_proj, k_proj,
+ * v_proj, o_proj, gate_proj, up_proj, down_proj). The head (lm_head, or the
+ * tied embedding) is read in chunks of gphq_prepare_head_chunk_rows rows
+ * (max(intermediate, 4096)) over hidden-rotated rows into the Q8B buffer of
+ * gphq_lm_head_layout: gphq_prepare_head_job describes the chunk starting at
+ * vocabulary row row0, gphq_prepare_head runs them all from src_bf16_dev
+ * [vocab][hidden]. gphq_prepare_lm_work_bytes is the scratch every job of the
+ * model fits in. Each run waits for its stream (one-time setup). */
+#define GPHQ_LAYER_PROJECTIONS 7
+int gphq_prepare_layer_jobs(const gphq_lm_config *cfg, const float *input_norm_host, const float *post_norm_host,
+                            void *dst_dev, int64_t dst_bytes, gphq_prepare_job *jobs);
+int64_t gphq_prepare_head_chunk_rows(const gphq_lm_config *cfg);
+int gphq_prepare_head_job(const gphq_lm_config *cfg, int64_t row0, void *dst_dev, int64_t dst_bytes,
+                          gphq_prepare_job *job);
+int64_t gphq_prepare_lm_work_bytes(const gphq_lm_config *cfg);
+int gphq_prepare_layer(const gphq_lm_config *cfg, const uint16_t *const *src_bf16_dev, const float *input_norm_host,
+                       const float *post_norm_host, void *dst_dev, int64_t dst_bytes, void *work_dev,
+                       int64_t work_bytes, void *stream);
+int gphq_prepare_head(const gphq_lm_config *cfg, const uint16_t *src_bf16_dev, void *dst_dev, int64_t dst_bytes,
+                      void *work_dev, int64_t work_bytes, void *stream);
 
 /* ---- qwen3lm batched pass (prefill) ----------------------------------------
  * Replaces the GPU path of Evaluator.HiddenLastExtendInto (evaluator.go:

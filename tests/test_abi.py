@@ -135,3 +135,53 @@ def test_gemv_vec_rejects_misaligned_vectors():
     assert lib.gphq_gemv_vec(gphq.FMT_Q8B, p, p, p, 66, p, 64, 2, 64, 64, p, big, None) == gphq.ERR_DIMENSIONS
     assert lib.gphq_gemv_vec(gphq.FMT_Q8B, p, p, ctypes.c_void_p(260), 64, p, 64, 2, 64, 64, p, big, None) == \
         gphq.ERR_DIMENSIONS
+
+
+@pytest.mark.parametrize("fmt", [gphq.FMT_Q8B, gphq.FMT_Q8, gphq.FMT_Q4])
+def test_prepare_layer_jobs_are_prepare_gpus_list(fmt):
+    # gpu_darwin.go:400-415: q, k, v, o, gate, up, down with their norms,
+    # rotations, destination rows and layer-buffer offsets (no device work).
+    import numpy as np
+
+    cfg = _lm_cfg(fmt=fmt)
+    L, _ = gphq.lm_layer_layout(cfg)
+    an, mn = np.full(4096, 2.0, np.float32), np.full(4096, 3.0, np.float32)
+    jobs, (a, m) = gphq.prepare_layer_jobs(cfg, an, mn)
+    h, qd, kv, inter, hd = 4096, 4096, 1024, 12288, 128
+    down_in = (0, 0) if fmt == gphq.FMT_Q8B else (inter, 0)
+    want = [  # n, k, norm, in, out, base, sc, step, row0
+        (qd, h, a, (h, 0), (0, 0), L.qkv, L.qkv_scale, 1, 0),
+        (kv, h, a, (h, 0), (0, 0), L.qkv, L.qkv_scale, 1, qd),
+        (kv, h, a, (h, 0), (0, hd), L.qkv, L.qkv_scale, 1, qd + kv),
+        (h, qd, None, (0, hd), (h, 0), L.o, L.o_scale, 1, 0),
+        (inter, h, m, (h, 0), (0, 0), L.gu, L.gu_scale, 2, 0),
+        (inter, h, m, (h, 0), (0, 0), L.gu, L.gu_scale, 2, 1),
+        (h, inter, None, down_in, (h, 0), L.d, L.d_scale, 1, 0),
+    ]
+    for j, (n, k, norm, rin, rout, base, sc, step, row0) in zip(jobs, want):
+        assert (j.n, j.k, j.base, j.sc, j.step, j.row0, j.fmt) == (n, k, base, sc, step, row0, fmt)
+        assert (j.in_rot.width, j.in_rot.tile) == rin and (j.out_rot.width, j.out_rot.tile) == rout
+        assert j.norm_host == (None if norm is None else norm.ctypes.data)
+        assert j.scale_mul == 1.0 and not j.src_bf16_dev
+
+
+def test_prepare_head_jobs_chunk_the_vocabulary():
+    # gpu_darwin.go:432-436: chunks of max(inter, 4096) rows, Q8B, hidden input rotation.
+    lib = gphq.load()
+    cfg = _lm_cfg(vocab=151936)
+    chunk = lib.gphq_prepare_head_chunk_rows(ctypes.byref(cfg))
+    assert chunk == 12288
+    rows, so, _ = gphq.lm_head_layout(cfg)
+    seen = 0
+    for r in range(0, 151936, chunk):
+        j = gphq.PrepareJob()
+        assert lib.gphq_prepare_head_job(ctypes.byref(cfg), r, None, 0, ctypes.byref(j)) == gphq.OK
+        assert (j.n, j.k, j.fmt, j.row0, j.step, j.base, j.sc) == (min(chunk, 151936 - r), 4096, gphq.FMT_Q8B, r,
+                                                                      1, 0, so)
+        assert (j.in_rot.width, j.out_rot.width, j.out_rot.tile) == (4096, 0, 0)
+        seen += j.n
+    assert seen == 151936
+    assert lib.gphq_prepare_head_job(ctypes.byref(cfg), 151936, None, 0, ctypes.byref(j)) == gphq.ERR_DIMENSIONS
+    need = lib.gphq_prepare_lm_work_bytes(ctypes.byref(cfg))
+    assert need == max(lib.gphq_prepare_work_bytes(n, k) for n, k in
+                       [(4096, 4096), (1024, 4096), (12288, 4096), (4096, 12288), (12288, 4096)])

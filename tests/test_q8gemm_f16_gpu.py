@@ -188,6 +188,46 @@ def test_pack_bf16_golden_buffer_and_borrowed_storage():
         gphq.Weights(3, 65, buffer=torch.zeros(short, dtype=torch.uint8, device="cuda"))
 
 
+def reference_buffer(h_rows, scales, k, n):
+    """The bytes of a reference NewWeightsF16Buffer after PackBF16: FP16 values
+    in the panel layout [n/64][k/2][64][2] (packed.go:233-239), then n fp32
+    row scales (packed.go:95-121)."""
+    panels = orc.pack_panels(np.ascontiguousarray(h_rows, np.uint16).reshape(-1), k, n)
+    return np.concatenate([panels.view(np.uint8), np.ascontiguousarray(scales, np.float32).view(np.uint8)])
+
+
+def test_load_reference_f16_buffer_bytes():
+    # A wcache-mapped buffer in the reference's own layout (weights.go:362-370)
+    # loads into device weights equal to packing the same BF16 rows here.
+    g = np.load(os.path.join(GOLDEN, "f16_buffer.npz"))
+    lib = gphq.load()
+    assert lib.gphq_q8gemm_reference_f16_bytes(3, 65) == 1284  # packed.go:78-93 for K = 3, N = 65
+    for k, n in [(3, 65), (32, 129)]:
+        ref = reference_buffer(g[f"h_{k}_{n}"], g[f"scales_{k}_{n}"], k, n)
+        assert ref.size == lib.gphq_q8gemm_reference_f16_bytes(k, n)
+        loaded = gphq.Weights(k, n, f16=True)
+        loaded.load_reference(ref)
+        packed = gphq.Weights(k, n, f16=True)
+        packed.pack_bf16(g[f"bf16_{k}_{n}"])
+        want = orc.f16_to_f32(g[f"h_{k}_{n}"]).reshape(n, k) * g[f"scales_{k}_{n}"][:, None]
+        assert np.array_equal(onehot_weights(loaded, k, n), want)
+        # Products through both are bit-identical.
+        rng = np.random.default_rng(k)
+        x = rng.standard_normal((5, k)).astype(np.float32)
+        outs = []
+        for w in (loaded, packed):
+            ws = gphq.Workspace(k, 5)
+            dst = fill(5 * n)
+            gphq.mul_into(dst, dev(x), 5, w, ws)
+            outs.append(host(dst).view(np.uint32))
+        assert np.array_equal(outs[0], outs[1])
+        with pytest.raises(gphq.GphqError, match="invalid dimensions"):
+            loaded.load_reference(ref[:-1])
+    bad = reference_buffer(g["h_3_65"], np.where(np.arange(65) == 7, np.inf, g["scales_3_65"]), 3, 65)
+    with pytest.raises(gphq.GphqError, match="non-finite"):
+        gphq.Weights(3, 65, f16=True).load_reference(bad)
+
+
 def test_pack_bf16_counts_rounding_and_rejects_non_finite():
     k, n = 32, 4
     v = np.zeros(k * n, np.float32)
