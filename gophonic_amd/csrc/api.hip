@@ -91,6 +91,20 @@ const char *gphq_error_string(int status) {
         return "qwen3: cannot reuse the rows at this anchor";
     case GPHQ_ERR_EMBED_ROWS:
         return "qwen3: embedding values do not fill one row per placeholder";
+    case GPHQ_ERR_IO:
+        return "gphq: file I/O failed";
+    case GPHQ_ERR_FORMAT:
+        return "safetensors: invalid file or index";
+    case GPHQ_ERR_TENSOR_MISSING:
+        return "safetensors: checkpoint is missing the tensor";
+    case GPHQ_ERR_TENSOR_SHAPE:
+        return "safetensors: tensor has another shape";
+    case GPHQ_ERR_TENSOR_DTYPE:
+        return "safetensors: tensor has another dtype or size";
+    case GPHQ_ERR_TENSOR_NON_FINITE:
+        return "safetensors: tensor has a non-finite value";
+    case GPHQ_ERR_READ_RANGE:
+        return "read outside the tensor";
     }
     return "gphq: unknown status";
 }

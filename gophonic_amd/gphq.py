@@ -46,6 +46,13 @@ ERR_SCRATCH_LIMIT = -30
 ERR_TAIL_SHAPE = -31
 ERR_REUSE = -32
 ERR_EMBED_ROWS = -33
+ERR_IO = -34
+ERR_FORMAT = -35
+ERR_TENSOR_MISSING = -36
+ERR_TENSOR_SHAPE = -37
+ERR_TENSOR_DTYPE = -38
+ERR_TENSOR_NON_FINITE = -39
+ERR_READ_RANGE = -40
 TAIL_MAX_ROWS = 256
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
@@ -58,6 +65,41 @@ _i64p = ctypes.POINTER(ctypes.c_int64)
 # name -> (restype, argtypes); every symbol include/gphq.h declares.
 SIGNATURES = {
     "gphq_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "gphq_error_detail": (ctypes.c_char_p, []),
+    "gphq_checkpoint_open": (ctypes.c_int, [ctypes.c_char_p, _vpp]),
+    "gphq_checkpoint_close": (None, [_vp]),
+    "gphq_checkpoint_has": (ctypes.c_int, [_vp, ctypes.c_char_p]),
+    "gphq_checkpoint_info": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _vp, _i64, _i64p]),
+    "gphq_checkpoint_lookup": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _i64, _vp]),
+    "gphq_checkpoint_read_bits": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _i64, _i64]),
+    "gphq_checkpoint_bf16": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _i64, _vp, _i64]),
+    "gphq_checkpoint_bf16_device": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _i64, _vp, _i64]),
+    "gphq_checkpoint_float32": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _i64, _vp, _i64]),
+    "gphq_checkpoint_map_bf16": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _i64, _vpp, _vpp]),
+    "gphq_mapping_free": (None, [_vp]),
+    "gphq_gptq_row_bytes": (ctypes.c_int, [ctypes.c_int, _i64, _i64p, _i64p]),
+    "gphq_gptq_fingerprint": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "gphq_gptq_path": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _i64]),
+    "gphq_gptq_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, _vp, _vpp]),
+    "gphq_gptq_close": (None, [_vp]),
+    "gphq_gptq_bits": (ctypes.c_int, [_vp]),
+    "gphq_gptq_projection": (ctypes.c_int, [_vp, ctypes.c_char_p, _i64p, _i64p]),
+    "gphq_gptq_place": (ctypes.c_int, [_vp, ctypes.c_char_p, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
+                                       ctypes.POINTER(ctypes.c_int)]),
+    "gphq_gptq_create": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, _vpp]),
+    "gphq_gptq_write": (ctypes.c_int, [_vp, _vp, _i64]),
+    "gphq_gptq_write_device": (ctypes.c_int, [_vp, _vp, _i64]),
+    "gphq_gptq_commit": (ctypes.c_int, [_vp]),
+    "gphq_gptq_abort": (None, [_vp]),
+    "gphq_wcache_round_up": (_i64, [_i64]),
+    "gphq_wcache_key": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, _vp, _i64, ctypes.c_char_p, _i64]),
+    "gphq_wcache_sha256": (ctypes.c_int, [_vp, _i64, _vp]),
+    "gphq_wcache_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, _i64, _vpp]),
+    "gphq_wcache_fresh": (ctypes.c_int, [_vp]),
+    "gphq_wcache_payload": (_vp, [_vp, _i64p]),
+    "gphq_wcache_done": (None, [_vp, _vp, _i64]),
+    "gphq_wcache_commit": (None, [_vp]),
+    "gphq_wcache_close": (ctypes.c_int, [_vp]),
     "gphq_last_hip_error": (ctypes.c_int, []),
     "gphq_version": (ctypes.c_char_p, []),
     "gphq_q8gemv_mul_into": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),

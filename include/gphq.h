@@ -97,9 +97,22 @@ extern "C" {
 #define GPHQ_ERR_REUSE (-32)
 /* evaluator.go:208-210 "qwen3: %d embedding values for %d placeholders of width %d" */
 #define GPHQ_ERR_EMBED_ROWS (-33)
+/* File formats (safetensors, GPTQ file, weight cache); gphq_error_detail()
+ * holds the reference's formatted message for each. */
+#define GPHQ_ERR_IO (-34)              /* open / read / write / rename failed */
+#define GPHQ_ERR_FORMAT (-35)          /* safetensors.go:85-127: bad header, index or offsets */
+#define GPHQ_ERR_TENSOR_MISSING (-36)  /* safetensors.go:145 "checkpoint is missing %s" */
+#define GPHQ_ERR_TENSOR_SHAPE (-37)    /* safetensors.go:151-156 "%s has shape %v, want %v" */
+#define GPHQ_ERR_TENSOR_DTYPE (-38)    /* safetensors.go:157-160, 171-173 wrong dtype or size */
+#define GPHQ_ERR_TENSOR_NON_FINITE (-39) /* safetensors.go:245-248 "%s has a non-finite value" */
+#define GPHQ_ERR_READ_RANGE (-40)      /* safetensors.go:206-208 "read outside the tensor" */
 
 /* The reference message for a status code ("" for GPHQ_OK). Static storage. */
 const char *gphq_error_string(int status);
+/* The calling thread's formatted message of its last file-format failure
+ * (tensor names, shapes), "" after a success. Valid until the thread's next
+ * file-format call. */
+const char *gphq_error_detail(void);
 /* The hipError_t of the most recent GPHQ_ERR_HIP on the calling thread. */
 int gphq_last_hip_error(void);
 /* Library version, "major.minor.patch". */
@@ -703,6 +716,104 @@ int64_t gphq_gptq_round_work_bytes(int64_t n, int64_t k);
  * stored + 8) and FP16 group scales (q4GroupScale) [n][k/32]. */
 int gphq_gptq_round(float *w_dev, int64_t n, int64_t k, const float *u_dev, const uint8_t *dead_dev, int bits,
                     void *codes_dev, void *scales_dev, void *work_dev, int64_t work_bytes, void *stream);
+
+/* ---- safetensors checkpoints (internal/safetensors/safetensors.go) --------
+ * Open reads the tensor index of dir: model.safetensors, or the shards of
+ * model.safetensors.index.json's weight_map (safetensors.go:39-82, header
+ * rules 85-127). Tensors are read on demand: Lookup checks the shape and the
+ * dtype's byte count (140-162); BF16 reads raw BF16 bits (165-176, host, or
+ * device through a host copy); ReadBits reads count 16-bit values from
+ * element offset (203-213); Float32 widens BF16 / F16 / F32 and rejects
+ * non-finite values (217-251); MapBF16 maps the bits read-only (178-200,
+ * released by gphq_mapping_free). dtype codes: */
+#define GPHQ_DTYPE_BF16 1
+#define GPHQ_DTYPE_F16 2
+#define GPHQ_DTYPE_F32 3
+typedef struct gphq_checkpoint gphq_checkpoint;
+typedef struct gphq_mapping gphq_mapping;
+int gphq_checkpoint_open(const char *dir, gphq_checkpoint **out);
+void gphq_checkpoint_close(gphq_checkpoint *c);
+int gphq_checkpoint_has(const gphq_checkpoint *c, const char *name);
+/* Tensor.DType (0 for another type) and Tensor.Shape (up to max_ndim dims). */
+int gphq_checkpoint_info(const gphq_checkpoint *c, const char *name, int32_t *dtype, int64_t *shape, int64_t max_ndim,
+                         int64_t *ndim);
+int gphq_checkpoint_lookup(const gphq_checkpoint *c, const char *name, const int64_t *shape, int64_t ndim,
+                           int32_t *dtype);
+int gphq_checkpoint_read_bits(const gphq_checkpoint *c, const char *name, uint16_t *dst, int64_t count,
+                              int64_t offset);
+int gphq_checkpoint_bf16(const gphq_checkpoint *c, const char *name, const int64_t *shape, int64_t ndim, uint16_t *dst,
+                         int64_t dst_len);
+int gphq_checkpoint_bf16_device(const gphq_checkpoint *c, const char *name, const int64_t *shape, int64_t ndim,
+                                uint16_t *dst_dev, int64_t dst_len);
+int gphq_checkpoint_float32(const gphq_checkpoint *c, const char *name, const int64_t *shape, int64_t ndim, float *dst,
+                            int64_t dst_len);
+int gphq_checkpoint_map_bf16(const gphq_checkpoint *c, const char *name, const int64_t *shape, int64_t ndim,
+                             gphq_mapping **out, const uint16_t **bits);
+void gphq_mapping_free(gphq_mapping *m);
+
+/* ---- GPTQ weight file "GPHQ0001" (qwen3lm/gptq.go:36-196, 227-270) --------
+ * The file cmd/qwen3-gptq writes next to the checkpoint as
+ * gophonic-gptq-<format>.bin ("gpu": 8 bits, GPHQ_FMT_Q8 rows; "gpu-q4": 4
+ * bits, GPHQ_FMT_Q4 rows): a 24-byte header (magic, bits, fingerprint, u64
+ * LE), then per layer and projection (q, k, v, o, gate, up, down) all rows'
+ * codes, then all rows' scales (gptqRowBytes: 8 bits k and 4 bytes a row, 4
+ * bits k/2 and 2*(k/32)). The fingerprint is snapshotFingerprint: FNV-1a 64
+ * over "name size mtime_ns\n" of the sorted *.safetensors and config.json
+ * files of dir. gphq_gptq_open leaves *out NULL (status GPHQ_OK) when there is
+ * no file, or it holds other bits, another fingerprint or another size.
+ * gphq_gptq_projection gives a tensor's offsets from its name after the
+ * decoder prefix ("layers.3.mlp.up_proj.weight"; 1 if held, else 0);
+ * gphq_gptq_place copies one into a device layer buffer, source row r at row
+ * row0 + r*step of the codes at byte base and of the scales at sc (*placed 0
+ * when not held). The writer writes the header to <file>.tmp, appends
+ * projections in file order (host bytes, or device bytes such as
+ * gphq_gptq_round's), and renames on commit. */
+typedef struct gphq_gptq_file gphq_gptq_file;
+typedef struct gphq_gptq_writer gphq_gptq_writer;
+int gphq_gptq_row_bytes(int bits, int64_t k, int64_t *codes, int64_t *scales);
+int gphq_gptq_fingerprint(const char *dir, uint64_t *out);
+int gphq_gptq_path(const char *dir, const char *format, char *out, int64_t out_len);
+int gphq_gptq_open(const char *dir, const char *format, const gphq_lm_config *cfg, gphq_gptq_file **out);
+void gphq_gptq_close(gphq_gptq_file *g);
+int gphq_gptq_bits(const gphq_gptq_file *g);
+int gphq_gptq_projection(const gphq_gptq_file *g, const char *name, int64_t *codes_off, int64_t *scales_off);
+int gphq_gptq_place(const gphq_gptq_file *g, const char *name, int64_t n, int64_t k, void *buf_dev, int64_t buf_bytes,
+                    int64_t base, int64_t sc, int64_t row0, int64_t step, int *placed);
+int gphq_gptq_create(const char *dir, const char *format, gphq_gptq_writer **out);
+int gphq_gptq_write(gphq_gptq_writer *w, const void *data, int64_t len);
+int gphq_gptq_write_device(gphq_gptq_writer *w, const void *data_dev, int64_t len);
+int gphq_gptq_commit(gphq_gptq_writer *w);
+void gphq_gptq_abort(gphq_gptq_writer *w);
+
+/* ---- prepared-weight cache "GPHWCACH" (internal/wcache/wcache.go) --------
+ * Key (wcache.go:59-86): "<sanitized dir name>-<sha256(abs dir)[:4] hex>.
+ * <sanitized kind>.<sha256(parts NUL-terminated, then name NUL size NUL
+ * mtime_ns NUL of each regular file of dir in name order)[:12] hex>".
+ * Open (109-140) maps the complete entry <cache_dir>/<key>.bin read-only
+ * (fresh 0), or returns a zeroed writable fresh entry (a temporary file under
+ * an advisory lock on <cache_dir>/<key up to its last '.'>.lock, so one
+ * process prepares while others wait; anonymous memory when cache_dir is ""
+ * or cannot be written; cache_dir NULL: $GOPHONIC_CACHE, else
+ * $XDG_CACHE_HOME or ~/.cache, /gophonic). The file is a GPHQ_WCACHE_ALIGN
+ * header (magic, total size, complete flag) and the payload rounded up to
+ * GPHQ_WCACHE_ALIGN. Commit (207-258) syncs the payload, then the complete
+ * flag, renames the entry into place, removes the entries it replaces (same
+ * name and kind) and temporaries over an hour old, and maps it again
+ * read-only (take payload pointers after Commit). Done (198-205) starts
+ * writing a filled region back. Close discards a fresh entry. Layout's Take
+ * rounds each region up with gphq_wcache_round_up. */
+#define GPHQ_WCACHE_ALIGN (16 << 10)
+typedef struct gphq_wcache_file gphq_wcache_file;
+int64_t gphq_wcache_round_up(int64_t n);
+int gphq_wcache_key(const char *dir, const char *kind, const char *const *parts, int64_t nparts, char *out,
+                    int64_t out_len);
+int gphq_wcache_sha256(const void *data, int64_t len, uint8_t *out32);
+int gphq_wcache_open(const char *cache_dir, const char *key, int64_t size, gphq_wcache_file **out);
+int gphq_wcache_fresh(const gphq_wcache_file *f);
+void *gphq_wcache_payload(gphq_wcache_file *f, int64_t *len);
+void gphq_wcache_done(gphq_wcache_file *f, const void *region, int64_t len);
+void gphq_wcache_commit(gphq_wcache_file *f);
+int gphq_wcache_close(gphq_wcache_file *f);
 
 #ifdef __cplusplus
 }
