@@ -31,7 +31,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--rotations", type=int, default=32)
     ap.add_argument("--mode", choices=["batch", "graph", "eager"], default="batch")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="bound of the config-1 CPU baseline sample (each other CPU line takes half)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true", help="skip the config-2 int8 GEMM lines")
     ap.add_argument("--no-gptq", action="store_true", help="skip the config-5 GPTQ int4 lines")
@@ -497,11 +498,19 @@ def prefill_config(torch, gphq, lm, geom, tokens, reps, label):
     }
 
 
+FORMAT_DESC = {
+    "q8b": "Q8B: int8 codes with one FP16 scale per 32-value block (the reference's gpu-q8 format), Q8B head",
+    "q8b_f32": "Q8B_F32: int8 codes with one fp32 scale per 32-value block (BASELINE config 1's scales), Q8B head",
+    "q8": "Q8: int8 codes with one fp32 scale per row (the reference's gpu format), Q8B head",
+    "q4": "Q4: 4-bit codes with one FP16 scale per 32-value block (the reference's gpu-q4 format), Q8B head",
+}
+
+
 def decode_benchmarks(args, torch, gphq):
     fmt = {"q8b": gphq.FMT_Q8B, "q8b_f32": gphq.FMT_Q8B_F32, "q8": gphq.FMT_Q8, "q4": gphq.FMT_Q4}[args.decode_fmt]
     graph = not args.decode_eager
     want = set(args.decode_configs.split(","))
-    res = {"fmt": args.decode_fmt}
+    res = {"fmt": args.decode_fmt, "weights": FORMAT_DESC[args.decode_fmt]}
     if "3" in want:
         lm, wb = decode_model(torch, gphq, QWEN3_06B, fmt, 3)
         res["config3"] = decode_config(torch, gphq, lm, wb, QWEN3_06B, 1, 1024, 256, 16, graph,
@@ -521,6 +530,15 @@ def decode_benchmarks(args, torch, gphq):
                                                "config 4b: Qwen3-8B-shaped decode at context 4096, 16 lanes")
         del lm
         torch.cuda.empty_cache()
+    if "4b1" in want and fmt != gphq.FMT_Q8B_F32:
+        # The same line with fp32 block scales (config 1's scale format, 9.72 GB a step).
+        lm, wb = decode_model(torch, gphq, QWEN3_8B, gphq.FMT_Q8B_F32, 4)
+        line = decode_config(torch, gphq, lm, wb, QWEN3_8B, 1, 4096, 64, 8, graph,
+                             "config 4b: Qwen3-8B-shaped decode at context 4096, 1 lane, fp32 block scales")
+        line["weights"] = FORMAT_DESC["q8b_f32"]
+        res["config4b_1_q8b_f32"] = line
+        del lm
+        torch.cuda.empty_cache()
     return res
 
 
@@ -538,30 +556,32 @@ def measured_traffic(kernel):
 
 def cpu_baseline(seconds):
     """The reference's amd64 q8gemv path (scalarMulInto, single thread),
-    restated in C (oracle), on the config-1 shape with per-row scales."""
-    from oracle import oracle as orc
+    restated in C (oracle), on the config-1 shape with per-row scales; with
+    the host's core count and CPU model."""
+    from oracle import cpu_baseline as cb
 
-    K = N = 4096
-    rng = np.random.default_rng(1)
-    x = rng.standard_normal(K).astype(np.float32)
-    q = rng.integers(-127, 128, N * K).astype(np.int8)
-    s = (np.abs(rng.standard_normal(N)) * 0.01).astype(np.float32)
-    orc.q8gemv_mul_into(x, q, s, K, N)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        orc.q8gemv_mul_into(x, q, s, K, N)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    unit = N * K + N * 4 + K * 4 + N * 4
+    out = cb.config1(seconds)
+    out.update(cb.host_info())
+    return out
+
+
+def cpu_baselines(seconds):
+    """The reference's CPU paths for configs 2, 3 and 4b (C restatements of
+    its amd64 code: scalar int8 panels split across T workers), at T = 1 and
+    T = min(cores, 16) (the reference's default worker cap)."""
+    from oracle import cpu_baseline as cb
+
+    T = cb.max_threads()
+    ts = [1, T] if T > 1 else [1]
+    q06 = dict(QWEN3_06B, head_dim=128)
+    q8 = dict(QWEN3_8B, head_dim=128)
     return {
-        "value": unit * reps / el / 1e9,
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{reps} x q8gemv.scalarMulInto 4096x4096 (per-row fp32 scales, the reference's amd64 path), "
-        f"C restatement -O2 -ffp-contract=off, 1 thread, {el:.1f} s",
+        "host": cb.host_info(),
+        "config2_int8_tile": [cb.config2(seconds, t) for t in ts],
+        "config3_decode": cb.decode(q06, 1024, seconds, ts),
+        "config4b_decode": cb.decode(q8, 4096, seconds, [T], layers_run=2),
+        "path": "the reference's CPU int8 path (WorkspaceI8 per-row activation quantization, scalarMulPanelsI8 "
+        "over 64-column panels per worker, fp32 attention): C restatement, -O2 -ffp-contract=off",
     }
 
 
@@ -585,6 +605,7 @@ def main():
     gptq = None if args.no_gptq else gptq_config5(args, torch, gphq)
     decode = None if args.no_decode else decode_benchmarks(args, torch, gphq)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    cpus = None if args.no_cpu else cpu_baselines(args.cpu_seconds / 2)
     # The persistent GEMV's template shape for config 1 (gemv.hip persistent_shape):
     # <format, K steps per wave, rows per group, K slices, waves per block, GEMVs per launch>.
     kernel = "gemvp_kernel<Q8B_F32,2,4,2,4,32>" if args.mode == "batch" else "gemvp_kernel<Q8B_F32,2,4,2,8,1>"
@@ -618,11 +639,15 @@ def main():
             "unit": "GB/s",
             "frac": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": None if traffic is None else
+            "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this launch, copy-kernel calibrated "
+            "(profiles/gemvp_config1_traffic.md)",
             "kernel": kernel,
             "per_launch_us": round(r["per_launch_us"], 3),
             "bytes_per_launch": r["bytes_per_launch"],
         },
         "cpu_baseline": cpu,
+        "cpu_baselines": cpus,
         "single_launch": None if single is None else {
             "gbs": round(single["achieved_gbs"], 2),
             "frac": round(single["achieved_gbs"] / HBM_PEAK_GBS, 4),
@@ -634,6 +659,7 @@ def main():
         "gemm_config2_block32_int8": gemm_b32i8,
         "gptq_config5": gptq,
         "decode_ms_per_token": (decode or {}).get("config4b_1", {}).get("ms_per_step"),
+        "decode_weights": (decode or {}).get("weights"),
         "prefill_4096_ms": (decode or {}).get("config4a", {}).get("ms"),
         "decode": decode,
         "check": {"rel_l2_vs_float64": r["rel_l2"]},

@@ -14,6 +14,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define OUTPUT_PANEL 64 /* q8gemm/packed.go:17 */
@@ -780,4 +781,219 @@ void orc_prepare_projection(const uint16_t *bf16, int64_t n, int64_t k, const fl
             }
         }
     }
+}
+
+/* ------------------------------------------------------------------ */
+/* CPU decode step for the CPU baseline (bench.py cpu_baseline only; no
+ * parity claim rests on it): one token of a dense Qwen3 through the
+ * reference's CPU int8 path (qwen3lm/ops.go:96-214 with WeightsInt8): per
+ * projection input, RMSNorm (rmsNorm32), the input rotation of int8
+ * projections (ops.go:110-122), per-row int8 quantization (int8.go:106-168)
+ * and scalarMulPanelsI8 (int8.go:200-211) split over 64-column panels across
+ * T workers (ops.go:153-214); head RMSNorm + RoPE, softmax attention over the
+ * fp32 K/V cache, SwiGLU, residual adds; final norm and the int8 head. The
+ * workers meet at a barrier between stages, as the reference's pool does. */
+
+typedef struct {
+    int64_t hidden, heads, kv_heads, head_dim, inter, vocab, layers, cap;
+    float eps;
+} orc_lm_geom;
+
+typedef struct {
+    const int8_t *w[7];      /* q, k, v, o, gate, up, down: [n][k] */
+    const float *s[7];       /* per-row scales */
+    const float *attn_norm, *mlp_norm, *q_norm, *k_norm;
+} orc_lm_layer_i8;
+
+typedef struct {
+    const orc_lm_geom *g;
+    const orc_lm_layer_i8 *L;
+    float *kc, *vc;          /* [layers][cap][kvd] */
+    const float *cosv, *sinv; /* [head_dim/2] at this position */
+    const float *final_norm;
+    const int8_t *head;
+    const float *head_s;
+    float *h, *x, *qkv, *ctx, *tmp, *act, *logits, *scores;
+    int8_t *qa;
+    float rs;
+    int pos, threads;
+    pthread_barrier_t bar;
+} lm_step_ctx;
+
+static void rms_norm32(float *out, const float *x, const float *w, int64_t n, float eps) {
+    /* kernels_scalar.go sumSquares in float64, then float32 scaling (ops.go:251-254). */
+    double ss = 0;
+    for (int64_t i = 0; i < n; i++) ss += (double)x[i] * x[i];
+    const float inv = (float)(1.0 / sqrt(ss / (double)n + eps));
+    for (int64_t i = 0; i < n; i++) out[i] = x[i] * inv * (w ? w[i] : 1.0f);
+}
+
+static void fwht_blocks(float *v, int64_t n) {
+    int64_t block = 1;
+    while (block < 4096 && n % (2 * block) == 0) block *= 2;
+    const float scale = (float)(1.0 / sqrt((double)block));
+    for (int64_t b = 0; b < n; b += block) {
+        for (int64_t i = 0; i < block; i++) v[b + i] *= scale;
+        orc_fwht(v + b, block);
+    }
+}
+
+static void quantize_row(lm_step_ctx *c, const float *x, int64_t k) {
+    float s, inv;
+    orc_i8_row_scale(orc_max_abs(x, k), &s, &inv);
+    c->rs = s;
+    for (int64_t i = 0; i < k; i++) c->qa[i] = orc_i8_quantize(x[i] * inv);
+}
+
+/* This worker's share of panels of an n x k int8 projection of c->qa. */
+static void project_share(lm_step_ctx *c, int t, const int8_t *w, const float *s, int64_t k, int64_t n, float *y) {
+    const int64_t panels = (n + OUTPUT_PANEL - 1) / OUTPUT_PANEL;
+    const int64_t p0 = panels * t / c->threads, p1 = panels * (t + 1) / c->threads;
+    orc_i8_mul_panels(y, n, c->qa, &c->rs, 1, w, s, k, n, p0, p1);
+}
+
+typedef struct {
+    lm_step_ctx *c;
+    int t;
+} lm_worker;
+
+static void *lm_step_worker(void *arg) {
+    lm_step_ctx *c = ((lm_worker *)arg)->c;
+    const int t = ((lm_worker *)arg)->t;
+    const orc_lm_geom *g = c->g;
+    const int64_t H = g->hidden, hd = g->head_dim, qd = g->heads * hd, kvd = g->kv_heads * hd, I = g->inter;
+    const int64_t grp = g->heads / g->kv_heads, n = c->pos + 1;
+    for (int64_t l = 0; l < g->layers; l++) {
+        const orc_lm_layer_i8 *L = &c->L[l];
+        float *kc = c->kc + l * g->cap * kvd, *vc = c->vc + l * g->cap * kvd;
+        if (t == 0) {
+            rms_norm32(c->x, c->h, L->attn_norm, H, g->eps);
+            fwht_blocks(c->x, H);
+            quantize_row(c, c->x, H);
+        }
+        pthread_barrier_wait(&c->bar);
+        project_share(c, t, L->w[0], L->s[0], H, qd, c->qkv);
+        project_share(c, t, L->w[1], L->s[1], H, kvd, c->qkv + qd);
+        project_share(c, t, L->w[2], L->s[2], H, kvd, c->qkv + qd + kvd);
+        pthread_barrier_wait(&c->bar);
+        /* K/V append, then attention per query head (heads split over workers). */
+        if (t == 0) {
+            for (int64_t kh = 0; kh < g->kv_heads; kh++) {
+                float *kr = c->qkv + qd + kh * hd;
+                rms_norm32(kr, kr, L->k_norm, hd, g->eps);
+                for (int64_t d = 0; d < hd / 2; d++) {
+                    const float a = kr[d], b = kr[d + hd / 2];
+                    kr[d] = a * c->cosv[d] - b * c->sinv[d];
+                    kr[d + hd / 2] = b * c->cosv[d] + a * c->sinv[d];
+                }
+                memcpy(kc + c->pos * kvd + kh * hd, kr, hd * 4);
+                memcpy(vc + c->pos * kvd + kh * hd, c->qkv + qd + kvd + kh * hd, hd * 4);
+            }
+        }
+        pthread_barrier_wait(&c->bar);
+        for (int64_t qh = t; qh < g->heads; qh += c->threads) {
+            float *q = c->qkv + qh * hd;
+            rms_norm32(q, q, L->q_norm, hd, g->eps);
+            for (int64_t d = 0; d < hd / 2; d++) {
+                const float a = q[d], b = q[d + hd / 2];
+                q[d] = a * c->cosv[d] - b * c->sinv[d];
+                q[d + hd / 2] = b * c->cosv[d] + a * c->sinv[d];
+            }
+            const int64_t kh = qh / grp;
+            float *sc = c->scores + t * g->cap;
+            float mx = -INFINITY;
+            const float scale = (float)(1.0 / sqrt((double)hd));
+            for (int64_t j = 0; j < n; j++) {
+                float s = 0;
+                for (int64_t d = 0; d < hd; d++) s += q[d] * kc[j * kvd + kh * hd + d];
+                sc[j] = s * scale;
+                mx = sc[j] > mx ? sc[j] : mx;
+            }
+            float sum = 0;
+            for (int64_t j = 0; j < n; j++) sum += (sc[j] = expf(sc[j] - mx));
+            float *o = c->ctx + qh * hd;
+            for (int64_t d = 0; d < hd; d++) o[d] = 0;
+            for (int64_t j = 0; j < n; j++) {
+                const float p = sc[j] / sum;
+                for (int64_t d = 0; d < hd; d++) o[d] += p * vc[j * kvd + kh * hd + d];
+            }
+        }
+        pthread_barrier_wait(&c->bar);
+        if (t == 0) {
+            memcpy(c->x, c->ctx, qd * 4);
+            for (int64_t b = 0; b < qd; b += hd) fwht_blocks(c->x + b, hd);
+            quantize_row(c, c->x, qd);
+        }
+        pthread_barrier_wait(&c->bar);
+        project_share(c, t, L->w[3], L->s[3], qd, H, c->tmp);
+        pthread_barrier_wait(&c->bar);
+        if (t == 0) {
+            for (int64_t i = 0; i < H; i++) c->h[i] += c->tmp[i];
+            rms_norm32(c->x, c->h, L->mlp_norm, H, g->eps);
+            fwht_blocks(c->x, H);
+            quantize_row(c, c->x, H);
+        }
+        pthread_barrier_wait(&c->bar);
+        project_share(c, t, L->w[4], L->s[4], H, I, c->act);
+        project_share(c, t, L->w[5], L->s[5], H, I, c->act + I);
+        pthread_barrier_wait(&c->bar);
+        if (t == 0) {
+            for (int64_t i = 0; i < I; i++) {
+                const float gt = c->act[i], up = c->act[I + i];
+                c->act[i] = gt / (1.0f + expf(-gt)) * up;
+            }
+            fwht_blocks(c->act, I);
+            quantize_row(c, c->act, I);
+        }
+        pthread_barrier_wait(&c->bar);
+        project_share(c, t, L->w[6], L->s[6], I, H, c->tmp);
+        pthread_barrier_wait(&c->bar);
+        if (t == 0)
+            for (int64_t i = 0; i < H; i++) c->h[i] += c->tmp[i];
+    }
+    if (t == 0) {
+        rms_norm32(c->x, c->h, c->final_norm, H, g->eps);
+        fwht_blocks(c->x, H);
+        quantize_row(c, c->x, H);
+    }
+    pthread_barrier_wait(&c->bar);
+    if (c->head) project_share(c, t, c->head, c->head_s, H, g->vocab, c->logits);
+    pthread_barrier_wait(&c->bar);
+    return 0;
+}
+
+/* One decode step at position pos (the K/V cache holds rows 0..pos-1):
+ * h [hidden] is the embedded token on entry and the residual on return;
+ * logits [vocab]. head may be NULL (no head product). */
+void orc_lm_step_i8(const orc_lm_geom *g, const orc_lm_layer_i8 *layers, float *kc, float *vc, int pos,
+                    const float *cosv, const float *sinv, const float *final_norm, const int8_t *head,
+                    const float *head_s, float *h, float *logits, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    const int64_t H = g->hidden, qd = g->heads * g->head_dim, kvd = g->kv_heads * g->head_dim, I = g->inter;
+    const int64_t big = H > qd ? (H > 2 * I ? H : 2 * I) : (qd > 2 * I ? qd : 2 * I);
+    lm_step_ctx c;
+    memset(&c, 0, sizeof c);
+    c.g = g, c.L = layers, c.kc = kc, c.vc = vc, c.cosv = cosv, c.sinv = sinv, c.final_norm = final_norm;
+    c.head = head, c.head_s = head_s, c.h = h, c.logits = logits, c.pos = pos, c.threads = threads;
+    float *mem = (float *)calloc((size_t)(big * 3 + qd + 2 * kvd + qd + (int64_t)threads * g->cap), sizeof(float));
+    c.x = mem;
+    c.tmp = c.x + big;
+    c.act = c.tmp + big;
+    c.qkv = c.act + big;
+    c.ctx = c.qkv + qd + 2 * kvd;
+    c.scores = c.ctx + qd;
+    c.qa = (int8_t *)malloc((size_t)big);
+    pthread_barrier_init(&c.bar, 0, (unsigned)threads);
+    pthread_t tid[64];
+    lm_worker w[64];
+    for (int t = 0; t < threads; t++) {
+        w[t] = (lm_worker){&c, t};
+        if (t) pthread_create(&tid[t], 0, lm_step_worker, &w[t]);
+    }
+    lm_step_worker(&w[0]);
+    for (int t = 1; t < threads; t++) pthread_join(tid[t], 0);
+    pthread_barrier_destroy(&c.bar);
+    free(c.qa);
+    free(mem);
 }
