@@ -57,23 +57,47 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (a + b) + (c + d);
 }
 
-// In-place unnormalized Walsh-Hadamard transform of each `block` run of
-// v[0..n) in LDS, stage h = 1, 2, 4, ...: the butterfly network of
-// qwen3lm/hadamard.go:62-78 (each stage's butterflies are independent, so the
-// fp32 result equals the sequential network's bit for bit). All threads of
-// the block take part; ends with a barrier.
-__device__ inline void lds_fwht(float *v, int n, int block) {
-    const int halfBlock = block >> 1;
-    for (int h = 1; h < block; h <<= 1) {
-        for (int idx = threadIdx.x; idx < (n >> 1); idx += blockDim.x) {
-            const int b = idx / halfBlock, i = idx - b * halfBlock;
-            const int j = b * block + (i / h) * 2 * h + (i % h);
-            const float a = v[j], c = v[j + h];
-            v[j] = a + c;
-            v[j + h] = a - c;
-        }
-        __syncthreads();
+// One round of lds_fwht: the R = 2^r stages h = 2^s .. 2^(s+r-1) at once.
+// Each item owns the R values whose index differs only in bits s..s+r-1
+// (base = idx with r zero bits inserted at bit s), runs the r stages on them
+// in registers, stage by stage in the network's order, and stores them back.
+template <int R>
+__device__ __forceinline__ void fwht_round(float *v, int n, int s) {
+    constexpr int r = R == 8 ? 3 : R == 4 ? 2 : 1;
+    const int h = 1 << s;
+    for (int idx = threadIdx.x; idx < (n >> r); idx += blockDim.x) {
+        const int base = ((idx >> s) << (s + r)) | (idx & (h - 1));
+        float a[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) a[j] = v[base + j * h];
+#pragma unroll
+        for (int m = 1; m < R; m <<= 1)
+#pragma unroll
+            for (int j = 0; j < R; ++j)
+                if (!(j & m)) {
+                    const float x = a[j], y = a[j + m];
+                    a[j] = x + y;
+                    a[j + m] = x - y;
+                }
+#pragma unroll
+        for (int j = 0; j < R; ++j) v[base + j * h] = a[j];
     }
+    __syncthreads();
+}
+
+// In-place unnormalized Walsh-Hadamard transform of each `block` run of
+// v[0..n) in LDS (block a power of two dividing n), stages h = 1, 2, 4, ...:
+// the butterfly network of qwen3lm/hadamard.go:62-78. Every value goes
+// through the same additions in the same order as in the sequential network,
+// so the fp32 result equals it bit for bit; three stages share one pass over
+// LDS. All threads of the block take part; the caller has made v visible
+// (barrier) before the call, and the call ends with a barrier.
+__device__ inline void lds_fwht(float *v, int n, int block) {
+    const int lb = __builtin_ctz((unsigned)block);
+    int s = 0;
+    for (; s + 3 <= lb; s += 3) fwht_round<8>(v, n, s);
+    if (lb - s == 2) fwht_round<4>(v, n, s);
+    if (lb - s == 1) fwht_round<2>(v, n, s);
 }
 
 // qwen3lm/hadamard.go:24-47 newRotation(k): fills k signs (+-1) and returns

@@ -168,7 +168,7 @@ __global__ __launch_bounds__(1024) void lm_embed_kernel(const uint16_t *__restri
 
 // The online Hadamard of down's input (gpu.metal:339-367 rotate): grid
 // (n/block, lanes); x[lane][b*block ..] = H . (signs*scale . x).
-__global__ __launch_bounds__(256) void lm_rotate_kernel(float *__restrict__ x, int stride,
+__global__ __launch_bounds__(512) void lm_rotate_kernel(float *__restrict__ x, int stride,
                                                         const float *__restrict__ signs, int block) {
     extern __shared__ float v[];
     float *base = x + (size_t)blockIdx.y * stride + (size_t)blockIdx.x * block;
@@ -258,8 +258,9 @@ __device__ __forceinline__ float rescale(float m, float mn) { return m == -INFIN
 // so the norms are computed while the keys are in flight; each iteration
 // issues the next iteration's loads before its arithmetic. The new key
 // (position pos, the last one) is taken from LDS by the block that holds it,
-// after its cached keys.
-template <int GROUP, int KPI>
+// after its cached keys. Keys stream through a ring of NB register buffers
+// of KPI keys each: while one buffer is consumed the next NB-1 are in flight.
+template <int GROUP, int KPI, int NB>
 __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     constexpr int NI = (GROUP + 4) / 4;  // norm items per wavefront, at most
     __shared__ float qs[GROUP][kHeadDim];
@@ -302,17 +303,16 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     }
 
     // Keys of step `it`: rows past the block's cached keys (jc, once the
-    // position is known) load row j0 instead, or, for step 0, whose loads are
-    // issued before the position arrives, the row clamped to the capacity.
-    float kr[KPI][8], vr[KPI][8];
-    bool valid[KPI];
+    // position is known; the capacity before) load row j0 instead.
+    float kb[NB][KPI][8], vb[NB][KPI][8];
+    bool okb[NB][KPI];
     int jc = cap;
     auto load_keys = [&](int it, float (&kd)[KPI][8], float (&vd)[KPI][8], bool (&ok)[KPI]) {
 #pragma unroll
         for (int u = 0; u < KPI; ++u) {
             const int j = j0 + (it * KPI + u) * 16 + rowgroup;
             ok[u] = j < jc;
-            const int jj = ok[u] ? j : (it == 0 ? cap - 1 : j0);
+            const int jj = ok[u] ? j : j0;
             const float4 k0 = *(const float4 *)(kc + (size_t)jj * a.kvd + d0);
             const float4 k1 = *(const float4 *)(kc + (size_t)jj * a.kvd + d1);
             const float4 v0 = *(const float4 *)(vc + (size_t)jj * a.kvd + d0);
@@ -323,24 +323,27 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
             vd[u][4] = v1.x, vd[u][5] = v1.y, vd[u][6] = v1.z, vd[u][7] = v1.w;
         }
     };
-    load_keys(0, kr, vr, valid);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) load_keys(b, kb[b], vb[b], okb[b]);
     const int n = pos + 1;
     if (j0 >= n) return;  // no keys of this lane's context
     const int j1 = min(n, j0 + chunk);
     const bool owner = j1 == n;  // this block holds the new key
     jc = owner ? j1 - 1 : j1;    // cached keys [j0, jc)
     const int iters = (jc - j0 + 16 * KPI - 1) / (16 * KPI);
-    // Step 0's rows past jc (loaded speculatively) are zeroed, so masked keys
-    // never multiply stale cache contents.
+    // The ring's first rows past jc (loaded before the position arrived) are
+    // zeroed, so masked keys never multiply stale cache contents.
 #pragma unroll
-    for (int u = 0; u < KPI; ++u) {
-        valid[u] = j0 + u * 16 + rowgroup < jc;
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            kr[u][i] = valid[u] ? kr[u][i] : 0.0f;
-            vr[u][i] = valid[u] ? vr[u][i] : 0.0f;
+        for (int u = 0; u < KPI; ++u) {
+            okb[b][u] = j0 + (b * KPI + u) * 16 + rowgroup < jc;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                kb[b][u][i] = okb[b][u] ? kb[b][u][i] : 0.0f;
+                vb[b][u][i] = okb[b][u] ? vb[b][u][i] : 0.0f;
+            }
         }
-    }
     const float rc = a.rope[(size_t)pos * 64 + lane], rs = a.rope[a.sin_off + (size_t)pos * 64 + lane];
 
     // Head RMSNorm and RoPE (gpu.metal:380-388 normRopeAt). Lane l holds the
@@ -421,31 +424,26 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
             m[hh] = mn;
         }
     };
-    for (int it = 0; it < iters; ++it) {
-        float kn2[KPI][8], vn2[KPI][8];
-        bool ok2[KPI];
-        if (it + 1 < iters) load_keys(it + 1, kn2, vn2, ok2);
-        step(kr, vr, valid);
-        if (it + 1 < iters) {
+    for (int it0 = 0; it0 < iters; it0 += NB) {
 #pragma unroll
-            for (int u = 0; u < KPI; ++u) {
-                valid[u] = ok2[u];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) kr[u][i] = kn2[u][i], vr[u][i] = vn2[u][i];
+        for (int b = 0; b < NB; ++b) {
+            if (it0 + b < iters) {
+                step(kb[b], vb[b], okb[b]);
+                if (it0 + b + NB < iters) load_keys(it0 + b + NB, kb[b], vb[b], okb[b]);
             }
         }
     }
     if (owner) {  // the new key, on row group 0
 #pragma unroll
         for (int u = 0; u < KPI; ++u) {
-            valid[u] = u == 0 && rowgroup == 0;
+            okb[0][u] = u == 0 && rowgroup == 0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                kr[u][i] = knew[d0 + i], kr[u][4 + i] = knew[d1 + i];
-                vr[u][i] = vnew[d0 + i], vr[u][4 + i] = vnew[d1 + i];
+                kb[0][u][i] = knew[d0 + i], kb[0][u][4 + i] = knew[d1 + i];
+                vb[0][u][i] = vnew[d0 + i], vb[0][u][4 + i] = vnew[d1 + i];
             }
         }
-        step(kr, vr, valid);
+        step(kb[0], vb[0], okb[0]);
     }
     // Merge the wave's four row groups (lanes l, l^16, l^32, l^48 hold the
     // same dims): xor 16, then xor 32.
@@ -627,7 +625,7 @@ __global__ __launch_bounds__(1024) void lm_argmax_kernel(const ArgmaxArgs a) {
 template <int G>
 int launch_attend_g(const AttnArgs &a, int lanes, hipStream_t st) {
     constexpr int KPI = G <= 4 ? 2 : 1;
-    hipLaunchKernelGGL((lm_attend_kernel<G, KPI>), dim3(a.splits, a.kvh, lanes), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((lm_attend_kernel<G, KPI, 3>), dim3(a.splits, a.kvh, lanes), dim3(256), 0, st, a);
     return launch_status();
 }
 
@@ -716,7 +714,7 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool 
         GPHQ_TRY(gemv(ws, lanes, fmt, PRO_NORM, EPI_SWIGLU, buf, L.gu, L.gu_scale, ws->h, H, ws->act, I, H, 2 * I,
                       st));
         if (fmt != GPHQ_FMT_Q8B) {  // gpu_darwin.go:209-215: Q8B skips down's input rotation
-            hipLaunchKernelGGL(lm_rotate_kernel, dim3((unsigned)(I / lm->iblock), lanes), dim3(256),
+            hipLaunchKernelGGL(lm_rotate_kernel, dim3((unsigned)(I / lm->iblock), lanes), dim3(512),
                                lm->iblock * sizeof(float), st, ws->act, (int)I, lm->isigns, (int)lm->iblock);
             GPHQ_TRY(launch_status());
         }
@@ -862,7 +860,7 @@ int lm_embed_launch(const gphq_lm *lm, const int32_t *tok, int rows, float *h, h
 
 int lm_rotate_launch(const gphq_lm *lm, float *act, int rows, long stride, hipStream_t st) {
     const int64_t I = lm->cfg.intermediate;
-    hipLaunchKernelGGL(lm_rotate_kernel, dim3((unsigned)(I / lm->iblock), rows), dim3(256),
+    hipLaunchKernelGGL(lm_rotate_kernel, dim3((unsigned)(I / lm->iblock), rows), dim3(512),
                        lm->iblock * sizeof(float), st, act, (int)stride, lm->isigns, (int)lm->iblock);
     return launch_status();
 }
