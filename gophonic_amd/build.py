@@ -31,13 +31,21 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source extra flags. q8b_gemm: keep MFMA results in VGPRs (the compiler
+# otherwise places them in AGPRs, which costs one v_accvgpr_read per result
+# on a kernel bound by its VALU work).
+FILE_FLAGS = {
+    "q8b_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def sources():
     return sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")))
 
 
 def _compile(src, verbose):
     obj = os.path.join(OBJ, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC] + HIP_FLAGS + ["-c", src, "-o", obj]
+    cmd = [HIPCC] + HIP_FLAGS + FILE_FLAGS.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

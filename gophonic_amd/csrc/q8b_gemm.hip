@@ -11,6 +11,8 @@
 // every block's int32 products come out of one MFMA with a zero accumulator;
 // the fp32 scale-accumulate that follows is VALU work (three instructions per
 // output and block), which bounds this kernel well below the int8 MFMA rate.
+#include <type_traits>
+
 #include "common.h"
 
 using namespace gphq;
@@ -20,6 +22,7 @@ namespace {
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // One thread per (row, 32-value block): scale = max/127 and inverse = 127/max
 // (both 0 unless 0 < max < inf, int8.go:106-119), codes RNE(x * inverse)
@@ -77,78 +80,129 @@ struct Q8bArgs {
     int m, k, n, gridM, gridN;
 };
 
+// 16-byte chunk c of a row of KSB*32 bytes in LDS, swizzled within each
+// 128-byte half by the row (big_swz), so fragment reads of consecutive rows
+// at one chunk hit distinct banks.
+__device__ __forceinline__ int q8b_swz(int row, int c) { return (c & ~7) | big_swz(row, c & 7); }
+
 // BM x BN output tiles, WGM x WGN wavefronts of (BM/WGM) x (BN/WGN) as 32x32
-// MFMA tiles. Per 128-byte K step (four blocks) both code tiles pass through
-// LDS in 128-byte rows with XOR-swizzled 16-byte chunks (big_swz), the step's
-// block scales as [block][row] floats; double buffered, the next step's global
-// loads one step ahead in registers. Rows past m or n load row m-1 / n-1 and
-// are not stored; blocks past k are skipped.
-template <int BM, int BN, int WGM, int WGN>
+// MFMA tiles. Per K step of KSB blocks (KSB*32 bytes) both code tiles pass
+// through LDS in rows of 16-byte chunks (q8b_swz), the step's block scales as
+// [block][row] floats; double buffered, the next step's global loads one step
+// ahead in registers. Rows past m or n load row m-1 / n-1 and are not
+// stored; blocks past k are skipped, and so are the scale-accumulates of a
+// tile's rows 16..31 when they are all past m.
+//
+// Per block the wavefront issues the MFMAs of block b+1 before the
+// scale-accumulate of block b (two sets of int32 results), so the matrix
+// cores run beside the VALU chain; the chain itself keeps block order.
+template <int BM, int BN, int WGM, int WGN, int KSB>
 __global__ __launch_bounds__(64 * WGM * WGN) void q8b_gemm_kernel(const Q8bArgs a) {
     constexpr int NT = 64 * WGM * WGN;
     constexpr int TI = BM / WGM / 32, TJ = BN / WGN / 32;
-    constexpr int AL = BM * 8 / NT, BL = BN * 8 / NT;  // 16-byte code units per thread and step
-    static_assert(AL >= 1 && BL >= 1 && BM + BN <= NT, "loader split");
-    __shared__ i32x4 As[2][BM * 8];
-    __shared__ i32x4 Bs[2][BN * 8];
-    __shared__ float Sa[2][4][BM];
-    __shared__ float Sb[2][4][BN];
+    constexpr int CH = 2 * KSB;                          // 16-byte chunks per row and step
+    constexpr int AL = BM * CH / NT, BL = BN * CH / NT;  // chunks per thread and step
+    constexpr int SU = (BM + BN) * (KSB / 4);            // float4 scale units per step
+    constexpr int SL = (SU + NT - 1) / NT;
+    static_assert(AL * NT == BM * CH && BL * NT == BN * CH && KSB % 4 == 0, "loader split");
+    __shared__ i32x4 As[2][BM * CH];
+    __shared__ i32x4 Bs[2][BN * CH];
+    __shared__ float Sa[2][KSB][BM];
+    __shared__ float Sb[2][KSB][BN];
     int bm, bn;
     tile_order(blockIdx.x, a.gridM, a.gridN, bm, bn);
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const int wm = wv / WGN, wn = wv % WGN;
     const int m0 = bm * BM, n0 = bn * BN;
-    const int kb = a.k >> 5, steps = (kb + 3) >> 2;
+    const int kb = a.k >> 5, steps = (kb + KSB - 1) / KSB;
 
-    // Loader: unit u = i*NT + t is row u/8, 16-byte chunk u%8 of the step's
-    // 128 bytes; chunks past k load zeros. Threads t < BM load A's scale row
-    // t, threads NT-BN .. NT-1 B's scale row t-(NT-BN) (four floats each).
+    // Loader: unit u = i*NT + t is row u/CH, 16-byte chunk u%CH of the
+    // step's bytes; chunks past k load zeros. Scale unit v = i*NT + t is one
+    // float4 (four blocks) of A's row v (v < BM*KSB/4 ordering: row-major over
+    // rows, then quads) or of B's row.
+    // A full step (every chunk inside k, the usual case) loads without
+    // per-chunk conditions. first marks the loads of step 1, which stay in
+    // registers across the first step: relaxed atomic loads, so that the
+    // compiler does not merge them with the in-loop loads of the same
+    // registers into one load at the top of the loop (which would wait for
+    // each step's codes as they are stored).
     i32x4 ar[AL], br[BL];
-    float4 sr;
-    auto gload = [&](int st) {
-        const int kbyte = st * 128;
+    float4 sr[SL];
+    auto ld = [&](const int8_t *p, bool first) -> i32x4 {
+        if (!first) return *(const i32x4 *)p;
+        const long lo = __hip_atomic_load((const long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const long hi = __hip_atomic_load((const long *)p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return i32x4{(int)lo, (int)(lo >> 32), (int)hi, (int)(hi >> 32)};
+    };
+    auto gload = [&](int st, bool first) {
+        const int kbyte = st * KSB * 32;
+        if (kbyte + KSB * 32 <= a.k) {
 #pragma unroll
-        for (int i = 0; i < AL; ++i) {
-            const int u = i * NT + t, row = u >> 3, ch = u & 7;
-            const int gr = min(m0 + row, a.m - 1);
-            ar[i] = kbyte + ch * 16 < a.k ? *(const i32x4 *)(a.qa + (long)gr * a.k + kbyte + ch * 16) : i32x4{0, 0, 0, 0};
+            for (int i = 0; i < AL; ++i) {
+                const int u = i * NT + t, row = u / CH, ch = u % CH;
+                ar[i] = ld(a.qa + (long)min(m0 + row, a.m - 1) * a.k + kbyte + ch * 16, first);
+            }
+#pragma unroll
+            for (int i = 0; i < BL; ++i) {
+                const int u = i * NT + t, row = u / CH, ch = u % CH;
+                br[i] = ld(a.qw + (long)min(n0 + row, a.n - 1) * a.k + kbyte + ch * 16, first);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < AL; ++i) {
+                const int u = i * NT + t, row = u / CH, ch = u % CH;
+                const int gr = min(m0 + row, a.m - 1);
+                ar[i] = kbyte + ch * 16 < a.k ? ld(a.qa + (long)gr * a.k + kbyte + ch * 16, first) : i32x4{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int i = 0; i < BL; ++i) {
+                const int u = i * NT + t, row = u / CH, ch = u % CH;
+                const int gr = min(n0 + row, a.n - 1);
+                br[i] = kbyte + ch * 16 < a.k ? ld(a.qw + (long)gr * a.k + kbyte + ch * 16, first) : i32x4{0, 0, 0, 0};
+            }
         }
 #pragma unroll
-        for (int i = 0; i < BL; ++i) {
-            const int u = i * NT + t, row = u >> 3, ch = u & 7;
-            const int gr = min(n0 + row, a.n - 1);
-            br[i] = kbyte + ch * 16 < a.k ? *(const i32x4 *)(a.qw + (long)gr * a.k + kbyte + ch * 16) : i32x4{0, 0, 0, 0};
-        }
-        const int b0 = st * 4;
-        sr = float4{0.f, 0.f, 0.f, 0.f};
-        const float *srow = nullptr;
-        if (t < BM)
-            srow = a.da + (long)min(m0 + t, a.m - 1) * kb;
-        else if (t >= NT - BN)
-            srow = a.dw + (long)min(n0 + t - (NT - BN), a.n - 1) * kb;
-        if (srow) {
-            sr.x = srow[b0];
-            if (b0 + 1 < kb) sr.y = srow[b0 + 1];
-            if (b0 + 2 < kb) sr.z = srow[b0 + 2];
-            if (b0 + 3 < kb) sr.w = srow[b0 + 3];
+        for (int i = 0; i < SL; ++i) {
+            const int v = i * NT + t;
+            float4 f = float4{0.f, 0.f, 0.f, 0.f};
+            if (v < SU) {
+                const int quad = v % (KSB / 4), row = v / (KSB / 4);
+                const int b0 = st * KSB + quad * 4;
+                float sv[4];
+                if (row < BM) {
+                    const float *sp = a.da + (long)min(m0 + row, a.m - 1) * kb;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sv[e] = b0 + e < kb ? sp[b0 + e] : 0.0f;
+                } else {
+                    const float *sp = a.dw + (long)min(n0 + row - BM, a.n - 1) * kb;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sv[e] = b0 + e < kb ? sp[b0 + e] : 0.0f;
+                }
+                f = float4{sv[0], sv[1], sv[2], sv[3]};
+            }
+            sr[i] = f;
         }
     };
     auto lstore = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < AL; ++i) {
-            const int u = i * NT + t, row = u >> 3;
-            As[buf][row * 8 + big_swz(row, u & 7)] = ar[i];
+            const int u = i * NT + t, row = u / CH;
+            As[buf][row * CH + q8b_swz(row, u % CH)] = ar[i];
         }
 #pragma unroll
         for (int i = 0; i < BL; ++i) {
-            const int u = i * NT + t, row = u >> 3;
-            Bs[buf][row * 8 + big_swz(row, u & 7)] = br[i];
+            const int u = i * NT + t, row = u / CH;
+            Bs[buf][row * CH + q8b_swz(row, u % CH)] = br[i];
         }
-        if (t < BM) {
-            Sa[buf][0][t] = sr.x, Sa[buf][1][t] = sr.y, Sa[buf][2][t] = sr.z, Sa[buf][3][t] = sr.w;
-        } else if (t >= NT - BN) {
-            const int r = t - (NT - BN);
-            Sb[buf][0][r] = sr.x, Sb[buf][1][r] = sr.y, Sb[buf][2][r] = sr.z, Sb[buf][3][r] = sr.w;
+#pragma unroll
+        for (int i = 0; i < SL; ++i) {
+            const int v = i * NT + t;
+            if (v < SU) {
+                const int quad = v % (KSB / 4), row = v / (KSB / 4);
+                float *dst = row < BM ? &Sa[buf][quad * 4][row] : &Sb[buf][quad * 4][row - BM];
+                const int stride = row < BM ? BM : BN;
+                dst[0] = sr[i].x, dst[stride] = sr[i].y, dst[2 * stride] = sr[i].z, dst[3 * stride] = sr[i].w;
+            }
         }
     };
 
@@ -157,65 +211,77 @@ __global__ __launch_bounds__(64 * WGM * WGN) void q8b_gemm_kernel(const Q8bArgs 
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x16{};
-    gload(0);
+    // Row tile i's rows 16..31 hold rows of the matrix (else their
+    // scale-accumulates are skipped; the wave takes the branch as one).
+    bool hi[TI], allhi = true;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        hi[i] = m0 + wm * (32 * TI) + 32 * i + 16 < a.m;
+        allhi = allhi && hi[i];
+    }
+    gload(0, false);
     lstore(0);
-    if (steps > 1) gload(1);
+    if (steps > 1) gload(1, true);
     __syncthreads();
     const int fr = lane & 31, fh = lane >> 5;
     for (int st = 0; st < steps; ++st) {
         const int cur = st & 1;
-        const int nb = min(4, kb - st * 4);
-        auto block = [&](int b) {
+        const int nb = min(KSB, kb - st * KSB);
+        // The step's MFMAs run in units (block b, row tile i, column tile j),
+        // block-major; unit u+1's MFMA is issued before unit u's
+        // scale-accumulate, so the matrix cores work beside the VALU chain.
+        constexpr int UN = KSB * TI * TJ;
+        auto issue = [&](int u, i32x16 &d) {
+            const int b = u / (TI * TJ), i = (u / TJ) % TI, j = u % TJ;
             const int c = 2 * b + fh;
-            i32x4 fa[TI], fb[TJ];
-#pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                const int r = wm * (32 * TI) + 32 * i + fr;
-                fa[i] = As[cur][r * 8 + big_swz(r, c)];
-            }
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const int r = wn * (32 * TJ) + 32 * j + fr;
-                fb[j] = Bs[cur][r * 8 + big_swz(r, c)];
-            }
-            // Scales: this lane's 16 result rows of tile i are 4 runs of 4
-            // consecutive rows; its column's weight scale is one float.
-            float4 sa[TI][4];
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    sa[i][q] = *(const float4 *)&Sa[cur][b][wm * (32 * TI) + 32 * i + 8 * q + 4 * fh];
-            float sb[TJ];
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) sb[j] = Sb[cur][b][wn * (32 * TJ) + 32 * j + fr];
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) {
-                    const i32x16 dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], i32x16{}, 0, 0, 0);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float s4[4] = {sa[i][q].x, sa[i][q].y, sa[i][q].z, sa[i][q].w};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float s = __fmul_rn(s4[e], sb[j]);
-                            acc[i][j][4 * q + e] = __builtin_fmaf((float)dot[4 * q + e], s, acc[i][j][4 * q + e]);
-                        }
-                    }
-                }
+            const int ra = wm * (32 * TI) + 32 * i + fr, rb = wn * (32 * TJ) + 32 * j + fr;
+            d = __builtin_amdgcn_mfma_i32_32x32x32_i8(As[cur][ra * CH + q8b_swz(ra, c)],
+                                                     Bs[cur][rb * CH + q8b_swz(rb, c)], i32x16{}, 0, 0, 0);
         };
-        // Unrolled over a full step for one tile per wavefront; with more the
-        // registers of four blocks in flight cost more than the overlap gains.
-        if (TI * TJ == 1 && nb == 4) {
+        // acc = fmaf(float(dot), da * dw, acc) for unit u. This lane's 16
+        // results of a tile are 4 runs of 4 consecutive rows; its column's
+        // weight scale is one float. FULL: a whole step of blocks and every
+        // row tile's rows 16..31 inside m (no conditions in the loop).
+        auto apply = [&](auto full_c, int u, const i32x16 &d) {
+            constexpr bool FULL = decltype(full_c)::value;
+            const int b = u / (TI * TJ), i = (u / TJ) % TI, j = u % TJ;
+            const float sb = Sb[cur][b][wn * (32 * TJ) + 32 * j + fr];
 #pragma unroll
-            for (int b = 0; b < 4; ++b) block(b);
-        } else {
-            for (int b = 0; b < nb; ++b) block(b);
-        }
+            for (int q = 0; q < 4; ++q) {
+                if (!FULL && q >= 2 && !hi[i]) continue;
+                const float4 s4 = *(const float4 *)&Sa[cur][b][wm * (32 * TI) + 32 * i + 8 * q + 4 * fh];
+                const float sa[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float s = __fmul_rn(sa[e], sb);
+                    acc[i][j][4 * q + e] = __builtin_fmaf((float)d[4 * q + e], s, acc[i][j][4 * q + e]);
+                }
+            }
+        };
+        auto units = [&](auto full_c) {
+            constexpr bool FULL = decltype(full_c)::value;
+            const int un = FULL ? UN : nb * TI * TJ;
+            i32x16 d0, d1;
+            issue(0, d0);
+#pragma unroll
+            for (int u = 0; u < UN; u += 2) {
+                if (FULL || u < un) {
+                    if (FULL || u + 1 < un) issue(u + 1, d1);
+                    apply(full_c, u, d0);
+                }
+                if (FULL || u + 1 < un) {
+                    if (u + 2 < UN && (FULL || u + 2 < un)) issue(u + 2, d0);
+                    apply(full_c, u + 1, d1);
+                }
+            }
+        };
+        if (nb == KSB && allhi)
+            units(std::true_type{});
+        else
+            units(std::false_type{});
         if (st + 1 < steps) {
             lstore(cur ^ 1);
-            if (st + 2 < steps) gload(st + 2);
+            if (st + 2 < steps) gload(st + 2, false);
         }
         __syncthreads();
     }
@@ -233,68 +299,133 @@ __global__ __launch_bounds__(64 * WGM * WGN) void q8b_gemm_kernel(const Q8bArgs 
         }
 }
 
-// M <= 2 (K a multiple of 1024): one wavefront per group of kRowsRW weight
-// rows, so the grid is N / 4 blocks wide instead of N / 128. Lane l takes
-// 16-byte chunk l of each 1 KiB K step of its rows and of every activation
-// row; v_dot4_i32_i8 gives exact int32 partial dots, lanes l and l ^ 1 add
-// their halves into the 32-value block's dot (exact), which is staged in LDS
-// with both scale vectors. Lane (r, i) then runs output (i, row r)'s chain
-// acc = fmaf(float(dot_b), da[i][b] * dw[r][b], acc) in block order: the
-// operations of the tiled kernel and of the oracle, so the result is the same
-// bit for bit.
-constexpr int kRowsRW = 4;
-// Each activation row adds a pass over the lane's K chunks and a chain per
-// output: measured at K = 4096, N = 12288, M = 1 takes 23 us (the tiled
-// kernel 47 us) and M = 16 192 us, so the kernel stops at two rows.
-constexpr int kRowsMaxM = 2;
-__global__ __launch_bounds__(64) void q8b_rows_kernel(const Q8bArgs a) {
-    extern __shared__ float sm[];
-    const int KB = a.k >> 5, m = a.m, lane = threadIdx.x;
-    float *dots = sm;                     // [kRowsRW][m][KB]
-    float *sw = dots + kRowsRW * m * KB;  // [kRowsRW][KB] weight block scales
-    float *sa = sw + kRowsRW * KB;        // [m][KB] activation block scales
-    const int n0 = blockIdx.x * kRowsRW;
-    for (int i = lane; i < kRowsRW * KB; i += 64) {
-        const int r = i / KB, b = i - r * KB;
-        sw[i] = a.dw[(size_t)min(n0 + r, a.n - 1) * KB + b];
-    }
-    for (int i = lane; i < m * KB; i += 64) sa[i] = a.da[i];
-    const int steps = a.k >> 10;
-    for (int s = 0; s < steps; ++s) {
-        const size_t kb = (size_t)s * 1024 + (size_t)lane * 16;
-        i32x4 w[kRowsRW];
+// M <= 16 * TI: one wavefront (and block) per 16 weight rows, all
+// activation rows in TI tiles of 16. A step is 128 bytes of K (four
+// blocks): the wavefront loads its 16 weight rows and 16 * TI activation
+// rows with 16-byte loads, eight lanes per row (whole 128-byte lines), their
+// block scales with one float per lane, and keeps D steps of loads in
+// flight in a register ring. Each step passes through the wavefront's own
+// LDS (rows padded to 144 bytes), from which every block is one
+// v_mfma_i32_16x16x32_i8 per activation tile (lane l supplies bytes
+// 8(l/16)..+8 of the block for row or column l%16 and receives rows
+// 4(l/16)..+3 of column l%16). The chain per output is the tiled kernel's,
+// in block order: acc = fmaf(float(dot_b), da * dw, acc), so the results
+// are the same bit for bit.
+template <int TI, int D>
+__global__ __launch_bounds__(64) void q8b_small_kernel(const Q8bArgs a) {
+    constexpr int RS = 144;             // LDS row stride of the code tiles, bytes
+    constexpr int AR = 16 * TI;         // activation rows
+    __shared__ __align__(16) int8_t wl[16 * RS];
+    __shared__ __align__(16) int8_t al[AR * RS];
+    __shared__ float swl[16][4];                // [weight row][block of the step]
+    __shared__ __align__(16) float sal[4][AR];  // [block of the step][activation row]
+    const int lane = threadIdx.x, kb = a.k >> 5, steps = kb >> 2;
+    const int n0 = blockIdx.x * 16;
+    const int lr = lane >> 3, lc = lane & 7;  // loader: row lr (+8h), 16-byte chunk lc
+    const int c = lane & 15, g = lane >> 4;   // MFMA lane: row/column c, byte group g
+    const int8_t *wp[2];
+    wp[0] = a.qw + (size_t)min(n0 + lr, a.n - 1) * a.k + lc * 16;
+    wp[1] = a.qw + (size_t)min(n0 + lr + 8, a.n - 1) * a.k + lc * 16;
+    const int8_t *ap[2 * TI];
 #pragma unroll
-        for (int r = 0; r < kRowsRW; ++r) w[r] = *(const i32x4 *)(a.qw + (size_t)min(n0 + r, a.n - 1) * a.k + kb);
-        for (int i = 0; i < m; ++i) {
-            const i32x4 x = *(const i32x4 *)(a.qa + (size_t)i * a.k + kb);
+    for (int h = 0; h < 2 * TI; ++h) ap[h] = a.qa + (size_t)min(lr + 8 * h, a.m - 1) * a.k + lc * 16;
+    // Scales: lane l takes block l%4 of the step of weight row l/4 and of
+    // activation rows l/4 + 16i.
+    const float *dwp = a.dw + (size_t)min(n0 + (lane >> 2), a.n - 1) * kb + (lane & 3);
+    const float *dap[TI];
 #pragma unroll
-            for (int r = 0; r < kRowsRW; ++r) {
-                int d = __builtin_amdgcn_sdot4(x.x, w[r].x, 0, false);
-                d = __builtin_amdgcn_sdot4(x.y, w[r].y, d, false);
-                d = __builtin_amdgcn_sdot4(x.z, w[r].z, d, false);
-                d = __builtin_amdgcn_sdot4(x.w, w[r].w, d, false);
-                d += __shfl_xor(d, 1);
-                if (!(lane & 1)) dots[(r * m + i) * KB + s * 32 + (lane >> 1)] = (float)d;
+    for (int i = 0; i < TI; ++i) dap[i] = a.da + (size_t)min((lane >> 2) + 16 * i, a.m - 1) * kb + (lane & 3);
+    i32x4 wr[D][2], ar[D][2 * TI];
+    float sw[D], sa[D][TI];
+    auto load = [&](int p, int st, bool first) {
+        const size_t off = (size_t)st * 128;
+        auto ld = [&](const int8_t *q, bool stream) -> i32x4 {
+            if (!first) return stream ? __builtin_nontemporal_load((const i32x4 *)q) : *(const i32x4 *)q;
+            // Relaxed atomic loads for the first fill: with plain loads at
+            // both the ring's entry and its refill the compiler merges them
+            // into one load at the top of the loop, which waits for each
+            // step as it is used.
+            const long lo = __hip_atomic_load((const long *)q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            const long hi = __hip_atomic_load((const long *)q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            return i32x4{(int)lo, (int)(lo >> 32), (int)hi, (int)(hi >> 32)};
+        };
+        auto lf = [&](const float *q) -> float {
+            return first ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) : *q;
+        };
+        wr[p][0] = ld(wp[0] + off, true);
+        wr[p][1] = ld(wp[1] + off, true);
+#pragma unroll
+        for (int h = 0; h < 2 * TI; ++h) ar[p][h] = ld(ap[h] + off, false);
+        sw[p] = lf(dwp + 4 * st);
+#pragma unroll
+        for (int i = 0; i < TI; ++i) sa[p][i] = lf(dap[i] + 4 * st);
+    };
+    f32x4 acc[TI];
+#pragma unroll
+    for (int i = 0; i < TI; ++i) acc[i] = f32x4{};
+#pragma unroll
+    for (int p = 0; p < D; ++p) load(p, min(p, steps - 1), true);
+    for (int s0 = 0; s0 < steps; s0 += D) {
+#pragma unroll
+        for (int p = 0; p < D; ++p) {
+            const int st = s0 + p;
+            // The step to LDS (this wavefront alone reads it back).
+            *(i32x4 *)&wl[lr * RS + lc * 16] = wr[p][0];
+            *(i32x4 *)&wl[(lr + 8) * RS + lc * 16] = wr[p][1];
+#pragma unroll
+            for (int h = 0; h < 2 * TI; ++h) *(i32x4 *)&al[(lr + 8 * h) * RS + lc * 16] = ar[p][h];
+            swl[lane >> 2][lane & 3] = sw[p];
+#pragma unroll
+            for (int i = 0; i < TI; ++i) sal[lane & 3][(lane >> 2) + 16 * i] = sa[p][i];
+            load(p, min(st + D, steps - 1), false);
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const long wv = *(const long *)&wl[c * RS + 32 * b + 8 * g];
+                const float w1 = swl[c][b];
+#pragma unroll
+                for (int i = 0; i < TI; ++i) {
+                    const long av = *(const long *)&al[(16 * i + c) * RS + 32 * b + 8 * g];
+                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, i32x4{}, 0, 0, 0);
+                    const float4 s4 = *(const float4 *)&sal[b][16 * i + 4 * g];
+                    const float s_[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][e] = __builtin_fmaf((float)d[e], __fmul_rn(s_[e], w1), acc[i][e]);
+                }
             }
+            __builtin_amdgcn_wave_barrier();
+            if (st + 1 >= steps) break;
         }
     }
-    __syncthreads();
-    if (lane < kRowsRW * m) {
-        const int r = lane / m, i = lane - r * m;
-        const float *dr = dots + (r * m + i) * KB, *wr = sw + r * KB, *ar = sa + i * KB;
-        float acc = 0.0f;
-        for (int b = 0; b < KB; ++b) acc = fmaf(dr[b], ar[b] * wr[b], acc);
-        if (n0 + r < a.n) a.y[(size_t)i * a.n + n0 + r] = acc;
+    const int col = n0 + c;
+    if (col < a.n) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = 16 * i + 4 * g + e;
+                if (row < a.m) a.y[(size_t)row * a.n + col] = acc[i][e];
+            }
     }
 }
 
-size_t rows_lds_bytes(int m, int k) { return (size_t)(kRowsRW * m + kRowsRW + m) * (k / 32) * 4; }
+template <int TI, int D>
+int go_small(const Q8bArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL((q8b_small_kernel<TI, D>), dim3((unsigned)((a.n + 15) / 16)), dim3(64), 0, st, a);
+    return launch_status();
+}
 
-template <int BM, int BN, int WGM, int WGN>
+// Ring depth 8 steps (4 KiB of weight rows in flight per wavefront).
+template <int TI>
+int launch_small(const Q8bArgs &a, hipStream_t st) {
+    return go_small<TI, 8>(a, st);
+}
+
+template <int BM, int BN, int WGM, int WGN, int KSB>
 int launch_q8b(Q8bArgs a, hipStream_t st) {
     a.gridM = (a.m + BM - 1) / BM;
     a.gridN = (a.n + BN - 1) / BN;
-    hipLaunchKernelGGL((q8b_gemm_kernel<BM, BN, WGM, WGN>), dim3((unsigned)(a.gridM * a.gridN)),
+    hipLaunchKernelGGL((q8b_gemm_kernel<BM, BN, WGM, WGN, KSB>), dim3((unsigned)(a.gridM * a.gridN)),
                        dim3(64 * WGM * WGN), 0, st, a);
     return launch_status();
 }
@@ -324,15 +455,16 @@ int gphq_q8b_gemm(const int8_t *qa_dev, const float *da_dev, const int8_t *qw_de
     if (k == 0) return fill_f32(y_dev, (size_t)m * n, 0.0f, (hipStream_t)stream);
     Q8bArgs a{qa_dev, da_dev, qw_dev, dw_dev, y_dev, (int)m, (int)k, (int)n, 0, 0};
     hipStream_t st = (hipStream_t)stream;
-    // 128 x 128 tiles from M = 256; below, 32-row tiles keep the grid wide;
-    // up to 2 rows, the dot-product kernel.
-    if (m >= 256) return launch_q8b<128, 128, 2, 2>(a, st);
-    if (m <= kRowsMaxM && k % 1024 == 0 && rows_lds_bytes((int)m, (int)k) <= 65536) {
-        hipLaunchKernelGGL(q8b_rows_kernel, dim3((unsigned)((n + kRowsRW - 1) / kRowsRW)), dim3(64),
-                           rows_lds_bytes((int)m, (int)k), st, a);
-        return launch_status();
-    }
-    return launch_q8b<32, 128, 1, 4>(a, st);
+    // Shapes measured on MI355X at K = 4096, N = 12288: from M = 256,
+    // 128 x 192 tiles of eight wavefronts (one per CU at M = 512); from
+    // M = 33, 64 x 64 tiles with 256-byte K steps; up to 32 rows (k a
+    // multiple of 128), one wavefront per 16 weight rows with a ring of
+    // steps in flight.
+    if (m >= 256) return launch_q8b<128, 192, 4, 2, 4>(a, st);
+    if (m > 32) return launch_q8b<64, 64, 2, 2, 8>(a, st);
+    if (k % 128) return launch_q8b<64, 64, 2, 2, 4>(a, st);
+    if (m > 16) return launch_small<2>(a, st);
+    return launch_small<1>(a, st);
 }
 
 }  // extern "C"

@@ -43,7 +43,8 @@ def test_quantize_bit_exact_with_special_blocks():
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 64, 96), (5, 4096, 200), (37, 160, 130), (128, 4096, 384), (300, 1024, 257),
-                                   (1, 4096, 1001), (16, 2048, 301), (3, 8192, 77), (2, 1024, 3), (17, 1024, 64)])
+                                   (1, 4096, 1001), (16, 2048, 301), (3, 8192, 77), (2, 1024, 3), (17, 1024, 64),
+                                   (32, 4096, 130), (24, 96, 50), (33, 4096, 96), (255, 512, 100), (256, 160, 97)])
 def test_gemm_bit_exact(m, k, n):
     import torch
 
@@ -59,12 +60,13 @@ def test_gemm_bit_exact(m, k, n):
     assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
-def test_config2_shape_rows_bit_exact():
-    # BASELINE configuration 2 at M = 512 (K = 4096, N = 12288): sampled rows
-    # against the oracle (rows are independent).
+@pytest.mark.parametrize("m", [1, 16, 128, 512])
+def test_config2_shape_rows_bit_exact(m):
+    # BASELINE configuration 2 (K = 4096, N = 12288) at each bench M: sampled
+    # rows against the oracle (rows are independent).
     import torch
 
-    m, k, n = 512, 4096, 12288
+    k, n = 4096, 12288
     g = torch.Generator(device="cuda").manual_seed(2)
     x = torch.randn((m, k), device="cuda", generator=g)
     qw = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g)
@@ -73,9 +75,9 @@ def test_config2_shape_rows_bit_exact():
     d = torch.empty((m, k // 32), device="cuda")
     gphq.q8b_quantize(x, m, k, q, d)
     y = torch.empty((m, n), device="cuda")
-    print("q8b gemm config 2 m=512", flush=True)
+    print(f"q8b gemm config 2 m={m}", flush=True)
     gphq.q8b_gemm(q, d, qw, dw, y, m, k, n)
-    rows = [0, 131, 255, 256, 511]
+    rows = sorted({0, min(m - 1, 131), min(m - 1, 255), min(m - 1, 256), m - 1})
     qh, dh = q.cpu().numpy()[rows], d.cpu().numpy()[rows]
     want = orc.q8b_gemm(qh, dh, qw.cpu().numpy(), dw.cpu().numpy(), len(rows), k, n)
     assert np.array_equal(y.cpu().numpy()[rows].view(np.uint32), want.view(np.uint32))
