@@ -315,10 +315,11 @@ template <int TI, int D>
 __global__ __launch_bounds__(64) void q8b_small_kernel(const Q8bArgs a) {
     constexpr int RS = 144;             // LDS row stride of the code tiles, bytes
     constexpr int AR = 16 * TI;         // activation rows
-    __shared__ __align__(16) int8_t wl[16 * RS];
-    __shared__ __align__(16) int8_t al[AR * RS];
-    __shared__ float swl[16][4];                // [weight row][block of the step]
-    __shared__ __align__(16) float sal[4][AR];  // [block of the step][activation row]
+    static_assert(D % 2 == 0, "the ring pairs with two LDS buffers");
+    __shared__ __align__(16) int8_t wl[2][16 * RS];
+    __shared__ __align__(16) int8_t al[2][AR * RS];
+    __shared__ float swl[2][16][4];                // [buffer][weight row][block of the step]
+    __shared__ __align__(16) float sal[2][4][AR];  // [buffer][block of the step][activation row]
     const int lane = threadIdx.x, kb = a.k >> 5, steps = kb >> 2;
     const int n0 = blockIdx.x * 16;
     const int lr = lane >> 3, lc = lane & 7;  // loader: row lr (+8h), 16-byte chunk lc
@@ -360,34 +361,43 @@ __global__ __launch_bounds__(64) void q8b_small_kernel(const Q8bArgs a) {
 #pragma unroll
         for (int i = 0; i < TI; ++i) sa[p][i] = lf(dap[i] + 4 * st);
     };
+    // Ring slot p to LDS buffer buf (this wavefront alone reads it back).
+    auto stage = [&](int p, int buf) {
+        *(i32x4 *)&wl[buf][lr * RS + lc * 16] = wr[p][0];
+        *(i32x4 *)&wl[buf][(lr + 8) * RS + lc * 16] = wr[p][1];
+#pragma unroll
+        for (int h = 0; h < 2 * TI; ++h) *(i32x4 *)&al[buf][(lr + 8 * h) * RS + lc * 16] = ar[p][h];
+        swl[buf][lane >> 2][lane & 3] = sw[p];
+#pragma unroll
+        for (int i = 0; i < TI; ++i) sal[buf][lane & 3][(lane >> 2) + 16 * i] = sa[p][i];
+    };
     f32x4 acc[TI];
 #pragma unroll
     for (int i = 0; i < TI; ++i) acc[i] = f32x4{};
 #pragma unroll
     for (int p = 0; p < D; ++p) load(p, min(p, steps - 1), true);
+    stage(0, 0);
+    load(0, min(D, steps - 1), false);
+    // Step st is computed from LDS buffer st&1 while step st+1 is staged
+    // into the other one, so the LDS round trip of a step overlaps the MFMAs
+    // and scale-accumulates of the one before.
     for (int s0 = 0; s0 < steps; s0 += D) {
 #pragma unroll
         for (int p = 0; p < D; ++p) {
-            const int st = s0 + p;
-            // The step to LDS (this wavefront alone reads it back).
-            *(i32x4 *)&wl[lr * RS + lc * 16] = wr[p][0];
-            *(i32x4 *)&wl[(lr + 8) * RS + lc * 16] = wr[p][1];
-#pragma unroll
-            for (int h = 0; h < 2 * TI; ++h) *(i32x4 *)&al[(lr + 8 * h) * RS + lc * 16] = ar[p][h];
-            swl[lane >> 2][lane & 3] = sw[p];
-#pragma unroll
-            for (int i = 0; i < TI; ++i) sal[lane & 3][(lane >> 2) + 16 * i] = sa[p][i];
-            load(p, min(st + D, steps - 1), false);
+            const int st = s0 + p, cur = p & 1;  // D is even, so st&1 == p&1
+            const int pn = (p + 1) % D;
+            stage(pn, cur ^ 1);
+            load(pn, min(st + 1 + D, steps - 1), false);
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const long wv = *(const long *)&wl[c * RS + 32 * b + 8 * g];
-                const float w1 = swl[c][b];
+                const long wv = *(const long *)&wl[cur][c * RS + 32 * b + 8 * g];
+                const float w1 = swl[cur][c][b];
 #pragma unroll
                 for (int i = 0; i < TI; ++i) {
-                    const long av = *(const long *)&al[(16 * i + c) * RS + 32 * b + 8 * g];
+                    const long av = *(const long *)&al[cur][(16 * i + c) * RS + 32 * b + 8 * g];
                     const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, i32x4{}, 0, 0, 0);
-                    const float4 s4 = *(const float4 *)&sal[b][16 * i + 4 * g];
+                    const float4 s4 = *(const float4 *)&sal[cur][b][16 * i + 4 * g];
                     const float s_[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) acc[i][e] = __builtin_fmaf((float)d[e], __fmul_rn(s_[e], w1), acc[i][e]);
@@ -415,10 +425,10 @@ int go_small(const Q8bArgs &a, hipStream_t st) {
     return launch_status();
 }
 
-// Ring depth 8 steps (4 KiB of weight rows in flight per wavefront).
+// Ring depth 8 steps for one activation tile, 4 for two (registers).
 template <int TI>
 int launch_small(const Q8bArgs &a, hipStream_t st) {
-    return go_small<TI, 8>(a, st);
+    return go_small<TI, TI == 1 ? 8 : 4>(a, st);
 }
 
 template <int BM, int BN, int WGM, int WGN, int KSB>
