@@ -286,7 +286,7 @@ __device__ __forceinline__ float f16r(float x) {
     return (float)(_Float16)x;
 }
 
-// q4GroupScale (gptq.go:800-827) of the 32 values held one per lane by lanes
+// q4GroupScale (gptq.go:764-791) of the 32 values held one per lane by lanes
 // g .. g+31 of the wavefront (the caller's x is the lane's value): peak = the
 // value of largest magnitude, lowest column on ties; 16 FP16 candidates
 // f16(peak / -8 * (1 - 0.02 step)); the candidate with the smallest float64

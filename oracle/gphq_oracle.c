@@ -199,7 +199,7 @@ void orc_quantize_row_q4(const float *row, int64_t k, uint8_t *dst, uint16_t *sc
     }
 }
 
-/* qwen3lm/gptq.go:798-827 q4GroupScale: the same 16-candidate search as
+/* qwen3lm/gptq.go:762-791 q4GroupScale: the same 16-candidate search as
  * quantizeRowQ4, but the squared error is accumulated in float64. */
 float orc_q4_group_scale(const float *v, int64_t len) {
     float peak = 0.0f;
@@ -601,11 +601,6 @@ static float mm_weight(int fmt, const void *codes, const void *scales, const uin
     if (fmt == 8) return (float)((const int8_t *)codes)[row * k + i];
     if (fmt == 9) {
         float d = orc_f16_to_f32(((const uint16_t *)scales)[row * (k / 32) + i / 32]);
-        float c = (float)((const int8_t *)codes)[row * k + i];
-        return orc_f16_to_f32(orc_f32_to_f16(c * d));
-    }
-    if (fmt == 10) { /* Q8B with fp32 block scales: half(code) * half(d), rounded to half */
-        float d = orc_f16_to_f32(orc_f32_to_f16(((const float *)scales)[row * (k / 32) + i / 32]));
         float c = (float)((const int8_t *)codes)[row * k + i];
         return orc_f16_to_f32(orc_f32_to_f16(c * d));
     }

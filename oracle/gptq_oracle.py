@@ -55,7 +55,7 @@ def inverse_factor(h):
 
 
 def q4_group_scale(v):
-    """gptq.go:800-827 (the C oracle's restatement, float64 error sums)."""
+    """gptq.go:764-791 (the C oracle's restatement, float64 error sums)."""
     return float(orc.q4_group_scale(np.asarray(v, np.float32)))
 
 

@@ -170,7 +170,7 @@ def quantize_row_q4(row, mul=1.0):
 
 
 def q4_group_scale(v):
-    """qwen3lm q4GroupScale (gptq.go:798-827)."""
+    """qwen3lm q4GroupScale (gptq.go:762-791)."""
     v = _c(v, np.float32)
     return np.float32(lib().orc_q4_group_scale(_p(v, _f32p), v.size))
 
