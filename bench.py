@@ -608,7 +608,7 @@ def main():
     cpus = None if args.no_cpu else cpu_baselines(args.cpu_seconds / 2)
     # The persistent GEMV's template shape for config 1 (gemv.hip persistent_shape):
     # <format, K steps per wave, rows per group, K slices, waves per block, GEMVs per launch>.
-    kernel = "gemvp_kernel<Q8B_F32,2,4,2,4,32>" if args.mode == "batch" else "gemvp_kernel<Q8B_F32,2,4,2,8,1>"
+    kernel = "gemvb_kernel<Q8B_F32,4,2,2,8>" if args.mode == "batch" else "gemvp_kernel<Q8B_F32,2,4,2,8,1>"
     traffic = measured_traffic(kernel) if args.rotations == 32 else None
     out = {
         "metric": "Q8 GEMV HBM GB/s (% of peak) + Qwen3-8B Q8 decode ms/token, 1 MI355X",

@@ -24,6 +24,8 @@
 // sums and applies the row scale after the reduction (also q8gemv/scalar.go);
 // Q4 takes one 32-value block per lane step and computes
 // acc = fma(d, sum(nib*x) - 8*sum(x), acc).
+#include <type_traits>
+
 #include "common.h"
 
 namespace gphq {
@@ -62,18 +64,16 @@ __device__ __forceinline__ float sext_byte_f(uint32_t v, int i) {
 }
 
 // Dot product of 16 int8 codes (one 128-bit load) with 16 fp32 activations,
-// as four 4-wide dot products summed (gpu.metal:91-92).
+// as four 4-wide dot products summed (gpu.metal:91-92). Written as explicit
+// fmaf chains so every kernel that inlines it rounds the same way (left to
+// contraction, the compiler may fuse differently in different kernels, and
+// the batch and single-GEMV paths must agree bit for bit).
+__device__ __forceinline__ float dot4(uint32_t w, const float4 x) {
+    return fmaf(sext_byte_f(w, 3), x.w, fmaf(sext_byte_f(w, 2), x.z, fmaf(sext_byte_f(w, 1), x.y, sext_byte_f(w, 0) * x.x)));
+}
 __device__ __forceinline__ float dot16(const u32x4 w, const float4 x0, const float4 x1, const float4 x2,
                                        const float4 x3) {
-    float d0 = sext_byte_f(w.x, 0) * x0.x + sext_byte_f(w.x, 1) * x0.y + sext_byte_f(w.x, 2) * x0.z +
-               sext_byte_f(w.x, 3) * x0.w;
-    float d1 = sext_byte_f(w.y, 0) * x1.x + sext_byte_f(w.y, 1) * x1.y + sext_byte_f(w.y, 2) * x1.z +
-               sext_byte_f(w.y, 3) * x1.w;
-    float d2 = sext_byte_f(w.z, 0) * x2.x + sext_byte_f(w.z, 1) * x2.y + sext_byte_f(w.z, 2) * x2.z +
-               sext_byte_f(w.z, 3) * x2.w;
-    float d3 = sext_byte_f(w.w, 0) * x3.x + sext_byte_f(w.w, 1) * x3.y + sext_byte_f(w.w, 2) * x3.z +
-               sext_byte_f(w.w, 3) * x3.w;
-    return d0 + d1 + d2 + d3;
+    return ((dot4(w.x, x0) + dot4(w.y, x1)) + dot4(w.z, x2)) + dot4(w.w, x3);
 }
 
 template <int FMT>
@@ -456,6 +456,111 @@ __global__ __launch_bounds__(64 * WPB) void gemvp_kernel(const GemvBatch<MAXB> b
     }
 }
 
+// Batch GEMV (gphq_gemv_batch, 8-bit formats, K = NS * 1024 up to 4096): a
+// wavefront holds all of x (NS KiB steps) in registers and walks a
+// contiguous run of row groups of RW rows (set by set), with the next
+// group's codes and block scales requested before the current group's
+// arithmetic (two register buffers); no LDS and no barriers. Each row's sum
+// is formed as the persistent kernel forms it for the same K: SL slices of
+// NS/SL steps, each accumulated in step order and reduced across the
+// wavefront, then added in slice order, so a batch launch gives the same
+// bits as single launches. Measured on MI355X at config 1 (32 sets of
+// 4096 x 4096 Q8B_F32, 605 MB): 96.5 us per launch against 100-103 for the
+// persistent kernel with LDS slice merges.
+template <int FMT, int NS, int SL, int RW, int WPB>
+__global__ __launch_bounds__(64 * WPB) void gemvb_kernel(const GemvBatch<kMaxBatch> b, int count, int per) {
+    static_assert(NS % SL == 0, "slices of whole steps");
+    constexpr int K = NS * 1024, SS = NS / SL;
+    constexpr size_t kb = K >> 5;
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int N = b.N;
+    const int gps = (N + RW - 1) / RW;
+    const int total = gps * count;
+    int g = wave * per;
+    const int gend = min(g + per, total);
+    if (g >= gend) return;
+    float4 xr[NS][4];
+    u32x4 w[2][NS][RW];
+    float d[2][NS][RW];
+    auto issue = [&](int gg, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const int set = gg / gps, lg = gg - set * gps;
+        const GemvSet &s = b.set[set];
+        const int row0 = lg * RW;
+        const int8_t *W = (const int8_t *)s.codes;
+        if constexpr (FMT != GPHQ_FMT_Q8) {
+#pragma unroll
+            for (int j = 0; j < NS; ++j)
+#pragma unroll
+                for (int r = 0; r < RW; ++r)
+                    d[buf][j][r] = block_scale<FMT>(s.scales, (size_t)min(row0 + r, N - 1) * kb + j * 32 + (lane >> 1));
+        }
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                w[buf][j][r] = __builtin_nontemporal_load(
+                    (const u32x4 *)(W + (size_t)min(row0 + r, N - 1) * K + j * 1024 + lane * 16));
+    };
+    auto load_x = [&](int set) {
+        const float *x = b.set[set].x;
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xr[j][i] = *((const float4 *)(x + j * 1024 + lane * 16) + i);
+    };
+    auto compute = [&](int gg, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const int set = gg / gps, lg = gg - set * gps;
+        float t[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) t[r] = 0.0f;
+#pragma unroll
+        for (int sl = 0; sl < SL; ++sl) {
+            float acc[RW];
+#pragma unroll
+            for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+#pragma unroll
+            for (int jj = 0; jj < SS; ++jj) {
+                const int j = sl * SS + jj;
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    const float v = dot16(w[buf][j][r], xr[j][0], xr[j][1], xr[j][2], xr[j][3]);
+                    if constexpr (FMT == GPHQ_FMT_Q8)
+                        acc[r] += v;
+                    else
+                        acc[r] = fmaf(d[buf][j][r], v, acc[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+                const float ws = wave_sum(acc[r]);
+                t[r] = sl == 0 ? ws : t[r] + ws;
+            }
+        }
+        if (lane == 0) finish_group<FMT, PRO_PLAIN, EPI_STORE, RW>(b.set[set], t, lg * RW, N, 1.0f);
+    };
+    int cur = g / gps;
+    load_x(cur);
+    issue(g, std::integral_constant<int, 0>{});
+    for (; g < gend; g += 2) {
+        if (g + 1 < gend) issue(g + 1, std::integral_constant<int, 1>{});
+        if (g / gps != cur) {
+            cur = g / gps;
+            load_x(cur);
+        }
+        compute(g, std::integral_constant<int, 0>{});
+        if (g + 1 >= gend) break;
+        if (g + 2 < gend) issue(g + 2, std::integral_constant<int, 0>{});
+        if ((g + 1) / gps != cur) {
+            cur = (g + 1) / gps;
+            load_x(cur);
+        }
+        compute(g + 1, std::integral_constant<int, 1>{});
+    }
+}
+
 // GPTQ int4 GEMV (GPHQ_FMT_GPTQ4_G128 at one activation row): codes int32
 // [N][K/8] (nibble i of word j is k = 8j + i), FP16 scales [N][K/128], 4-bit
 // zero points u8 [N][K/128]; y[n] = sum_g s_g * sum_{k in g} (q - z_g) *
@@ -735,8 +840,42 @@ static int launch_persistent(const GemvBatch<MAXB> &b, int count, const Persiste
 
 // The persistent path for one format, or GPHQ_ERR_UNSUPPORTED when the shape
 // is not one it takes (the caller then uses the per-tile kernel).
+// The batch kernel for K = 1024 .. 4096 (slices as persistent_shape's batch
+// shape for that K): RW = 2 rows per group, 8 wavefronts per block, 3 blocks
+// per CU (measured at config 1).
+template <int FMT, int NS, int SL>
+static int go_batch(const GemvBatch<kMaxBatch> &b, int count, hipStream_t stream) {
+    constexpr int RW = 2, WPB = 8, BPC = 3;
+    const long total = (long)((b.N + RW - 1) / RW) * count;
+    const long blocks = std::max(1L, std::min((total + WPB - 1) / WPB, (long)device_cus() * BPC));
+    const int per = (int)((total + blocks * WPB - 1) / (blocks * WPB));
+    hipLaunchKernelGGL((gemvb_kernel<FMT, NS, SL, RW, WPB>), dim3((unsigned)blocks), dim3(64 * WPB), 0, stream, b,
+                       count, per);
+    return launch_status();
+}
+
+template <int FMT>
+static int launch_batch_b(const GemvBatch<kMaxBatch> &b, int count, hipStream_t stream) {
+    switch (b.K) {
+    case 1024: return go_batch<FMT, 1, 1>(b, count, stream);
+    case 2048: return go_batch<FMT, 2, 1>(b, count, stream);
+    case 3072: return b.N > 4096 ? go_batch<FMT, 3, 1>(b, count, stream) : go_batch<FMT, 3, 3>(b, count, stream);
+    case 4096: return go_batch<FMT, 4, 2>(b, count, stream);
+    }
+    return GPHQ_ERR_UNSUPPORTED;
+}
+
 template <int PRO, int EPI, int MAXB>
 static int try_persistent(int fmt, const GemvBatch<MAXB> &b, int count, hipStream_t stream) {
+    if constexpr (MAXB > 1 && PRO == PRO_PLAIN && EPI == EPI_STORE) {
+        int st = GPHQ_ERR_UNSUPPORTED;
+        switch (fmt) {
+        case GPHQ_FMT_Q8: st = launch_batch_b<GPHQ_FMT_Q8>(b, count, stream); break;
+        case GPHQ_FMT_Q8B: st = launch_batch_b<GPHQ_FMT_Q8B>(b, count, stream); break;
+        case GPHQ_FMT_Q8B_F32: st = launch_batch_b<GPHQ_FMT_Q8B_F32>(b, count, stream); break;
+        }
+        if (st != GPHQ_ERR_UNSUPPORTED) return st;
+    }
     PersistentShape p;
     if (!persistent_shape(b.K, b.N, MAXB > 1, p)) return GPHQ_ERR_UNSUPPORTED;
     switch (fmt) {
