@@ -544,8 +544,8 @@ def decode_benchmarks(args, torch, gphq):
 
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed FETCH_SIZE / WRITE_SIZE
-    profile (profiles/gemvp_config1_traffic.md), or None."""
-    path = os.path.join(ROOT, "profiles", "gemvp_config1_traffic.json")
+    profile (profiles/gemvb_config1_traffic.md), or None."""
+    path = os.path.join(ROOT, "profiles", "gemvb_config1_traffic.json")
     try:
         with open(path) as f:
             rec = json.load(f)
@@ -606,8 +606,9 @@ def main():
     decode = None if args.no_decode else decode_benchmarks(args, torch, gphq)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     cpus = None if args.no_cpu else cpu_baselines(args.cpu_seconds / 2)
-    # The persistent GEMV's template shape for config 1 (gemv.hip persistent_shape):
-    # <format, K steps per wave, rows per group, K slices, waves per block, GEMVs per launch>.
+    # The config-1 kernels (gemv.hip): the batch kernel <format, K steps per wave, slices,
+    # rows per group, waves per block>; the single-GEMV persistent kernel <format, K steps
+    # per wave, rows per group, K slices, waves per block, GEMVs per launch>.
     kernel = "gemvb_kernel<Q8B_F32,4,2,2,8>" if args.mode == "batch" else "gemvp_kernel<Q8B_F32,2,4,2,8,1>"
     traffic = measured_traffic(kernel) if args.rotations == 32 else None
     out = {
@@ -641,7 +642,7 @@ def main():
             "traffic": traffic,
             "traffic_source": None if traffic is None else
             "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this launch, copy-kernel calibrated "
-            "(profiles/gemvp_config1_traffic.md)",
+            "(profiles/gemvb_config1_traffic.md)",
             "kernel": kernel,
             "per_launch_us": round(r["per_launch_us"], 3),
             "bytes_per_launch": r["bytes_per_launch"],
