@@ -563,13 +563,13 @@ int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const
     a.c1 = c1;
     a.tileN0 = c0 / 16;
     // Shapes picked by measurement on MI355X at K = 4096, N = 12288 (M = 512:
-    // 78.5 us with 128 x 64 LDS tiles, 55.8 with 128 x 128 big tiles, 54.3
-    // with 256 x 128).
+    // 78.5 us with 128 x 64 LDS tiles, 49.0 with 256 x 128 big tiles, 46.1
+    // with 128 x 192, one tile per CU).
     if (M <= 16) return launch_i8gemm<1, 2, 1, 2, 4, 4>(a, stream);
     if (M <= 64) return launch_i8gemm<4, 1, 1, 2, 4, 4>(a, stream);
     if (M <= 192) return launch_i8gemm_lds<128, 64, 2, 2, 4>(a, stream);
     if (M < 512) return launch_i8gemm_big<128, 128, 2, 2>(a, stream);
-    return launch_i8gemm_big<256, 128, 4, 2>(a, stream);
+    return launch_i8gemm_big<128, 192, 4, 2>(a, stream);
 }
 
 int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {
