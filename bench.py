@@ -40,9 +40,9 @@ def parse():
     ap.add_argument("--decode-fmt", choices=["q8b", "q8b_f32", "q8", "q4"], default="q8b",
                     help="layer weight format of the decode models (the reference's decode batch uses Q8B)")
     ap.add_argument("--decode-eager", action="store_true", help="launch decode steps without the HIP graph")
-    ap.add_argument("--decode-configs", default="3,4a,4b1,4b16",
+    ap.add_argument("--decode-configs", default="3,4a,4a8,4b1,4b16",
                     help="model lines to run: 3 (Qwen3-0.6B decode), 4a (Qwen3-8B 4096-token prefill), "
-                    "4b1 / 4b16 (Qwen3-8B decode, 1 / 16 lanes)")
+                    "4a8 (4a on the int8 route, Q8 layers), 4b1 / 4b16 (Qwen3-8B decode, 1 / 16 lanes)")
     return ap.parse_args()
 
 
@@ -456,14 +456,18 @@ def decode_config(torch, gphq, lm, weight_bytes, geom, lanes, ctx, steps, warmup
     }
 
 
-def prefill_config(torch, gphq, lm, geom, tokens, reps, label):
+def prefill_config(torch, gphq, lm, geom, tokens, reps, label, int8=False):
     """Config 4a: one `tokens`-token prompt evaluated by the batched pass
     (gphq_prefill_extend, one pass of `tokens` rows) into a fresh prefix, timed
     with HIP events on the launch stream over `reps` prefills after one
     untimed prefill. FLOPs are algorithmic: 2 per weight per token for the
-    projections, 4 * head_dim per (query head, visible key) for attention."""
+    projections, 4 * head_dim per (query head, visible key) for attention.
+    int8: the int8 route (Q8 layers; per-row int8 activations, exact int32
+    products on int8 MFMA)."""
     stream = torch.cuda.current_stream()
     ws = gphq.Prefill(lm, tokens)
+    if int8:
+        ws.set_arith(gphq.PASS_INT8)
     kv = gphq.Prefix(lm, tokens)
     rng = np.random.default_rng(tokens)
     ids = rng.integers(0, geom["vocab"], tokens)
@@ -483,7 +487,7 @@ def prefill_config(torch, gphq, lm, geom, tokens, reps, label):
     proj = 2.0 * weights * tokens
     attn = 4.0 * 128 * geom["heads"] * L * tokens * (tokens + 1) / 2
     tf = (proj + attn) / (ms / 1e3) / 1e12
-    return {
+    rec = {
         "workload": label,
         "tokens": tokens,
         "reps": reps,
@@ -496,6 +500,14 @@ def prefill_config(torch, gphq, lm, geom, tokens, reps, label):
         "arithmetic": "FP16 weight/activation tiles, fp32 accumulate (the reference mm); FP16 attention tiles",
         "finite": bool(torch.isfinite(hidden).all().item()),
     }
+    if int8:
+        # Projections on int8 MFMA, attention on FP16 MFMA: the fraction of
+        # each peak the whole pass would reach if it ran at that rate alone.
+        del rec["fp16_mfma_frac"]
+        rec["arithmetic"] = ("int8 route: per-row int8 activations (WorkspaceI8) x Q8 per-row int8 weights, exact "
+                             "int32 sums, MulPanelsI8 scaling (the reference's CPU int8 path); FP16 attention tiles")
+        rec["int8_mfma_frac_of_projection_ops"] = round(proj / (ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4)
+    return rec
 
 
 FORMAT_DESC = {
@@ -528,6 +540,16 @@ def decode_benchmarks(args, torch, gphq):
         if "4b16" in want:
             res["config4b_16"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 16, 4096, 32, 4, graph,
                                                "config 4b: Qwen3-8B-shaped decode at context 4096, 16 lanes")
+        del lm
+        torch.cuda.empty_cache()
+    if "4a8" in want:
+        # Config 4a on the int8 route: Q8 layers (one fp32 scale per row, the
+        # format the int8 route multiplies exactly).
+        lm, _ = decode_model(torch, gphq, QWEN3_8B, gphq.FMT_Q8, 4)
+        line = prefill_config(torch, gphq, lm, QWEN3_8B, 4096, 3,
+                              "config 4a: Qwen3-8B-shaped 4096-token prefill, one batched pass, int8 route", int8=True)
+        line["weights"] = FORMAT_DESC["q8"]
+        res["config4a_int8"] = line
         del lm
         torch.cuda.empty_cache()
     if "4b1" in want and fmt != gphq.FMT_Q8B_F32:

@@ -111,6 +111,29 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// ---- int8 activation quantization (WorkspaceI8) --------------------------------
+
+// quantize (int8.go:163-168): round half to even, saturate; a NaN (x * 0 for a
+// non-finite row) converts to 0, as Go's float->int8 conversion does on amd64
+// and arm64.
+__device__ __forceinline__ int8_t quantize_i8(float v) {
+    if (v != v) return 0;
+    const float r = rintf(v);
+    return (int8_t)fminf(fmaxf(r, -128.0f), 127.0f);
+}
+
+// SetRowScale (int8.go:106-112): max/127 and 127/max for finite positive max,
+// else 0 and 0. fp32 division is correctly rounded (hipcc default).
+__device__ __forceinline__ void i8_row_scale(float m, float &scale, float &inv) {
+    if (m > 0.0f && !isinf(m) && m == m) {
+        scale = m / 127.0f;
+        inv = 127.0f / m;
+    } else {
+        scale = 0.0f;
+        inv = 0.0f;
+    }
+}
+
 // ---- GEMM tiling helpers ------------------------------------------------------
 
 // Block b's output tile (bm, bn). Workgroups are dispatched to the 8 XCDs

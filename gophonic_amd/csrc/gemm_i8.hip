@@ -61,27 +61,6 @@ __global__ void i8_pack_tiles_kernel(const int8_t *__restrict__ src, int8_t *__r
 }
 
 // ---- activation quantizer ---------------------------------------------------
-// quantize (int8.go:163-168): round half to even, saturate; a NaN (x * 0 for a
-// non-finite row) converts to 0, as Go's float->int8 conversion does on amd64
-// and arm64.
-__device__ __forceinline__ int8_t quantize_i8(float v) {
-    if (v != v) return 0;
-    const float r = rintf(v);
-    return (int8_t)fminf(fmaxf(r, -128.0f), 127.0f);
-}
-
-// SetRowScale (int8.go:106-112): max/127 and 127/max for finite positive max,
-// else 0 and 0. fp32 division is correctly rounded (hipcc default).
-__device__ __forceinline__ void i8_row_scale(float m, float &scale, float &inv) {
-    if (m > 0.0f && !isinf(m) && m == m) {
-        scale = m / 127.0f;
-        inv = 127.0f / m;
-    } else {
-        scale = 0.0f;
-        inv = 0.0f;
-    }
-}
-
 // Workspace Pack fused: per row (one block each), MaxAbs with NaN propagation
 // (gemm.go:138-150), SetRowScale, then quantize every column into the tile
 // layout (and zero the row's K padding).
@@ -169,10 +148,77 @@ __global__ __launch_bounds__(256) void i8_pack_range_kernel(const float *__restr
     }
 }
 
+// The qwen3lm batched pass's int8 activations, the CPU provider's int8 route
+// (qwen3lm/ops.go:96-147: the row is normalized, SetRowScale(MaxAbs), then
+// PackRange) over the GPU layer formats: per row v = x * f with f the RMSNorm
+// factor (MODE 2, the FP16 packer's sum order) or 1 (MODE 1); SetRowScale of
+// max|v| (NaN-propagating); q = quantize(v * inv) written row-major
+// [rows][K]; rowScale[r] = max / 127. One block per row, the row in
+// registers (CPT chunks of 16 values per thread).
+template <int MODE, int CPT>
+__global__ __launch_bounds__(256) void i8_act_rows_kernel(const float *__restrict__ x, long stride, int K, float eps,
+                                                          int8_t *__restrict__ act, float *__restrict__ rowScale) {
+    __shared__ float sss[4], smx[4];
+    __shared__ int snan[4];
+    const int row = blockIdx.x;
+    const float *xr = x + (size_t)row * stride;
+    float4 v[CPT][4];
+    float ss = 0.0f, mx = 0.0f;
+    int nan = 0;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int k = 16 * ((int)threadIdx.x + 256 * c);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[c][q] = k < K ? *(const float4 *)(xr + k + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
+            ss += v[c][q].x * v[c][q].x + v[c][q].y * v[c][q].y + v[c][q].z * v[c][q].z + v[c][q].w * v[c][q].w;
+            mx = fmaxf(fmaxf(fmaxf(mx, fabsf(v[c][q].x)), fmaxf(fabsf(v[c][q].y), fabsf(v[c][q].z))), fabsf(v[c][q].w));
+            nan |= (v[c][q].x != v[c][q].x) | (v[c][q].y != v[c][q].y) | (v[c][q].z != v[c][q].z) |
+                   (v[c][q].w != v[c][q].w);
+        }
+    }
+    ss = wave_sum(ss);
+    for (int off = 32; off > 0; off >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+        nan |= __shfl_xor(nan, off);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sss[threadIdx.x >> 6] = ss;
+        smx[threadIdx.x >> 6] = mx;
+        snan[threadIdx.x >> 6] = nan;
+    }
+    __syncthreads();
+    const float f = MODE == 2 ? 1.0f / sqrtf(((sss[0] + sss[1]) + (sss[2] + sss[3])) / (float)K + eps) : 1.0f;
+    // max |x * f| is (max |x|) * f: rounding is monotonic.
+    float m = __fmul_rn(fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3])), f);
+    if (snan[0] | snan[1] | snan[2] | snan[3]) m = __builtin_nanf("");
+    float scale, inv;
+    i8_row_scale(m, scale, inv);
+    if (threadIdx.x == 0) rowScale[row] = scale;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int k = 16 * ((int)threadIdx.x + 256 * c);
+        if (k >= K) continue;
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float e[4] = {v[c][q].x, v[c][q].y, v[c][q].z, v[c][q].w};
+            uint32_t packed = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float y = MODE == 2 ? __fmul_rn(e[i], f) : e[i];
+                packed |= (uint32_t)(uint8_t)quantize_i8(__fmul_rn(y, inv)) << (8 * i);
+            }
+            w[q] = packed;
+        }
+        *(uint4 *)(act + (size_t)row * K + k) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 // ---- GEMM ------------------------------------------------------------------
 struct I8GemmArgs {
-    const int8_t *A;      // activations, tile layout, MT x KT groups
-    const int8_t *B;      // weights, tile layout, NT x KT groups
+    const int8_t *A;      // activations, tile layout, MT x KT groups (row-major [M][K] for I8_ROWS)
+    const int8_t *B;      // weights, tile layout, NT x KT groups (row-major [N][K] for I8_ROWS)
     const float *rowScale;  // [M]
     const float *colScale;  // [N]
     float *dst;
@@ -181,7 +227,12 @@ struct I8GemmArgs {
     int c0, c1;  // output columns [c0, c1)
     int tileN0;  // first 16-column tile covered by the grid
     int gridM, gridN;  // blocks along M and N
+    int K;             // row length in bytes of row-major operands (a multiple of 16)
 };
+
+// Operand layouts and epilogues of the big-tile kernel.
+enum { I8_TILES = 0, I8_ROWS = 1 };
+enum { I8_EPI_STORE = 0, I8_EPI_ADD = 1, I8_EPI_SWIGLU = 2 };
 
 template <int TM, int TN, int WM, int WN, int SK, int U>
 __global__ __launch_bounds__(64 * WM * WN * SK) void i8gemm_kernel(const I8GemmArgs a) {
@@ -400,14 +451,17 @@ __global__ __launch_bounds__(64 * WM * WN) void i8gemm_lds_kernel(const I8GemmAr
 }
 
 // Large-M variant: BM x BN block tiles (WGM x WGN wavefronts, each a grid of
-// 32 x 32 v_mfma_i32_32x32x32_i8 tiles), 128-deep K steps (two tile-layout
-// groups) staged through LDS as 128-byte rows with the row-swizzled 16-byte
-// chunks of the FP16 big-tile GEMM, double-buffered with the next step's
-// global loads in flight; XCD-grouped tile order. Exact int32 sums, so the
-// bits equal the other kernels'.
-template <int BM, int BN, int WGM, int WGN>
+// 32 x 32 v_mfma_i32_32x32x32_i8 tiles), 128-deep K steps staged through LDS
+// as 128-byte rows with the row-swizzled 16-byte chunks of the FP16 big-tile
+// GEMM, double-buffered with the next step's global loads in flight;
+// XCD-grouped tile order. Exact int32 sums, so the bits equal the other
+// kernels'. Operands come in the tile layout (two 64-deep groups per step) or,
+// for I8_ROWS, as row-major int8 rows (8 consecutive lanes read one row's 128
+// bytes of the step). Epilogue: (float32(sum) * colScale) * rowScale, then a
+// store, an add into dst (I8_EPI_ADD), or the SwiGLU of interleaved gate/up
+// columns into dst[row][col / 2] (I8_EPI_SWIGLU).
+template <int BM, int BN, int WGM, int WGN, int LAYOUT, int EPI>
 __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8GemmArgs a) {
-    typedef float f32x16 __attribute__((ext_vector_type(16)));
     typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
     constexpr int NT = 64 * WGM * WGN;
     constexpr int TI = BM / WGM / 32, TJ = BN / WGN / 32;
@@ -422,26 +476,41 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
     const int rt0 = bm * (BM / 16), ct0 = a.tileN0 + bn * (BN / 16);
     const int MT = (a.M + 15) >> 4, KT = a.KT;
     const int steps = (KT + 1) / 2;
-    // Unit u = i*NT + t of a step: 16-row tile u/128, group (u/64)%2 of the
-    // step, lane slot u%64 (row slot%16, K bytes 16*(slot/16) of the group).
+    // Tile layout: unit u = i*NT + t of a step is 16-row tile u/128, group
+    // (u/64)%2 of the step, lane slot u%64 (row slot%16, K bytes
+    // 16*(slot/16) of the group). Rows: unit u is row u/8, chunk u%8.
     auto gload = [&](const int8_t *base, int tile0, int tiles, int u, int st) {
-        const int kt = 2 * st + ((u >> 6) & 1);
         i32x4 v = i32x4{0, 0, 0, 0};
-        if (kt < KT)
-            v = *(const i32x4 *)(base + ((size_t)min(tile0 + (u >> 7), tiles - 1) * KT + kt) * 1024 +
-                                 (size_t)(u & 63) * 16);
+        if constexpr (LAYOUT == I8_ROWS) {
+            // Rows past the operand's last read that row again (their
+            // outputs are not stored); K past the row end reads zero.
+            const int k = st * 128 + (u & 7) * 16;
+            if (k < a.K) v = *(const i32x4 *)(base + (size_t)min(tile0 * 16 + (u >> 3), tiles - 1) * a.K + k);
+        } else {
+            const int kt = 2 * st + ((u >> 6) & 1);
+            if (kt < KT)
+                v = *(const i32x4 *)(base + ((size_t)min(tile0 + (u >> 7), tiles - 1) * KT + kt) * 1024 +
+                                     (size_t)(u & 63) * 16);
+        }
         return v;
     };
     auto lidx = [](int u) {
-        const int r = (u >> 7) * 16 + (u & 15);
-        return r * 8 + big_swz(r, ((u >> 6) & 1) * 4 + ((u & 63) >> 4));
+        if constexpr (LAYOUT == I8_ROWS) {
+            const int r = u >> 3;
+            return r * 8 + big_swz(r, u & 7);
+        } else {
+            const int r = (u >> 7) * 16 + (u & 15);
+            return r * 8 + big_swz(r, ((u >> 6) & 1) * 4 + ((u & 63) >> 4));
+        }
     };
+    // Row bounds passed to gload: 16-row tiles in the tile layout, rows for I8_ROWS.
+    const int aRows = LAYOUT == I8_ROWS ? a.M : MT, bRows = LAYOUT == I8_ROWS ? a.N : a.NT;
     i32x4 ar[AL], br[BL];
     auto load = [&](int st) {
 #pragma unroll
-        for (int i = 0; i < AL; ++i) ar[i] = gload(a.A, rt0, MT, i * NT + t, st);
+        for (int i = 0; i < AL; ++i) ar[i] = gload(a.A, rt0, aRows, i * NT + t, st);
 #pragma unroll
-        for (int i = 0; i < BL; ++i) br[i] = gload(a.B, ct0, a.NT, i * NT + t, st);
+        for (int i = 0; i < BL; ++i) br[i] = gload(a.B, ct0, bRows, i * NT + t, st);
     };
     auto store = [&](int buf) {
 #pragma unroll
@@ -497,28 +566,57 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
         __syncthreads();
     }
     // Epilogue as MulPanelsI8: (float32(sum) * colScale) * rowScale.
+    if constexpr (EPI == I8_EPI_STORE) {
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
-        if (col < a.c0 || col >= a.c1) continue;
-        const float cs = a.colScale[col];
+        for (int j = 0; j < TJ; ++j) {
+            const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
+            if (col < a.c0 || col >= a.c1) continue;
+            const float cs = a.colScale[col];
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = (rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3);
-                if (row < a.M)
-                    a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row]);
-            }
+                for (int e = 0; e < 16; ++e) {
+                    const int row = (rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3);
+                    if (row < a.M)
+                        a.dst[(size_t)row * a.stride + col] =
+                            __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row]);
+                }
+        }
+    } else {
+        // Every lane runs the SwiGLU exchange, so no lane leaves the loop early.
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
+            const bool colOk = col >= a.c0 && col < a.c1;
+            const float cs = colOk ? a.colScale[col] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = (rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3);
+                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row < a.M ? row : 0]);
+                    if constexpr (EPI == I8_EPI_SWIGLU) {
+                        // The up value of the neighbouring lane (DPP quad_perm [1,0,3,2]).
+                        const float u = __builtin_bit_cast(
+                            float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+                        if (colOk && !(col & 1) && row < a.M)
+                            a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
+                    } else if (colOk && row < a.M) {
+                        // One fp32 add into the residual, done in L2 (each
+                        // element has one owner, so the sum is y + v exactly).
+                        __builtin_amdgcn_global_atomic_fadd_f32(a.dst + (size_t)row * a.stride + col, v);
+                    }
+                }
+        }
     }
 }
 
-template <int BM, int BN, int WGM, int WGN>
+template <int BM, int BN, int WGM, int WGN, int LAYOUT = I8_TILES, int EPI = I8_EPI_STORE>
 static int launch_i8gemm_big(I8GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
     a.gridN = (tiles * 16 + BN - 1) / BN;
     a.gridM = (a.M + BM - 1) / BM;
-    hipLaunchKernelGGL((i8gemm_big_kernel<BM, BN, WGM, WGN>), dim3((unsigned)(a.gridM * a.gridN)),
+    hipLaunchKernelGGL((i8gemm_big_kernel<BM, BN, WGM, WGN, LAYOUT, EPI>), dim3((unsigned)(a.gridM * a.gridN)),
                        dim3(64 * WGM * WGN), 0, stream, a);
     return launch_status();
 }
@@ -570,6 +668,63 @@ int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const
     if (M <= 192) return launch_i8gemm_lds<128, 64, 2, 2, 4>(a, stream);
     if (M < 512) return launch_i8gemm_big<128, 128, 2, 2>(a, stream);
     return launch_i8gemm_big<128, 192, 4, 2>(a, stream);
+}
+
+template <int MODE>
+static int launch_i8_act_rows(const float *x, long stride, int rows, int K, float eps, int8_t *act, float *rowScale,
+                              hipStream_t stream) {
+    const int chunks = K / 16;
+    if (chunks <= 256)
+        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, 1>), dim3(rows), dim3(256), 0, stream, x, stride, K, eps, act,
+                           rowScale);
+    else if (chunks <= 512)
+        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, 2>), dim3(rows), dim3(256), 0, stream, x, stride, K, eps, act,
+                           rowScale);
+    else if (chunks <= 768)
+        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, 3>), dim3(rows), dim3(256), 0, stream, x, stride, K, eps, act,
+                           rowScale);
+    else
+        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, 4>), dim3(rows), dim3(256), 0, stream, x, stride, K, eps, act,
+                           rowScale);
+    return launch_status();
+}
+
+// int8 activations of the batched pass (see i8_act_rows_kernel): x rows
+// `stride` floats apart and 16-byte aligned, K % 16 == 0, K <= 16384; act is
+// row-major [rows][K].
+int lm_i8_act(const float *x, long stride, int rows, int K, bool norm, float eps, int8_t *act, float *rowScale,
+              hipStream_t stream) {
+    if (rows == 0) return GPHQ_OK;
+    if (norm) return launch_i8_act_rows<2>(x, stride, rows, K, eps, act, rowScale, stream);
+    return launch_i8_act_rows<1>(x, stride, rows, K, eps, act, rowScale, stream);
+}
+
+// One projection of the batched pass on the int8 route: y = (float32(A W^T)
+// * w_scale) * a_scale for row-major int8 activations A [M][K] and Q8 codes W
+// [N][K] (one fp32 scale per weight row), then epi 0 stores y[M][N], 1 adds
+// it into y, 2 stores the SwiGLU of interleaved gate/up columns into
+// y[M][N/2]; y rows are y_stride floats apart. K % 16 == 0.
+int lm_i8_mm(int epi, const int8_t *act, const float *a_scale, const int8_t *codes, const float *w_scale, float *y,
+             long y_stride, int M, int K, int N, hipStream_t stream) {
+    if (M == 0 || N == 0) return GPHQ_OK;
+    I8GemmArgs a{};
+    a.A = act;
+    a.B = codes;
+    a.rowScale = a_scale;
+    a.colScale = w_scale;
+    a.dst = y;
+    a.stride = y_stride;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.KT = (K + 63) / 64;
+    a.NT = (N + 15) / 16;
+    a.c0 = 0;
+    a.c1 = N;
+    a.tileN0 = 0;
+    if (epi == 0) return launch_i8gemm_big<256, 128, 4, 2, I8_ROWS, I8_EPI_STORE>(a, stream);
+    if (epi == 1) return launch_i8gemm_big<256, 128, 4, 2, I8_ROWS, I8_EPI_ADD>(a, stream);
+    return launch_i8gemm_big<256, 128, 4, 2, I8_ROWS, I8_EPI_SWIGLU>(a, stream);
 }
 
 int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {

@@ -36,6 +36,10 @@ int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float e
                 hipStream_t stream);
 int lm_mm_launch(int fmt, int epi, const void *codes, const void *scales, const _Float16 *act, const float *rowInv,
                  float *y, long y_stride, int M, int K, int N, hipStream_t stream);
+int lm_i8_act(const float *x, long stride, int rows, int K, bool norm, float eps, int8_t *act, float *rowScale,
+              hipStream_t stream);
+int lm_i8_mm(int epi, const int8_t *act, const float *a_scale, const int8_t *codes, const float *w_scale, float *y,
+             long y_stride, int M, int K, int N, hipStream_t stream);
 }  // namespace gphq
 
 using namespace gphq;
@@ -49,6 +53,9 @@ struct gphq_prefill {
     int32_t *tok, *nonfinite;
     int32_t *rowpos, *rowstart;  // packed passes: each row's position and its sequence's first row
     float *okc = nullptr, *ovc = nullptr;  // packed passes' own K/V [layers][rows][kv_dim], on first use
+    int arith = GPHQ_PASS_FP16;
+    int8_t *a8 = nullptr;  // int8 route: row-major activations [rows][K] and their row scales, on first use
+    float *s8 = nullptr;
     std::vector<void *> allocs;
 };
 
@@ -352,12 +359,19 @@ int launch_flash(int group, const FlashArgs &a, int kvh, hipStream_t st) {
     return GPHQ_ERR_UNSUPPORTED;
 }
 
-// One projection of a pass over R rows: the fp32 GEMV for one row, else the
-// activation tiles (normalized for PRO_NORM) and the FP16 MFMA GEMM.
+// One projection of a pass over R rows. FP16 route: the fp32 GEMV for one
+// row, else the activation tiles (normalized for PRO_NORM) and the FP16 MFMA
+// GEMM. int8 route (Q8 layers): every row quantized per row, then the exact
+// int8 MFMA GEMM with MulPanelsI8's scaling.
 int project(gphq_prefill *ws, int R, int pro, int epi, const uint8_t *buf, int64_t codes, int64_t scales,
             const float *x, int64_t K, float *y, int64_t ystride, int64_t N, hipStream_t st) {
     const gphq_lm_config &c = ws->lm->cfg;
     const float eps = (float)c.eps;
+    if (ws->arith == GPHQ_PASS_INT8) {
+        GPHQ_TRY(lm_i8_act(x, (long)K, R, (int)K, pro == PRO_NORM, eps, ws->a8, ws->s8, st));
+        return lm_i8_mm(epi, ws->a8, ws->s8, (const int8_t *)(buf + codes), (const float *)(buf + scales), y,
+                        (long)ystride, R, (int)K, (int)N, st);
+    }
     if (R == 1) return gemv_fused_launch(c.fmt, pro, epi, buf + codes, buf + scales, x, y, (int)K, (int)N, eps, st);
     GPHQ_TRY(lm_act_pack(x, (long)K, R, (int)K, pro == PRO_NORM, eps, ws->a16, ws->rinv, st));
     return lm_mm_launch(c.fmt, epi, buf + codes, buf + scales, ws->a16, ws->rinv, y, (long)ystride, R, (int)K, (int)N,
@@ -486,6 +500,55 @@ void gphq_prefill_free(gphq_prefill *ws) {
 }
 
 int gphq_prefill_rows(const gphq_prefill *ws) { return ws ? ws->rows : 0; }
+
+int gphq_prefill_set_arith(gphq_prefill *ws, int arith) {
+    if (!ws) return GPHQ_ERR_WORKSPACE;
+    if (arith != GPHQ_PASS_FP16 && arith != GPHQ_PASS_INT8) return GPHQ_ERR_UNSUPPORTED;
+    if (arith == GPHQ_PASS_INT8) {
+        const gphq_lm *lm = ws->lm;
+        if (lm->cfg.fmt != GPHQ_FMT_Q8) return GPHQ_ERR_UNSUPPORTED;
+        if (!ws->a8) {
+            const int64_t kmax = std::max({(int64_t)lm->cfg.hidden, lm->qd, (int64_t)lm->cfg.intermediate});
+            hipError_t e = hipMalloc((void **)&ws->a8, (size_t)ws->rows * kmax);
+            if (e != hipSuccess) {
+                ws->a8 = nullptr;
+                return hip_status(e);
+            }
+            ws->allocs.push_back(ws->a8);
+            e = hipMalloc((void **)&ws->s8, (size_t)ws->rows * 4);
+            if (e != hipSuccess) {
+                ws->s8 = nullptr;
+                return hip_status(e);
+            }
+            ws->allocs.push_back(ws->s8);
+        }
+    }
+    ws->arith = arith;
+    return GPHQ_OK;
+}
+
+int gphq_prefill_arith(const gphq_prefill *ws) { return ws ? ws->arith : GPHQ_PASS_FP16; }
+
+int gphq_prefill_project(gphq_prefill *ws, int64_t layer, int proj, const float *x_dev, int64_t rows, float *y_dev,
+                         void *stream) {
+    if (!ws) return GPHQ_ERR_WORKSPACE;
+    const gphq_lm *lm = ws->lm;
+    const gphq_lm_config &c = lm->cfg;
+    if (layer < 0 || layer >= c.layers || proj < 0 || proj > 3) return GPHQ_ERR_DIMENSIONS;
+    if (rows < 1 || rows > ws->rows) return GPHQ_ERR_PASS_ROWS;
+    if (!x_dev || !y_dev) return GPHQ_ERR_DIMENSIONS;
+    const gphq_lm_layer &L = lm->layers[layer];
+    const uint8_t *buf = (const uint8_t *)L.buf_dev;
+    const int64_t H = c.hidden, I = c.intermediate, qd = lm->qd, qkvw = qd + 2 * lm->kvd;
+    hipStream_t st = (hipStream_t)stream;
+    const int R = (int)rows;
+    switch (proj) {
+    case 0: return project(ws, R, PRO_NORM, EPI_STORE, buf, L.qkv, L.qkv_scale, x_dev, H, y_dev, qkvw, qkvw, st);
+    case 1: return project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.o, L.o_scale, x_dev, qd, y_dev, H, H, st);
+    case 2: return project(ws, R, PRO_NORM, EPI_SWIGLU, buf, L.gu, L.gu_scale, x_dev, H, y_dev, I, 2 * I, st);
+    default: return project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.d, L.d_scale, x_dev, I, y_dev, H, H, st);
+    }
+}
 
 int gphq_prefill_extend(gphq_prefill *ws, gphq_prefix *kv, int64_t keep, const int32_t *tokens, int64_t n,
                         float *hidden_dev, int64_t hidden_len, void *stream) {

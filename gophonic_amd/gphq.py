@@ -56,6 +56,7 @@ ERR_READ_RANGE = -40
 TAIL_MAX_ROWS = 256
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
+PASS_FP16, PASS_INT8 = 0, 1  # gphq_prefill_set_arith
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -192,6 +193,9 @@ SIGNATURES = {
     "gphq_q8b_quantize": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
     "gphq_q8b_gemm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "gphq_prefill_check": (ctypes.c_int, [_vp, _vp]),
+    "gphq_prefill_set_arith": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "gphq_prefill_arith": (ctypes.c_int, [_vp]),
+    "gphq_prefill_project": (ctypes.c_int, [_vp, _i64, ctypes.c_int, _vp, _i64, _vp, _vp]),
     "gphq_gptq_work_bytes": (_i64, [_i64]),
     "gphq_gptq_factor": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "gphq_gptq_round_work_bytes": (_i64, [_i64, _i64]),
@@ -849,6 +853,20 @@ class Prefill:
 
     def check(self, stream=None):
         return check(load().gphq_prefill_check(self.h, stream_handle(stream)))
+
+    def set_arith(self, arith):
+        """PASS_FP16 (the GPU provider's mm) or PASS_INT8 (the CPU provider's
+        int8 route, Q8 layers only)."""
+        check(load().gphq_prefill_set_arith(self.h, arith))
+
+    @property
+    def arith(self):
+        return load().gphq_prefill_arith(self.h)
+
+    def project(self, layer, proj, x, rows, y, stream=None):
+        """One projection of a pass (0 QKV, 1 O add, 2 gate/up SwiGLU, 3 down
+        add) on `rows` rows of device tensor x into device tensor y."""
+        check(load().gphq_prefill_project(self.h, layer, proj, ptr(x), rows, ptr(y), stream_handle(stream)))
 
 
 def lm_from_stored(geom_kwargs, fmt, layers, embed_bf16, final_norm, head, device="cuda"):

@@ -672,6 +672,31 @@ int gphq_prefill_batch(gphq_prefill *ws, const gphq_prefix *shared, int64_t past
 /* Waits for the stream; GPHQ_ERR_NON_FINITE_STATE if an extension since the
  * last check produced a non-finite hidden value. */
 int gphq_prefill_check(gphq_prefill *ws, void *stream);
+/* Projection arithmetic of the workspace's passes. GPHQ_PASS_FP16 (the
+ * default) is the GPU provider's mm (FP16 tiles, fp32 sums, the fp32 GEMV
+ * for one-token passes). GPHQ_PASS_INT8 is the CPU provider's int8 route
+ * (qwen3lm/ops.go:96-147, 198-215: each projection input row normalized where
+ * the pass normalizes it, quantized with WorkspaceI8's per-row rule,
+ * int8.go:106-168, and multiplied exactly in int32 with MulPanelsI8's scaling
+ * (float32(sum) * weight row scale) * activation row scale, int8.go:170-211),
+ * for every pass including one-token ones, over the Q8 layer format's per-row
+ * int8 codes and scales on int8 MFMA. GPHQ_ERR_UNSUPPORTED for other layer
+ * formats. The int8 route allocates rows x max(hidden, q_dim, intermediate)
+ * bytes on first selection. */
+#define GPHQ_PASS_FP16 0
+#define GPHQ_PASS_INT8 1
+int gphq_prefill_set_arith(gphq_prefill *ws, int arith);
+int gphq_prefill_arith(const gphq_prefill *ws);
+/* One projection of a pass (ops.go:198-215 projectPanel over every panel; the
+ * GPU provider's mm dispatch of encodeBatch, gpu_darwin.go:1703-1764) on
+ * `rows` (<= the workspace's rows) rows of x_dev with the workspace's
+ * arithmetic: proj 0 = QKV of RMS-normalized rows stored into y_dev
+ * [rows][q_dim + 2 kv_dim]; 1 = O, y_dev [rows][hidden] += x [rows][q_dim] W^T;
+ * 2 = gate/up of normalized rows, SwiGLU stored into y_dev [rows][intermediate];
+ * 3 = down, y_dev [rows][hidden] += x [rows][intermediate] W^T (x as the pass
+ * holds it: after the intermediate rotation for Q8/Q4). Enqueued on stream. */
+int gphq_prefill_project(gphq_prefill *ws, int64_t layer, int proj, const float *x_dev, int64_t rows, float *y_dev,
+                         void *stream);
 
 /* ---- Block-32 int8 GEMM (BASELINE configuration 2 as worded there) -----------
  * No counterpart in the reference, whose q8gemm int8 path scales per row

@@ -271,6 +271,22 @@ class DecodeOracle:
         a, b = v[:, :half], v[:, half:]
         return np.concatenate([a * c - b * s, b * c + a * s], axis=1)
 
+    def _mm(self, x, w):
+        """x [rows][k] @ w^T in float64; with int8 activations (the CPU
+        provider's int8 route, qwen3lm/ops.go:96-147, 198-215) each row of x is
+        first replaced by its WorkspaceI8 quantization s * q (int8.go:106-168:
+        s = max|x|/127, q = round-half-even(x * 127/max|x|) saturated to
+        [-128, 127]; a row with no finite positive maximum gives zeros)."""
+        if not self.int8:
+            return x @ w.T
+        m = np.abs(x).max(axis=1, keepdims=True)
+        ok = np.isfinite(m) & (m > 0)
+        safe = np.where(ok, m, 1.0)
+        q = np.clip(np.rint(x * (127.0 / safe)), -128, 127)
+        return np.where(ok, q * (safe / 127.0), 0.0) @ w.T
+
+    int8 = False
+
     def prefill(self, cache, base, tokens, last_only=False, embeds=None, tail=None):
         """All rows of tokens at positions base.. at once (the batched pass,
         gpu_darwin.go:1703-1764: each row attends cache rows 0..its own
@@ -286,7 +302,10 @@ class DecodeOracle:
         embeds: (token, rows [occurrences][hidden]) -- Embeds
         (evaluator.go:150-163, gpu_darwin.go:1582-1590): the i-th occurrence
         of token takes row i (float32, unrotated like an embedding row)
-        instead of the embedding table's row."""
+        instead of the embedding table's row.
+
+        With int8 = True every projection multiplies per-row int8-quantized
+        inputs (_mm), the arithmetic of the int8 route."""
         g = self.g
         T = len(tokens)
         hd = g.head_dim
@@ -306,8 +325,8 @@ class DecodeOracle:
         for li, W in enumerate(self.W):
             rows = slice(T - tail, T) if tail is not None and li == len(self.W) - 1 else slice(0, T)
             hn = self._norm_rows(h)
-            kv = hn @ W["qkv"][g.qd:].T
-            qs = hn[rows] @ W["qkv"][: g.qd].T
+            kv = self._mm(hn, W["qkv"][g.qd:])
+            qs = self._mm(hn[rows], W["qkv"][: g.qd])
             kc, vc = cache[li]
             for kh in range(g.kv_heads):
                 k = kv[:, kh * hd:(kh + 1) * hd]
@@ -322,14 +341,14 @@ class DecodeOracle:
                 s = np.where(mask[rows], q @ kc[: base + T, kh * hd:(kh + 1) * hd].T, -np.inf)
                 p = np.exp(s - s.max(axis=1, keepdims=True))
                 ctx[:, qh * hd:(qh + 1) * hd] = (p / p.sum(axis=1, keepdims=True)) @ vc[: base + T, kh * hd:(kh + 1) * hd]
-            h = h[rows] + ctx @ W["o"].T
-            gu = self._norm_rows(h) @ W["gu"].T
+            h = h[rows] + self._mm(ctx, W["o"])
+            gu = self._mm(self._norm_rows(h), W["gu"])
             gate, up = gu[:, 0::2], gu[:, 1::2]
             with np.errstate(over="ignore"):
                 act = gate / (1.0 + np.exp(-gate)) * up
             if self.fmt != FMT_Q8B:
-                act = rot_apply(act, self.irot)
-            h = h + act @ W["down"].T
+                act = rot_apply(act, self.irot).reshape(act.shape)
+            h = h + self._mm(act, W["down"])
         return h
 
     def finish(self, h):

@@ -96,6 +96,60 @@ def one_layer():
     return _ONE["lm"], _ONE["orc"]
 
 
+def one_layer_q8():
+    """(lm, oracle) of a one-layer Qwen3-8B-width Q8 (per-row int8) model with
+    the full head, for the batched pass's int8 route."""
+    if "lm8" not in _ONE:
+        lm, _, st = gphq.lm_random(dict(QWEN3_8B, layers=1), gphq.FMT_Q8, seed=82, host=True)
+        g = lo.Geometry(hidden=4096, layers=1, heads=32, kv_heads=8, head_dim=128, inter=12288, vocab=VOCAB,
+                        max_pos=8192)
+        layers = [lo.Layer(qkv=L["qkv"], o=L["o"], gu=L["gu"], down=L["down"], q_norm=L["q_norm"],
+                           k_norm=L["k_norm"]) for L in st["layers"]]
+        _ONE.update(lm8=lm, orc8=lo.DecodeOracle(g, lo.FMT_Q8, layers, st["embed"], st["final_norm"], st["head"]))
+    return _ONE["lm8"], _ONE["orc8"]
+
+
+def test_prefill_4096_tokens_one_layer_8b_int8_route():
+    # Config 4a's pass on the int8 route (Q8 layers, per-row int8 activations,
+    # exact int32 products on int8 MFMA): the last state against the float64
+    # pass and against the float64 pass with the same per-row quantization,
+    # each distance (1 - cosine) at most twice that of exact int8 arithmetic
+    # from float64 (the single-projection tests show the arithmetic exact);
+    # the K/V rows, whose QKV input is the exact embedding rows, to the
+    # quantizing pass at the batched pass's 0.99999.
+    import torch
+
+    lm, orc = one_layer_q8()
+    g = orc.g
+    rng = np.random.default_rng(4097)
+    toks = rng.integers(0, g.vocab, CTX)
+    pf = gphq.Prefill(lm, CTX)
+    pf.set_arith(gphq.PASS_INT8)
+    kv = gphq.Prefix(lm, CTX + 8)
+    hidden = torch.empty(g.hidden, device="cuda")
+    pf.extend(kv, 0, toks, hidden)
+    pf.check()
+    got_k, got_v = read_cache(kv, CTX)
+    want_hidden, _ = orc.finish_rows(orc.prefill(orc.new_cache(CTX + 8), 0, toks, last_only=True))
+    cache = orc.new_cache(CTX + 8)
+    orc.int8 = True
+    try:
+        want8, _ = orc.finish_rows(orc.prefill(cache, 0, toks, last_only=True))
+    finally:
+        orc.int8 = False
+    got = hidden.cpu().numpy()
+    c, c8, e8 = cosine(want_hidden[0], got), cosine(want8[0], got), 1.0 - cosine(want_hidden[0], want8[0])
+    print(f"4096-row int8 pass: last-row cosine {c:.8f} to float64 (exact int8 {1 - e8:.8f}), {c8:.8f} to int8")
+    assert 1.0 - c <= 2.0 * e8 and 1.0 - c8 <= 2.0 * e8, (c, c8, e8)
+    rows = sorted({0, 1, 2047, CTX - 1} | set(rng.integers(0, CTX, 28).tolist()))
+    for r in rows:
+        for name, want, gotr in (("k", cache[0][0], got_k), ("v", cache[0][1], got_v)):
+            for kh in range(g.kv_heads):
+                sl = slice(kh * g.head_dim, (kh + 1) * g.head_dim)
+                c = cosine(want[r, sl], gotr[r, sl])
+                assert c >= COS, (name, r, kh, c)
+
+
 def test_prefill_4096_tokens_one_layer_8b():
     # Config 4a's pass at one layer: 4096 rows in one batched pass into a
     # fresh prefix. The last row's post-final-norm state and sampled K/V rows

@@ -329,3 +329,42 @@ def test_prepare_projection_oracle_roundtrip():
     step = np.abs(want).reshape(n, k // 32, 32).max(axis=2, keepdims=True) / 127
     err = np.abs(deq - want).reshape(n, k // 32, 32)
     assert (err <= 0.5 * step * 1.01 + 1e-6).all()
+
+
+def test_int8_route_quantization_matches_pinned_quantizer():
+    """The int8 mode's per-row quantization (DecodeOracle._mm) against the
+    pinned C quantizer of WorkspaceI8 (orc.i8_pack_rows, bit-exact with
+    int8.go:106-168): on float32 rows the codes agree except where float32's
+    x * (127/max) and float64's land on opposite sides of a rounding boundary
+    (then by one step), and the step s = max/127 equals the C scale to float32
+    rounding. Rows of zeros, a NaN and an infinity quantize to zero."""
+    rng = np.random.default_rng(8)
+    rows, k = 64, 1024
+    x = (rng.standard_normal((rows, k)) * rng.uniform(1e-3, 1e3, (rows, 1))).astype(np.float32)
+    x[3] = 0.0
+    x[4, 7] = np.nan
+    x[5, 9] = np.inf
+    x[6, :8] = [127.0, -127.0, 63.5, -63.5, 0.5, -0.5, 1.5, -2.5]  # exact ties at max 127
+    x[6, 8:] = 0.0
+    o = lo.DecodeOracle.__new__(lo.DecodeOracle)
+    o.int8 = True
+    x64 = x.astype(np.float64)
+    deq = o._mm(x64, np.eye(k))  # the quantized rows s * q themselves
+    q_c, s_c, _ = orc.i8_pack_rows(x, rows, k)
+    for r in range(rows):
+        if r in (3, 4, 5):
+            assert not deq[r].any() and not q_c[r].any() and s_c[r] == 0
+            continue
+        s = np.abs(x64[r]).max() / 127.0
+        assert abs(s - float(s_c[r])) <= 2 * np.spacing(np.float32(s_c[r])), r
+        q = np.rint(deq[r] / s)
+        diff = q - q_c[r].astype(np.float64)
+        assert np.abs(diff).max() <= 1, r
+        assert np.mean(diff == 0) >= 0.999, r
+    # Ties round to even, saturation at -128..127 as the C quantizer.
+    assert np.array_equal(np.rint(deq[6, :8] / (127.0 / 127.0)), [127, -127, 64, -64, 0, -0, 2, -2])
+    assert np.array_equal(q_c[6, :8], [127, -127, 64, -64, 0, 0, 2, -2])
+    o.int8 = False
+    y = rng.standard_normal((3, k))
+    w = rng.standard_normal((5, k))
+    assert np.array_equal(o._mm(y, w), y @ w.T)
