@@ -63,7 +63,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // in registers, stage by stage in the network's order, and stores them back.
 template <int R>
 __device__ __forceinline__ void fwht_round(float *v, int n, int s) {
-    constexpr int r = R == 8 ? 3 : R == 4 ? 2 : 1;
+    constexpr int r = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : 1;
     const int h = 1 << s;
     for (int idx = threadIdx.x; idx < (n >> r); idx += blockDim.x) {
         const int base = ((idx >> s) << (s + r)) | (idx & (h - 1));
@@ -98,6 +98,64 @@ __device__ inline void lds_fwht(float *v, int n, int block) {
     for (; s + 3 <= lb; s += 3) fwht_round<8>(v, n, s);
     if (lb - s == 2) fwht_round<4>(v, n, s);
     if (lb - s == 1) fwht_round<2>(v, n, s);
+}
+
+// A row held in registers by a one-block-per-row kernel of 256 threads
+// (thread t owns chunks of 16 values at 16 * (t + 256 c), c < CPT; values
+// past K are zero and stay so) is rotated in place: x * signs (the scale
+// folded into signs), then lds_fwht over the row in blocks of `block`, in
+// K floats of dynamic LDS.
+//
+// The network's first stages (h = 1 .. 8, up to the block) pair values of one
+// thread's 16-value chunk, so they run in registers before the row goes to
+// LDS; the rest run as radix-16 rounds (then 8, 4, 2) from stage h = 16,
+// whose 16 consecutive items read consecutive words. Same butterflies in the
+// same stage order as lds_fwht, so the same bits.
+template <int CPT>
+__device__ __forceinline__ void rotate_row_lds(float4 (&v)[CPT][4], int K, const float *__restrict__ signs, int block) {
+    extern __shared__ float rot_lds[];
+    const int lb = __builtin_ctz((unsigned)block);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int k = 16 * ((int)threadIdx.x + 256 * c);
+        if (k >= K) continue;
+        float a[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 s = *(const float4 *)(signs + k + 4 * q);
+            a[4 * q] = v[c][q].x * s.x;
+            a[4 * q + 1] = v[c][q].y * s.y;
+            a[4 * q + 2] = v[c][q].z * s.z;
+            a[4 * q + 3] = v[c][q].w * s.w;
+        }
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) {
+            if (m >= block) break;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (!(j & m)) {
+                    const float x = a[j], y = a[j + m];
+                    a[j] = x + y;
+                    a[j + m] = x - y;
+                }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *(float4 *)(rot_lds + k + 4 * q) = float4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+    }
+    __syncthreads();
+    int s = 4;
+    for (; s + 4 <= lb; s += 4) fwht_round<16>(rot_lds, K, s);
+    if (lb - s == 3) fwht_round<8>(rot_lds, K, s);
+    if (lb - s == 2) fwht_round<4>(rot_lds, K, s);
+    if (lb - s == 1) fwht_round<2>(rot_lds, K, s);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int k = 16 * ((int)threadIdx.x + 256 * c);
+        if (k >= K) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = *(const float4 *)(rot_lds + k + 4 * q);
+    }
 }
 
 // qwen3lm/hadamard.go:24-47 newRotation(k): fills k signs (+-1) and returns

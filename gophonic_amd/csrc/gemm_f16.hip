@@ -804,11 +804,12 @@ int f16_act_pack(const float *x, long stride, int rows, int K, int kt, int mode,
 // slot of the FP16 tile layout. MODE 0: half(x); 1: half(x * 2^e); 2:
 // half(x * f * 2^e) with the RMSNorm factor f, as f16_act_pack_kernel modes
 // 1, 4 and 3 (rowInv[row] = 2^-e for 1 and 2). K % 16 == 0, rows 16-byte
-// aligned; chunks past K (up to the 64-value tile) are zero.
-template <int MODE, int CPT>
+// aligned; chunks past K (up to the 64-value tile) are zero. ROT rotates the
+// row first (rotate_row_lds: the down projection's online Hadamard).
+template <int MODE, int CPT, bool ROT>
 __global__ __launch_bounds__(256) void act_pack_rows_kernel(const float *__restrict__ x, long stride, int K, int kt,
-                                                            float eps, _Float16 *__restrict__ act,
-                                                            float *__restrict__ rowInv) {
+                                                            float eps, const float *__restrict__ signs, int block,
+                                                            _Float16 *__restrict__ act, float *__restrict__ rowInv) {
     __shared__ float sss[4], smx[4];
     const int row = blockIdx.x;
     const float *xr = x + (size_t)row * stride;
@@ -819,8 +820,13 @@ __global__ __launch_bounds__(256) void act_pack_rows_kernel(const float *__restr
     for (int c = 0; c < CPT; ++c) {
         const int k = 16 * ((int)threadIdx.x + 256 * c);
 #pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = k < K ? *(const float4 *)(xr + k + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    if constexpr (ROT) rotate_row_lds<CPT>(v, K, signs, block);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+#pragma unroll
         for (int q = 0; q < 4; ++q) {
-            v[c][q] = k < K ? *(const float4 *)(xr + k + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
             ss += v[c][q].x * v[c][q].x + v[c][q].y * v[c][q].y + v[c][q].z * v[c][q].z + v[c][q].w * v[c][q].w;
             mx = fmaxf(fmaxf(fmaxf(mx, fabsf(v[c][q].x)), fmaxf(fabsf(v[c][q].y), fabsf(v[c][q].z))), fabsf(v[c][q].w));
         }
@@ -858,31 +864,39 @@ __global__ __launch_bounds__(256) void act_pack_rows_kernel(const float *__restr
     }
 }
 
-template <int MODE>
+template <int MODE, bool ROT = false>
 static int launch_act_pack_rows(const float *x, long stride, int rows, int K, float eps, _Float16 *act,
-                                float *rowInv, hipStream_t stream) {
+                                float *rowInv, hipStream_t stream, const float *signs = nullptr, int block = 0) {
     const int kt = (K + 63) / 64, chunks = kt * 4;
+    // A rotated row occupies LDS only in whole 16-value chunks below K.
+    const size_t lds = ROT ? (size_t)K * sizeof(float) : 0;
+#define GPHQ_ACTPACK(CPT)                                                                                              \
+    hipLaunchKernelGGL((act_pack_rows_kernel<MODE, CPT, ROT>), dim3(rows), dim3(256), lds, stream, x, stride, K, kt,   \
+                       eps, signs, block, act, rowInv)
     if (chunks <= 256)
-        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, 1>), dim3(rows), dim3(256), 0, stream, x, stride, K, kt, eps,
-                           act, rowInv);
+        GPHQ_ACTPACK(1);
     else if (chunks <= 512)
-        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, 2>), dim3(rows), dim3(256), 0, stream, x, stride, K, kt, eps,
-                           act, rowInv);
+        GPHQ_ACTPACK(2);
     else if (chunks <= 768)
-        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, 3>), dim3(rows), dim3(256), 0, stream, x, stride, K, kt, eps,
-                           act, rowInv);
+        GPHQ_ACTPACK(3);
     else
-        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, 4>), dim3(rows), dim3(256), 0, stream, x, stride, K, kt, eps,
-                           act, rowInv);
+        GPHQ_ACTPACK(4);
+#undef GPHQ_ACTPACK
     return launch_status();
 }
 
 // The qwen3lm batched pass's activation tiles, half(x * f * 2^e) with f the
 // RMSNorm factor (norm true) or 1, and rowInv[r] = 2^-e per row. x rows are
-// `stride` floats apart, 16-byte aligned, K % 16 == 0, K <= 16384.
-int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, _Float16 *act, float *rowInv,
-                hipStream_t stream) {
+// `stride` floats apart, 16-byte aligned, K % 16 == 0, K <= 16384. signs
+// (device, K values with the rotation's scale folded in) rotate each row
+// first, in blocks of `block`; null for none.
+int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, const float *signs, int block,
+                _Float16 *act, float *rowInv, hipStream_t stream) {
     if (rows == 0) return GPHQ_OK;
+    if (signs) {
+        if (norm) return GPHQ_ERR_UNSUPPORTED;  // no pass normalizes a rotated input
+        return launch_act_pack_rows<1, true>(x, stride, rows, K, eps, act, rowInv, stream, signs, block);
+    }
     if (norm) return launch_act_pack_rows<2>(x, stride, rows, K, eps, act, rowInv, stream);
     return launch_act_pack_rows<1>(x, stride, rows, K, eps, act, rowInv, stream);
 }

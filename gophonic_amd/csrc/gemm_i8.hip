@@ -154,9 +154,15 @@ __global__ __launch_bounds__(256) void i8_pack_range_kernel(const float *__restr
 // factor (MODE 2, the FP16 packer's sum order) or 1 (MODE 1); SetRowScale of
 // max|v| (NaN-propagating); q = quantize(v * inv) written row-major
 // [rows][K]; rowScale[r] = max / 127. One block per row, the row in
-// registers (CPT chunks of 16 values per thread).
-template <int MODE, int CPT>
+// registers (CPT chunks of 16 values per thread). ROT first rotates the row
+// as the down projection's input (the online Hadamard, gpu.metal:339-367;
+// the CPU path's scaleRow, qwen3lm/ops.go:111-122): x * signs (signs carry
+// the 1/sqrt(block) scale), then the butterfly network of each block in LDS
+// (K floats of dynamic LDS), the same arithmetic as the decode step's
+// rotation kernel.
+template <int MODE, int CPT, bool ROT>
 __global__ __launch_bounds__(256) void i8_act_rows_kernel(const float *__restrict__ x, long stride, int K, float eps,
+                                                          const float *__restrict__ signs, int block,
                                                           int8_t *__restrict__ act, float *__restrict__ rowScale) {
     __shared__ float sss[4], smx[4];
     __shared__ int snan[4];
@@ -169,8 +175,13 @@ __global__ __launch_bounds__(256) void i8_act_rows_kernel(const float *__restric
     for (int c = 0; c < CPT; ++c) {
         const int k = 16 * ((int)threadIdx.x + 256 * c);
 #pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = k < K ? *(const float4 *)(xr + k + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    if constexpr (ROT) rotate_row_lds<CPT>(v, K, signs, block);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+#pragma unroll
         for (int q = 0; q < 4; ++q) {
-            v[c][q] = k < K ? *(const float4 *)(xr + k + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
             ss += v[c][q].x * v[c][q].x + v[c][q].y * v[c][q].y + v[c][q].z * v[c][q].z + v[c][q].w * v[c][q].w;
             mx = fmaxf(fmaxf(fmaxf(mx, fabsf(v[c][q].x)), fmaxf(fabsf(v[c][q].y), fabsf(v[c][q].z))), fabsf(v[c][q].w));
             nan |= (v[c][q].x != v[c][q].x) | (v[c][q].y != v[c][q].y) | (v[c][q].z != v[c][q].z) |
@@ -670,33 +681,39 @@ int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const
     return launch_i8gemm_big<128, 192, 4, 2>(a, stream);
 }
 
-template <int MODE>
-static int launch_i8_act_rows(const float *x, long stride, int rows, int K, float eps, int8_t *act, float *rowScale,
-                              hipStream_t stream) {
+template <int MODE, bool ROT>
+static int launch_i8_act_rows(const float *x, long stride, int rows, int K, float eps, const float *signs, int block,
+                              int8_t *act, float *rowScale, hipStream_t stream) {
     const int chunks = K / 16;
+    const size_t lds = ROT ? (size_t)K * sizeof(float) : 0;
+#define GPHQ_I8ACT(CPT)                                                                                                \
+    hipLaunchKernelGGL((i8_act_rows_kernel<MODE, CPT, ROT>), dim3(rows), dim3(256), lds, stream, x, stride, K, eps,     \
+                       signs, block, act, rowScale)
     if (chunks <= 256)
-        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, 1>), dim3(rows), dim3(256), 0, stream, x, stride, K, eps, act,
-                           rowScale);
+        GPHQ_I8ACT(1);
     else if (chunks <= 512)
-        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, 2>), dim3(rows), dim3(256), 0, stream, x, stride, K, eps, act,
-                           rowScale);
+        GPHQ_I8ACT(2);
     else if (chunks <= 768)
-        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, 3>), dim3(rows), dim3(256), 0, stream, x, stride, K, eps, act,
-                           rowScale);
+        GPHQ_I8ACT(3);
     else
-        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, 4>), dim3(rows), dim3(256), 0, stream, x, stride, K, eps, act,
-                           rowScale);
+        GPHQ_I8ACT(4);
+#undef GPHQ_I8ACT
     return launch_status();
 }
 
 // int8 activations of the batched pass (see i8_act_rows_kernel): x rows
 // `stride` floats apart and 16-byte aligned, K % 16 == 0, K <= 16384; act is
-// row-major [rows][K].
-int lm_i8_act(const float *x, long stride, int rows, int K, bool norm, float eps, int8_t *act, float *rowScale,
-              hipStream_t stream) {
+// row-major [rows][K]. signs (device, K values with the rotation's scale
+// folded in) rotate each row first, in blocks of `block`; null for none.
+int lm_i8_act(const float *x, long stride, int rows, int K, bool norm, float eps, const float *signs, int block,
+              int8_t *act, float *rowScale, hipStream_t stream) {
     if (rows == 0) return GPHQ_OK;
-    if (norm) return launch_i8_act_rows<2>(x, stride, rows, K, eps, act, rowScale, stream);
-    return launch_i8_act_rows<1>(x, stride, rows, K, eps, act, rowScale, stream);
+    if (signs) {
+        if (norm) return GPHQ_ERR_UNSUPPORTED;  // no pass normalizes a rotated input
+        return launch_i8_act_rows<1, true>(x, stride, rows, K, eps, signs, block, act, rowScale, stream);
+    }
+    if (norm) return launch_i8_act_rows<2, false>(x, stride, rows, K, eps, nullptr, 0, act, rowScale, stream);
+    return launch_i8_act_rows<1, false>(x, stride, rows, K, eps, nullptr, 0, act, rowScale, stream);
 }
 
 // One projection of the batched pass on the int8 route: y = (float32(A W^T)
@@ -722,9 +739,18 @@ int lm_i8_mm(int epi, const int8_t *act, const float *a_scale, const int8_t *cod
     a.c0 = 0;
     a.c1 = N;
     a.tileN0 = 0;
-    if (epi == 0) return launch_i8gemm_big<256, 128, 4, 2, I8_ROWS, I8_EPI_STORE>(a, stream);
-    if (epi == 1) return launch_i8gemm_big<256, 128, 4, 2, I8_ROWS, I8_EPI_ADD>(a, stream);
-    return launch_i8gemm_big<256, 128, 4, 2, I8_ROWS, I8_EPI_SWIGLU>(a, stream);
+    // Tile shapes by measurement on MI355X at M = 4096 (Qwen3-8B's projections):
+    // 256 x 256 tiles when the grid fits one tile per CU (O: 135 -> 121 us,
+    // down: 270 -> 241 us against 256 x 128), else 128 x 192 (gate/up: 640 ->
+    // 564 us, QKV: 151 -> 142 us). SwiGLU's 256 x 256 instance spills.
+    const long big = (long)((M + 255) / 256) * ((N + 255) / 256);
+    if (epi != 2 && big <= 256) {
+        if (epi == 0) return launch_i8gemm_big<256, 256, 4, 2, I8_ROWS, I8_EPI_STORE>(a, stream);
+        return launch_i8gemm_big<256, 256, 4, 2, I8_ROWS, I8_EPI_ADD>(a, stream);
+    }
+    if (epi == 0) return launch_i8gemm_big<128, 192, 4, 2, I8_ROWS, I8_EPI_STORE>(a, stream);
+    if (epi == 1) return launch_i8gemm_big<128, 192, 4, 2, I8_ROWS, I8_EPI_ADD>(a, stream);
+    return launch_i8gemm_big<128, 192, 4, 2, I8_ROWS, I8_EPI_SWIGLU>(a, stream);
 }
 
 int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {

@@ -32,12 +32,12 @@
 namespace gphq {
 int gemv_fused_launch(int fmt, int pro, int epi, const void *codes, const void *scales, const float *x, float *y,
                       int K, int N, float eps, hipStream_t stream);
-int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, _Float16 *act, float *rowInv,
-                hipStream_t stream);
+int lm_act_pack(const float *x, long stride, int rows, int K, bool norm, float eps, const float *signs, int block,
+                _Float16 *act, float *rowInv, hipStream_t stream);
 int lm_mm_launch(int fmt, int epi, const void *codes, const void *scales, const _Float16 *act, const float *rowInv,
                  float *y, long y_stride, int M, int K, int N, hipStream_t stream);
-int lm_i8_act(const float *x, long stride, int rows, int K, bool norm, float eps, int8_t *act, float *rowScale,
-              hipStream_t stream);
+int lm_i8_act(const float *x, long stride, int rows, int K, bool norm, float eps, const float *signs, int block,
+              int8_t *act, float *rowScale, hipStream_t stream);
 int lm_i8_mm(int epi, const int8_t *act, const float *a_scale, const int8_t *codes, const float *w_scale, float *y,
              long y_stride, int M, int K, int N, hipStream_t stream);
 }  // namespace gphq
@@ -362,18 +362,27 @@ int launch_flash(int group, const FlashArgs &a, int kvh, hipStream_t st) {
 // One projection of a pass over R rows. FP16 route: the fp32 GEMV for one
 // row, else the activation tiles (normalized for PRO_NORM) and the FP16 MFMA
 // GEMM. int8 route (Q8 layers): every row quantized per row, then the exact
-// int8 MFMA GEMM with MulPanelsI8's scaling.
+// int8 MFMA GEMM with MulPanelsI8's scaling. rot: the input is the down
+// projection's, rotated first for Q8/Q4 layers (gpu_darwin.go:209-215) by the
+// packer itself (in place, before the GEMV, for one row).
 int project(gphq_prefill *ws, int R, int pro, int epi, const uint8_t *buf, int64_t codes, int64_t scales,
-            const float *x, int64_t K, float *y, int64_t ystride, int64_t N, hipStream_t st) {
-    const gphq_lm_config &c = ws->lm->cfg;
+            const float *x, int64_t K, float *y, int64_t ystride, int64_t N, hipStream_t st, bool rot = false) {
+    const gphq_lm *lm = ws->lm;
+    const gphq_lm_config &c = lm->cfg;
     const float eps = (float)c.eps;
+    const bool rotate = rot && c.fmt != GPHQ_FMT_Q8B;
+    const float *signs = rotate ? lm->isigns : nullptr;
+    const int block = rotate ? (int)lm->iblock : 0;
     if (ws->arith == GPHQ_PASS_INT8) {
-        GPHQ_TRY(lm_i8_act(x, (long)K, R, (int)K, pro == PRO_NORM, eps, ws->a8, ws->s8, st));
+        GPHQ_TRY(lm_i8_act(x, (long)K, R, (int)K, pro == PRO_NORM, eps, signs, block, ws->a8, ws->s8, st));
         return lm_i8_mm(epi, ws->a8, ws->s8, (const int8_t *)(buf + codes), (const float *)(buf + scales), y,
                         (long)ystride, R, (int)K, (int)N, st);
     }
-    if (R == 1) return gemv_fused_launch(c.fmt, pro, epi, buf + codes, buf + scales, x, y, (int)K, (int)N, eps, st);
-    GPHQ_TRY(lm_act_pack(x, (long)K, R, (int)K, pro == PRO_NORM, eps, ws->a16, ws->rinv, st));
+    if (R == 1) {
+        if (rotate) GPHQ_TRY(lm_rotate_launch(lm, const_cast<float *>(x), 1, (long)K, st));
+        return gemv_fused_launch(c.fmt, pro, epi, buf + codes, buf + scales, x, y, (int)K, (int)N, eps, st);
+    }
+    GPHQ_TRY(lm_act_pack(x, (long)K, R, (int)K, pro == PRO_NORM, eps, signs, block, ws->a16, ws->rinv, st));
     return lm_mm_launch(c.fmt, epi, buf + codes, buf + scales, ws->a16, ws->rinv, y, (long)ystride, R, (int)K, (int)N,
                         st);
 }
@@ -439,8 +448,7 @@ int encode_pass(gphq_prefill *ws, const PassKV &kv, int base, int R, hipStream_t
         GPHQ_TRY(launch_flash((int)lm->group, fa, (int)c.kv_heads, st));
         GPHQ_TRY(project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.o, L.o_scale, ws->ctx, qd, ws->h, H, H, st));
         GPHQ_TRY(project(ws, R, PRO_NORM, EPI_SWIGLU, buf, L.gu, L.gu_scale, ws->h, H, ws->act, I, 2 * I, st));
-        if (c.fmt != GPHQ_FMT_Q8B) GPHQ_TRY(lm_rotate_launch(lm, ws->act, R, (long)I, st));
-        GPHQ_TRY(project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.d, L.d_scale, ws->act, I, ws->h, H, H, st));
+        GPHQ_TRY(project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.d, L.d_scale, ws->act, I, ws->h, H, H, st, true));
     }
     return GPHQ_OK;
 }
@@ -546,7 +554,7 @@ int gphq_prefill_project(gphq_prefill *ws, int64_t layer, int proj, const float 
     case 0: return project(ws, R, PRO_NORM, EPI_STORE, buf, L.qkv, L.qkv_scale, x_dev, H, y_dev, qkvw, qkvw, st);
     case 1: return project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.o, L.o_scale, x_dev, qd, y_dev, H, H, st);
     case 2: return project(ws, R, PRO_NORM, EPI_SWIGLU, buf, L.gu, L.gu_scale, x_dev, H, y_dev, I, 2 * I, st);
-    default: return project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.d, L.d_scale, x_dev, I, y_dev, H, H, st);
+    default: return project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.d, L.d_scale, x_dev, I, y_dev, H, H, st, true);
     }
 }
 

@@ -693,8 +693,10 @@ int gphq_prefill_arith(const gphq_prefill *ws);
  * arithmetic: proj 0 = QKV of RMS-normalized rows stored into y_dev
  * [rows][q_dim + 2 kv_dim]; 1 = O, y_dev [rows][hidden] += x [rows][q_dim] W^T;
  * 2 = gate/up of normalized rows, SwiGLU stored into y_dev [rows][intermediate];
- * 3 = down, y_dev [rows][hidden] += x [rows][intermediate] W^T (x as the pass
- * holds it: after the intermediate rotation for Q8/Q4). Enqueued on stream. */
+ * 3 = down, y_dev [rows][hidden] += x' [rows][intermediate] W^T, where x' is
+ * x after the intermediate rotation for Q8/Q4 layers (rotate, gpu.metal:
+ * 339-367, applied by the projection's input packing; a one-row FP16-route
+ * call rotates x_dev in place). Enqueued on stream. */
 int gphq_prefill_project(gphq_prefill *ws, int64_t layer, int proj, const float *x_dev, int64_t rows, float *y_dev,
                          void *stream);
 

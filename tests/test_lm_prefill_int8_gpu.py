@@ -8,7 +8,8 @@ with MulPanelsI8's scaling (float32(sum) * weight scale) * row scale
 (int8.go:170-211), on int8 MFMA.
 
 * One projection (gphq_prefill_project) whose input is not normalized (O and
-  down, residual add) is bit-exact: the pinned C quantizer
+  down, residual add) is bit-exact: the pinned C rotation for down's input
+  (orc.rotation_apply_f32, hadamard.go:51-58), the pinned C quantizer
   (orc.i8_pack_rows), exact int64 sums, float32 scaling and the float32 add.
 * Normalized inputs (QKV, gate/up with SwiGLU) and whole passes are held to
   the float64 oracle with the same per-row quantization (DecodeOracle.int8).
@@ -109,7 +110,11 @@ def test_project_int8_residual_add_bit_exact(geom, proj, rows):
     print(f"project int8 proj={proj} rows={rows} k={k} n={n}", flush=True)
     ws.project(0, proj, xd, rows, yd)
     got = yd.cpu().numpy()
-    qa, sa, _ = orc.i8_pack_rows(x, rows, k)
+    xin = x
+    if proj == 3:  # Q8 down input: the intermediate rotation, in float32
+        rot = lo.rotation(k)
+        xin = np.stack([orc.rotation_apply_f32(row, rot) for row in x])
+    qa, sa, _ = orc.i8_pack_rows(xin, rows, k)
     sums = qa.astype(np.int64) @ W.astype(np.int64).T
     assert np.abs(sums).max() < 2**31
     v = (sums.astype(np.float32) * sw[None, :]) * sa[:, None]

@@ -86,7 +86,7 @@ _ONE = {}
 def one_layer():
     """(lm, oracle) of a one-layer Qwen3-8B-width Q8B model with the full head
     (built once per session; the oracle keeps the head as codes)."""
-    if not _ONE:
+    if "lm" not in _ONE:
         lm, _, st = gphq.lm_random(dict(QWEN3_8B, layers=1), gphq.FMT_Q8B, seed=81, host=True)
         g = lo.Geometry(hidden=4096, layers=1, heads=32, kv_heads=8, head_dim=128, inter=12288, vocab=VOCAB,
                         max_pos=8192)
