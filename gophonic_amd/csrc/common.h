@@ -61,7 +61,17 @@ __device__ __forceinline__ float wave_sum(float v) {
 // Each item owns the R values whose index differs only in bits s..s+r-1
 // (base = idx with r zero bits inserted at bit s), runs the r stages on them
 // in registers, stage by stage in the network's order, and stores them back.
-template <int R>
+// With PAD, value i lives at LDS word rot_pad(i): 16 words of padding per 256
+// values, so the four 16-item groups of a wavefront at stride 16 fall on
+// different banks, and the four 16-byte quads of each 16-value chunk rotated
+// by (i / 64) % 4, so 16 lanes storing or loading consecutive chunks 16 bytes
+// at a time cover all 64 banks once. Within 64 consecutive values the map is
+// a permutation, so rounds with a stride of 64 or more stay conflict-free.
+__device__ __forceinline__ int rot_pad(int i) {
+    return (i & ~15) + ((((i >> 2) + (i >> 6)) & 3) << 2) + (i & 3) + ((i >> 8) << 4);
+}
+
+template <int R, bool PAD = false>
 __device__ __forceinline__ void fwht_round(float *v, int n, int s) {
     constexpr int r = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : 1;
     const int h = 1 << s;
@@ -69,7 +79,7 @@ __device__ __forceinline__ void fwht_round(float *v, int n, int s) {
         const int base = ((idx >> s) << (s + r)) | (idx & (h - 1));
         float a[R];
 #pragma unroll
-        for (int j = 0; j < R; ++j) a[j] = v[base + j * h];
+        for (int j = 0; j < R; ++j) a[j] = v[PAD ? rot_pad(base + j * h) : base + j * h];
 #pragma unroll
         for (int m = 1; m < R; m <<= 1)
 #pragma unroll
@@ -80,7 +90,7 @@ __device__ __forceinline__ void fwht_round(float *v, int n, int s) {
                     a[j + m] = x - y;
                 }
 #pragma unroll
-        for (int j = 0; j < R; ++j) v[base + j * h] = a[j];
+        for (int j = 0; j < R; ++j) v[PAD ? rot_pad(base + j * h) : base + j * h] = a[j];
     }
     __syncthreads();
 }
@@ -104,13 +114,15 @@ __device__ inline void lds_fwht(float *v, int n, int block) {
 // (thread t owns chunks of 16 values at 16 * (t + 256 c), c < CPT; values
 // past K are zero and stay so) is rotated in place: x * signs (the scale
 // folded into signs), then lds_fwht over the row in blocks of `block`, in
-// K floats of dynamic LDS.
+// rot_lds_bytes(K) of dynamic LDS (the row padded by rot_pad).
 //
 // The network's first stages (h = 1 .. 8, up to the block) pair values of one
 // thread's 16-value chunk, so they run in registers before the row goes to
 // LDS; the rest run as radix-16 rounds (then 8, 4, 2) from stage h = 16,
 // whose 16 consecutive items read consecutive words. Same butterflies in the
 // same stage order as lds_fwht, so the same bits.
+inline size_t rot_lds_bytes(int K) { return (size_t)(K + (K >> 8) * 16 + 16) * sizeof(float); }
+
 template <int CPT>
 __device__ __forceinline__ void rotate_row_lds(float4 (&v)[CPT][4], int K, const float *__restrict__ signs, int block) {
     extern __shared__ float rot_lds[];
@@ -139,22 +151,23 @@ __device__ __forceinline__ void rotate_row_lds(float4 (&v)[CPT][4], int K, const
                     a[j + m] = x - y;
                 }
         }
+        // Each quad of 4 values stays contiguous under rot_pad.
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            *(float4 *)(rot_lds + k + 4 * q) = float4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+            *(float4 *)(rot_lds + rot_pad(k + 4 * q)) = float4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
     }
     __syncthreads();
     int s = 4;
-    for (; s + 4 <= lb; s += 4) fwht_round<16>(rot_lds, K, s);
-    if (lb - s == 3) fwht_round<8>(rot_lds, K, s);
-    if (lb - s == 2) fwht_round<4>(rot_lds, K, s);
-    if (lb - s == 1) fwht_round<2>(rot_lds, K, s);
+    for (; s + 4 <= lb; s += 4) fwht_round<16, true>(rot_lds, K, s);
+    if (lb - s == 3) fwht_round<8, true>(rot_lds, K, s);
+    if (lb - s == 2) fwht_round<4, true>(rot_lds, K, s);
+    if (lb - s == 1) fwht_round<2, true>(rot_lds, K, s);
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
         const int k = 16 * ((int)threadIdx.x + 256 * c);
         if (k >= K) continue;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = *(const float4 *)(rot_lds + k + 4 * q);
+        for (int q = 0; q < 4; ++q) v[c][q] = *(const float4 *)(rot_lds + rot_pad(k + 4 * q));
     }
 }
 

@@ -868,11 +868,16 @@ template <int MODE, bool ROT = false>
 static int launch_act_pack_rows(const float *x, long stride, int rows, int K, float eps, _Float16 *act,
                                 float *rowInv, hipStream_t stream, const float *signs = nullptr, int block = 0) {
     const int kt = (K + 63) / 64, chunks = kt * 4;
-    // A rotated row occupies LDS only in whole 16-value chunks below K.
-    const size_t lds = ROT ? (size_t)K * sizeof(float) : 0;
+    // A rotated row takes rot_lds_bytes(K) of dynamic LDS (69.7 KB at K = 16384).
+    const size_t lds = ROT ? rot_lds_bytes(K) : 0;
 #define GPHQ_ACTPACK(CPT)                                                                                              \
-    hipLaunchKernelGGL((act_pack_rows_kernel<MODE, CPT, ROT>), dim3(rows), dim3(256), lds, stream, x, stride, K, kt,   \
-                       eps, signs, block, act, rowInv)
+    do {                                                                                                               \
+        if (lds > 65536)                                                                                               \
+            (void)hipFuncSetAttribute((const void *)act_pack_rows_kernel<MODE, CPT, ROT>,                              \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                           \
+        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, CPT, ROT>), dim3(rows), dim3(256), lds, stream, x, stride, K,  \
+                           kt, eps, signs, block, act, rowInv);                                                        \
+    } while (0)
     if (chunks <= 256)
         GPHQ_ACTPACK(1);
     else if (chunks <= 512)

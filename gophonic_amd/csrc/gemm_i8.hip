@@ -685,10 +685,15 @@ template <int MODE, bool ROT>
 static int launch_i8_act_rows(const float *x, long stride, int rows, int K, float eps, const float *signs, int block,
                               int8_t *act, float *rowScale, hipStream_t stream) {
     const int chunks = K / 16;
-    const size_t lds = ROT ? (size_t)K * sizeof(float) : 0;
+    const size_t lds = ROT ? rot_lds_bytes(K) : 0;
 #define GPHQ_I8ACT(CPT)                                                                                                \
-    hipLaunchKernelGGL((i8_act_rows_kernel<MODE, CPT, ROT>), dim3(rows), dim3(256), lds, stream, x, stride, K, eps,     \
-                       signs, block, act, rowScale)
+    do {                                                                                                               \
+        if (lds > 65536)                                                                                               \
+            (void)hipFuncSetAttribute((const void *)i8_act_rows_kernel<MODE, CPT, ROT>,                                \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                           \
+        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, CPT, ROT>), dim3(rows), dim3(256), lds, stream, x, stride, K,    \
+                           eps, signs, block, act, rowScale);                                                          \
+    } while (0)
     if (chunks <= 256)
         GPHQ_I8ACT(1);
     else if (chunks <= 512)
