@@ -301,12 +301,17 @@ __global__ __launch_bounds__(64 * SK) void gemv_vec2_kernel(const Vec2Args a) {
 //     is bank-conflict free), while the next tile's loads are in flight. Per
 //     block: hi and lo MFMAs accumulate into one 16x16 result (16 vectors x
 //     16 rows), scaled by the weight block scale into fp32 accumulators; the
-//     K slices meet in LDS in slice order.
+//     K slices meet in LDS in slice order. Each wavefront parks a tile's
+//     partial sums in one of kVechCH LDS slots and moves on; every kVechCH
+//     tiles one barrier pair lets wavefront w add up slot w's slices and run
+//     that tile's epilogue, instead of two barriers and a one-wavefront
+//     epilogue per tile.
 // Measured on MI355X with 16 vectors (Qwen3-8B shapes, Q8B): the head 154 us
 // (was 383 us with the per-block kernel), gate/up 34 us (was 83), qkv 16.5 us
 // (was 33), o 13 us (was 20).
 constexpr int kVechNB = 16;        // K blocks of 32 values per wavefront slice
 constexpr int kVechMaxSlices = 8;  // 512 threads; the kernel holds ~230 VGPRs
+constexpr int kVechCH = 8;         // tiles whose slice sums are reduced together
 
 // One block of 1024 threads per vector; thread t holds float4 units t, t +
 // 1024, .. of the vector (K <= 4 * 1024 * kPrepUnits), so the vector is read
@@ -377,7 +382,8 @@ __global__ __launch_bounds__(64 * SK) void vech_kernel(const Vec2Args a, int ite
     // Scale bytes per row and slice in 16-byte loads (Q8's row scale is applied at the end).
     constexpr int SC = FMT == GPHQ_FMT_Q8B ? NB * 2 / 16 : FMT == GPHQ_FMT_Q8B_F32 ? NB * 4 / 16 : 1;
     __shared__ u32x4 stage[SK][STEPS * 128];
-    __shared__ f32x4 part[SK > 1 ? SK * 64 : 1];
+    constexpr int CH = SK < kVechCH ? SK : kVechCH;
+    __shared__ f32x4 part[SK > 1 ? CH * SK * 64 : 1];  // [slot][slice][lane]
     const int lane = threadIdx.x & 63;
     const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, m = lane & 15;
@@ -459,45 +465,56 @@ __global__ __launch_bounds__(64 * SK) void vech_kernel(const Vec2Args a, int ite
 #pragma unroll
             for (int q = 0; q < SC * 4; ++q) S[q] = Sn[q];
         }
-        if constexpr (SK > 1) {
-            if (ks != 0) part[ks * 64 + lane] = acc;
-            __syncthreads();
-            if (ks == 0)
-                for (int k2 = 1; k2 < SK; ++k2) acc += part[k2 * 64 + lane];
-            __syncthreads();
-            if (ks != 0 || !valid) continue;
-        } else {
-            if (!valid) break;
-        }
-        // Lane (g, m) holds vectors 4g..4g+3 of row tt*16 + m.
-        const int col = tt * 16 + m;
-        if constexpr (SPLIT) {  // this part's sums; vech_finish_kernel applies the rest
+        // Lane (g, m) holds vectors 4g..4g+3 of row t*16 + m.
+        auto epilogue = [&](int t, const f32x4 &r) {
+            const int col = t * 16 + m;
+            if constexpr (SPLIT) {  // this part's sums; vech_finish_kernel applies the rest
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int v = 4 * g + i;
+                    if (v < a.V && col < a.N) a.part[((size_t)blockIdx.y * a.V + v) * a.N + col] = r[i];
+                }
+                return;
+            }
+            float rs = 1.0f;
+            if constexpr (FMT == GPHQ_FMT_Q8) rs = ((const float *)a.scales)[min(col, a.N - 1)];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int v = 4 * g + i;
-                if (v < a.V && col < a.N) a.part[((size_t)blockIdx.y * a.V + v) * a.N + col] = acc[i];
+                const int vc = min(v, a.V - 1);
+                float val = r[i] * a.inv[vc];
+                if constexpr (NORM) val *= 1.0f / sqrtf(a.ssq[vc] / (float)a.K + a.eps);
+                if constexpr (FMT == GPHQ_FMT_Q8) val *= rs;
+                if constexpr (EPI == VEC_SWIGLU) {
+                    const float up = __shfl_xor(val, 1);  // lane m^1 holds row col^1
+                    if (v < a.V && col < a.N && (col & 1) == 0)
+                        a.y[(size_t)v * a.ystride + (col >> 1)] = val / (1.0f + expf(-val)) * up;
+                } else if (v < a.V && col < a.N) {
+                    if constexpr (EPI == VEC_ADD)
+                        a.y[(size_t)v * a.ystride + col] += val;
+                    else
+                        a.y[(size_t)v * a.ystride + col] = val;
+                }
             }
-            continue;
-        }
-        float rs = 1.0f;
-        if constexpr (FMT == GPHQ_FMT_Q8) rs = ((const float *)a.scales)[min(col, a.N - 1)];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int v = 4 * g + i;
-            const int vc = min(v, a.V - 1);
-            float val = acc[i] * a.inv[vc];
-            if constexpr (NORM) val *= 1.0f / sqrtf(a.ssq[vc] / (float)a.K + a.eps);
-            if constexpr (FMT == GPHQ_FMT_Q8) val *= rs;
-            if constexpr (EPI == VEC_SWIGLU) {
-                const float up = __shfl_xor(val, 1);  // lane m^1 holds row col^1
-                if (v < a.V && col < a.N && (col & 1) == 0)
-                    a.y[(size_t)v * a.ystride + (col >> 1)] = val / (1.0f + expf(-val)) * up;
-            } else if (v < a.V && col < a.N) {
-                if constexpr (EPI == VEC_ADD)
-                    a.y[(size_t)v * a.ystride + col] += val;
-                else
-                    a.y[(size_t)v * a.ystride + col] = val;
+        };
+        if constexpr (SK > 1) {
+            const int slot = it % CH;
+            part[(slot * SK + ks) * 64 + lane] = acc;
+            if (slot != CH - 1 && it != iters - 1) continue;  // the same for every wavefront
+            __syncthreads();
+            if (ks <= slot) {
+                // Wavefront ks reduces slot ks (tile tt - (slot - ks) blocks
+                // back) in slice order, as one wavefront adding the others'.
+                const f32x4 *ps = part + ks * SK * 64 + lane;
+                f32x4 r = ps[0];
+                for (int k2 = 1; k2 < SK; ++k2) r += ps[k2 * 64];
+                const int t = tt - (slot - ks) * (int)gridDim.x;
+                if (t < tiles) epilogue(t, r);
             }
+            __syncthreads();
+        } else {
+            if (!valid) break;
+            epilogue(tt, acc);
         }
     }
 }
