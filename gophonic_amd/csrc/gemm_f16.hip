@@ -177,26 +177,22 @@ __device__ __forceinline__ void load_b(const F16GemmArgs &a, int n, int kt, int 
 }
 
 // Epilogue of one lane's part of a 16x16 accumulator tile (or of a 4-row
-// group of a 32x32 one): rows row0 .. row0 + 3 of column col. Columns outside
-// [c0, c1) and rows past M are not written. Every lane of the wavefront calls
-// it (EPI_SWIGLU exchanges the gate and up values of neighbouring lanes).
+// group of a 32x32 one): rows row0 .. row0 + 3 of column col, with the
+// column's scale cs and the rows' scales ri (as epilogue_scales reads them).
+// Columns outside [c0, c1) and rows past M are not written. Every lane of the
+// wavefront calls it (EPI_SWIGLU exchanges the gate and up values of
+// neighbouring lanes).
 template <int EPI>
-__device__ __forceinline__ void epilogue(const F16GemmArgs &a, const f32x4 &acc, int row0, int col) {
+__device__ __forceinline__ void epilogue_scaled(const F16GemmArgs &a, const f32x4 &acc, int row0, int col, float cs,
+                                                const float (&ri)[4]) {
     const bool colOk = col >= a.c0 && col < a.c1;
-    float cs = 1.0f;
-    if constexpr (EPI == EPI_PANELS || EPI == EPI_ROWSCALE) {
-        if (colOk) cs = a.colScale[col];
-    }
-    if constexpr (EPI == EPI_ADD || EPI == EPI_SWIGLU) {
-        if (colOk && a.colScale) cs = a.colScale[col];
-    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int row = row0 + e;
         float v = acc[e];
-        // The qwen3lm pass's row scale 2^-e (exact); rows past M read row 0.
+        // The qwen3lm pass's row scale 2^-e (exact).
         if constexpr (EPI != EPI_PANELS) {
-            if (a.rowInv) v = __fmul_rn(v, a.rowInv[row < a.M ? row : 0]);
+            if (a.rowInv) v = __fmul_rn(v, ri[e]);
         }
         if constexpr (EPI == EPI_SWIGLU) {
             if (a.colScale) v = __fmul_rn(v, cs);
@@ -206,7 +202,7 @@ __device__ __forceinline__ void epilogue(const F16GemmArgs &a, const f32x4 &acc,
             if (colOk && !(col & 1) && row < a.M) a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
         } else if (colOk && row < a.M) {
             float *p = a.dst + (size_t)row * a.stride + col;
-            if constexpr (EPI == EPI_PANELS) v = __fmul_rn(__fmul_rn(v, cs), a.rowInv[row]);
+            if constexpr (EPI == EPI_PANELS) v = __fmul_rn(__fmul_rn(v, cs), ri[e]);
             if constexpr (EPI == EPI_ROWSCALE) v = __fmul_rn(v, cs);
             if constexpr (EPI == EPI_ADD) {
                 // One fp32 add into the residual, done in L2 without a return
@@ -219,6 +215,34 @@ __device__ __forceinline__ void epilogue(const F16GemmArgs &a, const f32x4 &acc,
             }
         }
     }
+}
+
+// The scales epilogue_scaled takes: the column's (1 where the epilogue has
+// none) and the four rows' (rows past M read the last row; they are not
+// written). Read before any store of the tile: the compiler cannot tell that
+// the stores do not alias the scales, so scales read between stores are
+// reloaded one at a time.
+template <int EPI>
+__device__ __forceinline__ float epilogue_col_scale(const F16GemmArgs &a, int col) {
+    const bool colOk = col >= a.c0 && col < a.c1;
+    if constexpr (EPI == EPI_PANELS || EPI == EPI_ROWSCALE) return colOk ? a.colScale[col] : 1.0f;
+    if constexpr (EPI == EPI_ADD || EPI == EPI_SWIGLU) return colOk && a.colScale ? a.colScale[col] : 1.0f;
+    return 1.0f;
+}
+__device__ __forceinline__ void epilogue_row_scales(const F16GemmArgs &a, int row0, float (&ri)[4]) {
+    if (!a.rowInv) {
+        ri[0] = ri[1] = ri[2] = ri[3] = 1.0f;
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ri[e] = a.rowInv[min(row0 + e, a.M - 1)];
+}
+
+template <int EPI>
+__device__ __forceinline__ void epilogue(const F16GemmArgs &a, const f32x4 &acc, int row0, int col) {
+    float ri[4];
+    epilogue_row_scales(a, row0, ri);
+    epilogue_scaled<EPI>(a, acc, row0, col, epilogue_col_scale<EPI>(a, col), ri);
 }
 
 template <int WF, int EPI, int TM, int TN, int WM, int WN, int SK, int U>
@@ -588,14 +612,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
             }
         return;
     }
+    // Every scale of the lane's outputs first, then the stores.
+    float ri[TI][4][4], cs[TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) epilogue_row_scales(a, m0 + wm * (32 * TI) + 32 * i + 8 * q + 4 * fh, ri[i][q]);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) cs[j] = epilogue_col_scale<EPI_T>(a, n0 + wn * (32 * TJ) + 32 * j + fr);
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                epilogue<EPI_T>(a, f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]},
-                                m0 + wm * (32 * TI) + 32 * i + 8 * q + 4 * fh, n0 + wn * (32 * TJ) + 32 * j + fr);
+                epilogue_scaled<EPI_T>(a,
+                                       f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                             acc[i][j][4 * q + 3]},
+                                       m0 + wm * (32 * TI) + 32 * i + 8 * q + 4 * fh,
+                                       n0 + wn * (32 * TJ) + 32 * j + fr, cs[j], ri[i][q]);
 }
 
 // Split-K finish (the reference's mm_finish, gpu.metal:953-982, for the store

@@ -576,7 +576,28 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
         }
         __syncthreads();
     }
-    // Epilogue as MulPanelsI8: (float32(sum) * colScale) * rowScale.
+    // Epilogue as MulPanelsI8: (float32(sum) * colScale) * rowScale. The
+    // lane's 16 rows of each 32-row tile come in runs of 4 (rows 8k + 4fh ..
+    // +3), so their scales are read up front as four 16-byte loads per tile:
+    // read inside the store loop, every store to dst (which may alias the
+    // scales, as far as the compiler knows) would force a reload and a wait.
+    float rsc[TI][16];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int row0 = (rt0 + (wm * TI + i) * 2) * 16 + 8 * k + 4 * fh;
+            float4 v;
+            if (row0 + 3 < a.M) {
+                v = *(const float4 *)(a.rowScale + row0);
+            } else {
+                v.x = a.rowScale[min(row0, a.M - 1)];
+                v.y = a.rowScale[min(row0 + 1, a.M - 1)];
+                v.z = a.rowScale[min(row0 + 2, a.M - 1)];
+                v.w = a.rowScale[min(row0 + 3, a.M - 1)];
+            }
+            rsc[i][4 * k] = v.x, rsc[i][4 * k + 1] = v.y, rsc[i][4 * k + 2] = v.z, rsc[i][4 * k + 3] = v.w;
+        }
     if constexpr (EPI == I8_EPI_STORE) {
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
@@ -589,8 +610,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
                 for (int e = 0; e < 16; ++e) {
                     const int row = (rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3);
                     if (row < a.M)
-                        a.dst[(size_t)row * a.stride + col] =
-                            __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row]);
+                        a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), rsc[i][e]);
                 }
         }
     } else {
@@ -605,7 +625,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int row = (rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3);
-                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row < a.M ? row : 0]);
+                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), rsc[i][e]);
                     if constexpr (EPI == I8_EPI_SWIGLU) {
                         // The up value of the neighbouring lane (DPP quad_perm [1,0,3,2]).
                         const float u = __builtin_bit_cast(
