@@ -576,34 +576,32 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
         }
         __syncthreads();
     }
-    // Epilogue as MulPanelsI8: (float32(sum) * colScale) * rowScale. The
-    // lane's 16 rows of each 32-row tile come in runs of 4 (rows 8k + 4fh ..
-    // +3), so their scales are read up front as four 16-byte loads per tile:
-    // read inside the store loop, every store to dst (which may alias the
-    // scales, as far as the compiler knows) would force a reload and a wait.
+    // Epilogue as MulPanelsI8: (float32(sum) * colScale) * rowScale. Every
+    // scale of the lane's outputs is read up front, unconditionally (rows past
+    // M read the last row; they are not written): read inside the store loop,
+    // or under a branch, each scale costs a wait, and the wait also drains
+    // every store issued before it (stores may alias the scales as far as the
+    // compiler knows, and the counter it waits on counts stores too).
     float rsc[TI][16];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int row0 = (rt0 + (wm * TI + i) * 2) * 16 + 8 * k + 4 * fh;
-            float4 v;
-            if (row0 + 3 < a.M) {
-                v = *(const float4 *)(a.rowScale + row0);
-            } else {
-                v.x = a.rowScale[min(row0, a.M - 1)];
-                v.y = a.rowScale[min(row0 + 1, a.M - 1)];
-                v.z = a.rowScale[min(row0 + 2, a.M - 1)];
-                v.w = a.rowScale[min(row0 + 3, a.M - 1)];
-            }
-            rsc[i][4 * k] = v.x, rsc[i][4 * k + 1] = v.y, rsc[i][4 * k + 2] = v.z, rsc[i][4 * k + 3] = v.w;
-        }
+        for (int e = 0; e < 16; ++e)
+            rsc[i][e] = a.rowScale[min((rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3), a.M - 1)];
+    // The column scales too (a column outside [c0, c1) reads c0's and is not
+    // written): a load after a store waits for the store as well.
+    float csc[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
+        csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
+    }
     if constexpr (EPI == I8_EPI_STORE) {
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
             const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
             if (col < a.c0 || col >= a.c1) continue;
-            const float cs = a.colScale[col];
+            const float cs = csc[j];
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -619,7 +617,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
         for (int j = 0; j < TJ; ++j) {
             const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
             const bool colOk = col >= a.c0 && col < a.c1;
-            const float cs = colOk ? a.colScale[col] : 0.0f;
+            const float cs = colOk ? csc[j] : 0.0f;
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -765,13 +763,14 @@ int lm_i8_mm(int epi, const int8_t *act, const float *a_scale, const int8_t *cod
     a.c1 = N;
     a.tileN0 = 0;
     // Tile shapes by measurement on MI355X at M = 4096 (Qwen3-8B's projections):
-    // 256 x 256 tiles when the grid fits one tile per CU (O: 135 -> 121 us,
-    // down: 270 -> 241 us against 256 x 128), else 128 x 192 (gate/up: 640 ->
-    // 564 us, QKV: 151 -> 142 us). SwiGLU's 256 x 256 instance spills.
+    // 256 x 256 tiles (one block per CU) when they fill whole waves of 256
+    // CUs (O: 125 -> 118 us, down: 295 -> 239, gate/up: 628 -> 549 against
+    // 128 x 192), else 128 x 192 (QKV's 384 tiles: 160 -> 138 us).
     const long big = (long)((M + 255) / 256) * ((N + 255) / 256);
-    if (epi != 2 && big <= 256) {
+    if (big % 256 == 0) {
         if (epi == 0) return launch_i8gemm_big<256, 256, 4, 2, I8_ROWS, I8_EPI_STORE>(a, stream);
-        return launch_i8gemm_big<256, 256, 4, 2, I8_ROWS, I8_EPI_ADD>(a, stream);
+        if (epi == 1) return launch_i8gemm_big<256, 256, 4, 2, I8_ROWS, I8_EPI_ADD>(a, stream);
+        return launch_i8gemm_big<256, 256, 4, 2, I8_ROWS, I8_EPI_SWIGLU>(a, stream);
     }
     if (epi == 0) return launch_i8gemm_big<128, 192, 4, 2, I8_ROWS, I8_EPI_STORE>(a, stream);
     if (epi == 1) return launch_i8gemm_big<128, 192, 4, 2, I8_ROWS, I8_EPI_ADD>(a, stream);
