@@ -224,9 +224,18 @@ __device__ __forceinline__ void epilogue_scaled(const F16GemmArgs &a, const f32x
 // reloaded one at a time.
 template <int EPI>
 __device__ __forceinline__ float epilogue_col_scale(const F16GemmArgs &a, int col) {
+    // Loaded unconditionally (a column outside [c0, c1) reads c0's) and then
+    // selected: a load under a lane condition makes later waits drain stores.
     const bool colOk = col >= a.c0 && col < a.c1;
-    if constexpr (EPI == EPI_PANELS || EPI == EPI_ROWSCALE) return colOk ? a.colScale[col] : 1.0f;
-    if constexpr (EPI == EPI_ADD || EPI == EPI_SWIGLU) return colOk && a.colScale ? a.colScale[col] : 1.0f;
+    if constexpr (EPI == EPI_PANELS || EPI == EPI_ROWSCALE) {
+        const float v = a.colScale[colOk ? col : a.c0];
+        return colOk ? v : 1.0f;
+    }
+    if constexpr (EPI == EPI_ADD || EPI == EPI_SWIGLU) {
+        if (!a.colScale) return 1.0f;
+        const float v = a.colScale[colOk ? col : a.c0];
+        return colOk ? v : 1.0f;
+    }
     return 1.0f;
 }
 __device__ __forceinline__ void epilogue_row_scales(const F16GemmArgs &a, int row0, float (&ri)[4]) {

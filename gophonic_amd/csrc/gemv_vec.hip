@@ -431,6 +431,16 @@ __global__ __launch_bounds__(64 * SK) void vech_kernel(const Vec2Args a, int ite
         ah[b] = *(const f16x8 *)(a.A + vec_a_offset(0, kb0 + b, KB, lane));
         al[b] = *(const f16x8 *)(a.A + vec_a_offset(1, kb0 + b, KB, lane));
     }
+    // The scale of each of the lane's 4 vectors (with the RMSNorm factor),
+    // read once: read in the epilogue, each would wait for the previous
+    // tile's stores as well.
+    float vscale[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int vc = min(4 * g + i, a.V - 1);
+        vscale[i] = a.inv[vc];
+        if constexpr (NORM) vscale[i] = vscale[i] * (1.0f / sqrtf(a.ssq[vc] / (float)a.K + a.eps));
+    }
     for (int it = 0; it < iters; ++it, tt += gridDim.x) {
         const bool valid = tt < tiles;
         const bool more = tt + (int)gridDim.x < tiles;
@@ -481,9 +491,8 @@ __global__ __launch_bounds__(64 * SK) void vech_kernel(const Vec2Args a, int ite
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int v = 4 * g + i;
-                const int vc = min(v, a.V - 1);
-                float val = r[i] * a.inv[vc];
-                if constexpr (NORM) val *= 1.0f / sqrtf(a.ssq[vc] / (float)a.K + a.eps);
+                // inv is a power of two, so r * (inv * f) rounds like (r * inv) * f.
+                float val = r[i] * vscale[i];
                 if constexpr (FMT == GPHQ_FMT_Q8) val *= rs;
                 if constexpr (EPI == VEC_SWIGLU) {
                     const float up = __shfl_xor(val, 1);  // lane m^1 holds row col^1
