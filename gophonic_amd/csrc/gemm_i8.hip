@@ -335,21 +335,31 @@ __global__ __launch_bounds__(64 * WM * WN * SK) void i8gemm_kernel(const I8GemmA
                 for (int j = 0; j < TN; ++j) acc[i][j] += red[(((wv + s) * TM + i) * TN + j) * 64 + lane];
     }
 
-    // Epilogue. Lane l of a 16x16 output tile holds rows 4*(l/16)+e, column l%16.
+    // Epilogue. Lane l of a 16x16 output tile holds rows 4*(l/16)+e, column
+    // l%16. The scales are read first, unconditionally (clamped indices;
+    // outputs outside the matrix are not written): scales read between
+    // stores would each wait for the stores too.
+    float rsc[TM][4], csc[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rsc[i][e] = a.rowScale[min((mt0 + i) * 16 + 4 * (lane >> 4) + e, a.M - 1)];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int col = (nt0 + j) * 16 + (lane & 15);
         if (col < a.c0 || col >= a.c1) continue;
-        const float cs = a.colScale[col];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
-                if (row < a.M) {
-                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row]);
-                    a.dst[(size_t)row * a.stride + col] = v;
-                }
+                if (row < a.M)
+                    a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], csc[j]), rsc[i][e]);
             }
         }
     }
@@ -442,20 +452,29 @@ __global__ __launch_bounds__(64 * WM * WN) void i8gemm_lds_kernel(const I8GemmAr
         buf ^= 1;
     }
 
+    // Scales first, unconditionally, as in i8gemm_kernel's epilogue.
+    float rsc[TM][4], csc[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            rsc[i][e] = a.rowScale[min((rt0 + wm * TM + i) * 16 + 4 * (lane >> 4) + e, a.M - 1)];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = (ct0 + wn * TN + j) * 16 + (lane & 15);
+        csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int col = (ct0 + wn * TN + j) * 16 + (lane & 15);
         if (col < a.c0 || col >= a.c1) continue;
-        const float cs = a.colScale[col];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int row = (rt0 + wm * TM + i) * 16 + 4 * (lane >> 4) + e;
-                if (row < a.M) {
-                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), a.rowScale[row]);
-                    a.dst[(size_t)row * a.stride + col] = v;
-                }
+                if (row < a.M)
+                    a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], csc[j]), rsc[i][e]);
             }
         }
     }
