@@ -480,6 +480,139 @@ __global__ __launch_bounds__(64 * WM * WN) void i8gemm_lds_kernel(const I8GemmAr
     }
 }
 
+// vmcnt(N) and lgkmcnt(0), expcnt untouched (gfx9 s_waitcnt encoding: vmcnt
+// in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// Skinny-M variant (up to 16 * NWV * RT activation rows per block, one block
+// per NTB weight column tiles; KT a multiple of SB). Every
+// operand fragment goes to LDS with a direct-to-LDS load
+// (global_load_lds_dwordx4: one 1 KiB fragment per wavefront instruction, no
+// registers held while in flight) into a ring of NS stages of SB K-steps; the
+// stage NS - 1 ahead is requested as each stage starts. Each wavefront owns
+// RT row tiles of A and loads their fragments itself; the NTB column tiles of
+// B are shared, each wavefront loading an equal share. Loads return in issue
+// order, so the wait at a stage's start is a count (the loads of the NS - 2
+// stages after it may stay in flight). The barrier is a plain s_barrier (a
+// __syncthreads fence would wait for every load in flight), after lgkmcnt(0)
+// so that the previous stage's LDS reads have finished before its slot is
+// refilled.
+template <int NWV, int RT, int NTB, int SB, int NS>
+__global__ __launch_bounds__(64 * NWV) void i8gemm_skinny_kernel(const I8GemmArgs a) {
+    constexpr int FB = NTB * SB;           // B fragments per stage
+    constexpr int FA = NWV * RT * SB;      // A fragments per stage
+    static_assert(FB % NWV == 0, "every wavefront issues the same number of stage loads");
+    constexpr int DB = FB / NWV;           // B loads per wavefront and stage
+    constexpr int D = DB + RT * SB;        // loads per wavefront and stage
+    static_assert(D * (NS - 2) < 64, "in-flight loads beyond the vmcnt range");
+    __shared__ i32x4 ring[NS][FB + FA][64];
+
+    const int G = a.gridM * a.gridN;
+    const int b = blockIdx.x;
+    int logical = b;
+    if (G % 8 == 0) logical = (b % 8) * (G / 8) + b / 8;
+    const int bm = logical % a.gridM, bn = logical / a.gridM;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int MT = (a.M + 15) >> 4, KT = a.KT;
+    const int S = KT / SB;
+    const int mt0 = (bm * NWV + wv) * RT;
+    const int nt0 = a.tileN0 + bn * NTB;
+
+    // Sources of this wavefront's loads at stage 0, in ring order: its B share
+    // (fragment f = wv + NWV * d is column tile f / SB, K-step f % SB), then its
+    // own A fragments (row tile i, K-step kk at FB + (wv * RT + i) * SB + kk).
+    const int8_t *src[D];
+    int dst[D];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+        const int f = wv + NWV * d;
+        src[d] = a.B + ((size_t)min(nt0 + f / SB, a.NT - 1) * KT + f % SB) * 1024 + (size_t)lane * 16;
+        dst[d] = f;
+    }
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int kk = 0; kk < SB; ++kk) {
+            const int d = DB + i * SB + kk;
+            src[d] = a.A + ((size_t)min(mt0 + i, MT - 1) * KT + kk) * 1024 + (size_t)lane * 16;
+            dst[d] = FB + (wv * RT + i) * SB + kk;
+        }
+    auto stage_load = [&](int s) {
+        const int slot = s % NS;
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(src[d] + (size_t)s * SB * 1024),
+                (__attribute__((address_space(3))) void *)&ring[slot][dst[d]][0], 16, 0, 0);
+    };
+
+    i32x4 acc[RT][NTB];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTB; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p)
+        if (p < S) stage_load(p);
+    for (int s = 0; s < S; ++s) {
+        // Loads of stages s + 1 .. min(S, s + NS - 1) - 1 may remain in flight.
+        const int after = min(S - 1 - s, NS - 2);
+        if (after == NS - 2)
+            wait_vm_lgkm0<D * (NS - 2)>();
+        else if (after == 1)
+            wait_vm_lgkm0<D>();
+        else
+            wait_vm_lgkm0<0>();
+        __builtin_amdgcn_s_barrier();
+        if (s + NS - 1 < S) stage_load(s + NS - 1);
+        const int slot = s % NS;
+#pragma unroll
+        for (int kk = 0; kk < SB; ++kk) {
+            i32x4 fa[RT], fb[NTB];
+#pragma unroll
+            for (int i = 0; i < RT; ++i) fa[i] = ring[slot][FB + (wv * RT + i) * SB + kk][lane];
+#pragma unroll
+            for (int j = 0; j < NTB; ++j) fb[j] = ring[slot][j * SB + kk][lane];
+#pragma unroll
+            for (int i = 0; i < RT; ++i)
+#pragma unroll
+                for (int j = 0; j < NTB; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    // Epilogue as in i8gemm_kernel: scales first, then the stores.
+    float rsc[RT][4], csc[NTB];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rsc[i][e] = a.rowScale[min((mt0 + i) * 16 + 4 * (lane >> 4) + e, a.M - 1)];
+#pragma unroll
+    for (int j = 0; j < NTB; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
+    }
+#pragma unroll
+    for (int j = 0; j < NTB; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        if (col < a.c0 || col >= a.c1) continue;
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
+                if (row < a.M)
+                    a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], csc[j]), rsc[i][e]);
+            }
+        }
+    }
+}
+
 // Large-M variant: BM x BN block tiles (WGM x WGN wavefronts, each a grid of
 // 32 x 32 v_mfma_i32_32x32x32_i8 tiles), 128-deep K steps staged through LDS
 // as 128-byte rows with the row-swizzled 16-byte chunks of the FP16 big-tile
@@ -679,6 +812,16 @@ static int launch_i8gemm_lds(I8GemmArgs a, hipStream_t stream) {
     return launch_status();
 }
 
+template <int NWV, int RT, int NTB, int SB, int NS>
+static int launch_i8gemm_skinny(I8GemmArgs a, hipStream_t stream) {
+    const int tiles = (a.c1 + 15) / 16 - a.tileN0;
+    a.gridN = (tiles + NTB - 1) / NTB;
+    a.gridM = (a.M + 16 * NWV * RT - 1) / (16 * NWV * RT);
+    const unsigned blocks = (unsigned)(a.gridM * a.gridN);
+    hipLaunchKernelGGL((i8gemm_skinny_kernel<NWV, RT, NTB, SB, NS>), dim3(blocks), dim3(64 * NWV), 0, stream, a);
+    return launch_status();
+}
+
 template <int TM, int TN, int WM, int WN, int SK, int U>
 static int launch_i8gemm(I8GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
@@ -710,8 +853,15 @@ int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const
     a.tileN0 = c0 / 16;
     // Shapes picked by measurement on MI355X at K = 4096, N = 12288 (M = 512:
     // 78.5 us with 128 x 64 LDS tiles, 49.0 with 256 x 128 big tiles, 46.1
-    // with 128 x 192, one tile per CU).
+    // with 128 x 192, one tile per CU; M = 32 / 64 / 128 / 256: 16.3 / 26 /
+    // 27.6 / 38.5 us before the skinny kernel, 11.6 / 12.5 / 18.5 / 32.5 with
+    // it).
     if (M <= 16) return launch_i8gemm<1, 2, 1, 2, 4, 4>(a, stream);
+    if (KT % 4 == 0) {  // skinny kernel: whole 4-step stages
+        if (M <= 32) return launch_i8gemm_skinny<2, 1, 3, 4, 4>(a, stream);
+        if (M <= 64) return launch_i8gemm_skinny<4, 1, 3, 4, 3>(a, stream);
+        if (M <= 256) return launch_i8gemm_skinny<4, 2, 3, 4, 3>(a, stream);
+    }
     if (M <= 64) return launch_i8gemm<4, 1, 1, 2, 4, 4>(a, stream);
     if (M <= 192) return launch_i8gemm_lds<128, 64, 2, 2, 4>(a, stream);
     if (M < 512) return launch_i8gemm_big<128, 128, 2, 2>(a, stream);

@@ -70,7 +70,10 @@ def oracle_out(x, rows, k, q, scales, n):
 
 SHAPES = [(1, 4, 1), (3, 7, 17), (12, 64, 64), (16, 257, 129), (12, 4096, 1024), (5, 12288, 64), (1, 32, 64),
           (1, 4096, 1024), (1, 12288, 200), (1, 96, 5), (17, 100, 33), (64, 640, 96), (100, 512, 300),
-          (200, 1024, 520)]
+          (200, 1024, 520),
+          # the skinny kernel (17..256 rows, K a multiple of 256): one-stage K,
+          # column tiles past N in a block, two row blocks
+          (24, 256, 200), (48, 256, 500), (130, 1024, 64), (256, 2048, 77), (33, 12288, 48)]
 
 
 @pytest.mark.parametrize("rows,k,n", SHAPES, ids=[f"M{r}K{k}N{n}" for r, k, n in SHAPES])
@@ -89,7 +92,7 @@ def test_mul_panels_i8_bit_exact(rows, k, n):
     assert np.array_equal(host(di).view(np.uint32), inv.view(np.uint32))
 
 
-@pytest.mark.parametrize("m", [1, 16, 128, 512])
+@pytest.mark.parametrize("m", [1, 16, 32, 64, 100, 128, 192, 256, 512])
 def test_config2_shapes_bit_exact(m):
     # K = 4096, N = 12288; exact integer sums via a float64
     # product of the integer codes (every partial sum is an integer < 2^53, so
@@ -127,7 +130,7 @@ def test_golden_tile():
 
 
 @pytest.mark.parametrize("rows,k,n", [(1, 64, 64), (8, 128, 128), (12, 4096, 1024), (16, 257, 200), (5, 12288, 64),
-                                      (3, 36, 30), (40, 300, 130)])
+                                      (3, 36, 30), (40, 300, 130), (24, 256, 330), (40, 512, 130), (120, 1024, 200)])
 def test_strips_and_panels_bit_identical(rows, k, n):
     # int8_test.go:146-179: strips, panels, and per-panel calls all agree.
     w, q, scales = int8_fixture(k, n, k + 7 * n)
