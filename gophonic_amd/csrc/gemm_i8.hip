@@ -792,6 +792,152 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
     }
 }
 
+// Large-M variant on direct-to-LDS loads: BM x BN block tiles (WGM x WGN
+// wavefronts, each a grid of 16 x 16 v_mfma_i32_16x16x64_i8 tiles), a ring of
+// NS stages of one 64-deep K-step, every operand fragment (16 rows x 64 bytes,
+// the tile layout's 1 KiB group) loaded with global_load_lds_dwordx4 and read
+// back by the lanes that own it (lane l at byte 16 l: no bank conflicts). The
+// stage NS - 1 ahead is requested as each stage starts; the wait is a count,
+// as in the skinny kernel. For I8_ROWS a fragment is gathered from 16
+// row-major rows (lane l: row l % 16, bytes 16 (l / 16) of the step), so the
+// same LDS image and MFMA code serve both layouts. Needs KT a multiple of 1
+// (tiles) or K a multiple of 64 (rows). Epilogues as the big-tile kernel's.
+template <int BM, int BN, int WGM, int WGN, int NS, int LAYOUT, int EPI>
+__global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8GemmArgs a) {
+    constexpr int NW = WGM * WGN;
+    constexpr int FA = BM / 16, FB = BN / 16, F = FA + FB;  // fragments per stage
+    constexpr int DMAX = (F + NW - 1) / NW, DREM = F % NW;  // loads per wavefront and stage
+    constexpr int TI = BM / 16 / WGM, TJ = BN / 16 / WGN;
+    static_assert(TI * 16 * WGM == BM && TJ * 16 * WGN == BN, "wave grid");
+    static_assert(DMAX * (NS - 2) < 64, "in-flight loads beyond the vmcnt range");
+    __shared__ i32x4 ring[NS][F][64];
+    int bm, bn;
+    tile_order(blockIdx.x, a.gridM, a.gridN, bm, bn);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int wm = wv / WGN, wn = wv % WGN;
+    const int rt0 = bm * FA, ct0 = a.tileN0 + bn * FB;
+    const int MT = (a.M + 15) >> 4, KT = a.KT;
+    // Loads of this wavefront: fragment f = wv + NW * d (A tiles first, then B).
+    const bool full = DREM == 0 || wv < DREM;  // issues DMAX loads per stage, else DMAX - 1
+    const int8_t *src[DMAX];
+    int dst[DMAX];
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d) {
+        const int f = min(wv + NW * d, F - 1);
+        dst[d] = f;
+        const bool isA = f < FA;
+        const int8_t *base = isA ? a.A : a.B;
+        const int tile = isA ? rt0 + f : ct0 + (f - FA);
+        if constexpr (LAYOUT == I8_ROWS) {
+            const int rows = isA ? a.M : a.N;
+            const int row = min(tile * 16 + (lane & 15), rows - 1);
+            src[d] = base + (size_t)row * a.K + (lane >> 4) * 16;
+        } else {
+            const int tiles = isA ? MT : a.NT;
+            src[d] = base + (size_t)min(tile, tiles - 1) * KT * 1024 + (size_t)lane * 16;
+        }
+    }
+    const size_t kstride = LAYOUT == I8_ROWS ? 64 : 1024;
+    auto stage_load = [&](int s) {
+        const int slot = s % NS;
+#pragma unroll
+        for (int d = 0; d < DMAX; ++d)
+            if (d < DMAX - 1 || full)
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(src[d] + (size_t)s * kstride),
+                    (__attribute__((address_space(3))) void *)&ring[slot][dst[d]][0], 16, 0, 0);
+    };
+    i32x4 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p)
+        if (p < KT) stage_load(p);
+    for (int s = 0; s < KT; ++s) {
+        const int after = min(KT - 1 - s, NS - 2);
+        if (after == NS - 2) {
+            if (full)
+                wait_vm_lgkm0<DMAX * (NS - 2)>();
+            else
+                wait_vm_lgkm0<(DMAX - 1) * (NS - 2)>();
+        } else if (after > 0) {
+            // Fewer stages in flight near the end: wait for all but `after` of them.
+            if (full) {
+                if (after == 1) wait_vm_lgkm0<DMAX>(); else wait_vm_lgkm0<0>();
+            } else {
+                if (after == 1) wait_vm_lgkm0<DMAX - 1>(); else wait_vm_lgkm0<0>();
+            }
+        } else {
+            wait_vm_lgkm0<0>();
+        }
+        __builtin_amdgcn_s_barrier();
+        if (s + NS - 1 < KT) stage_load(s + NS - 1);
+        const int slot = s % NS;
+        i32x4 fa[TI], fb[TJ];
+#pragma unroll
+        for (int i = 0; i < TI; ++i) fa[i] = ring[slot][wm * TI + i][lane];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) fb[j] = ring[slot][FA + wn * TJ + j][lane];
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    // Epilogue: lane l of a 16 x 16 tile holds rows 4 (l / 16) + e, column
+    // l % 16. Scales first, unconditionally, as in the other kernels.
+    const int mt0 = rt0 + wm * TI, nt0 = ct0 + wn * TJ;
+    float rsc[TI][4], csc[TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rsc[i][e] = a.rowScale[min((mt0 + i) * 16 + 4 * (lane >> 4) + e, a.M - 1)];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
+    }
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        const bool colOk = col >= a.c0 && col < a.c1;
+        if constexpr (EPI != I8_EPI_SWIGLU) {
+            if (!colOk) continue;
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
+                const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], colOk ? csc[j] : 0.0f), rsc[i][e]);
+                if constexpr (EPI == I8_EPI_STORE) {
+                    if (row < a.M) a.dst[(size_t)row * a.stride + col] = v;
+                } else if constexpr (EPI == I8_EPI_ADD) {
+                    if (row < a.M) __builtin_amdgcn_global_atomic_fadd_f32(a.dst + (size_t)row * a.stride + col, v);
+                } else {
+                    // The up value of the neighbouring lane (DPP quad_perm [1,0,3,2]).
+                    const float u = __builtin_bit_cast(
+                        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+                    if (colOk && !(col & 1) && row < a.M)
+                        a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
+                }
+            }
+    }
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int LAYOUT = I8_TILES, int EPI = I8_EPI_STORE>
+static int launch_i8gemm_dma(I8GemmArgs a, hipStream_t stream) {
+    const int tiles = (a.c1 + 15) / 16 - a.tileN0;
+    a.gridN = (tiles * 16 + BN - 1) / BN;
+    a.gridM = (a.M + BM - 1) / BM;
+    if (LAYOUT == I8_ROWS) a.KT = a.K / 64;
+    hipLaunchKernelGGL((i8gemm_dma_kernel<BM, BN, WGM, WGN, NS, LAYOUT, EPI>), dim3((unsigned)(a.gridM * a.gridN)),
+                       dim3(64 * WGM * WGN), 0, stream, a);
+    return launch_status();
+}
+
 template <int BM, int BN, int WGM, int WGN, int LAYOUT = I8_TILES, int EPI = I8_EPI_STORE>
 static int launch_i8gemm_big(I8GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
@@ -856,12 +1002,17 @@ int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const
     // with 128 x 192, one tile per CU; M = 32 / 64 / 128 / 256: 16.3 / 26 /
     // 27.6 / 38.5 us before the skinny kernel, 11.6 / 12.5 / 18.5 / 32.5 with
     // it).
+    // M = 192 / 256 / 384 / 512: 40.6 / 39.4 / 39.7 / 41.1 us with the
+    // register-staged big tiles, 24.0 / 24.5 / 35.5 / 36.4 with the
+    // direct-to-LDS ones.
     if (M <= 16) return launch_i8gemm<1, 2, 1, 2, 4, 4>(a, stream);
     if (KT % 4 == 0) {  // skinny kernel: whole 4-step stages
         if (M <= 32) return launch_i8gemm_skinny<2, 1, 3, 4, 4>(a, stream);
         if (M <= 64) return launch_i8gemm_skinny<4, 1, 3, 4, 3>(a, stream);
-        if (M <= 256) return launch_i8gemm_skinny<4, 2, 3, 4, 3>(a, stream);
+        if (M <= 128) return launch_i8gemm_skinny<4, 2, 3, 4, 3>(a, stream);
     }
+    if (M > 128 && M <= 256) return launch_i8gemm_dma<64, 192, 2, 4, 8>(a, stream);
+    if (M > 256 && M <= 512) return launch_i8gemm_dma<128, 192, 2, 4, 6>(a, stream);
     if (M <= 64) return launch_i8gemm<4, 1, 1, 2, 4, 4>(a, stream);
     if (M <= 192) return launch_i8gemm_lds<128, 64, 2, 2, 4>(a, stream);
     if (M < 512) return launch_i8gemm_big<128, 128, 2, 2>(a, stream);
