@@ -225,6 +225,22 @@ __device__ __forceinline__ void tile_order(int b, int gridM, int gridN, int &bm,
     bn = r / gm;
 }
 
+// vmcnt(N) and lgkmcnt(0), expcnt untouched (gfx9 s_waitcnt encoding: vmcnt
+// in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// One 16-byte-per-lane direct-to-LDS load (global_load_lds_dwordx4): lane l
+// writes its 16 bytes from `src` to lds + 16 l. `lds` is the same for every
+// lane. Counts in vmcnt like any vector load.
+__device__ __forceinline__ void lds_dma16(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                     (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+
 // 16-byte chunk index within a 128-byte LDS row of a GEMM operand tile,
 // swizzled by the row: fragment reads of 8 or 16 consecutive rows at one
 // chunk hit distinct banks.

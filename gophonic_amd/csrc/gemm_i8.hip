@@ -480,14 +480,6 @@ __global__ __launch_bounds__(64 * WM * WN) void i8gemm_lds_kernel(const I8GemmAr
     }
 }
 
-// vmcnt(N) and lgkmcnt(0), expcnt untouched (gfx9 s_waitcnt encoding: vmcnt
-// in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-}
-
 // Skinny-M variant (up to 16 * NWV * RT activation rows per block, one block
 // per NTB weight column tiles; KT a multiple of SB). Every
 // operand fragment goes to LDS with a direct-to-LDS load
@@ -545,9 +537,7 @@ __global__ __launch_bounds__(64 * NWV) void i8gemm_skinny_kernel(const I8GemmArg
         const int slot = s % NS;
 #pragma unroll
         for (int d = 0; d < D; ++d)
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(src[d] + (size_t)s * SB * 1024),
-                (__attribute__((address_space(3))) void *)&ring[slot][dst[d]][0], 16, 0, 0);
+            lds_dma16(src[d] + (size_t)s * SB * 1024, &ring[slot][dst[d]][0]);
     };
 
     i32x4 acc[RT][NTB];
@@ -843,9 +833,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8Gemm
 #pragma unroll
         for (int d = 0; d < DMAX; ++d)
             if (d < DMAX - 1 || full)
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)(src[d] + (size_t)s * kstride),
-                    (__attribute__((address_space(3))) void *)&ring[slot][dst[d]][0], 16, 0, 0);
+                lds_dma16(src[d] + (size_t)s * kstride, &ring[slot][dst[d]][0]);
     };
     i32x4 acc[TI][TJ];
 #pragma unroll
