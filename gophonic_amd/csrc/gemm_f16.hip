@@ -700,6 +700,18 @@ static int launch_by_m(F16GemmArgs a, hipStream_t stream) {
         // 128 x 128 tiles, with K split over extra blocks when the caller gave
         // scratch for the partial sums (store epilogues only).
         const long mid = (long)((a.M + 127) / 128) * ((width + 127) / 128);
+        if constexpr (WF == W_GPTQ_ROW && EPI == EPI_PLAIN) {
+            // 129..256 rows: one 256-row block per 128 columns with 2 K splits
+            // when that makes at least 192 blocks (measured at M = 256, K = 4096
+            // -> N = 12288: 66.8 -> 59.1 us; K = 12288 -> N = 4096 keeps 128 x 128
+            // tiles and 8 splits). The caller's scratch covers the 128 x 128
+            // split count, at least 2 here.
+            if (a.M > 128 && a.M <= 256 && a.part && (width + 127) / 128 * 2 >= 192 &&
+                mm_split_count(mid, a.KT, (long)a.M * (a.c1 - a.c0)) >= 2) {
+                a.splits = 2;
+                return launch_f16gemm_big<WF, EPI, 256, 128, 4, 2, 1>(a, stream);
+            }
+        }
         a.splits = 1;
         if constexpr (EPI == EPI_PLAIN || EPI == EPI_ROWSCALE)
             if (a.part) a.splits = mm_split_count(mid, a.KT, (long)a.M * (a.c1 - a.c0));

@@ -92,6 +92,22 @@ def test_mm_split_k_matches_fp16_tile_oracle(fmt, m, k, n):
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))  # deterministic
 
 
+def test_gptq_256_row_tiles_with_two_splits():
+    # 129..256 rows over at least 96 column tiles: GPTQ takes 256 x 128 tiles
+    # with two K splits; every output against the FP16-tile oracle, twice.
+    m, k, n = 200, 512, 12288
+    fmt = orc.FMT_GPTQ4_G128
+    rng = np.random.default_rng(17)
+    codes, scales, zeros = weights(fmt, rng, n, k)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    got = run_mm(fmt, codes, scales, x, m, k, n, zeros, split=True)
+    want, absum = orc.mm_f64(fmt, codes, scales, x, m, k, n, zeros=zeros)
+    assert np.isfinite(got).all()
+    assert np.all(np.abs(got - want) <= k * 2.0 ** -23 * absum + 1e-30)
+    again = run_mm(fmt, codes, scales, x, m, k, n, zeros, split=True)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
 @pytest.mark.parametrize("m,split", [(1, False), (256, False), (256, True)])
 @pytest.mark.parametrize("k,n", [(4096, 12288), (12288, 4096)])
 def test_gptq_g128_config5_within_2e3(m, split, k, n):
