@@ -782,17 +782,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
     }
 }
 
-// Large-M variant on direct-to-LDS loads: BM x BN block tiles (WGM x WGN
-// wavefronts, each a grid of 16 x 16 v_mfma_i32_16x16x64_i8 tiles), a ring of
-// NS stages of one 64-deep K-step, every operand fragment (16 rows x 64 bytes,
-// the tile layout's 1 KiB group) loaded with global_load_lds_dwordx4 and read
-// back by the lanes that own it (lane l at byte 16 l: no bank conflicts). The
-// stage NS - 1 ahead is requested as each stage starts; the wait is a count,
-// as in the skinny kernel. For I8_ROWS a fragment is gathered from 16
-// row-major rows (lane l: row l % 16, bytes 16 (l / 16) of the step), so the
-// same LDS image and MFMA code serve both layouts. Needs KT a multiple of 1
-// (tiles) or K a multiple of 64 (rows). Epilogues as the big-tile kernel's.
-template <int BM, int BN, int WGM, int WGN, int NS, int LAYOUT, int EPI>
+// Mid-M variant on direct-to-LDS loads (the tile layout, store epilogue):
+// BM x BN block tiles (WGM x WGN wavefronts, each a grid of 16 x 16
+// v_mfma_i32_16x16x64_i8 tiles), a ring of NS stages of one 64-deep K-step,
+// every operand fragment (the tile layout's 1 KiB group of 16 rows x 64
+// bytes) loaded with global_load_lds_dwordx4 and read back by the lanes that
+// own it (lane l at byte 16 l: no bank conflicts). The stage NS - 1 ahead is
+// requested as each stage starts; the wait is a count, as in the skinny
+// kernel. When the fragments of a stage do not split evenly over the
+// wavefronts, the first F % NW issue one more.
+template <int BM, int BN, int WGM, int WGN, int NS>
 __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8GemmArgs a) {
     constexpr int NW = WGM * WGN;
     constexpr int FA = BM / 16, FB = BN / 16, F = FA + FB;  // fragments per stage
@@ -815,25 +814,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8Gemm
     for (int d = 0; d < DMAX; ++d) {
         const int f = min(wv + NW * d, F - 1);
         dst[d] = f;
-        const bool isA = f < FA;
-        const int8_t *base = isA ? a.A : a.B;
-        const int tile = isA ? rt0 + f : ct0 + (f - FA);
-        if constexpr (LAYOUT == I8_ROWS) {
-            const int rows = isA ? a.M : a.N;
-            const int row = min(tile * 16 + (lane & 15), rows - 1);
-            src[d] = base + (size_t)row * a.K + (lane >> 4) * 16;
-        } else {
-            const int tiles = isA ? MT : a.NT;
-            src[d] = base + (size_t)min(tile, tiles - 1) * KT * 1024 + (size_t)lane * 16;
-        }
+        src[d] = f < FA ? a.A + (size_t)min(rt0 + f, MT - 1) * KT * 1024 + (size_t)lane * 16
+                        : a.B + (size_t)min(ct0 + (f - FA), a.NT - 1) * KT * 1024 + (size_t)lane * 16;
     }
-    const size_t kstride = LAYOUT == I8_ROWS ? 64 : 1024;
     auto stage_load = [&](int s) {
         const int slot = s % NS;
 #pragma unroll
         for (int d = 0; d < DMAX; ++d)
-            if (d < DMAX - 1 || full)
-                lds_dma16(src[d] + (size_t)s * kstride, &ring[slot][dst[d]][0]);
+            if (d < DMAX - 1 || full) lds_dma16(src[d] + (size_t)s * 1024, &ring[slot][dst[d]][0]);
     };
     i32x4 acc[TI][TJ];
 #pragma unroll
@@ -844,19 +832,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8Gemm
     for (int p = 0; p < NS - 1; ++p)
         if (p < KT) stage_load(p);
     for (int s = 0; s < KT; ++s) {
+        // Loads of the stages after s already requested may stay in flight.
         const int after = min(KT - 1 - s, NS - 2);
         if (after == NS - 2) {
             if (full)
                 wait_vm_lgkm0<DMAX * (NS - 2)>();
             else
                 wait_vm_lgkm0<(DMAX - 1) * (NS - 2)>();
-        } else if (after > 0) {
-            // Fewer stages in flight near the end: wait for all but `after` of them.
-            if (full) {
-                if (after == 1) wait_vm_lgkm0<DMAX>(); else wait_vm_lgkm0<0>();
-            } else {
-                if (after == 1) wait_vm_lgkm0<DMAX - 1>(); else wait_vm_lgkm0<0>();
-            }
+        } else if (after == 1) {
+            if (full)
+                wait_vm_lgkm0<DMAX>();
+            else
+                wait_vm_lgkm0<DMAX - 1>();
         } else {
             wait_vm_lgkm0<0>();
         }
@@ -874,8 +861,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8Gemm
             for (int j = 0; j < TJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
-    // Epilogue: lane l of a 16 x 16 tile holds rows 4 (l / 16) + e, column
-    // l % 16. Scales first, unconditionally, as in the other kernels.
+    // Epilogue as in i8gemm_kernel: lane l of a 16 x 16 tile holds rows
+    // 4 (l / 16) + e, column l % 16; scales first, then the stores.
     const int mt0 = rt0 + wm * TI, nt0 = ct0 + wn * TJ;
     float rsc[TI][4], csc[TJ];
 #pragma unroll
@@ -890,38 +877,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8Gemm
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int col = (nt0 + j) * 16 + (lane & 15);
-        const bool colOk = col >= a.c0 && col < a.c1;
-        if constexpr (EPI != I8_EPI_SWIGLU) {
-            if (!colOk) continue;
-        }
+        if (col < a.c0 || col >= a.c1) continue;
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
-                const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], colOk ? csc[j] : 0.0f), rsc[i][e]);
-                if constexpr (EPI == I8_EPI_STORE) {
-                    if (row < a.M) a.dst[(size_t)row * a.stride + col] = v;
-                } else if constexpr (EPI == I8_EPI_ADD) {
-                    if (row < a.M) __builtin_amdgcn_global_atomic_fadd_f32(a.dst + (size_t)row * a.stride + col, v);
-                } else {
-                    // The up value of the neighbouring lane (DPP quad_perm [1,0,3,2]).
-                    const float u = __builtin_bit_cast(
-                        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
-                    if (colOk && !(col & 1) && row < a.M)
-                        a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
-                }
+                if (row < a.M)
+                    a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], csc[j]), rsc[i][e]);
             }
     }
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int LAYOUT = I8_TILES, int EPI = I8_EPI_STORE>
+template <int BM, int BN, int WGM, int WGN, int NS>
 static int launch_i8gemm_dma(I8GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
     a.gridN = (tiles * 16 + BN - 1) / BN;
     a.gridM = (a.M + BM - 1) / BM;
-    if (LAYOUT == I8_ROWS) a.KT = a.K / 64;
-    hipLaunchKernelGGL((i8gemm_dma_kernel<BM, BN, WGM, WGN, NS, LAYOUT, EPI>), dim3((unsigned)(a.gridM * a.gridN)),
+    hipLaunchKernelGGL((i8gemm_dma_kernel<BM, BN, WGM, WGN, NS>), dim3((unsigned)(a.gridM * a.gridN)),
                        dim3(64 * WGM * WGN), 0, stream, a);
     return launch_status();
 }
