@@ -975,8 +975,7 @@ int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const
     if (M > 128 && M <= 256) return launch_i8gemm_dma<64, 192, 2, 4, 8>(a, stream);
     if (M > 256 && M <= 512) return launch_i8gemm_dma<128, 192, 2, 4, 6>(a, stream);
     if (M <= 64) return launch_i8gemm<4, 1, 1, 2, 4, 4>(a, stream);
-    if (M <= 192) return launch_i8gemm_lds<128, 64, 2, 2, 4>(a, stream);
-    if (M < 512) return launch_i8gemm_big<128, 128, 2, 2>(a, stream);
+    if (M <= 128) return launch_i8gemm_lds<128, 64, 2, 2, 4>(a, stream);
     return launch_i8gemm_big<128, 192, 4, 2>(a, stream);
 }
 

@@ -75,7 +75,9 @@ SHAPES = [(1, 4, 1), (3, 7, 17), (12, 64, 64), (16, 257, 129), (12, 4096, 1024),
           # column tiles past N in a block, two row blocks
           (24, 256, 200), (48, 256, 500), (130, 1024, 64), (256, 2048, 77), (33, 12288, 48),
           # direct-to-LDS big tiles (129..512 rows), K not a multiple of 256
-          (300, 640, 260), (512, 192, 200), (140, 64, 40)]
+          (300, 640, 260), (512, 192, 200), (140, 64, 40),
+          # K not a multiple of 256 from 65 rows (LDS kernel) and past 512 rows (big tiles)
+          (100, 640, 200), (600, 320, 130)]
 
 
 @pytest.mark.parametrize("rows,k,n", SHAPES, ids=[f"M{r}K{k}N{n}" for r, k, n in SHAPES])
