@@ -30,6 +30,14 @@ __host__ __device__ inline size_t tile_offset(long r, long k, long kt) {
     return ((size_t)(r >> 4) * kt + (k >> 6)) * 1024 + (size_t)((((k & 63) >> 4) << 4) + (r & 15)) * 16 + (k & 15);
 }
 
+// The batched pass's int8 activations ("row tiles"): the same 1 KiB groups of
+// 16 rows x 64 bytes, each row's 64 bytes contiguous inside the group, so a
+// row-at-a-time packer writes 64-byte pieces. The direct-to-LDS GEMM gathers
+// a group into the tile layout's lane order within its own 1 KiB.
+__host__ __device__ inline size_t rowtile_offset(long r, long k, long kt) {
+    return ((size_t)(r >> 4) * kt + (k >> 6)) * 1024 + (size_t)(r & 15) * 64 + (k & 63);
+}
+
 // ---- weight packing: row-major int8 [rows][K] -> tile layout ---------------
 // One thread per 16-byte lane chunk of the destination; rows past `rows`
 // (inside the last 16-row tile) and K padding are written as zero.
@@ -152,8 +160,8 @@ __global__ __launch_bounds__(256) void i8_pack_range_kernel(const float *__restr
 // (qwen3lm/ops.go:96-147: the row is normalized, SetRowScale(MaxAbs), then
 // PackRange) over the GPU layer formats: per row v = x * f with f the RMSNorm
 // factor (MODE 2, the FP16 packer's sum order) or 1 (MODE 1); SetRowScale of
-// max|v| (NaN-propagating); q = quantize(v * inv) written row-major
-// [rows][K]; rowScale[r] = max / 127. One block per row, the row in
+// max|v| (NaN-propagating); q = quantize(v * inv) written as row tiles
+// (rowtile_offset, K a multiple of 64); rowScale[r] = max / 127. One block per row, the row in
 // registers (CPT chunks of 16 values per thread). ROT first rotates the row
 // as the down projection's input (the online Hadamard, gpu.metal:339-367;
 // the CPU path's scaleRow, qwen3lm/ops.go:111-122): x * signs (signs carry
@@ -222,14 +230,14 @@ __global__ __launch_bounds__(256) void i8_act_rows_kernel(const float *__restric
             }
             w[q] = packed;
         }
-        *(uint4 *)(act + (size_t)row * K + k) = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4 *)(act + rowtile_offset(row, k, K >> 6)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
 // ---- GEMM ------------------------------------------------------------------
 struct I8GemmArgs {
-    const int8_t *A;      // activations, tile layout, MT x KT groups (row-major [M][K] for I8_ROWS)
-    const int8_t *B;      // weights, tile layout, NT x KT groups (row-major [N][K] for I8_ROWS)
+    const int8_t *A;      // activations, tile layout, MT x KT groups (row tiles for the batched pass)
+    const int8_t *B;      // weights, tile layout, NT x KT groups (row-major [N][K] for the batched pass)
     const float *rowScale;  // [M]
     const float *colScale;  // [N]
     float *dst;
@@ -238,11 +246,10 @@ struct I8GemmArgs {
     int c0, c1;  // output columns [c0, c1)
     int tileN0;  // first 16-column tile covered by the grid
     int gridM, gridN;  // blocks along M and N
-    int K;             // row length in bytes of row-major operands (a multiple of 16)
+    int K;             // row length in bytes of row-major weights (a multiple of 64)
 };
 
 // Operand layouts and epilogues of the big-tile kernel.
-enum { I8_TILES = 0, I8_ROWS = 1 };
 enum { I8_EPI_STORE = 0, I8_EPI_ADD = 1, I8_EPI_SWIGLU = 2 };
 
 template <int TM, int TN, int WM, int WN, int SK, int U>
@@ -608,12 +615,9 @@ __global__ __launch_bounds__(64 * NWV) void i8gemm_skinny_kernel(const I8GemmArg
 // as 128-byte rows with the row-swizzled 16-byte chunks of the FP16 big-tile
 // GEMM, double-buffered with the next step's global loads in flight;
 // XCD-grouped tile order. Exact int32 sums, so the bits equal the other
-// kernels'. Operands come in the tile layout (two 64-deep groups per step) or,
-// for I8_ROWS, as row-major int8 rows (8 consecutive lanes read one row's 128
-// bytes of the step). Epilogue: (float32(sum) * colScale) * rowScale, then a
-// store, an add into dst (I8_EPI_ADD), or the SwiGLU of interleaved gate/up
-// columns into dst[row][col / 2] (I8_EPI_SWIGLU).
-template <int BM, int BN, int WGM, int WGN, int LAYOUT, int EPI>
+// kernels'. Operands come in the tile layout (two 64-deep groups per step).
+// Epilogue: (float32(sum) * colScale) * rowScale, stored.
+template <int BM, int BN, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8GemmArgs a) {
     typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
     constexpr int NT = 64 * WGM * WGN;
@@ -629,35 +633,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
     const int rt0 = bm * (BM / 16), ct0 = a.tileN0 + bn * (BN / 16);
     const int MT = (a.M + 15) >> 4, KT = a.KT;
     const int steps = (KT + 1) / 2;
-    // Tile layout: unit u = i*NT + t of a step is 16-row tile u/128, group
-    // (u/64)%2 of the step, lane slot u%64 (row slot%16, K bytes
-    // 16*(slot/16) of the group). Rows: unit u is row u/8, chunk u%8.
+    // Unit u = i*NT + t of a step is 16-row tile u/128, group (u/64)%2 of the
+    // step, lane slot u%64 (row slot%16, K bytes 16*(slot/16) of the group).
     auto gload = [&](const int8_t *base, int tile0, int tiles, int u, int st) {
         i32x4 v = i32x4{0, 0, 0, 0};
-        if constexpr (LAYOUT == I8_ROWS) {
-            // Rows past the operand's last read that row again (their
-            // outputs are not stored); K past the row end reads zero.
-            const int k = st * 128 + (u & 7) * 16;
-            if (k < a.K) v = *(const i32x4 *)(base + (size_t)min(tile0 * 16 + (u >> 3), tiles - 1) * a.K + k);
-        } else {
-            const int kt = 2 * st + ((u >> 6) & 1);
-            if (kt < KT)
-                v = *(const i32x4 *)(base + ((size_t)min(tile0 + (u >> 7), tiles - 1) * KT + kt) * 1024 +
-                                     (size_t)(u & 63) * 16);
-        }
+        const int kt = 2 * st + ((u >> 6) & 1);
+        if (kt < KT)
+            v = *(const i32x4 *)(base + ((size_t)min(tile0 + (u >> 7), tiles - 1) * KT + kt) * 1024 +
+                                 (size_t)(u & 63) * 16);
         return v;
     };
     auto lidx = [](int u) {
-        if constexpr (LAYOUT == I8_ROWS) {
-            const int r = u >> 3;
-            return r * 8 + big_swz(r, u & 7);
-        } else {
-            const int r = (u >> 7) * 16 + (u & 15);
-            return r * 8 + big_swz(r, ((u >> 6) & 1) * 4 + ((u & 63) >> 4));
-        }
+        const int r = (u >> 7) * 16 + (u & 15);
+        return r * 8 + big_swz(r, ((u >> 6) & 1) * 4 + ((u & 63) >> 4));
     };
-    // Row bounds passed to gload: 16-row tiles in the tile layout, rows for I8_ROWS.
-    const int aRows = LAYOUT == I8_ROWS ? a.M : MT, bRows = LAYOUT == I8_ROWS ? a.N : a.NT;
+    const int aRows = MT, bRows = a.NT;
     i32x4 ar[AL], br[BL];
     auto load = [&](int st) {
 #pragma unroll
@@ -738,60 +728,39 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
         const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
         csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
     }
-    if constexpr (EPI == I8_EPI_STORE) {
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
-            if (col < a.c0 || col >= a.c1) continue;
-            const float cs = csc[j];
+    for (int j = 0; j < TJ; ++j) {
+        const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
+        if (col < a.c0 || col >= a.c1) continue;
+        const float cs = csc[j];
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = (rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3);
-                    if (row < a.M)
-                        a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), rsc[i][e]);
-                }
-        }
-    } else {
-        // Every lane runs the SwiGLU exchange, so no lane leaves the loop early.
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const int col = (ct0 + (wn * TJ + j) * 2) * 16 + fr;
-            const bool colOk = col >= a.c0 && col < a.c1;
-            const float cs = colOk ? csc[j] : 0.0f;
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = (rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3);
-                    const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), rsc[i][e]);
-                    if constexpr (EPI == I8_EPI_SWIGLU) {
-                        // The up value of the neighbouring lane (DPP quad_perm [1,0,3,2]).
-                        const float u = __builtin_bit_cast(
-                            float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
-                        if (colOk && !(col & 1) && row < a.M)
-                            a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
-                    } else if (colOk && row < a.M) {
-                        // One fp32 add into the residual, done in L2 (each
-                        // element has one owner, so the sum is y + v exactly).
-                        __builtin_amdgcn_global_atomic_fadd_f32(a.dst + (size_t)row * a.stride + col, v);
-                    }
-                }
-        }
+            for (int e = 0; e < 16; ++e) {
+                const int row = (rt0 + (wm * TI + i) * 2) * 16 + 8 * (e >> 2) + 4 * fh + (e & 3);
+                if (row < a.M)
+                    a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], cs), rsc[i][e]);
+            }
     }
 }
 
-// Mid-M variant on direct-to-LDS loads (the tile layout, store epilogue):
-// BM x BN block tiles (WGM x WGN wavefronts, each a grid of 16 x 16
-// v_mfma_i32_16x16x64_i8 tiles), a ring of NS stages of one 64-deep K-step,
-// every operand fragment (the tile layout's 1 KiB group of 16 rows x 64
-// bytes) loaded with global_load_lds_dwordx4 and read back by the lanes that
-// own it (lane l at byte 16 l: no bank conflicts). The stage NS - 1 ahead is
+// Direct-to-LDS variant: BM x BN block tiles (WGM x WGN wavefronts, each a
+// grid of 16 x 16 v_mfma_i32_16x16x64_i8 tiles), a ring of NS stages of one
+// 64-deep K-step, every operand fragment (the tile layout's 1 KiB group of
+// 16 rows x 64 bytes) loaded with global_load_lds_dwordx4 and read back by
+// the lanes that own it (lane l at byte 16 l: no bank conflicts). BROWS (the
+// batched pass) takes A as row tiles (rowtile_offset) and B from row-major
+// rows (a.K bytes each, K a multiple of 64): each fragment is gathered into
+// the same LDS image, lane l reading row l % 16 at byte 16 (l / 16) of the
+// step (for A inside one 1 KiB group). The stage NS - 1 ahead is
 // requested as each stage starts; the wait is a count, as in the skinny
 // kernel. When the fragments of a stage do not split evenly over the
-// wavefronts, the first F % NW issue one more.
-template <int BM, int BN, int WGM, int WGN, int NS>
+// wavefronts, the first F % NW issue one more. Epilogue (float32(sum) *
+// colScale) * rowScale, then a store, an fp32 atomic add into dst
+// (I8_EPI_ADD: one owner per element, so exactly dst + v) or the SwiGLU of
+// interleaved gate/up columns into dst[row][col / 2] (I8_EPI_SWIGLU, the
+// neighbouring column's value by DPP).
+template <int BM, int BN, int WGM, int WGN, int NS, bool BROWS, int EPI>
 __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8GemmArgs a) {
     constexpr int NW = WGM * WGN;
     constexpr int FA = BM / 16, FB = BN / 16, F = FA + FB;  // fragments per stage
@@ -814,14 +783,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8Gemm
     for (int d = 0; d < DMAX; ++d) {
         const int f = min(wv + NW * d, F - 1);
         dst[d] = f;
-        src[d] = f < FA ? a.A + (size_t)min(rt0 + f, MT - 1) * KT * 1024 + (size_t)lane * 16
-                        : a.B + (size_t)min(ct0 + (f - FA), a.NT - 1) * KT * 1024 + (size_t)lane * 16;
+        if (f < FA) {
+            // With BROWS, A comes as row tiles (rowtile_offset): lane l gathers
+            // row l % 16's bytes 16 (l / 16) of the group.
+            src[d] = a.A + (size_t)min(rt0 + f, MT - 1) * KT * 1024 +
+                     (BROWS ? (size_t)(lane & 15) * 64 + (lane >> 4) * 16 : (size_t)lane * 16);
+        } else if constexpr (BROWS) {
+            src[d] = a.B + (size_t)min((ct0 + (f - FA)) * 16 + (lane & 15), a.N - 1) * a.K + (lane >> 4) * 16;
+        } else {
+            src[d] = a.B + (size_t)min(ct0 + (f - FA), a.NT - 1) * KT * 1024 + (size_t)lane * 16;
+        }
     }
     auto stage_load = [&](int s) {
         const int slot = s % NS;
 #pragma unroll
         for (int d = 0; d < DMAX; ++d)
-            if (d < DMAX - 1 || full) lds_dma16(src[d] + (size_t)s * 1024, &ring[slot][dst[d]][0]);
+            if (d < DMAX - 1 || full)
+                lds_dma16(src[d] + (size_t)s * (BROWS && dst[d] >= FA ? 64 : 1024), &ring[slot][dst[d]][0]);
     };
     i32x4 acc[TI][TJ];
 #pragma unroll
@@ -877,34 +855,47 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8Gemm
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int col = (nt0 + j) * 16 + (lane & 15);
-        if (col < a.c0 || col >= a.c1) continue;
+        const bool colOk = col >= a.c0 && col < a.c1;
+        if constexpr (EPI != I8_EPI_SWIGLU) {
+            if (!colOk) continue;
+        }
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
-                if (row < a.M)
-                    a.dst[(size_t)row * a.stride + col] = __fmul_rn(__fmul_rn((float)acc[i][j][e], csc[j]), rsc[i][e]);
+                const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], csc[j]), rsc[i][e]);
+                if constexpr (EPI == I8_EPI_STORE) {
+                    if (row < a.M) a.dst[(size_t)row * a.stride + col] = v;
+                } else if constexpr (EPI == I8_EPI_ADD) {
+                    if (row < a.M) __builtin_amdgcn_global_atomic_fadd_f32(a.dst + (size_t)row * a.stride + col, v);
+                } else {
+                    // Every lane runs the exchange (DPP quad_perm [1,0,3,2]: lane l ^ 1 holds column col ^ 1).
+                    const float u = __builtin_bit_cast(
+                        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+                    if (colOk && !(col & 1) && row < a.M)
+                        a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
+                }
             }
     }
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS>
+template <int BM, int BN, int WGM, int WGN, int NS, bool BROWS = false, int EPI = I8_EPI_STORE>
 static int launch_i8gemm_dma(I8GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
     a.gridN = (tiles * 16 + BN - 1) / BN;
     a.gridM = (a.M + BM - 1) / BM;
-    hipLaunchKernelGGL((i8gemm_dma_kernel<BM, BN, WGM, WGN, NS>), dim3((unsigned)(a.gridM * a.gridN)),
+    hipLaunchKernelGGL((i8gemm_dma_kernel<BM, BN, WGM, WGN, NS, BROWS, EPI>), dim3((unsigned)(a.gridM * a.gridN)),
                        dim3(64 * WGM * WGN), 0, stream, a);
     return launch_status();
 }
 
-template <int BM, int BN, int WGM, int WGN, int LAYOUT = I8_TILES, int EPI = I8_EPI_STORE>
+template <int BM, int BN, int WGM, int WGN>
 static int launch_i8gemm_big(I8GemmArgs a, hipStream_t stream) {
     const int tiles = (a.c1 + 15) / 16 - a.tileN0;
     a.gridN = (tiles * 16 + BN - 1) / BN;
     a.gridM = (a.M + BM - 1) / BM;
-    hipLaunchKernelGGL((i8gemm_big_kernel<BM, BN, WGM, WGN, LAYOUT, EPI>), dim3((unsigned)(a.gridM * a.gridN)),
+    hipLaunchKernelGGL((i8gemm_big_kernel<BM, BN, WGM, WGN>), dim3((unsigned)(a.gridM * a.gridN)),
                        dim3(64 * WGM * WGN), 0, stream, a);
     return launch_status();
 }
@@ -1005,9 +996,11 @@ static int launch_i8_act_rows(const float *x, long stride, int rows, int K, floa
 }
 
 // int8 activations of the batched pass (see i8_act_rows_kernel): x rows
-// `stride` floats apart and 16-byte aligned, K % 16 == 0, K <= 16384; act is
-// row-major [rows][K]. signs (device, K values with the rotation's scale
-// folded in) rotate each row first, in blocks of `block`; null for none.
+// `stride` floats apart and 16-byte aligned, K % 64 == 0, K <= 16384; act is
+// in row tiles (rowtile_offset: ceil(rows / 16) * 16 rows of K bytes; rows
+// past `rows` in the last tile are not written). signs (device, K values with the
+// rotation's scale folded in) rotate each row first, in blocks of `block`;
+// null for none.
 int lm_i8_act(const float *x, long stride, int rows, int K, bool norm, float eps, const float *signs, int block,
               int8_t *act, float *rowScale, hipStream_t stream) {
     if (rows == 0) return GPHQ_OK;
@@ -1020,10 +1013,10 @@ int lm_i8_act(const float *x, long stride, int rows, int K, bool norm, float eps
 }
 
 // One projection of the batched pass on the int8 route: y = (float32(A W^T)
-// * w_scale) * a_scale for row-major int8 activations A [M][K] and Q8 codes W
-// [N][K] (one fp32 scale per weight row), then epi 0 stores y[M][N], 1 adds
-// it into y, 2 stores the SwiGLU of interleaved gate/up columns into
-// y[M][N/2]; y rows are y_stride floats apart. K % 16 == 0.
+// * w_scale) * a_scale for int8 activations A in row tiles (lm_i8_act)
+// and row-major Q8 codes W [N][K] (one fp32 scale per weight row), then epi 0
+// stores y[M][N], 1 adds it into y, 2 stores the SwiGLU of interleaved gate/up
+// columns into y[M][N/2]; y rows are y_stride floats apart. K % 64 == 0.
 int lm_i8_mm(int epi, const int8_t *act, const float *a_scale, const int8_t *codes, const float *w_scale, float *y,
              long y_stride, int M, int K, int N, hipStream_t stream) {
     if (M == 0 || N == 0) return GPHQ_OK;
@@ -1042,19 +1035,13 @@ int lm_i8_mm(int epi, const int8_t *act, const float *a_scale, const int8_t *cod
     a.c0 = 0;
     a.c1 = N;
     a.tileN0 = 0;
-    // Tile shapes by measurement on MI355X at M = 4096 (Qwen3-8B's projections):
-    // 256 x 256 tiles (one block per CU) when they fill whole waves of 256
-    // CUs (O: 125 -> 118 us, down: 295 -> 239, gate/up: 628 -> 549 against
-    // 128 x 192), else 128 x 192 (QKV's 384 tiles: 160 -> 138 us).
-    const long big = (long)((M + 255) / 256) * ((N + 255) / 256);
-    if (big % 256 == 0) {
-        if (epi == 0) return launch_i8gemm_big<256, 256, 4, 2, I8_ROWS, I8_EPI_STORE>(a, stream);
-        if (epi == 1) return launch_i8gemm_big<256, 256, 4, 2, I8_ROWS, I8_EPI_ADD>(a, stream);
-        return launch_i8gemm_big<256, 256, 4, 2, I8_ROWS, I8_EPI_SWIGLU>(a, stream);
-    }
-    if (epi == 0) return launch_i8gemm_big<128, 192, 4, 2, I8_ROWS, I8_EPI_STORE>(a, stream);
-    if (epi == 1) return launch_i8gemm_big<128, 192, 4, 2, I8_ROWS, I8_EPI_ADD>(a, stream);
-    return launch_i8gemm_big<128, 192, 4, 2, I8_ROWS, I8_EPI_SWIGLU>(a, stream);
+    // 256 x 256 tiles on direct-to-LDS loads, the weights gathered from their
+    // rows. Measured on MI355X at M = 4096 (Qwen3-8B's projections, store
+    // epilogue) against the register-staged big-tile kernel on row-major
+    // operands: QKV 152 -> 141 us, gate/up 527 -> 479, down 207 -> 187.
+    if (epi == 0) return launch_i8gemm_dma<256, 256, 4, 2, 4, true, I8_EPI_STORE>(a, stream);
+    if (epi == 1) return launch_i8gemm_dma<256, 256, 4, 2, 4, true, I8_EPI_ADD>(a, stream);
+    return launch_i8gemm_dma<256, 256, 4, 2, 4, true, I8_EPI_SWIGLU>(a, stream);
 }
 
 int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {

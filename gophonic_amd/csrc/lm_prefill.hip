@@ -54,7 +54,7 @@ struct gphq_prefill {
     int32_t *rowpos, *rowstart;  // packed passes: each row's position and its sequence's first row
     float *okc = nullptr, *ovc = nullptr;  // packed passes' own K/V [layers][rows][kv_dim], on first use
     int arith = GPHQ_PASS_FP16;
-    int8_t *a8 = nullptr;  // int8 route: row-major activations [rows][K] and their row scales, on first use
+    int8_t *a8 = nullptr;  // int8 route: activations in 16-row tiles and their row scales, on first use
     float *s8 = nullptr;
     std::vector<void *> allocs;
 };
@@ -515,9 +515,11 @@ int gphq_prefill_set_arith(gphq_prefill *ws, int arith) {
     if (arith == GPHQ_PASS_INT8) {
         const gphq_lm *lm = ws->lm;
         if (lm->cfg.fmt != GPHQ_FMT_Q8) return GPHQ_ERR_UNSUPPORTED;
+        // The int8 GEMM takes 64-deep K steps of 16-row activation tiles.
+        if (lm->cfg.hidden % 64 || lm->qd % 64 || lm->cfg.intermediate % 64) return GPHQ_ERR_UNSUPPORTED;
         if (!ws->a8) {
             const int64_t kmax = std::max({(int64_t)lm->cfg.hidden, lm->qd, (int64_t)lm->cfg.intermediate});
-            hipError_t e = hipMalloc((void **)&ws->a8, (size_t)ws->rows * kmax);
+            hipError_t e = hipMalloc((void **)&ws->a8, (size_t)((ws->rows + 15) / 16 * 16) * kmax);
             if (e != hipSuccess) {
                 ws->a8 = nullptr;
                 return hip_status(e);
