@@ -89,6 +89,7 @@ struct gphq_decode_batch {
     const gphq_lm *lm;
     int capacity;
     float *h, *qkv, *ctx, *act, *hn, *hidden, *logits, *part;
+    uint32_t *cand;  // argmax candidates [lanes][parts][key, index]
     int32_t *tok, *pos, *start, *nonfinite;
     void *vec_work;
     size_t vec_bytes;
@@ -570,33 +571,10 @@ __device__ __forceinline__ void consider(float v, int i, uint32_t &bk, uint32_t 
     }
 }
 
-// First-maximum argmax of each lane's logits (decode_batch.go:182-191
-// greedyArgmax; a NaN at index 0 keeps index 0): one block per lane. Writes
-// the next token, feeds it back as the lane's current token and advances the
-// lane's position.
-__global__ __launch_bounds__(1024) void lm_argmax_kernel(const ArgmaxArgs a) {
-    __shared__ uint32_t sk[16], si[16];
-    const int lane = blockIdx.x;
-    const float *x = a.logits + (size_t)lane * a.stride;
-    uint32_t bk = 0, bi = kNone;
-    const int n4 = a.vocab >> 2;
-    for (int c0 = threadIdx.x; c0 < n4; c0 += 4 * blockDim.x) {
-        float4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int c = c0 + u * blockDim.x;
-            v[u] = c < n4 ? *((const float4 *)x + c) : make_float4(NAN, NAN, NAN, NAN);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = 4 * (c0 + u * blockDim.x);
-            consider(v[u].x, i, bk, bi);
-            consider(v[u].y, i + 1, bk, bi);
-            consider(v[u].z, i + 2, bk, bi);
-            consider(v[u].w, i + 3, bk, bi);
-        }
-    }
-    for (int i = 4 * n4 + threadIdx.x; i < a.vocab; i += blockDim.x) consider(x[i], i, bk, bi);
+// Best (key, index) over the wavefront's lanes, then over the block's
+// wavefronts through LDS; the result lands in thread 0.
+template <int NW>
+__device__ __forceinline__ void block_best(uint32_t &bk, uint32_t &bi, uint32_t *sk, uint32_t *si) {
     for (int off = 32; off > 0; off >>= 1) {
         const uint32_t ko = __shfl_xor(bk, off), io = __shfl_xor(bi, off);
         if (better(ko, io, bk, bi)) bk = ko, bi = io;
@@ -609,9 +587,51 @@ __global__ __launch_bounds__(1024) void lm_argmax_kernel(const ArgmaxArgs a) {
     if (threadIdx.x != 0) return;
     bk = sk[0];
     bi = si[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+#pragma unroll
+    for (int w = 1; w < NW; ++w)
         if (better(sk[w], si[w], bk, bi)) bk = sk[w], bi = si[w];
-    const uint32_t first = __builtin_bit_cast(uint32_t, x[0]) & 0x7FFFFFFFu;
+}
+
+// First-maximum argmax of each lane's logits (decode_batch.go:182-191
+// greedyArgmax; a NaN at index 0 keeps index 0), in two launches: the
+// logits of a lane are split over kArgParts blocks, each writing its best
+// (key, index) to cand[lane][part]; then one block per lane takes the best
+// candidate (the order is total: key, then index, so the split does not
+// change the winner), writes the next token, feeds it back as the lane's
+// current token and advances the lane's position.
+constexpr int kArgParts = 128;
+
+__global__ __launch_bounds__(256) void lm_argmax_part_kernel(const ArgmaxArgs a, uint32_t *cand) {
+    __shared__ uint32_t sk[4], si[4];
+    const int part = blockIdx.x, lane = blockIdx.y;
+    const float *x = a.logits + (size_t)lane * a.stride;
+    const int n4 = a.vocab >> 2, per = (n4 + kArgParts - 1) / kArgParts;
+    const int u0 = part * per, u1 = min(n4, u0 + per);
+    uint32_t bk = 0, bi = kNone;
+    for (int u = u0 + threadIdx.x; u < u1; u += blockDim.x) {
+        const float4 v = *((const float4 *)x + u);
+        consider(v.x, 4 * u, bk, bi);
+        consider(v.y, 4 * u + 1, bk, bi);
+        consider(v.z, 4 * u + 2, bk, bi);
+        consider(v.w, 4 * u + 3, bk, bi);
+    }
+    if (part == kArgParts - 1)
+        for (int i = 4 * n4 + threadIdx.x; i < a.vocab; i += blockDim.x) consider(x[i], i, bk, bi);
+    block_best<4>(bk, bi, sk, si);
+    if (threadIdx.x == 0) {
+        cand[((size_t)lane * kArgParts + part) * 2] = bk;
+        cand[((size_t)lane * kArgParts + part) * 2 + 1] = bi;
+    }
+}
+
+__global__ __launch_bounds__(128) void lm_argmax_kernel(const ArgmaxArgs a, const uint32_t *cand) {
+    __shared__ uint32_t sk[2], si[2];
+    const int lane = blockIdx.x;
+    uint32_t bk = cand[((size_t)lane * kArgParts + threadIdx.x) * 2];
+    uint32_t bi = cand[((size_t)lane * kArgParts + threadIdx.x) * 2 + 1];
+    const uint32_t first = __builtin_bit_cast(uint32_t, a.logits[(size_t)lane * a.stride]) & 0x7FFFFFFFu;
+    block_best<2>(bk, bi, sk, si);
+    if (threadIdx.x != 0) return;
     const int32_t token = (first > 0x7F800000u || bi == kNone) ? 0 : (int32_t)bi;
     const int32_t p = a.pos[lane];
     if (a.run) a.run[(size_t)(p - a.start[lane]) * a.lanes + lane] = token;
@@ -727,7 +747,9 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool 
     GPHQ_TRY(gemv(ws, lanes, GPHQ_FMT_Q8B, PRO_PLAIN, EPI_STORE, lm->head, 0, lm->head_scale, ws->hn, H, ws->logits,
                   lm->head_rows, H, lm->head_rows, st));
     ArgmaxArgs ga{ws->logits, (int)lm->head_rows, (int)c.vocab, lanes, ws->tok, ws->pos, ws->start, next_out, run_out};
-    hipLaunchKernelGGL(lm_argmax_kernel, dim3(lanes), dim3(1024), 0, st, ga);
+    hipLaunchKernelGGL(lm_argmax_part_kernel, dim3(kArgParts, lanes), dim3(256), 0, st, ga, ws->cand);
+    GPHQ_TRY(launch_status());
+    hipLaunchKernelGGL(lm_argmax_kernel, dim3(lanes), dim3(kArgParts), 0, st, ga, (const uint32_t *)ws->cand);
     return launch_status();
 }
 
@@ -1120,6 +1142,7 @@ int gphq_decode_batch_new(const gphq_lm *lm, int64_t capacity, gphq_decode_batch
         {(void **)&ws->hidden, (size_t)capacity * H * 4},
         {(void **)&ws->logits, (size_t)capacity * lm->head_rows * 4},
         {(void **)&ws->part, partFloats * 4},
+        {(void **)&ws->cand, (size_t)capacity * kArgParts * 8},
         {(void **)&ws->tok, (size_t)capacity * 4},
         {(void **)&ws->pos, (size_t)capacity * 4},
         {(void **)&ws->start, (size_t)capacity * 4},
