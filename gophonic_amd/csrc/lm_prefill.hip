@@ -11,6 +11,8 @@
 //   * lm_qk_rope_kernel: head RMSNorm and RoPE of every query and key head,
 //     queries scaled by 1/sqrt(head_dim) in place, keys and values appended
 //     at cache rows base + m (gpu.metal:1027-1056 qkRope);
+//   * lm_kv_half_kernel: FP16 copies of the pass's 32-row K/V cache tiles,
+//     converted once per layer for every query block of the next kernel;
 //   * lm_flash_kernel: causal attention of each row m over cache rows
 //     0 .. base + m (gpu.metal:1099-1240 attendFlash);
 //   * the O projection added into the residual, the gate/up projection with
@@ -24,6 +26,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -53,6 +56,7 @@ struct gphq_prefill {
     int32_t *tok, *nonfinite;
     int32_t *rowpos, *rowstart;  // packed passes: each row's position and its sequence's first row
     float *okc = nullptr, *ovc = nullptr;  // packed passes' own K/V [layers][rows][kv_dim], on first use
+    _Float16 *kv16;  // FP16 K and V^T of the pass's 32-row cache tiles, per layer (lm_kv_half_kernel)
     int arith = GPHQ_PASS_FP16;
     int8_t *a8 = nullptr;  // int8 route: activations in 16-row tiles and their row scales, on first use
     float *s8 = nullptr;
@@ -117,13 +121,50 @@ __global__ __launch_bounds__(64) void lm_qk_rope_kernel(const RopeArgs a) {
     d[lane + 64] = src[lane + 64];
 }
 
+// FP16 copies of a pass's K/V cache tiles for lm_flash_kernel, made once per
+// layer instead of by every query block: absolute 32-row tiles k0 .. of the
+// layer's cache (rows from kvEnd on are zero). Per (tile, KV head), K as
+// [32 keys][128] and V^T as [128 dims][32 key positions] in the flash
+// kernel's LDS key order; the same fp32 -> FP16 rounding the flash kernel
+// applies to the fp32 tiles it stages itself, so attention's results do not
+// change.
+constexpr int kKvHalfTile = 2 * 32 * kHeadDim;  // halves per (tile, KV head): K then V^T
+inline int kv16_tiles(int64_t rows) { return (int)((rows + 31) / 32 + 1); }  // any alignment of the pass rows
+
+__global__ __launch_bounds__(256) void lm_kv_half_kernel(const float *__restrict__ kc, const float *__restrict__ vc,
+                                                         int kvd, int k0, int kvEnd, _Float16 *__restrict__ out) {
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    const int g = blockIdx.y, jb = (k0 + (int)blockIdx.x) * 32;
+    _Float16 *kt = out + ((size_t)blockIdx.x * gridDim.y + g) * kKvHalfTile;
+    _Float16 *vt = kt + 32 * kHeadDim;
+    for (int u = threadIdx.x; u < 32 * kHeadDim / 4; u += 256) {
+        const int key = u >> 5, d4 = 4 * (u & 31), j = jb + key;
+        const float4 x = j < kvEnd ? *(const float4 *)(kc + (size_t)j * kvd + g * kHeadDim + d4)
+                                   : float4{0.f, 0.f, 0.f, 0.f};
+        *(half4 *)(kt + key * kHeadDim + d4) = half4{(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w};
+    }
+    for (int u = threadIdx.x; u < 32 * kHeadDim / 4; u += 256) {
+        // Key group kg (keys 4kg..4kg+3) at position group 4*(kg/4) + {0, 2, 1, 3}[kg % 4].
+        const int d = u & (kHeadDim - 1), kg = u >> 7, r = kg & 3;
+        const int pg = (kg & ~3) + ((r == 1) ? 2 : (r == 2) ? 1 : r);
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = jb + 4 * kg + i;
+            v[i] = j < kvEnd ? vc[(size_t)j * kvd + g * kHeadDim + d] : 0.0f;
+        }
+        *(half4 *)(vt + d * 32 + 4 * pg) = half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    }
+}
+
 struct FlashArgs {
     const float *qkv;        // [rows][qkvw], queries prepared by lm_qk_rope_kernel
     const float *kc, *vc;    // this layer's cache [capacity][kvd] holding the pass's rows
     const float *pkc, *pvc;  // a shared prefix's cache rows [0, plen), seen by every row
     const int32_t *rowstart; // packed pass: the cache row where row m's sequence starts
+    const _Float16 *kv16;    // FP16 copies of cache tiles k0.. (lm_kv_half_kernel), or null
     float *ctx;              // [rows][qd]
-    int qkvw, qd, kvd, rows, base, plen;
+    int qkvw, qd, kvd, rows, base, plen, k0;
 };
 
 // Causal attention of pass rows m0 .. m0 + 32*RH - 1 (m0 = 32*RH * row block)
@@ -146,7 +187,15 @@ struct FlashArgs {
 // the softmax is exp2(s - m) against a reference maximum m that moves only
 // when a score exceeds it by more than 8; probabilities and values are FP16.
 // The running output is rescaled only when some lane's reference moved.
-template <int GROUP, int RH>
+template <int N, typename F, int I = 0>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, F, I + 1>(static_cast<F &&>(f));
+    }
+}
+
+template <int GROUP, int RH, int PF>
 __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashArgs a) {
     constexpr int NT = 64 * RH * GROUP;
     constexpr int RB = 32 * RH;  // rows per block
@@ -198,7 +247,30 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
 
     float4 kr[KITEMS];
     float4 vr[VITEMS];
-    auto load_tile = [&](int t) {
+    // Pass-cache tiles from k0 on come as FP16 copies (16-byte pieces, 512
+    // of K and 512 of V^T per tile), loaded PF tiles ahead into PF register
+    // sets (tile t in set t % PF); the prefix's and earlier rows' tiles, which
+    // come first, are staged from the fp32 cache one tile ahead.
+    constexpr int HITEMS = (32 * kHeadDim / 8 + NT - 1) / NT;
+    typedef int i32x4v __attribute__((ext_vector_type(4)));
+    i32x4v hk[PF][HITEMS], hv[PF][HITEMS];
+    auto half_src = [&](int t) -> const _Float16 * {
+        if (t < tA || !a.kv16) return nullptr;
+        const int k = tb0 + t - tA;
+        return k >= a.k0 ? a.kv16 + ((size_t)(k - a.k0) * gridDim.y + g) * kKvHalfTile : nullptr;
+    };
+    auto load_half = [&](const _Float16 *hs, auto set_c) __attribute__((always_inline)) {
+        constexpr int S = decltype(set_c)::value;
+#pragma unroll
+        for (int i = 0; i < HITEMS; ++i) {
+            const int idx = tid + i * NT;
+            if (idx < 32 * kHeadDim / 8) {
+                hk[S][i] = *(const i32x4v *)(hs + 8 * idx);
+                hv[S][i] = *(const i32x4v *)(hs + 32 * kHeadDim + 8 * idx);
+            }
+        }
+    };
+    auto load_tile = [&](int t) __attribute__((always_inline)) {
         const bool inA = t < tA;
         const int jb = tile_key(t), end = inA ? a.plen : kvEnd;
         const float *kb = inA ? pkbase : kbase, *vb = inA ? pvbase : vbase;
@@ -224,7 +296,19 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
             vr[i] = v;
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int t, auto set_c) __attribute__((always_inline)) {
+        constexpr int S = decltype(set_c)::value;
+        if (half_src(t)) {
+#pragma unroll
+            for (int i = 0; i < HITEMS; ++i) {
+                const int idx = tid + i * NT;
+                if (idx < 32 * kHeadDim / 8) {
+                    *(i32x4v *)(Ks + (idx >> 4) * KS + 8 * (idx & 15)) = hk[S][i];
+                    *(i32x4v *)(Vt + (idx >> 2) * VS + 8 * (idx & 3)) = hv[S][i];
+                }
+            }
+            return;
+        }
         typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 #pragma unroll
         for (int i = 0; i < KITEMS; ++i) {
@@ -254,16 +338,27 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = f32x16{};
     float mrun = -INFINITY, lrun = 0.0f;
-    load_tile(0);
-    for (int t = 0; t < tiles; ++t) {
+    // Loads ahead of tile t: the next tile if it is an fp32 one, tile t + PF
+    // if it is an FP16 one (into the set tile t has just left).
+    auto prefetch = [&](int t, auto set_c) __attribute__((always_inline)) {
+        if (t + 1 < tiles && !half_src(t + 1)) load_tile(t + 1);
+        if (t + PF < tiles)
+            if (const _Float16 *hs = half_src(t + PF)) load_half(hs, set_c);
+    };
+    if (!half_src(0)) load_tile(0);
+    static_for<PF>([&](auto set_c) {
+        if (decltype(set_c)::value < tiles)
+            if (const _Float16 *hs = half_src(decltype(set_c)::value)) load_half(hs, set_c);
+    });
+    auto tile_step = [&](int t, auto set_c) __attribute__((always_inline)) {
         const bool inA = t < tA;
         const int jb = tile_key(t);
         __syncthreads();  // the previous tile's LDS reads are done
-        store_tile();
+        store_tile(t, set_c);
         __syncthreads();
-        if (t + 1 < tiles) load_tile(t + 1);
+        prefetch(t, set_c);
         // Every key of the tile is outside this wave's rows' ranges.
-        if (!inA && (jb > waveLast || jb + KB - 1 < waveFirst)) continue;
+        if (!inA && (jb > waveLast || jb + KB - 1 < waveFirst)) return;
         f32x16 s = f32x16{};
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -322,7 +417,11 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
             o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)vrow, p0, o[c], 0, 0, 0);
             o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)(vrow + 16), p1, o[c], 0, 0, 0);
         }
-    }
+    };
+    for (int t0 = 0; t0 < tiles; t0 += PF)
+        static_for<PF>([&](auto set_c) {
+            if (t0 + decltype(set_c)::value < tiles) tile_step(t0 + decltype(set_c)::value, set_c);
+        });
     const int m = mw + q;
     if (m >= a.rows) return;
     const float inv = 1.0f / lrun;
@@ -340,7 +439,8 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
 template <int G>
 int launch_flash_g(const FlashArgs &a, int kvh, hipStream_t st) {
     constexpr int RH = G <= 4 ? 2 : 1;
-    hipLaunchKernelGGL((lm_flash_kernel<G, RH>), dim3((unsigned)((a.rows + 32 * RH - 1) / (32 * RH)), (unsigned)kvh),
+    constexpr int PF = 2;  // FP16 tiles in flight (3 and 4 measured the same)
+    hipLaunchKernelGGL((lm_flash_kernel<G, RH, PF>), dim3((unsigned)((a.rows + 32 * RH - 1) / (32 * RH)), (unsigned)kvh),
                        dim3(64 * RH * G), 0, st, a);
     return launch_status();
 }
@@ -427,6 +527,11 @@ int encode_pass(gphq_prefill *ws, const PassKV &kv, int base, int R, hipStream_t
     fa.base = base;
     fa.plen = kv.plen;
     fa.rowstart = kv.rowstart;
+    // The pass's cache rows (from row 0 in a packed pass) as FP16 tiles.
+    const int kvOff = kv.rowstart ? 0 : base, kvEnd = kvOff + R;
+    fa.kv16 = ws->kv16;
+    fa.k0 = kvOff / 32;
+    const int kvTiles = (kvEnd + 31) / 32 - fa.k0;
     for (int layer = 0; layer < c.layers; ++layer) {
         const gphq_lm_layer &L = lm->layers[layer];
         const uint8_t *buf = (const uint8_t *)L.buf_dev;
@@ -445,6 +550,9 @@ int encode_pass(gphq_prefill *ws, const PassKV &kv, int base, int R, hipStream_t
         GPHQ_TRY(launch_status());
         fa.kc = ra.kc;
         fa.vc = ra.vc;
+        hipLaunchKernelGGL(lm_kv_half_kernel, dim3((unsigned)kvTiles, (unsigned)c.kv_heads), dim3(256), 0, st, fa.kc,
+                           fa.vc, (int)kvd, fa.k0, kvEnd, ws->kv16);
+        GPHQ_TRY(launch_status());
         GPHQ_TRY(launch_flash((int)lm->group, fa, (int)c.kv_heads, st));
         GPHQ_TRY(project(ws, R, PRO_PLAIN, EPI_ADD, buf, L.o, L.o_scale, ws->ctx, qd, ws->h, H, H, st));
         GPHQ_TRY(project(ws, R, PRO_NORM, EPI_SWIGLU, buf, L.gu, L.gu_scale, ws->h, H, ws->act, I, 2 * I, st));
@@ -485,6 +593,7 @@ int gphq_prefill_new(const gphq_lm *lm, int64_t rows, gphq_prefill **out) {
         {(void **)&ws->tok, (size_t)rows * 4},        {(void **)&ws->nonfinite, 4},
         {(void **)&ws->rinv, (size_t)rows * 4},       {(void **)&ws->rowpos, (size_t)rows * 4},
         {(void **)&ws->rowstart, (size_t)rows * 4},
+        {(void **)&ws->kv16, (size_t)kv16_tiles(rows) * c.kv_heads * kKvHalfTile * 2},
     };
     for (auto &b : bufs) {
         const hipError_t e = hipMalloc(b.dst, b.bytes);
