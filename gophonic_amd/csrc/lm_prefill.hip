@@ -143,17 +143,28 @@ __global__ __launch_bounds__(256) void lm_kv_half_kernel(const float *__restrict
                                    : float4{0.f, 0.f, 0.f, 0.f};
         *(half4 *)(kt + key * kHeadDim + d4) = half4{(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w};
     }
+    // V: the tile's rows as FP16 into LDS ([key][dim]), then V^T rows of 16
+    // bytes: dim d, key positions 8p .. 8p + 7, where position group pg holds
+    // key group 4*(pg/4) + {0, 2, 1, 3}[pg % 4] (the map is its own inverse).
+    __shared__ _Float16 vs[32][kHeadDim + 8];
     for (int u = threadIdx.x; u < 32 * kHeadDim / 4; u += 256) {
-        // Key group kg (keys 4kg..4kg+3) at position group 4*(kg/4) + {0, 2, 1, 3}[kg % 4].
-        const int d = u & (kHeadDim - 1), kg = u >> 7, r = kg & 3;
-        const int pg = (kg & ~3) + ((r == 1) ? 2 : (r == 2) ? 1 : r);
-        float v[4];
+        const int key = u >> 5, d4 = 4 * (u & 31), j = jb + key;
+        const float4 x = j < kvEnd ? *(const float4 *)(vc + (size_t)j * kvd + g * kHeadDim + d4)
+                                   : float4{0.f, 0.f, 0.f, 0.f};
+        *(half4 *)&vs[key][d4] = half4{(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w};
+    }
+    __syncthreads();
+    typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+    for (int u = threadIdx.x; u < kHeadDim * 4; u += 256) {
+        const int d = u >> 2, p = u & 3;
+        half8v h;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = jb + 4 * kg + i;
-            v[i] = j < kvEnd ? vc[(size_t)j * kvd + g * kHeadDim + d] : 0.0f;
+        for (int i = 0; i < 8; ++i) {
+            const int pos = 8 * p + i, pg = pos >> 2, r = pg & 3;
+            const int kg = (pg & ~3) + ((r == 1) ? 2 : (r == 2) ? 1 : r);
+            h[i] = vs[4 * kg + (pos & 3)][d];
         }
-        *(half4 *)(vt + d * 32 + 4 * pg) = half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+        *(half8v *)(vt + d * 32 + 8 * p) = h;
     }
 }
 
