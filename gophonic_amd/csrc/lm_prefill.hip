@@ -82,14 +82,15 @@ struct RopeArgs {
     int qkvw, qd, kvd, heads, kvh, base, sin_off;
 };
 
-// qkRope (gpu.metal:1027-1056) for row m = blockIdx.y, head item blockIdx.x
-// (query heads, then key heads, then value heads); one wavefront, lane l
-// holding the rotary pair (l, l + 64). The same norm and rotation arithmetic
+// qkRope (gpu.metal:1027-1056) for row m = blockIdx.y, head items
+// 4 blockIdx.x .. + 3 (query heads, then key heads, then value heads), one
+// per wavefront, lane l holding the rotary pair (l, l + 64). The same norm and rotation arithmetic
 // as the decode step's attention kernel. Row m sits at position base + m and
 // cache row base + m, or, in a packed pass, at position rowpos[m] and cache
 // row m.
-__global__ __launch_bounds__(64) void lm_qk_rope_kernel(const RopeArgs a) {
-    const int h = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void lm_qk_rope_kernel(const RopeArgs a) {
+    const int h = blockIdx.x * 4 + (threadIdx.x >> 6), m = blockIdx.y, lane = threadIdx.x & 63;
+    if (h >= a.heads + 2 * a.kvh) return;
     float *row = a.qkv + (size_t)m * a.qkvw;
     const int pos = a.rowpos ? a.rowpos[m] : a.base + m;
     const size_t slot = (size_t)(a.rowpos ? m : pos) * a.kvd;
@@ -556,8 +557,8 @@ int encode_pass(gphq_prefill *ws, const PassKV &kv, int base, int R, hipStream_t
         }
         ra.qn = lm->norms + (size_t)layer * 2 * kHeadDim;
         ra.kn = ra.qn + kHeadDim;
-        hipLaunchKernelGGL(lm_qk_rope_kernel, dim3((unsigned)(c.heads + 2 * c.kv_heads), (unsigned)R), dim3(64), 0,
-                           st, ra);
+        hipLaunchKernelGGL(lm_qk_rope_kernel, dim3((unsigned)((c.heads + 2 * c.kv_heads + 3) / 4), (unsigned)R),
+                           dim3(256), 0, st, ra);
         GPHQ_TRY(launch_status());
         fa.kc = ra.kc;
         fa.vc = ra.vc;
