@@ -865,9 +865,14 @@ int f16_act_pack(const float *x, long stride, int rows, int K, int kt, int mode,
 template <int MODE, int CPT, bool ROT>
 __global__ __launch_bounds__(256) void act_pack_rows_kernel(const float *__restrict__ x, long stride, int K, int kt,
                                                             float eps, const float *__restrict__ signs, int block,
-                                                            _Float16 *__restrict__ act, float *__restrict__ rowInv) {
+                                                            _Float16 *__restrict__ act, float *__restrict__ rowInv,
+                                                            int rows) {
     __shared__ float sss[4], smx[4];
-    const int row = blockIdx.x;
+    // The 4 rows whose 32-byte slots share a 128-byte line of the tiles go to
+    // blocks b, b + 8, b + 16, b + 24, which the dispatcher places on one XCD
+    // (round robin over 8), so each line is completed in one L2.
+    const int bx = blockIdx.x, row = (bx & ~31) + 4 * (bx & 7) + ((bx >> 3) & 3);
+    if (row >= rows) return;
     const float *xr = x + (size_t)row * stride;
     const int chunks = kt * 4;
     float4 v[CPT][4];
@@ -931,8 +936,8 @@ static int launch_act_pack_rows(const float *x, long stride, int rows, int K, fl
         if (lds > 65536)                                                                                               \
             (void)hipFuncSetAttribute((const void *)act_pack_rows_kernel<MODE, CPT, ROT>,                              \
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                           \
-        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, CPT, ROT>), dim3(rows), dim3(256), lds, stream, x, stride, K,  \
-                           kt, eps, signs, block, act, rowInv);                                                        \
+        hipLaunchKernelGGL((act_pack_rows_kernel<MODE, CPT, ROT>), dim3((unsigned)((rows + 31) & ~31)), dim3(256), lds,\
+                           stream, x, stride, K, kt, eps, signs, block, act, rowInv, rows);                            \
     } while (0)
     if (chunks <= 256)
         GPHQ_ACTPACK(1);

@@ -171,10 +171,15 @@ __global__ __launch_bounds__(256) void i8_pack_range_kernel(const float *__restr
 template <int MODE, int CPT, bool ROT>
 __global__ __launch_bounds__(256) void i8_act_rows_kernel(const float *__restrict__ x, long stride, int K, float eps,
                                                           const float *__restrict__ signs, int block,
-                                                          int8_t *__restrict__ act, float *__restrict__ rowScale) {
+                                                          int8_t *__restrict__ act, float *__restrict__ rowScale,
+                                                          int rows) {
     __shared__ float sss[4], smx[4];
     __shared__ int snan[4];
-    const int row = blockIdx.x;
+    // The 2 rows whose 64-byte pieces share a 128-byte line of the row tiles
+    // go to blocks b and b + 8, which the dispatcher places on one XCD (round
+    // robin over 8), so each line is completed in one L2.
+    const int bx = blockIdx.x, row = (bx & ~15) + 2 * (bx & 7) + ((bx >> 3) & 1);
+    if (row >= rows) return;
     const float *xr = x + (size_t)row * stride;
     float4 v[CPT][4];
     float ss = 0.0f, mx = 0.0f;
@@ -980,8 +985,8 @@ static int launch_i8_act_rows(const float *x, long stride, int rows, int K, floa
         if (lds > 65536)                                                                                               \
             (void)hipFuncSetAttribute((const void *)i8_act_rows_kernel<MODE, CPT, ROT>,                                \
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                           \
-        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, CPT, ROT>), dim3(rows), dim3(256), lds, stream, x, stride, K,    \
-                           eps, signs, block, act, rowScale);                                                          \
+        hipLaunchKernelGGL((i8_act_rows_kernel<MODE, CPT, ROT>), dim3((unsigned)((rows + 15) & ~15)), dim3(256), lds,  \
+                           stream, x, stride, K, eps, signs, block, act, rowScale, rows);                              \
     } while (0)
     if (chunks <= 256)
         GPHQ_I8ACT(1);
