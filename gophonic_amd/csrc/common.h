@@ -233,6 +233,16 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
+// s_barrier between compiler-only memory barriers: the builtin alone is not a
+// memory operation to LLVM, so LDS reads of a ring slot could otherwise be
+// moved across it. The empty asm emits no instruction and no wait count, so
+// loads issued before it stay in flight.
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // One 16-byte-per-lane direct-to-LDS load (global_load_lds_dwordx4): lane l
 // writes its 16 bytes from `src` to lds + 16 l. `lds` is the same for every
 // lane. Counts in vmcnt like any vector load.

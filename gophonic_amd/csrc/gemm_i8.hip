@@ -501,8 +501,9 @@ __global__ __launch_bounds__(64 * WM * WN) void i8gemm_lds_kernel(const I8GemmAr
 // RT row tiles of A and loads their fragments itself; the NTB column tiles of
 // B are shared, each wavefront loading an equal share. Loads return in issue
 // order, so the wait at a stage's start is a count (the loads of the NS - 2
-// stages after it may stay in flight). The barrier is a plain s_barrier (a
-// __syncthreads fence would wait for every load in flight), after lgkmcnt(0)
+// stages after it may stay in flight). The barrier is s_barrier with
+// compiler-only fences around it (ring_barrier; a __syncthreads fence would
+// wait for every load in flight), after lgkmcnt(0)
 // so that the previous stage's LDS reads have finished before its slot is
 // refilled.
 template <int NWV, int RT, int NTB, int SB, int NS>
@@ -570,7 +571,7 @@ __global__ __launch_bounds__(64 * NWV) void i8gemm_skinny_kernel(const I8GemmArg
             wait_vm_lgkm0<D>();
         else
             wait_vm_lgkm0<0>();
-        __builtin_amdgcn_s_barrier();
+        ring_barrier();
         if (s + NS - 1 < S) stage_load(s + NS - 1);
         const int slot = s % NS;
 #pragma unroll
@@ -830,7 +831,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8Gemm
         } else {
             wait_vm_lgkm0<0>();
         }
-        __builtin_amdgcn_s_barrier();
+        ring_barrier();
         if (s + NS - 1 < KT) stage_load(s + NS - 1);
         const int slot = s % NS;
         i32x4 fa[TI], fb[TJ];

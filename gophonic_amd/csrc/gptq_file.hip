@@ -78,6 +78,33 @@ struct gphq_gptq_writer {
     std::string tmp, path;
 };
 
+// The projection a tensor name after the decoder prefix names
+// ("layers.3.mlp.up_proj.weight", gptq.go:145-165): 1 with its code and scale
+// offsets and its shape (rows, input width) from the file's configuration, or
+// 0 if the file does not hold it.
+static int find_projection(const gphq_gptq_file *g, const char *name, int64_t *codes_off, int64_t *scales_off, int64_t *n,
+                    int64_t *k) {
+    if (!g || !name) return 0;
+    if (strncmp(name, "layers.", 7) != 0) return 0;
+    char *end = nullptr;
+    errno = 0;
+    const long long layer = strtoll(name + 7, &end, 10);
+    if (end == name + 7 || errno || *end != '.' || layer < 0 || layer >= g->cfg.layers) return 0;
+    std::string rest = end + 1;
+    if (rest.size() >= 7 && rest.compare(rest.size() - 7, 7, ".weight") == 0) rest.resize(rest.size() - 7);
+    for (int p = 0; p < GPHQ_LAYER_PROJECTIONS; ++p)
+        if (rest == kProjections[p]) {
+            int64_t cb, sb;
+            projection_shape(g->cfg, p, n, k);
+            gphq_gptq_row_bytes(g->bits, *k, &cb, &sb);
+            const int64_t off = g->offsets[(size_t)(layer * GPHQ_LAYER_PROJECTIONS + p)];
+            if (codes_off) *codes_off = off;
+            if (scales_off) *scales_off = off + *n * cb;
+            return 1;
+        }
+    return 0;
+}
+
 extern "C" {
 
 int gphq_gptq_row_bytes(int bits, int64_t k, int64_t *codes, int64_t *scales) {
@@ -181,25 +208,8 @@ int gphq_gptq_bits(const gphq_gptq_file *g) { return g ? g->bits : 0; }
 int gphq_gptq_projection(const gphq_gptq_file *g, const char *name, int64_t *codes_off, int64_t *scales_off) {
     // gptq.go:145-165 projection: the offsets of a tensor named after the
     // decoder prefix ("layers.3.mlp.up_proj.weight"); 1 if the file holds it.
-    if (!g || !name) return 0;
-    if (strncmp(name, "layers.", 7) != 0) return 0;
-    char *end = nullptr;
-    errno = 0;
-    const long long layer = strtoll(name + 7, &end, 10);
-    if (end == name + 7 || errno || *end != '.' || layer < 0 || layer >= g->cfg.layers) return 0;
-    std::string rest = end + 1;
-    if (rest.size() >= 7 && rest.compare(rest.size() - 7, 7, ".weight") == 0) rest.resize(rest.size() - 7);
-    for (int p = 0; p < GPHQ_LAYER_PROJECTIONS; ++p)
-        if (rest == kProjections[p]) {
-            int64_t n, k, cb, sb;
-            projection_shape(g->cfg, p, &n, &k);
-            gphq_gptq_row_bytes(g->bits, k, &cb, &sb);
-            const int64_t off = g->offsets[(size_t)(layer * GPHQ_LAYER_PROJECTIONS + p)];
-            if (codes_off) *codes_off = off;
-            if (scales_off) *scales_off = off + n * cb;
-            return 1;
-        }
-    return 0;
+    int64_t n, k;
+    return find_projection(g, name, codes_off, scales_off, &n, &k);
 }
 
 int gphq_gptq_place(const gphq_gptq_file *g, const char *name, int64_t n, int64_t k, void *buf_dev, int64_t buf_bytes,
@@ -211,8 +221,13 @@ int gphq_gptq_place(const gphq_gptq_file *g, const char *name, int64_t n, int64_
     if (!g || !name || !placed || !buf_dev || n < 0 || k < 0 || row0 < 0 || step < 1 || base < 0 || sc < 0)
         return fail(GPHQ_ERR_DIMENSIONS, "gptq: bad arguments");
     *placed = 0;
-    int64_t codesAt = 0, scalesAt = 0;
-    if (!gphq_gptq_projection(g, name, &codesAt, &scalesAt)) return GPHQ_OK;
+    int64_t codesAt = 0, scalesAt = 0, fn = 0, fk = 0;
+    if (!find_projection(g, name, &codesAt, &scalesAt, &fn, &fk)) return GPHQ_OK;
+    // The file's own layout bounds what is read: a caller's n or k that is
+    // not the projection's shape would read into the next projection.
+    if (n != fn || k != fk)
+        return fail(GPHQ_ERR_DIMENSIONS, strf("gptq: %s is %lldx%lld in the file, not %lldx%lld", name, (long long)fn,
+                                              (long long)fk, (long long)n, (long long)k));
     int64_t cb, sb;
     GPHQ_TRY(gphq_gptq_row_bytes(g->bits, k, &cb, &sb));
     if (n == 0) {

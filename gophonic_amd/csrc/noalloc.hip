@@ -7,13 +7,15 @@
 //
 // Host code never passes the array's name to a kernel: the name is a
 // host-side stand-in, not a device address. The device address is resolved
-// once per device, with that device current, by hipGetSymbolAddress, and kept
-// per device; kernels take that address as their workspace argument.
+// per device, with that device current, by hipGetSymbolAddress on the first
+// call that succeeds, and kept per device; kernels take that address as
+// their workspace argument.
 //
 // Every call on one GPU shares that GPU's array and leaves its contents for
 // the next call. Nothing has to start at zero (the preparation kernel writes
 // every value the GEMV kernels read), but calls that overlap on one GPU (on
 // streams not ordered with each other) race on the array.
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -31,20 +33,30 @@ namespace {
 static __device__ __align__(256) uint8_t scratch[GPHQ_GEMV_VEC_NOALLOC_BYTES];
 
 constexpr int kMaxDevices = 64;
-std::once_flag g_once[kMaxDevices];
-void *g_ptr[kMaxDevices];
-hipError_t g_err[kMaxDevices];
+std::mutex g_mu[kMaxDevices];
+std::atomic<void *> g_ptr[kMaxDevices];
 
-// The device address of this device's scratch array (resolved on the first
-// call with the device current), or GPHQ_ERR_HIP.
+// The device address of this device's scratch array, resolved with the device
+// current on the first call that succeeds (a failed lookup is not kept, so a
+// later call tries again), or GPHQ_ERR_HIP. The lookup may run while the
+// caller's stream is being captured: this thread's capture mode is relaxed
+// around it, which lets a call that is not a stream operation run without
+// invalidating the capture.
 int scratch_for(int dev, void **out) {
-    std::call_once(g_once[dev], [dev] {
-        void *p = nullptr;
-        g_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        g_ptr[dev] = g_err[dev] == hipSuccess ? p : nullptr;
-    });
-    if (g_err[dev] != hipSuccess) return hip_status(g_err[dev]);
-    *out = g_ptr[dev];
+    void *p = g_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_mu[dev]);
+        p = g_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+            GPHQ_TRY(hip_status(hipThreadExchangeStreamCaptureMode(&mode)));
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            GPHQ_TRY(hip_status(hipThreadExchangeStreamCaptureMode(&mode)));
+            if (e != hipSuccess || !p) return hip_status(e != hipSuccess ? e : hipErrorInvalidSymbol);
+            g_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
     return GPHQ_OK;
 }
 

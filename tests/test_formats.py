@@ -223,6 +223,30 @@ def test_gptq_file_ignored_when_stale_or_truncated(tmp_path):
         fm.GptqWriter(tmp_path, "gpu-q8")
 
 
+@pytest.mark.parametrize("fmt", ["gpu", "gpu-q4"])
+def test_gptq_place_rejects_a_shape_other_than_the_files(tmp_path, fmt):
+    # place reads n rows of the projection's row bytes from the file's own
+    # offsets, so n and k must be the projection's shape under the file's
+    # configuration; anything else would read the next projection's bytes.
+    # The check comes before any device work, so a host buffer stands in.
+    import torch
+
+    (tmp_path / "model.safetensors").write_bytes(b"weights")
+    cfg = tiny_cfg(gphq.FMT_Q8 if fmt == "gpu" else gphq.FMT_Q4)
+    write_gptq(tmp_path, fmt, cfg)
+    g = fm.GptqFile.open(tmp_path, fmt, cfg)
+    buf = torch.zeros(1 << 20, dtype=torch.uint8)
+    name = "layers.1.mlp.up_proj.weight"
+    n, k = proj_shapes(cfg)[5]
+    for bad_n, bad_k in [(n, k + 32), (n, k - 32), (n + 1, k), (n - 1, k)]:
+        with pytest.raises(gphq.GphqError) as e:
+            g.place(name, bad_n, bad_k, buf, 0, 1 << 19)
+        assert e.value.status == gphq.ERR_DIMENSIONS
+        assert f"is {n}x{k} in the file, not {bad_n}x{bad_k}" in str(e.value)
+    assert not buf.any()
+    g.close()
+
+
 # ---- weight cache -----------------------------------------------------------------
 
 def test_sha256_known_answers():

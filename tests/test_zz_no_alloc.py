@@ -2,8 +2,13 @@
 scratch, for callers that cannot allocate) against gphq_gemv_vec with a
 caller workspace: the same kernels, so the same bits, through the C ABI.
 Two calls in a row, the second with a smaller input, so the second runs on
-the scratch the first left behind; then a request beyond the static array.
+the scratch the first left behind; then a request beyond the static array;
+then, in a fresh process, a first call made under HIP graph capture.
 """
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 
@@ -78,3 +83,49 @@ def test_noalloc_rejects_more_than_its_scratch():
     assert e.value.status == gphq.ERR_SCRATCH_LIMIT
     torch.cuda.synchronize()
     assert (y == -7.0).all()
+
+
+# Run in a fresh process, so that the scratch address is first looked up
+# while the stream is being captured (torch.cuda.graph's default global
+# capture mode). Each replay follows eager work on the same inputs and is
+# checked bit for bit against gphq_gemv_vec with a caller workspace.
+CAPTURE_CHILD = r"""
+import sys
+import numpy as np
+import torch
+from gophonic_amd import gphq
+
+fmt, lanes, k, n = gphq.FMT_Q8B, 4, 4096, 1024
+rng = np.random.default_rng(11)
+codes = torch.from_numpy(rng.integers(-127, 128, n * k).astype(np.int8)).cuda()
+scales = torch.from_numpy((np.abs(rng.standard_normal(n * k // 32)) * 0.01).astype(np.float16)).cuda()
+x = torch.zeros(lanes * k, device="cuda")
+y = torch.full((lanes * n,), -7.0, device="cuda")
+work = torch.empty(gphq.gemv_vec_workspace_bytes(lanes, k), dtype=torch.uint8, device="cuda")
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    gphq.gemv_vec_noalloc(fmt, codes, scales, x, y, lanes, k, n)
+for rep in range(3):
+    x.copy_(torch.from_numpy(rng.standard_normal(lanes * k).astype(np.float32)).cuda())
+    y.fill_(-7.0)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    want = torch.full((lanes * n,), -9.0, device="cuda")
+    gphq.gemv_vec(fmt, codes, scales, x, want, lanes, k, n, work)
+    torch.cuda.synchronize()
+    same = np.array_equal(y.cpu().numpy().view(np.uint32), want.cpu().numpy().view(np.uint32))
+    print(f"replay {rep}: {'equal' if same else 'DIFFERENT'}", flush=True)
+    if not same:
+        sys.exit(1)
+print("capture ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=root + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    res = subprocess.run([sys.executable, "-c", CAPTURE_CHILD], cwd=root, env=env, capture_output=True, text=True,
+                         timeout=240)
+    assert res.returncode == 0 and "capture ok" in res.stdout, res.stdout + res.stderr
