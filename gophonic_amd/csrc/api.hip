@@ -105,6 +105,12 @@ const char *gphq_error_string(int status) {
         return "safetensors: tensor has a non-finite value";
     case GPHQ_ERR_READ_RANGE:
         return "read outside the tensor";
+    case GPHQ_ERR_GPTQ_WIDTH:
+        return "qwen3: GPTQ needs projection widths that are multiples of 4096";
+    case GPHQ_ERR_CALIBRATION_EMPTY:
+        return "qwen3: empty calibration set";
+    case GPHQ_ERR_CALIBRATION_SHAPE:
+        return "qwen3: calibration sequences take 1 to 256 tokens each and 4096 in all";
     }
     return "gphq: unknown status";
 }

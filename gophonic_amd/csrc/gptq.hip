@@ -407,6 +407,19 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gptq_round_block_kernel(co
 
 }  // namespace
 
+namespace gphq {
+
+// C [M][N] (row stride ldc) = A [M][K] . B^T for B [N][K] (row-major, strides
+// lda / ldb), fp32 with fp32 sums; with accumulate, C += the product (the
+// whole sum formed first and added once, as `c[i] += d[i]` after a separate
+// product). The calibration pass's projections and residual adds.
+int sgemm_abt(int M, int N, int K, const float *a, long lda, const float *b, long ldb, float *c, long ldc,
+              bool accumulate, hipStream_t st) {
+    return sgemm<0, 1>(M, N, K, 1.0f, a, lda, b, ldb, c, ldc, accumulate, false, st);
+}
+
+}  // namespace gphq
+
 extern "C" {
 
 int64_t gphq_gptq_work_bytes(int64_t k) {

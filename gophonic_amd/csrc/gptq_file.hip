@@ -66,6 +66,14 @@ std::string path_for(const char *dir, const char *format) {
 
 }  // namespace
 
+namespace gphq {
+
+// The GPTQ format's bits ("gpu" 8, "gpu-q4" 4), or GPHQ_ERR_UNSUPPORTED with
+// the reference's message (gptq.go:197-206).
+int gptq_format_bits(const char *format, int *bits) { return format_bits(format, bits); }
+
+}  // namespace gphq
+
 struct gphq_gptq_file {
     int fd = -1;
     int bits = 0;

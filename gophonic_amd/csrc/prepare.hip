@@ -261,7 +261,53 @@ int64_t region_bytes(int fmt, int64_t rows, int64_t k, bool scales) {
 
 }  // namespace
 
+namespace gphq {
+
+// The float32 stage of a projection job (steps 1-3 above): BF16 rows [n][k]
+// times the folded norm (norm_host, or null), the input rotation along each
+// row, the output rotation across the rows, into out [n][k] -- the values the
+// quantizers read, which are the reference's float32 matrix bit for bit.
+// tables: 2k + n floats of device scratch for the norm and the signs. The
+// rotations must fit (spec_ok; n a multiple of the output block). Waits for
+// the stream (the host tables are copied from temporaries).
+int prepare_rows_f32(const uint16_t *src, int64_t n, int64_t k, const float *norm_host, gphq_rotation_spec in_rot,
+                     gphq_rotation_spec out_rot, float *out, float *tables, hipStream_t st) {
+    if (n <= 0 || k <= 0 || k > kMaxPrepWidth || n > INT32_MAX || !src || !out || !tables)
+        return GPHQ_ERR_DIMENSIONS;
+    if (!spec_ok(in_rot, k) || !spec_ok(out_rot, n)) return GPHQ_ERR_DIMENSIONS;
+    // The output rotation mixes rows in blocks: the rows must fill whole blocks.
+    std::vector<float> in_s, out_s;
+    float in_scale = 1.0f, out_scale = 1.0f;
+    int in_block = 0, out_block = 0;
+    const bool has_in = in_rot.width || in_rot.tile, has_out = out_rot.width || out_rot.tile;
+    if (has_in) in_block = spec_signs(in_rot, k, in_s, &in_scale);
+    if (has_out) {
+        out_block = spec_signs(out_rot, n, out_s, &out_scale);
+        if (n % out_block) return GPHQ_ERR_DIMENSIONS;
+    }
+    float *norm_d = tables, *in_d = norm_d + k, *out_d = in_d + k;
+    if (norm_host) GPHQ_TRY(hip_status(hipMemcpyAsync(norm_d, norm_host, k * 4, hipMemcpyHostToDevice, st)));
+    if (has_in) GPHQ_TRY(hip_status(hipMemcpyAsync(in_d, in_s.data(), k * 4, hipMemcpyHostToDevice, st)));
+    if (has_out) GPHQ_TRY(hip_status(hipMemcpyAsync(out_d, out_s.data(), n * 4, hipMemcpyHostToDevice, st)));
+    RowsArgs ra{src, norm_host ? norm_d : nullptr, has_in ? in_d : nullptr, has_out ? out_d : nullptr, out, (int)k,
+                in_block, in_scale};
+    hipLaunchKernelGGL(prep_rows_kernel, dim3((unsigned)n), dim3(256), k * 4, st, ra);
+    GPHQ_TRY(launch_status());
+    if (has_out) {
+        int cols = std::max(1, std::min<int>(64, kMaxPrepWidth / out_block));
+        while (k % cols) cols >>= 1;
+        hipLaunchKernelGGL(prep_cols_fwht_kernel, dim3((unsigned)(k / cols), (unsigned)(n / out_block)), dim3(256),
+                           (size_t)out_block * cols * 4, st, out, (int)k, out_block, cols, out_scale);
+        GPHQ_TRY(launch_status());
+    }
+    // The host-side signs and norm must outlive their copies.
+    return hip_status(hipStreamSynchronize(st));
+}
+
+}  // namespace gphq
+
 extern "C" {
+
 
 int64_t gphq_prepare_work_bytes(int64_t n, int64_t k) {
     if (n <= 0 || k <= 0 || k > kMaxPrepWidth) return GPHQ_ERR_DIMENSIONS;
@@ -285,34 +331,10 @@ int gphq_prepare_projection(const gphq_prepare_job *j, void *work_dev, int64_t w
         return GPHQ_ERR_DIMENSIONS;
     if ((fmt != GPHQ_FMT_Q8 && j->sc % 2) || ((fmt == GPHQ_FMT_Q8 || fmt == GPHQ_FMT_Q8B_F32) && j->sc % 4))
         return GPHQ_ERR_DIMENSIONS;
-    // The output rotation mixes rows in blocks: the rows must fill whole blocks.
-    std::vector<float> in_s, out_s;
-    float in_scale = 1.0f, out_scale = 1.0f;
-    int in_block = 0, out_block = 0;
-    const bool has_in = j->in_rot.width || j->in_rot.tile, has_out = j->out_rot.width || j->out_rot.tile;
-    if (has_in) in_block = spec_signs(j->in_rot, k, in_s, &in_scale);
-    if (has_out) {
-        out_block = spec_signs(j->out_rot, n, out_s, &out_scale);
-        if (n % out_block) return GPHQ_ERR_DIMENSIONS;
-    }
-    hipStream_t st = (hipStream_t)stream;
     float *work = (float *)work_dev;
-    float *norm_d = work + n * k, *in_d = norm_d + k, *out_d = in_d + k;
-    if (j->norm_host)
-        GPHQ_TRY(hip_status(hipMemcpyAsync(norm_d, j->norm_host, k * 4, hipMemcpyHostToDevice, st)));
-    if (has_in) GPHQ_TRY(hip_status(hipMemcpyAsync(in_d, in_s.data(), k * 4, hipMemcpyHostToDevice, st)));
-    if (has_out) GPHQ_TRY(hip_status(hipMemcpyAsync(out_d, out_s.data(), n * 4, hipMemcpyHostToDevice, st)));
-    RowsArgs ra{j->src_bf16_dev, j->norm_host ? norm_d : nullptr, has_in ? in_d : nullptr,
-                has_out ? out_d : nullptr, work, (int)k, in_block, in_scale};
-    hipLaunchKernelGGL(prep_rows_kernel, dim3((unsigned)n), dim3(256), k * 4, st, ra);
-    GPHQ_TRY(launch_status());
-    if (has_out) {
-        int cols = std::max(1, std::min<int>(64, kMaxPrepWidth / out_block));
-        while (k % cols) cols >>= 1;
-        hipLaunchKernelGGL(prep_cols_fwht_kernel, dim3((unsigned)(k / cols), (unsigned)(n / out_block)), dim3(256),
-                           (size_t)out_block * cols * 4, st, work, (int)k, out_block, cols, out_scale);
-        GPHQ_TRY(launch_status());
-    }
+    GPHQ_TRY(prepare_rows_f32(j->src_bf16_dev, n, k, j->norm_host, j->in_rot, j->out_rot, work, work + n * k,
+                              (hipStream_t)stream));
+    hipStream_t st = (hipStream_t)stream;
     QuantArgs qa{work, (uint8_t *)j->dst_dev, (long)j->base, (long)j->sc, (long)j->step, (long)j->row0,
                  (int)n, (int)k, j->scale_mul};
     const unsigned blocks32 = (unsigned)((n * (k / 32) + 255) / 256);

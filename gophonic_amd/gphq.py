@@ -53,6 +53,9 @@ ERR_TENSOR_SHAPE = -37
 ERR_TENSOR_DTYPE = -38
 ERR_TENSOR_NON_FINITE = -39
 ERR_READ_RANGE = -40
+ERR_GPTQ_WIDTH = -41
+ERR_CALIBRATION_EMPTY = -42
+ERR_CALIBRATION_SHAPE = -43
 TAIL_MAX_ROWS = 256
 
 FMT_Q4, FMT_Q8, FMT_Q8B, FMT_Q8B_F32 = 4, 8, 9, 10
@@ -200,6 +203,12 @@ SIGNATURES = {
     "gphq_gptq_factor": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "gphq_gptq_round_work_bytes": (_i64, [_i64, _i64]),
     "gphq_gptq_round": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, ctypes.c_int, _vp, _vp, _vp, _i64, _vp]),
+    "gphq_gptq_calibration_new": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _i64, _vpp, _vp]),
+    "gphq_gptq_calibration_free": (None, [_vp]),
+    "gphq_gptq_calibration_layer": (ctypes.c_int, [_vp, _vpp, _vp, _vp, _vp, _vp, ctypes.c_int, _vpp, _vpp, _vp]),
+    "gphq_gptq_calibration_rows": (ctypes.c_int, [_vp, ctypes.c_int, _vp, _i64, _i64p, _i64p, _vp]),
+    "gphq_gptq_calibration_sequences": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64p]),
+    "gphq_gptq_quantize": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
 }
 
 FMT_GPTQ4_G128 = 12
@@ -1137,3 +1146,96 @@ def gptq_round(w, n, k, u, dead, bits, codes, scales, stream=None):
     work = torch.empty(load().gphq_gptq_round_work_bytes(n, k), dtype=torch.uint8, device=w.device)
     return check(load().gphq_gptq_round(ptr(w), n, k, ptr(u), ptr(dead), bits, ptr(codes), ptr(scales), ptr(work),
                                         work.numel(), stream_handle(stream)))
+
+
+# ---- GPTQ calibration pass (gphq_gptq_calibration_* / gphq_gptq_quantize) ----
+
+CAL_RESIDUAL, CAL_ATTN_INPUT, CAL_CONTEXT, CAL_MLP_INPUT, CAL_DOWN_INPUT = range(5)
+GPTQ_MAX_SEQ, GPTQ_MAX_ROWS = 256, 4096  # gptqMaxSeq, gptqMaxRows (gptq.go:39-40)
+GPTQ_PROGRESS = ctypes.CFUNCTYPE(None, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p)
+
+
+def gptq_calibration_sequences(text_lens):
+    """calibrationSequences' cut (gptq.go:275-287): the sequence lengths of
+    tokenized texts of the given lengths."""
+    import numpy as np
+
+    lens = np.ascontiguousarray(text_lens, dtype=np.int64)
+    n = ctypes.c_int64()
+    check(load().gphq_gptq_calibration_sequences(lens.ctypes.data if lens.size else None, lens.size, None, 0,
+                                                 ctypes.byref(n)))
+    out = np.zeros(max(n.value, 1), np.int64)
+    check(load().gphq_gptq_calibration_sequences(lens.ctypes.data if lens.size else None, lens.size, out.ctypes.data,
+                                                 n.value, ctypes.byref(n)))
+    return out[: n.value]
+
+
+class GptqCalibration:
+    """gphq_gptq_calibration: the calibration pass of QuantizeGPTQ
+    (newCalibration / calibration.layer, qwen3lm/gptq.go:344-524) over token-id
+    sequences, on the device. embed: BF16 bits [vocab][hidden] (int16 or
+    uint16 device tensor), kept alive by this object."""
+
+    def __init__(self, cfg, sequences, embed, stream=None):
+        import numpy as np
+
+        self.cfg = cfg
+        lens = np.array([len(s) for s in sequences], np.int64)
+        ids = np.concatenate([np.asarray(s, np.int32) for s in sequences]) if len(sequences) else np.zeros(0, np.int32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        self.h = ctypes.c_void_p()
+        self._embed = embed
+        check(load().gphq_gptq_calibration_new(ctypes.byref(cfg), ids.ctypes.data if ids.size else None,
+                                               lens.ctypes.data if lens.size else None, lens.size, ptr(embed),
+                                               embed.numel(), ctypes.byref(self.h), stream_handle(stream)))
+
+    def close(self):
+        if self.h:
+            load().gphq_gptq_calibration_free(self.h)
+            self.h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def layer(self, srcs, input_norm, post_norm, q_norm, k_norm, bits, codes, scales, stream=None):
+        """calibration.layer: srcs = the seven BF16 projections (device
+        tensors, LAYER_PROJECTIONS order); norms float32 host arrays; codes /
+        scales = seven uint8 device tensors sized by gptqRowBytes."""
+        import numpy as np
+
+        arr = lambda ts: (ctypes.c_void_p * 7)(*[t.data_ptr() for t in ts])
+        norms = [np.ascontiguousarray(v, np.float32) for v in (input_norm, post_norm, q_norm, k_norm)]
+        check(load().gphq_gptq_calibration_layer(self.h, arr(srcs), *[v.ctypes.data for v in norms], bits,
+                                                 arr(codes), arr(scales), stream_handle(stream)))
+
+    def rows(self, which, stream=None):
+        """A copy of one set of rows [rows][width] as a float32 device tensor."""
+        import torch
+
+        r, w = ctypes.c_int64(), ctypes.c_int64()
+        check(load().gphq_gptq_calibration_rows(self.h, which, None, 0, ctypes.byref(r), ctypes.byref(w), None))
+        out = torch.empty((r.value, w.value), dtype=torch.float32, device="cuda")
+        check(load().gphq_gptq_calibration_rows(self.h, which, out.data_ptr(), out.numel(), None, None,
+                                                stream_handle(stream)))
+        return out
+
+
+def gptq_quantize(path, fmt, cfg, texts, progress=None, stream=None):
+    """QuantizeGPTQ (qwen3lm/gptq.go:197-266) for tokenized calibration texts:
+    writes gophonic-gptq-<fmt>.bin next to the checkpoint in path."""
+    import numpy as np
+
+    lens = np.array([len(t) for t in texts], np.int64)
+    ids = np.ascontiguousarray(np.concatenate([np.asarray(t, np.int32) for t in texts]) if len(texts)
+                               else np.zeros(0, np.int32), np.int32)
+    cb = GPTQ_PROGRESS(lambda layer, layers, user: progress(layer, layers)) if progress else None
+    st = load().gphq_gptq_quantize(str(path).encode(), fmt.encode(), ctypes.byref(cfg),
+                                   ids.ctypes.data if ids.size else None, lens.ctypes.data if lens.size else None,
+                                   lens.size, ctypes.cast(cb, ctypes.c_void_p) if cb else None, None,
+                                   stream_handle(stream))
+    if st != OK:
+        detail = load().gphq_error_detail().decode()
+        raise GphqError(st, detail or error_string(st))

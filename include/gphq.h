@@ -106,6 +106,11 @@ extern "C" {
 #define GPHQ_ERR_TENSOR_DTYPE (-38)    /* safetensors.go:157-160, 171-173 wrong dtype or size */
 #define GPHQ_ERR_TENSOR_NON_FINITE (-39) /* safetensors.go:245-248 "%s has a non-finite value" */
 #define GPHQ_ERR_READ_RANGE (-40)      /* safetensors.go:206-208 "read outside the tensor" */
+/* GPTQ calibration (qwen3lm/gptq.go). */
+#define GPHQ_ERR_GPTQ_WIDTH (-41)        /* gptq.go:211-213 "qwen3: GPTQ needs projection widths that are multiples of 4096" */
+#define GPHQ_ERR_CALIBRATION_EMPTY (-42) /* gptq.go:324-326 "qwen3: empty calibration set" */
+#define GPHQ_ERR_CALIBRATION_SHAPE (-43) /* a sequence outside 1..256 tokens (gptqMaxSeq) or more than 4096 rows
+                                            (gptqMaxRows); the reference's own sequence builder never makes one */
 
 /* The reference message for a status code ("" for GPHQ_OK). Static storage. */
 const char *gphq_error_string(int status);
@@ -743,6 +748,72 @@ int64_t gphq_gptq_round_work_bytes(int64_t n, int64_t k);
  * stored + 8) and FP16 group scales (q4GroupScale) [n][k/32]. */
 int gphq_gptq_round(float *w_dev, int64_t n, int64_t k, const float *u_dev, const uint8_t *dead_dev, int bits,
                     void *codes_dev, void *scales_dev, void *work_dev, int64_t work_bytes, void *stream);
+
+/* ---- GPTQ calibration pass (cmd/qwen3-gptq -> qwen3lm.QuantizeGPTQ) --------
+ * Replaces QuantizeGPTQ's model pass (gptq.go:191-266) and its calibration
+ * (newCalibration, calibration.weights / layer / attention, normalizedRows,
+ * project; gptq.go:330-600) on the device: the model runs layer by layer in
+ * FP32 over the calibration rows in the GPU backend's basis (residual rotated
+ * by the hidden rotation, RMSNorm weights folded into the next projections,
+ * value rows and o inputs per-head rotated, down inputs rotated by the
+ * intermediate rotation), and each projection is rounded with GPTQ
+ * (gphq_gptq_factor / gphq_gptq_round) against the inputs the rounded layers
+ * before it produce; the next projections and the residual advance through the
+ * rounded matrices. fp32 throughout; sums run in another order than the
+ * reference's, so results agree to fp32 rounding, not bit for bit. The
+ * tokenizer stays with the caller: calibration text arrives as token ids.
+ *
+ * gphq_gptq_calibration_new (newCalibration, gptq.go:344-383): nseq sequences
+ * of seq_lens[s] tokens (1..256 each, gptqMaxSeq; at most 4096 in all,
+ * gptqMaxRows), ids concatenated in ids; each row embedded from the BF16 table
+ * [vocab][hidden] (device, embed_len values) and rotated; row positions count
+ * from 0 in each sequence. cfg as gphq_lm_new (its fmt is ignored). Waits for
+ * the stream. GPHQ_ERR_CALIBRATION_EMPTY without rows.
+ * gphq_gptq_calibration_layer (calibration.layer, gptq.go:437-524): one layer
+ * from its seven BF16 projections src_bf16_dev[7] (device [n][k]: q_proj,
+ * k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj), the float32 input /
+ * post-attention norms [hidden] and q / k norms [128] (host); bits 8 or 4;
+ * codes_dev[p] / scales_dev[p] receive projection p as gphq_gptq_round
+ * writes it (gptqRowBytes per row), in the file's layout. The residual
+ * advances through the rounded layer. Waits for the stream.
+ * gphq_gptq_calibration_rows: the shape [rows][width] of one set of rows
+ * and, with dst_dev, a stream-ordered copy of them (dst_len floats at least):
+ * the residual (after the last layer run, or the embedded rows before any),
+ * or the last layer's attention input (normalized rows, q/k/v's GPTQ input),
+ * context (o's), MLP input (gate/up's) or down input (rotated SwiGLU rows).
+ * gphq_gptq_calibration_sequences (calibrationSequences' add, gptq.go:275-287):
+ * the sequence lengths ntexts tokenized texts give, each text cut into pieces
+ * of at most 256 tokens until 4096 are taken; with seq_lens NULL only *nseq.
+ * gphq_gptq_quantize (QuantizeGPTQ, gptq.go:197-266): format "gpu" (8 bits)
+ * or "gpu-q4" (4 bits) -- else GPHQ_ERR_UNSUPPORTED --, widths that are
+ * multiples of 4096 (GPHQ_ERR_GPTQ_WIDTH), the texts' token ids cut as above
+ * (GPHQ_ERR_CALIBRATION_EMPTY without any), the checkpoint of dir
+ * (model.embed_tokens.weight and the layers' BF16 projections and norms) and
+ * its GPHQ0001 file written through gphq_gptq_create / commit, layer by layer;
+ * progress(layer, layers, user) after each (may be NULL). The temporary file
+ * is removed on any error. */
+typedef struct gphq_gptq_calibration gphq_gptq_calibration;
+typedef void (*gphq_gptq_progress)(int64_t layer, int64_t layers, void *user);
+#define GPHQ_CAL_RESIDUAL 0
+#define GPHQ_CAL_ATTN_INPUT 1
+#define GPHQ_CAL_CONTEXT 2
+#define GPHQ_CAL_MLP_INPUT 3
+#define GPHQ_CAL_DOWN_INPUT 4
+int gphq_gptq_calibration_new(const gphq_lm_config *cfg, const int32_t *ids, const int64_t *seq_lens, int64_t nseq,
+                              const uint16_t *embed_bf16_dev, int64_t embed_len, gphq_gptq_calibration **out,
+                              void *stream);
+void gphq_gptq_calibration_free(gphq_gptq_calibration *cal);
+int gphq_gptq_calibration_layer(gphq_gptq_calibration *cal, const uint16_t *const *src_bf16_dev,
+                                const float *input_norm_host, const float *post_norm_host, const float *q_norm_host,
+                                const float *k_norm_host, int bits, void *const *codes_dev, void *const *scales_dev,
+                                void *stream);
+int gphq_gptq_calibration_rows(const gphq_gptq_calibration *cal, int which, float *dst_dev, int64_t dst_len,
+                               int64_t *rows, int64_t *width, void *stream);
+int gphq_gptq_calibration_sequences(const int64_t *text_lens, int64_t ntexts, int64_t *seq_lens, int64_t max_seqs,
+                                    int64_t *nseq);
+int gphq_gptq_quantize(const char *dir, const char *format, const gphq_lm_config *cfg, const int32_t *ids,
+                       const int64_t *text_lens, int64_t ntexts, gphq_gptq_progress progress, void *user,
+                       void *stream);
 
 /* ---- safetensors checkpoints (internal/safetensors/safetensors.go) --------
  * Open reads the tensor index of dir: model.safetensors, or the shards of

@@ -363,3 +363,16 @@ def test_one_preparer(tmp_path):
     assert not f.fresh and f.payload()[0] == 42
     f.close()
     first.close()
+
+
+def test_gptq_calibration_sequences_cut_like_the_reference():
+    # calibrationSequences' add (gptq.go:275-287): each text's tokens in
+    # pieces of at most 256 (gptqMaxSeq) until 4096 (gptqMaxRows) are taken;
+    # empty texts give nothing.
+    assert gphq.gptq_calibration_sequences([]).tolist() == []
+    assert gphq.gptq_calibration_sequences([0, 5, 0]).tolist() == [5]
+    assert gphq.gptq_calibration_sequences([600, 3]).tolist() == [256, 256, 88, 3]
+    got = gphq.gptq_calibration_sequences([1000] * 5)
+    assert got.sum() == 4096 and got.max() == 256
+    assert got.tolist() == [256, 256, 256, 232] * 4 + [96]
+    assert gphq.gptq_calibration_sequences([4096, 10]).tolist() == [256] * 16
