@@ -11,7 +11,9 @@ cpu_baseline leg may import this module; the product library never does.
   (WorkspaceI8 quantizer int8.go:106-168, scalarMulPanelsI8 int8.go:200-211)
   with 64-column panels split across T workers (qwen3lm/ops.go:153-214).
 * configs 3 / 4b: one decode step of the CPU int8 path (orc_lm_step_i8:
-  qwen3lm/ops.go:96-214 over WeightsInt8 rows), T workers.
+  qwen3lm/ops.go:96-254 over WeightsInt8 rows, with the reference's
+  hidden / context / intermediate input rotations), T workers; equal to the
+  float64 CpuInt8Oracle to relative 1e-5 (tests/test_cpu_baseline.py).
 
 T is 1 and min(cores, 16): the reference's default worker cap
 (qwen3/model.go:39,99-108).

@@ -779,15 +779,19 @@ void orc_prepare_projection(const uint16_t *bf16, int64_t n, int64_t k, const fl
 }
 
 /* ------------------------------------------------------------------ */
-/* CPU decode step for the CPU baseline (bench.py cpu_baseline only; no
- * parity claim rests on it): one token of a dense Qwen3 through the
- * reference's CPU int8 path (qwen3lm/ops.go:96-214 with WeightsInt8): per
- * projection input, RMSNorm (rmsNorm32), the input rotation of int8
- * projections (ops.go:110-122), per-row int8 quantization (int8.go:106-168)
- * and scalarMulPanelsI8 (int8.go:200-211) split over 64-column panels across
- * T workers (ops.go:153-214); head RMSNorm + RoPE, softmax attention over the
+/* CPU decode step for the CPU baseline (bench.py cpu_baseline): one token of
+ * a dense Qwen3 through the reference's CPU int8 path (qwen3lm/ops.go:96-254
+ * with WeightsInt8, weights.go:314-349): the residual unrotated; per
+ * projection input, RMSNorm with its weight (rmsNorm32), the int8
+ * projections' input rotation (ops.go:110-122: newRotation of the hidden
+ * width for q/k/v/gate/up and the head, of q_dim for o, of the intermediate
+ * width for down), per-row int8 quantization (int8.go:106-168) and
+ * scalarMulPanelsI8 (int8.go:200-211) split over 64-column panels across T
+ * workers (ops.go:153-214); head RMSNorm + RoPE, softmax attention over the
  * fp32 K/V cache, SwiGLU, residual adds; final norm and the int8 head. The
- * workers meet at a barrier between stages, as the reference's pool does. */
+ * workers meet at a barrier between stages, as the reference's pool does.
+ * Pinned to the float64 CpuInt8Oracle (oracle/lm_oracle.py), itself pinned to
+ * the GPU-basis decode oracle, in tests/test_cpu_baseline.py. */
 
 typedef struct {
     int64_t hidden, heads, kv_heads, head_dim, inter, vocab, layers, cap;
@@ -812,6 +816,12 @@ typedef struct {
     int8_t *qa;
     float rs;
     int pos, threads;
+    /* The int8 projections' input rotations (weights.go:314-316): newRotation
+     * of the hidden width, of the attention context (q_dim) and of the
+     * intermediate width. */
+    float *rot_h, *rot_c, *rot_i;
+    int64_t blk_h, blk_c, blk_i;
+    float sc_h, sc_c, sc_i;
     pthread_barrier_t bar;
 } lm_step_ctx;
 
@@ -821,16 +831,6 @@ static void rms_norm32(float *out, const float *x, const float *w, int64_t n, fl
     for (int64_t i = 0; i < n; i++) ss += (double)x[i] * x[i];
     const float inv = (float)(1.0 / sqrt(ss / (double)n + eps));
     for (int64_t i = 0; i < n; i++) out[i] = x[i] * inv * (w ? w[i] : 1.0f);
-}
-
-static void fwht_blocks(float *v, int64_t n) {
-    int64_t block = 1;
-    while (block < 4096 && n % (2 * block) == 0) block *= 2;
-    const float scale = (float)(1.0 / sqrt((double)block));
-    for (int64_t b = 0; b < n; b += block) {
-        for (int64_t i = 0; i < block; i++) v[b + i] *= scale;
-        orc_fwht(v + b, block);
-    }
 }
 
 static void quantize_row(lm_step_ctx *c, const float *x, int64_t k) {
@@ -863,7 +863,7 @@ static void *lm_step_worker(void *arg) {
         float *kc = c->kc + l * g->cap * kvd, *vc = c->vc + l * g->cap * kvd;
         if (t == 0) {
             rms_norm32(c->x, c->h, L->attn_norm, H, g->eps);
-            fwht_blocks(c->x, H);
+            orc_rotation_apply(c->rot_h, c->blk_h, c->sc_h, c->x, H);
             quantize_row(c, c->x, H);
         }
         pthread_barrier_wait(&c->bar);
@@ -916,7 +916,7 @@ static void *lm_step_worker(void *arg) {
         pthread_barrier_wait(&c->bar);
         if (t == 0) {
             memcpy(c->x, c->ctx, qd * 4);
-            for (int64_t b = 0; b < qd; b += hd) fwht_blocks(c->x + b, hd);
+            orc_rotation_apply(c->rot_c, c->blk_c, c->sc_c, c->x, qd);
             quantize_row(c, c->x, qd);
         }
         pthread_barrier_wait(&c->bar);
@@ -925,7 +925,7 @@ static void *lm_step_worker(void *arg) {
         if (t == 0) {
             for (int64_t i = 0; i < H; i++) c->h[i] += c->tmp[i];
             rms_norm32(c->x, c->h, L->mlp_norm, H, g->eps);
-            fwht_blocks(c->x, H);
+            orc_rotation_apply(c->rot_h, c->blk_h, c->sc_h, c->x, H);
             quantize_row(c, c->x, H);
         }
         pthread_barrier_wait(&c->bar);
@@ -937,7 +937,7 @@ static void *lm_step_worker(void *arg) {
                 const float gt = c->act[i], up = c->act[I + i];
                 c->act[i] = gt / (1.0f + expf(-gt)) * up;
             }
-            fwht_blocks(c->act, I);
+            orc_rotation_apply(c->rot_i, c->blk_i, c->sc_i, c->act, I);
             quantize_row(c, c->act, I);
         }
         pthread_barrier_wait(&c->bar);
@@ -948,7 +948,7 @@ static void *lm_step_worker(void *arg) {
     }
     if (t == 0) {
         rms_norm32(c->x, c->h, c->final_norm, H, g->eps);
-        fwht_blocks(c->x, H);
+        orc_rotation_apply(c->rot_h, c->blk_h, c->sc_h, c->x, H);
         quantize_row(c, c->x, H);
     }
     pthread_barrier_wait(&c->bar);
@@ -979,6 +979,12 @@ void orc_lm_step_i8(const orc_lm_geom *g, const orc_lm_layer_i8 *layers, float *
     c.ctx = c.qkv + qd + 2 * kvd;
     c.scores = c.ctx + qd;
     c.qa = (int8_t *)malloc((size_t)big);
+    c.rot_h = (float *)malloc((size_t)(H + qd + I) * sizeof(float));
+    c.rot_c = c.rot_h + H;
+    c.rot_i = c.rot_c + qd;
+    c.blk_h = orc_rotation(H, c.rot_h, &c.sc_h);
+    c.blk_c = orc_rotation(qd, c.rot_c, &c.sc_c);
+    c.blk_i = orc_rotation(I, c.rot_i, &c.sc_i);
     pthread_barrier_init(&c.bar, 0, (unsigned)threads);
     pthread_t tid[64];
     lm_worker w[64];
@@ -990,5 +996,6 @@ void orc_lm_step_i8(const orc_lm_geom *g, const orc_lm_layer_i8 *layers, float *
     for (int t = 1; t < threads; t++) pthread_join(tid[t], 0);
     pthread_barrier_destroy(&c.bar);
     free(c.qa);
+    free(c.rot_h);
     free(mem);
 }

@@ -389,3 +389,89 @@ def greedy_argmax_np(values):
         return 0
     w = np.where(np.isnan(v), -np.inf, v)
     return int(np.argmax(w))
+
+
+def quantize_rows_i8(x):
+    """WorkspaceI8's per-row quantization (int8.go:106-168) in float64, as the
+    dequantized values s * q: s = max|x| / 127, q = round-half-even(x * 127 /
+    max|x|) saturated to [-128, 127]; a row with no finite positive maximum
+    gives zeros."""
+    x = np.atleast_2d(np.asarray(x, np.float64))
+    m = np.abs(x).max(axis=1, keepdims=True)
+    ok = np.isfinite(m) & (m > 0)
+    safe = np.where(ok, m, 1.0)
+    q = np.clip(np.rint(x * (127.0 / safe)), -128, 127)
+    return np.where(ok, q * (safe / 127.0), 0.0)
+
+
+class CpuInt8Oracle:
+    """float64 restatement of the reference CPU provider's int8 decode step
+    (qwen3lm/ops.go:96-254 over WeightsInt8 rows, weights.go:314-349,
+    738-831): the residual stream is not rotated; each projection input is
+    RMS-normalized with its norm weight, rotated by the projection's input
+    rotation (newRotation of the hidden width for q/k/v/gate/up and the head,
+    of q_dim for o, of the intermediate width for down), quantized per row
+    (quantize_rows_i8) and multiplied by the int8 rows times their per-row
+    scales (the rows store W R^T, quantizeRotatedRows). Head RMSNorm and RoPE,
+    softmax attention over the K/V cache, SwiGLU and the residual adds as in
+    the GPU step. With quantize=False the activations are used unquantized and
+    the step is the model's own forward pass (pinned against DecodeOracle in
+    tests/test_cpu_baseline.py).
+
+    layers: dicts with w (seven [n][k] arrays: q, k, v, o, gate, up, down),
+    s (seven per-row scales, or None for float rows), attn_norm, mlp_norm,
+    q_norm, k_norm; head (w, s) likewise."""
+
+    def __init__(self, geom, layers, final_norm, head, quantize=True):
+        g = self.g = geom
+        self.rot = {"h": rotation(g.hidden), "c": rotation(g.qd), "i": rotation(g.inter)}
+        f64 = lambda v: np.asarray(v, np.float64)
+        deq = lambda w, s: f64(w) if s is None else f64(w) * f64(s)[:, None]
+        self.L = [dict(w=[deq(w, s) for w, s in zip(L["w"], L["s"])], attn=f64(L["attn_norm"]),
+                       mlp=f64(L["mlp_norm"]), qn=f64(L["q_norm"]), kn=f64(L["k_norm"])) for L in layers]
+        self.final_norm = f64(final_norm)
+        self.head = deq(*head)
+        self.quantize = quantize
+
+    def _norm(self, v, w=None):
+        inv = 1.0 / np.sqrt(np.dot(v, v) / len(v) + self.g.eps)
+        return v * inv if w is None else v * inv * w
+
+    def _proj(self, x, rot, w):
+        x = rot_apply(x, self.rot[rot])
+        if self.quantize:
+            x = quantize_rows_i8(x)[0]
+        return w @ x
+
+    def step(self, h, kc, vc, pos, cos, sin):
+        """One token at position pos: h (the embedding row, unrotated) ->
+        (residual, post-final-norm state, logits); appends K/V at pos of each
+        layer's cache (kc[l], vc[l]: [cap][kv_dim]); cos / sin: the RoPE row."""
+        g = self.g
+        hd, half, grp = g.head_dim, g.head_dim // 2, g.heads // g.kv_heads
+        h = np.array(h, np.float64)
+        c, s = np.asarray(cos, np.float64), np.asarray(sin, np.float64)
+        rope = lambda v: np.concatenate([v[:half] * c - v[half:] * s, v[half:] * c + v[:half] * s])
+        scale = 1.0 / np.sqrt(hd)
+        for li, L in enumerate(self.L):
+            W = L["w"]
+            x = self._norm(h, L["attn"])
+            q, k, v = self._proj(x, "h", W[0]), self._proj(x, "h", W[1]), self._proj(x, "h", W[2])
+            for kh in range(g.kv_heads):
+                kc[li][pos, kh * hd:(kh + 1) * hd] = rope(self._norm(k[kh * hd:(kh + 1) * hd], L["kn"]))
+                vc[li][pos, kh * hd:(kh + 1) * hd] = v[kh * hd:(kh + 1) * hd]
+            ctx = np.empty(g.qd)
+            for qh in range(g.heads):
+                kh = qh // grp
+                qv = rope(self._norm(q[qh * hd:(qh + 1) * hd], L["qn"]))
+                sc = kc[li][: pos + 1, kh * hd:(kh + 1) * hd] @ qv * scale
+                p = np.exp(sc - sc.max())
+                ctx[qh * hd:(qh + 1) * hd] = (p / p.sum()) @ vc[li][: pos + 1, kh * hd:(kh + 1) * hd]
+            h = h + self._proj(ctx, "c", W[3])
+            x = self._norm(h, L["mlp"])
+            gate, up = self._proj(x, "h", W[4]), self._proj(x, "h", W[5])
+            with np.errstate(over="ignore"):
+                act = gate / (1.0 + np.exp(-gate)) * up
+            h = h + self._proj(act, "i", W[6])
+        hidden = self._norm(h, self.final_norm)
+        return h, hidden, self._proj(hidden, "h", self.head)
