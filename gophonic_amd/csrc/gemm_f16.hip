@@ -499,12 +499,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
     const int kper = (KT + a.splits - 1) / a.splits;
     const int k0 = sp * kper, k1 = min(KT, k0 + kper);
 
-    // A loader: 2 KB groups (16 rows x 64 K) of the FP16 tile layout; load i
-    // of thread t is 16-byte unit u = i*NT + t: group u/128 (rows
-    // 16*group ..), slot (t%128)/2 (row slot%16, K values 16*(slot/16) +
-    // 8*(t%2) ..), the same slot for every i.
-    const int aslot = (t & 127) >> 1, achunk = 2 * (aslot >> 4) + (t & 1);
-    const _Float16 *abase = a.A + (size_t)(t & 127) * 8;
+    // A loader: 2 KB groups (16 rows x 64 K) of the FP16 tile layout, one per
+    // 128 threads and load i (group i*NT/128 + t/128). Thread t takes row t%16
+    // and 16-byte chunk (t/16)%8 (K values 8*chunk ..) of its group: in the
+    // tile layout that is half chunk%2 of fragment lane row + 16*(chunk/2),
+    // unit 2*lane + half. Each 8-lane phase of an LDS write (128 bytes a
+    // cycle) then covers 8 consecutive rows at one chunk, 8 distinct swizzled
+    // slots, and a wavefront's loads still cover 1 KB of the group.
+    const int arow = t & 15, achunk = (t >> 4) & 7;
+    const _Float16 *abase = a.A + (size_t)(2 * (arow + 16 * (achunk >> 1)) + (achunk & 1)) * 8;
     const int mtb = (m0 >> 4) + (t >> 7);
     // B loader: piece i of thread t is row (i*NT + t)/4 of the tile, 16 K
     // values at 16*(t%4) of the step.
@@ -525,7 +528,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void f16gemm_big_kernel(const F16Ge
     auto lstore = [&](int set, int buf) {
 #pragma unroll
         for (int i = 0; i < AL; ++i) {
-            const int r = 16 * (i * (NT / 128) + (t >> 7)) + (aslot & 15);
+            const int r = 16 * (i * (NT / 128) + (t >> 7)) + arow;
             As[buf][r * 8 + big_swz(r, achunk)] = ar[set][i];
         }
 #pragma unroll
