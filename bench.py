@@ -404,14 +404,16 @@ def decode_model(torch, gphq, geom, fmt, seed):
     return lm, weight_bytes
 
 
-def decode_config(torch, gphq, lm, weight_bytes, geom, lanes, ctx, steps, warmup, graph, label):
+def decode_config(torch, gphq, lm, weight_bytes, geom, lanes, ctx, steps, warmup, graph, label, cap_factor=1):
     """Greedy decode of `steps` tokens per lane at context `ctx` (the K/V
     cache prefilled by the batched pass over random ids, lane 0's prefix
-    copied to the others), timed with HIP events on the launch stream."""
+    copied to the others), timed with HIP events on the launch stream. Each
+    prefix holds cap_factor times the rows the run needs (the reference's
+    callers double capacity, qwen3/chat.go:760-769)."""
     stream = torch.cuda.current_stream()
     ws = gphq.DecodeBatch(lm, lanes)
     ws.set_graph(graph)
-    cap = ctx + max(steps, warmup) + 1
+    cap = cap_factor * (ctx + max(steps, warmup) + 1)
     kvs = [gphq.Prefix(lm, cap) for _ in range(lanes)]
     rng = np.random.default_rng(ctx + lanes)
     t0 = time.perf_counter()
@@ -451,6 +453,7 @@ def decode_config(torch, gphq, lm, weight_bytes, geom, lanes, ctx, steps, warmup
         "achieved_gbs": round(step_bytes / (ms_tok / 1e3) / 1e9, 1),
         "hbm_frac": round(step_bytes / (ms_tok / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
         "graph": bool(graph),
+        "capacity": int(cap),
         "prefill_s": round(prefill_s, 2),
         "distinct_tokens": int(len(np.unique(toks))),
     }
@@ -537,6 +540,9 @@ def decode_benchmarks(args, torch, gphq):
         if "4b1" in want:
             res["config4b_1"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 1, 4096, 64, 8, graph,
                                               "config 4b: Qwen3-8B-shaped decode at context 4096, 1 lane")
+            res["config4b_1_cap2x"] = decode_config(
+                torch, gphq, lm, wb, QWEN3_8B, 1, 4096, 64, 8, graph,
+                "config 4b: Qwen3-8B-shaped decode at context 4096, 1 lane, prefix capacity twice the need", 2)
         if "4b16" in want:
             res["config4b_16"] = decode_config(torch, gphq, lm, wb, QWEN3_8B, 16, 4096, 32, 4, graph,
                                                "config 4b: Qwen3-8B-shaped decode at context 4096, 16 lanes")

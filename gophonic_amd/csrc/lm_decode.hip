@@ -104,6 +104,7 @@ struct gphq_decode_batch {
     hipGraphExec_t step_exec = nullptr;
     std::vector<gphq_prefix *> graph_kvs;
     std::vector<uint64_t> graph_kv_gens;  // the prefixes' generations at capture
+    std::vector<int> graph_chunks;        // the attention key ranges its first loads expect
     uint64_t graph_lm_gen = 0;            // the model's binding generation at capture
     float *graph_hidden = nullptr;
     int32_t *graph_out = nullptr;
@@ -222,14 +223,14 @@ __global__ __launch_bounds__(1024) void lm_final_kernel(const float *__restrict_
     if (threadIdx.x == 0 && bad) nonfinite[one_flag ? 0 : lane] = 1;
 }
 
-// Keys per attention block of a prefix with `capacity` rows: the capacity
-// spread over at most `splits` blocks, at least kMinChunk each, a multiple of
-// 16. Fixed per prefix, so a block knows its key range before it has read the
-// lane's position; at a context of n keys the blocks in use, ceil(n / chunk),
-// are never empty.
-static int attn_chunk(int64_t capacity, int splits) {
-    const int64_t chunk = (capacity + splits - 1) / splits;
-    return (int)std::max<int64_t>(kMinChunk, (chunk + 15) & ~15);
+// Keys per attention block at a context of n keys: n spread over at most
+// `splits` blocks, at least kMinChunk each, a multiple of 16; the blocks in
+// use, ceil(n / chunk), are never empty and never more than `splits`. A
+// function of n alone, so a step's attention sums in the same order however
+// the steps are enqueued (one by one, or replayed from one captured graph).
+__host__ __device__ inline int attn_chunk(int64_t n, int splits) {
+    const int64_t chunk = (n + splits - 1) / splits;
+    return (int)(chunk + 15 < kMinChunk ? kMinChunk : (chunk + 15) & ~15);
 }
 
 struct AttnArgs {
@@ -241,7 +242,7 @@ struct AttnArgs {
     const int32_t *pos;    // [lanes]
     float *ctx;            // [lanes][qd]
     float *part;           // [lanes][kvh][splits][GROUP][kPart]
-    int chunk[kMaxLanes];  // keys per block (attn_chunk of the lane's prefix)
+    int chunk[kMaxLanes];  // the expected keys per block (attn_chunk of the context the host expects)
     int cap[kMaxLanes];    // the lane's prefix capacity
     float eps, scale;
     int qkvw, qd, kvd, kvh, splits, sin_off;
@@ -270,9 +271,11 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     __shared__ float wacc[4][GROUP][kHeadDim];
     const int lid = blockIdx.z, g = blockIdx.y, sp = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int chunk = a.chunk[lid], cap = a.cap[lid];
-    const int j0 = sp * chunk;
-    if (j0 >= cap) return;
+    const int cap = a.cap[lid];
+    // The key range follows from the position (attn_chunk); until it has
+    // arrived, the keys of the range the host expects are loaded.
+    int chunk = a.chunk[lid];
+    int j0 = sp * chunk;
     const int pos = a.pos[lid];
     const float *qkv = a.qkv + (size_t)lid * a.qkvw;
     float *kc = a.kc[lid] + g * kHeadDim;
@@ -304,7 +307,7 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     }
 
     // Keys of step `it`: rows past the block's cached keys (jc, once the
-    // position is known; the capacity before) load row j0 instead.
+    // position is known; the capacity before) load row 0 instead.
     float kb[NB][KPI][8], vb[NB][KPI][8];
     bool okb[NB][KPI];
     int jc = cap;
@@ -313,7 +316,7 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
         for (int u = 0; u < KPI; ++u) {
             const int j = j0 + (it * KPI + u) * 16 + rowgroup;
             ok[u] = j < jc;
-            const int jj = ok[u] ? j : j0;
+            const int jj = ok[u] ? j : 0;
             const float4 k0 = *(const float4 *)(kc + (size_t)jj * a.kvd + d0);
             const float4 k1 = *(const float4 *)(kc + (size_t)jj * a.kvd + d1);
             const float4 v0 = *(const float4 *)(vc + (size_t)jj * a.kvd + d0);
@@ -327,7 +330,14 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) load_keys(b, kb[b], vb[b], okb[b]);
     const int n = pos + 1;
-    if (j0 >= n) return;  // no keys of this lane's context
+    const int want = attn_chunk(n, a.splits);
+    if (sp * want >= n) return;  // no keys of this lane's context
+    if (want != chunk) {         // the expected range was another: load the block's own
+        chunk = want;
+        j0 = sp * chunk;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load_keys(b, kb[b], vb[b], okb[b]);
+    }
     const int j1 = min(n, j0 + chunk);
     const bool owner = j1 == n;  // this block holds the new key
     jc = owner ? j1 - 1 : j1;    // cached keys [j0, jc)
@@ -522,7 +532,7 @@ __global__ __launch_bounds__(128) void lm_attn_merge_kernel(const AttnArgs a, in
         ms = lp[threadIdx.x * stride];
         ls = lp[threadIdx.x * stride + 1];
     }
-    const int chunk = a.chunk[lid];
+    const int chunk = attn_chunk(pos + 1, a.splits);
     const int used = (pos + 1 + chunk - 1) / chunk;
 #pragma unroll
     for (int s = 0; s < kMaxSplits; ++s) v[s] = s < used ? v[s] : 0.0f;
@@ -686,10 +696,13 @@ int gemv(gphq_decode_batch *ws, int lanes, int fmt, int pro, int epi, const uint
 }
 
 // Enqueues one decode step for `lanes` lanes whose tokens and positions are
-// already in ws->tok / ws->pos. head: run the final norm, head and argmax;
-// hidden_out receives each lane's post-final-norm state.
-int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool head, float *hidden_out,
-                int32_t *next_out, int32_t *run_out, hipStream_t st) {
+// already in ws->tok / ws->pos. keys[l]: the context (position + 1) the host
+// expects lane l's step to have, which sizes the attention blocks' first key
+// loads; the blocks take their ranges from the device-side position. head:
+// run the final norm, head and argmax; hidden_out receives each lane's
+// post-final-norm state.
+int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, const int64_t *keys, bool head,
+                float *hidden_out, int32_t *next_out, int32_t *run_out, hipStream_t st) {
     const gphq_lm *lm = ws->lm;
     const gphq_lm_config &c = lm->cfg;
     const int64_t H = c.hidden, I = c.intermediate, qkvw = lm->qd + 2 * lm->kvd;
@@ -720,7 +733,7 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, bool 
             const size_t off = (size_t)layer * kvs[l]->capacity * lm->kvd;
             aa.kc[l] = kvs[l]->kc + off;
             aa.vc[l] = kvs[l]->vc + off;
-            aa.chunk[l] = attn_chunk(kvs[l]->capacity, aa.splits);
+            aa.chunk[l] = attn_chunk(keys[l], aa.splits);
             aa.cap[l] = (int)kvs[l]->capacity;
         }
         aa.qn = lm->norms + (size_t)layer * 2 * kHeadDim;
@@ -813,6 +826,7 @@ void drop_graph(gphq_decode_batch *ws) {
     ws->step_exec = nullptr;
     ws->graph_kvs.clear();
     ws->graph_kv_gens.clear();
+    ws->graph_chunks.clear();
 }
 
 void free_batch(gphq_decode_batch *ws) {
@@ -829,22 +843,25 @@ void free_batch(gphq_decode_batch *ws) {
 // generation (a freed prefix's host address may come back from
 // gphq_prefix_new with other K/V buffers; its generation does not), plus the
 // output pointers and the GEMV mode.
-bool graph_matches(const gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, const float *hidden,
-                   const int32_t *out) {
+bool graph_matches(const gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, const int64_t *keys,
+                   const float *hidden, const int32_t *out) {
     if (!ws->step_exec || (int)ws->graph_kvs.size() != lanes || ws->graph_hidden != hidden || ws->graph_out != out ||
         ws->graph_vec_min != ws->vec_min_lanes || ws->graph_lm_gen != ws->lm->gen)
         return false;
     for (int l = 0; l < lanes; ++l)
-        if (ws->graph_kvs[(size_t)l] != kvs[l] || ws->graph_kv_gens[(size_t)l] != kvs[l]->gen) return false;
+        if (ws->graph_kvs[(size_t)l] != kvs[l] || ws->graph_kv_gens[(size_t)l] != kvs[l]->gen ||
+            ws->graph_chunks[(size_t)l] != attn_chunk(keys[l], attention_splits(ws->lm, lanes)))
+            return false;
     return true;
 }
 
-int step_graph(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, float *hidden, int32_t *out) {
-    if (graph_matches(ws, kvs, lanes, hidden, out)) return GPHQ_OK;
+int step_graph(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, const int64_t *keys, float *hidden,
+               int32_t *out) {
+    if (graph_matches(ws, kvs, lanes, keys, hidden, out)) return GPHQ_OK;
     drop_graph(ws);
     if (!ws->capture) GPHQ_TRY(hip_status(hipStreamCreateWithFlags(&ws->capture, hipStreamNonBlocking)));
     GPHQ_TRY(hip_status(hipStreamBeginCapture(ws->capture, hipStreamCaptureModeRelaxed)));
-    const int st = encode_step(ws, kvs, lanes, true, hidden, nullptr, out, ws->capture);
+    const int st = encode_step(ws, kvs, lanes, keys, true, hidden, nullptr, out, ws->capture);
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(ws->capture, &graph);
     if (st != GPHQ_OK || e != hipSuccess) {
@@ -858,6 +875,8 @@ int step_graph(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, float 
         return hip_status(ie);
     }
     ws->graph_kvs.assign(kvs, kvs + lanes);
+    ws->graph_chunks.resize((size_t)lanes);
+    for (int l = 0; l < lanes; ++l) ws->graph_chunks[(size_t)l] = attn_chunk(keys[l], attention_splits(ws->lm, lanes));
     ws->graph_kv_gens.resize((size_t)lanes);
     for (int l = 0; l < lanes; ++l) ws->graph_kv_gens[(size_t)l] = kvs[l]->gen;
     ws->graph_lm_gen = ws->lm->gen;
@@ -1182,7 +1201,9 @@ int gphq_decode_batch_into(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64
     if (!hidden_dev || logits_len < lanes * ws->lm->cfg.vocab) return GPHQ_ERR_BATCH_SHAPE;
     hipStream_t st = (hipStream_t)stream;
     GPHQ_TRY(seed(ws, (int)lanes, positions, tokens, 0, st));
-    GPHQ_TRY(encode_step(ws, kvs, (int)lanes, true, hidden_dev, nullptr, nullptr, st));
+    int64_t keys[kMaxLanes];
+    for (int64_t l = 0; l < lanes; ++l) keys[l] = positions[l] + 1;
+    GPHQ_TRY(encode_step(ws, kvs, (int)lanes, keys, true, hidden_dev, nullptr, nullptr, st));
     const gphq_lm *lm = ws->lm;
     return hip_status(hipMemcpy2DAsync(logits_dev, (size_t)lm->cfg.vocab * 4, ws->logits, (size_t)lm->head_rows * 4,
                                        (size_t)lm->cfg.vocab * 4, (size_t)lanes, hipMemcpyDeviceToDevice, st));
@@ -1195,7 +1216,9 @@ int gphq_decode_batch_greedy_into(gphq_decode_batch *ws, gphq_prefix *const *kvs
     if (!hidden_dev) return GPHQ_ERR_BATCH_SHAPE;
     hipStream_t st = (hipStream_t)stream;
     GPHQ_TRY(seed(ws, (int)lanes, positions, tokens, 0, st));
-    return encode_step(ws, kvs, (int)lanes, true, hidden_dev, next_dev, nullptr, st);
+    int64_t keys[kMaxLanes];
+    for (int64_t l = 0; l < lanes; ++l) keys[l] = positions[l] + 1;
+    return encode_step(ws, kvs, (int)lanes, keys, true, hidden_dev, next_dev, nullptr, st);
 }
 
 int gphq_decode_greedy_run(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t lanes, const int64_t *positions,
@@ -1211,13 +1234,17 @@ int gphq_decode_greedy_run(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64
         return GPHQ_ERR_OVERLAP;
     hipStream_t st = (hipStream_t)stream;
     float *hid = hidden_dev ? hidden_dev : ws->hidden;
-    if (ws->use_graph) GPHQ_TRY(step_graph(ws, kvs, (int)lanes, hid, tokens_out_dev));
+    int64_t keys[kMaxLanes];
+    for (int64_t l = 0; l < lanes; ++l) keys[l] = positions[l] + steps;  // the last step's context
+    if (ws->use_graph) GPHQ_TRY(step_graph(ws, kvs, (int)lanes, keys, hid, tokens_out_dev));
     GPHQ_TRY(seed(ws, (int)lanes, positions, tokens, 0, st));
     for (int64_t t = 0; t < steps; ++t) {
-        if (ws->use_graph)
+        if (ws->use_graph) {
             GPHQ_TRY(hip_status(hipGraphLaunch(ws->step_exec, st)));
-        else
-            GPHQ_TRY(encode_step(ws, kvs, (int)lanes, true, hid, nullptr, tokens_out_dev, st));
+        } else {
+            for (int64_t l = 0; l < lanes; ++l) keys[l] = positions[l] + t + 1;
+            GPHQ_TRY(encode_step(ws, kvs, (int)lanes, keys, true, hid, nullptr, tokens_out_dev, st));
+        }
     }
     return GPHQ_OK;
 }
@@ -1234,9 +1261,11 @@ int gphq_decode_extend(gphq_decode_batch *ws, gphq_prefix *const *kvs, int64_t l
     if (steps < 1) return GPHQ_ERR_BATCH_SHAPE;
     GPHQ_TRY(validate(ws, kvs, lanes, positions, tokens, steps, nullptr, 0, nullptr, nullptr, false));
     hipStream_t st = (hipStream_t)stream;
+    int64_t keys[kMaxLanes];
     for (int64_t t = 0; t < steps; ++t) {
         GPHQ_TRY(seed(ws, (int)lanes, positions, tokens + t * lanes, t, st));
-        GPHQ_TRY(encode_step(ws, kvs, (int)lanes, false, nullptr, nullptr, nullptr, st));
+        for (int64_t l = 0; l < lanes; ++l) keys[l] = positions[l] + t + 1;
+        GPHQ_TRY(encode_step(ws, kvs, (int)lanes, keys, false, nullptr, nullptr, nullptr, st));
     }
     return GPHQ_OK;
 }

@@ -523,3 +523,78 @@ def test_logits_validation_errors():
     torch.cuda.synchronize()
     assert (out == -7.0).all()
     assert gphq.error_string(gphq.ERR_LOGITS_SHAPE).startswith("qwen3: logits")
+
+
+# A small model with a long RoPE table, for contexts of a few thousand keys.
+LONG = lo.Geometry(hidden=256, layers=2, heads=2, kv_heads=1, head_dim=128, inter=512, vocab=96, max_pos=4096)
+
+
+def test_attention_ranges_follow_the_context_not_the_capacity():
+    # The attention blocks take their key ranges from the lane's context
+    # alone. A prefix with twice the rows it needs (the reference's callers
+    # double capacity, qwen3/chat.go:760-769) decodes the same bits as one
+    # sized to the need, step by step, eagerly, or replayed from one captured
+    # step; here the run crosses a change of range (2048 keys over 32 splits
+    # take 64 keys each, 2049 take 80), so a replayed step first loads the
+    # range the capture expected and then its own. The first step matches the
+    # float64 oracle over the same cache rows.
+    import torch
+
+    g = LONG
+    model = lc.random_model(g, lo.FMT_Q8B, 23)
+    oracle = lc.oracle_for(model)
+    lm = device_model(model)
+    rng = np.random.default_rng(8)
+    ctx, steps = 2040, 16
+    src = gphq.Prefix(lm, ctx + steps + 1)
+    pf = gphq.Prefill(lm, 512)
+    pf.extend(src, 0, list(rng.integers(0, g.vocab, ctx)), torch.empty(g.hidden, device="cuda"))
+    pf.check()
+    first = int(rng.integers(0, g.vocab))
+    ws = gphq.DecodeBatch(lm, 1)
+
+    def fresh(cap):
+        kv = gphq.Prefix(lm, cap)
+        kv.copy_from(src, ctx)
+        return kv
+
+    # The oracle's first step over the prefilled rows.
+    kc, vc, cap = src.kv()
+    rows = _read_dev_floats(kc, g.layers * cap * g.kvd).reshape(g.layers, cap, g.kvd)
+    vrows = _read_dev_floats(vc, g.layers * cap * g.kvd).reshape(g.layers, cap, g.kvd)
+    cache = [(rows[i].astype(np.float64).copy(), vrows[i].astype(np.float64).copy()) for i in range(g.layers)]
+    want_h, want_l, _ = oracle.step(cache, ctx, first)
+    kv = fresh(ctx + steps + 1)
+    h1 = torch.empty((1, g.hidden), device="cuda")
+    l1 = torch.empty((1, g.vocab), device="cuda")
+    ws.into([kv], [ctx], [first], h1, l1)
+    rh, _ = err(want_h, h1.cpu().numpy()[0])
+    rl, _ = err(want_l, l1.cpu().numpy()[0])
+    assert rh <= REL and rl <= REL, (rh, rl)
+
+    def step_by_step(cap):
+        kv = fresh(cap)
+        hid = torch.empty((1, g.hidden), device="cuda")
+        nxt = torch.empty(1, dtype=torch.int32, device="cuda")
+        tok, toks = first, []
+        for s in range(steps):
+            ws.greedy_into([kv], [ctx + s], [tok], hid, nxt)
+            tok = int(nxt.cpu().numpy()[0])
+            toks.append(tok)
+        return np.array(toks), hid.cpu().numpy()
+
+    def run(cap, graph):
+        kv = fresh(cap)
+        ws.set_graph(graph)
+        out = torch.full((steps, 1), -1, dtype=torch.int32, device="cuda")
+        hid = torch.empty((1, g.hidden), device="cuda")
+        ws.greedy_run([kv], [ctx], [first], steps, out, hid)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()[:, 0], hid.cpu().numpy()
+
+    want_t, want_hid = step_by_step(ctx + steps + 1)
+    for cap in (ctx + steps + 1, 2 * (ctx + steps)):
+        for got_t, got_hid in (step_by_step(cap), run(cap, False), run(cap, True)):
+            np.testing.assert_array_equal(got_t, want_t)
+            np.testing.assert_array_equal(got_hid, want_hid)
+    ws.check()
