@@ -582,6 +582,20 @@ def measured_traffic(kernel):
     return rec["traffic_bytes_per_launch"] if rec.get("kernel") == kernel else None
 
 
+def profiled_launch(kernel):
+    """The committed rocprofv3 kernel-trace summary of `kernel`
+    (profiles/gemvb_config1_kernel_stats.json, made from the run in
+    profiles/gemvb_config1_kernel_stats.md), or None: its average duration per
+    launch, the host it ran on and when."""
+    path = os.path.join(ROOT, "profiles", "gemvb_config1_kernel_stats.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return rec if rec.get("kernel") == kernel else None
+
+
 def cpu_baseline(seconds):
     """The reference's amd64 q8gemv path (scalarMulInto, single thread),
     restated in C (oracle), on the config-1 shape with per-row scales; with
@@ -639,6 +653,7 @@ def main():
     # per wave, rows per group, K slices, waves per block, GEMVs per launch>.
     kernel = "gemvb_kernel<Q8B_F32,4,2,2,8>" if args.mode == "batch" else "gemvp_kernel<Q8B_F32,2,4,2,8,1>"
     traffic = measured_traffic(kernel) if args.rotations == 32 else None
+    prof = profiled_launch(kernel) if args.rotations == 32 else None
     out = {
         "metric": "Q8 GEMV HBM GB/s (% of peak) + Qwen3-8B Q8 decode ms/token, 1 MI355X",
         "value": round(value, 2),
@@ -674,6 +689,14 @@ def main():
             "kernel": kernel,
             "per_launch_us": round(r["per_launch_us"], 3),
             "bytes_per_launch": r["bytes_per_launch"],
+            # The same launch's average duration in the committed rocprofv3
+            # kernel trace (another run, usually another box of the pool) and
+            # the fraction it gives, beside this run's HIP-event figures.
+            "profile_us": None if prof is None else prof["avg_us"],
+            "frac_profile": None if prof is None else
+            round(r["bytes_per_launch"] / (prof["avg_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "profile_source": None if prof is None else
+            f"profiles/gemvb_config1_kernel_stats.md ({prof['calls']} launches on {prof['host']}, {prof['date']})",
         },
         "cpu_baseline": cpu,
         "cpu_baselines": cpus,
