@@ -457,15 +457,19 @@ __global__ __launch_bounds__(64 * WPB) void gemvp_kernel(const GemvBatch<MAXB> b
 }
 
 // Batch GEMV (gphq_gemv_batch, 8-bit formats, K = NS * 1024 up to 4096): a
-// wavefront holds all of x (NS KiB steps) in registers and walks a
-// contiguous run of row groups of RW rows (set by set), with the next
-// group's codes and block scales requested before the current group's
-// arithmetic (two register buffers); no LDS and no barriers. Each row's sum
-// is formed as the persistent kernel forms it for the same K: SL slices of
-// NS/SL steps, each accumulated in step order and reduced across the
-// wavefront, then added in slice order, so a batch launch gives the same
-// bits as single launches. Measured on MI355X at config 1 (32 sets of
-// 4096 x 4096 Q8B_F32, 605 MB): 96.5 us per launch against 100-103 for the
+// wavefront holds all of x (NS KiB steps) in registers and walks row groups
+// of RW rows (set by set), with the next group's codes and block scales
+// requested before the current group's arithmetic (two register buffers); no
+// LDS and no barriers. A block owns a contiguous run of WPB * per groups and
+// its wavefronts take them in turn (wavefront i: groups i, i + WPB, ...), so
+// the block's loads in flight cover one contiguous stretch of the weights.
+// Each row's sum is formed as the persistent kernel forms it for the same K:
+// SL slices of NS/SL steps, each accumulated in step order and reduced
+// across the wavefront, then added in slice order, so a batch launch gives
+// the same bits as single launches. Measured on MI355X at config 1 (32 sets
+// of 4096 x 4096 Q8B_F32, 605 MB): 88.1-88.5 us per launch with 4-wavefront
+// blocks, 8 per CU, against 90.5-91 us when each wavefront walked its own
+// contiguous run (8-wavefront blocks, 3 per CU) and 100-103 us for the
 // persistent kernel with LDS slice merges.
 template <int FMT, int NS, int SL, int RW, int WPB>
 __global__ __launch_bounds__(64 * WPB) void gemvb_kernel(const GemvBatch<kMaxBatch> b, int count, int per) {
@@ -473,12 +477,12 @@ __global__ __launch_bounds__(64 * WPB) void gemvb_kernel(const GemvBatch<kMaxBat
     constexpr int K = NS * 1024, SS = NS / SL;
     constexpr size_t kb = K >> 5;
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int N = b.N;
     const int gps = (N + RW - 1) / RW;
     const int total = gps * count;
-    int g = wave * per;
-    const int gend = min(g + per, total);
+    const int base = blockIdx.x * WPB * per;
+    int g = base + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gend = min(base + WPB * per, total);
     if (g >= gend) return;
     float4 xr[NS][4];
     u32x4 w[2][NS][RW];
@@ -544,20 +548,20 @@ __global__ __launch_bounds__(64 * WPB) void gemvb_kernel(const GemvBatch<kMaxBat
     int cur = g / gps;
     load_x(cur);
     issue(g, std::integral_constant<int, 0>{});
-    for (; g < gend; g += 2) {
-        if (g + 1 < gend) issue(g + 1, std::integral_constant<int, 1>{});
+    for (; g < gend; g += 2 * WPB) {
+        if (g + WPB < gend) issue(g + WPB, std::integral_constant<int, 1>{});
         if (g / gps != cur) {
             cur = g / gps;
             load_x(cur);
         }
         compute(g, std::integral_constant<int, 0>{});
-        if (g + 1 >= gend) break;
-        if (g + 2 < gend) issue(g + 2, std::integral_constant<int, 0>{});
-        if ((g + 1) / gps != cur) {
-            cur = (g + 1) / gps;
+        if (g + WPB >= gend) break;
+        if (g + 2 * WPB < gend) issue(g + 2 * WPB, std::integral_constant<int, 0>{});
+        if ((g + WPB) / gps != cur) {
+            cur = (g + WPB) / gps;
             load_x(cur);
         }
-        compute(g + 1, std::integral_constant<int, 1>{});
+        compute(g + WPB, std::integral_constant<int, 1>{});
     }
 }
 
@@ -841,11 +845,13 @@ static int launch_persistent(const GemvBatch<MAXB> &b, int count, const Persiste
 // The persistent path for one format, or GPHQ_ERR_UNSUPPORTED when the shape
 // is not one it takes (the caller then uses the per-tile kernel).
 // The batch kernel for K = 1024 .. 4096 (slices as persistent_shape's batch
-// shape for that K): RW = 2 rows per group, 8 wavefronts per block, 3 blocks
-// per CU (measured at config 1).
+// shape for that K): RW = 2 rows per group, 4 wavefronts per block, 8 blocks
+// per CU (measured at config 1). The kernel's registers allow 3 wavefronts
+// per SIMD, so 3 blocks of a CU are resident at once and the rest start as
+// blocks finish.
 template <int FMT, int NS, int SL>
 static int go_batch(const GemvBatch<kMaxBatch> &b, int count, hipStream_t stream) {
-    constexpr int RW = 2, WPB = 8, BPC = 3;
+    constexpr int RW = 2, WPB = 4, BPC = 8;
     const long total = (long)((b.N + RW - 1) / RW) * count;
     const long blocks = std::max(1L, std::min((total + WPB - 1) / WPB, (long)device_cus() * BPC));
     const int per = (int)((total + blocks * WPB - 1) / (blocks * WPB));
