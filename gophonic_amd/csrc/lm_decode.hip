@@ -91,6 +91,10 @@ struct gphq_decode_batch {
     float *h, *qkv, *ctx, *act, *hn, *hidden, *logits, *part;
     uint32_t *cand;  // argmax candidates [lanes][parts][key, index]
     int32_t *tok, *pos, *start, *nonfinite;
+    // [lanes][128]: cos then sin of the RoPE angles at the lane's current
+    // position, written wherever the position is (seed and argmax kernels),
+    // so attention loads them without first waiting for the position.
+    float *rope_cur;
     void *vec_work;
     size_t vec_bytes;
     float *vec_split;  // partial sums of the K-split multi-vector GEMV
@@ -132,6 +136,9 @@ struct SeedArgs {
     int32_t pos[kMaxLanes];
     int lanes;
     int32_t *tok_dev, *pos_dev, *start_dev;
+    const float *rope;  // cos [positions][64], then sin at +sin_off
+    float *rope_cur;
+    int sin_off, positions;
 };
 
 __global__ void lm_seed_kernel(const SeedArgs a) {
@@ -140,6 +147,11 @@ __global__ void lm_seed_kernel(const SeedArgs a) {
         a.tok_dev[l] = a.tok[l];
         a.pos_dev[l] = a.pos[l];
         a.start_dev[l] = a.pos[l];
+    }
+    for (int i = threadIdx.x; i < a.lanes * 128; i += blockDim.x) {
+        const int l = i >> 7, t = i & 127, p = a.pos[l];
+        if (p < a.positions)
+            a.rope_cur[i] = t < 64 ? a.rope[(size_t)p * 64 + t] : a.rope[a.sin_off + (size_t)p * 64 + t - 64];
     }
 }
 
@@ -239,6 +251,7 @@ struct AttnArgs {
     float *vc[kMaxLanes];  // this layer's cache rows per lane, [capacity][kvd]
     const float *qn, *kn;  // this layer's head norms [128]
     const float *rope;     // cos [positions][64], then sin at +sin_off
+    const float *rope_cur;  // [lanes][128], the rows of rope at each lane's position
     const int32_t *pos;    // [lanes]
     float *ctx;            // [lanes][qd]
     float *part;           // [lanes][kvh][splits][GROUP][kPart]
@@ -276,7 +289,7 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     // arrived, the keys of the range the host expects are loaded.
     int chunk = a.chunk[lid];
     int j0 = sp * chunk;
-    const int pos = a.pos[lid];
+    int pos = a.pos[lid];
     const float *qkv = a.qkv + (size_t)lid * a.qkvw;
     float *kc = a.kc[lid] + g * kHeadDim;
     float *vc = a.vc[lid] + g * kHeadDim;
@@ -284,6 +297,7 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     const int rowgroup = wave * 4 + sub;  // 0..15
     const int d0 = li * 4, d1 = 64 + li * 4;
 
+    const float rc = a.rope_cur[lid * 128 + lane], rs = a.rope_cur[lid * 128 + 64 + lane];
     // Norm inputs: item GROUP is the new key, the others the query heads.
     float x0[NI], x1[NI], w0[NI], w1[NI];
     float nv0 = 0.0f, nv1 = 0.0f;
@@ -329,6 +343,10 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     };
 #pragma unroll
     for (int b = 0; b < NB; ++b) load_keys(b, kb[b], vb[b], okb[b]);
+    // The position is used only once every load above has been issued: the
+    // compiler otherwise moves its first use (and the wait for it) ahead of
+    // the norm and key loads, which then start one memory round trip late.
+    asm volatile("" : "+v"(pos));
     const int n = pos + 1;
     const int want = attn_chunk(n, a.splits);
     if (sp * want >= n) return;  // no keys of this lane's context
@@ -355,7 +373,6 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
                 vb[b][u][i] = okb[b][u] ? vb[b][u][i] : 0.0f;
             }
         }
-    const float rc = a.rope[(size_t)pos * 64 + lane], rs = a.rope[a.sin_off + (size_t)pos * 64 + lane];
 
     // Head RMSNorm and RoPE (gpu.metal:380-388 normRopeAt). Lane l holds the
     // rotary pair (l, l+64).
@@ -511,27 +528,27 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
 // The merge of attention's split partials (grid: q_heads, lanes; 128
 // threads, thread d owns dim d): weights 2^(m_s - max) per split, then
 // ctx = sum_s w_s A_s / sum_s w_s l_s, splits in order. Every load is issued
-// up front (thread d reads dim d of each used split, 64 threads read the
-// maxima and sums), so the kernel waits for memory once.
+// up front (thread d reads dim d of all kMaxSplits slots, thread t the
+// maximum and sum of slot t % kMaxSplits; the partial buffer holds
+// kMaxSplits slots per head, so these stay inside it), and the position
+// selects the splits in use afterwards, so the kernel waits for memory once.
 __global__ __launch_bounds__(128) void lm_attn_merge_kernel(const AttnArgs a, int group) {
     __shared__ float cw[kMaxSplits];
     __shared__ float linv;
     const int h = blockIdx.x, lid = blockIdx.y;
     const int g = h / group, hh = h - g * group;
-    const int pos = a.pos[lid];
+    int pos = a.pos[lid];
     const float *lp = a.part + (((size_t)lid * a.kvh + g) * a.splits * group + hh) * kPart;
     const size_t stride = (size_t)group * kPart;
     const int d = threadIdx.x;
-    // Every split's partial is loaded with the position; the splits in use
-    // are selected once it has arrived (the others hold stale values).
+    // Every slot is loaded with the position; the splits in use are
+    // selected once it has arrived (the other slots hold stale values).
     float v[kMaxSplits];
 #pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) v[s] = s < a.splits ? lp[(size_t)s * stride + 2 + d] : 0.0f;
-    float ms = -INFINITY, ls = 0.0f;
-    if (threadIdx.x < 64 && threadIdx.x < a.splits) {
-        ms = lp[threadIdx.x * stride];
-        ls = lp[threadIdx.x * stride + 1];
-    }
+    for (int s = 0; s < kMaxSplits; ++s) v[s] = lp[(size_t)s * stride + 2 + d];
+    const int ts = threadIdx.x & (kMaxSplits - 1);
+    float ms = lp[ts * stride], ls = lp[ts * stride + 1];
+    asm volatile("" : "+v"(pos));  // first use after the loads (see lm_attend_kernel)
     const int chunk = attn_chunk(pos + 1, a.splits);
     const int used = (pos + 1 + chunk - 1) / chunk;
 #pragma unroll
@@ -562,6 +579,9 @@ struct ArgmaxArgs {
     const int32_t *start;
     int32_t *next;  // optional [lanes]
     int32_t *run;   // optional [steps][lanes], indexed by pos - start
+    const float *rope;  // the RoPE table and the rows at the lanes' positions (SeedArgs)
+    float *rope_cur;
+    int sin_off, positions;
 };
 
 constexpr uint32_t kNone = 0xFFFFFFFFu;
@@ -640,6 +660,14 @@ __global__ __launch_bounds__(128) void lm_argmax_kernel(const ArgmaxArgs a, cons
     uint32_t bk = cand[((size_t)lane * kArgParts + threadIdx.x) * 2];
     uint32_t bi = cand[((size_t)lane * kArgParts + threadIdx.x) * 2 + 1];
     const uint32_t first = __builtin_bit_cast(uint32_t, a.logits[(size_t)lane * a.stride]) & 0x7FFFFFFFu;
+    // The RoPE row of the next position (read by every thread before thread
+    // 0 advances the position below, past block_best's barriers).
+    static_assert(kArgParts == 128, "one thread per RoPE value of the row");
+    const int32_t pn = a.pos[lane] + 1;
+    if (pn < a.positions) {
+        const int t = threadIdx.x;
+        a.rope_cur[lane * 128 + t] = t < 64 ? a.rope[(size_t)pn * 64 + t] : a.rope[a.sin_off + (size_t)pn * 64 + t - 64];
+    }
     block_best<2>(bk, bi, sk, si);
     if (threadIdx.x != 0) return;
     const int32_t token = (first > 0x7F800000u || bi == kNone) ? 0 : (int32_t)bi;
@@ -713,6 +741,7 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, const
     AttnArgs aa{};
     aa.qkv = ws->qkv;
     aa.rope = lm->rope;
+    aa.rope_cur = ws->rope_cur;
     aa.pos = ws->pos;
     aa.ctx = ws->ctx;
     aa.part = ws->part;
@@ -759,7 +788,8 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, const
     GPHQ_TRY(launch_status());
     GPHQ_TRY(gemv(ws, lanes, GPHQ_FMT_Q8B, PRO_PLAIN, EPI_STORE, lm->head, 0, lm->head_scale, ws->hn, H, ws->logits,
                   lm->head_rows, H, lm->head_rows, st));
-    ArgmaxArgs ga{ws->logits, (int)lm->head_rows, (int)c.vocab, lanes, ws->tok, ws->pos, ws->start, next_out, run_out};
+    ArgmaxArgs ga{ws->logits, (int)lm->head_rows, (int)c.vocab, lanes, ws->tok, ws->pos, ws->start, next_out, run_out,
+                  lm->rope, ws->rope_cur, (int)(lm->positions * 64), (int)lm->positions};
     hipLaunchKernelGGL(lm_argmax_part_kernel, dim3(kArgParts, lanes), dim3(256), 0, st, ga, ws->cand);
     GPHQ_TRY(launch_status());
     hipLaunchKernelGGL(lm_argmax_kernel, dim3(lanes), dim3(kArgParts), 0, st, ga, (const uint32_t *)ws->cand);
@@ -777,6 +807,10 @@ int seed(gphq_decode_batch *ws, int lanes, const int64_t *positions, const int32
     s.tok_dev = ws->tok;
     s.pos_dev = ws->pos;
     s.start_dev = ws->start;
+    s.rope = ws->lm->rope;
+    s.rope_cur = ws->rope_cur;
+    s.sin_off = (int)(ws->lm->positions * 64);
+    s.positions = (int)ws->lm->positions;
     hipLaunchKernelGGL(lm_seed_kernel, dim3(1), dim3(64), 0, st, s);
     return launch_status();
 }
@@ -1165,6 +1199,7 @@ int gphq_decode_batch_new(const gphq_lm *lm, int64_t capacity, gphq_decode_batch
         {(void **)&ws->tok, (size_t)capacity * 4},
         {(void **)&ws->pos, (size_t)capacity * 4},
         {(void **)&ws->start, (size_t)capacity * 4},
+        {(void **)&ws->rope_cur, (size_t)capacity * 128 * 4},
         {(void **)&ws->nonfinite, (size_t)capacity * 4},
         {(void **)&ws->vec_work, ws->vec_bytes},
         {(void **)&ws->vec_split, ws->vec_split_bytes},
