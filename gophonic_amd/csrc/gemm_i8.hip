@@ -750,6 +750,50 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
     }
 }
 
+// Epilogue of the direct-to-LDS kernels, as in i8gemm_kernel: lane l of a
+// 16 x 16 tile holds rows 4 (l / 16) + e, column l % 16; scales first, then
+// the stores. mt0 / nt0: the wavefront's first row and column tile.
+template <int TI, int TJ, int EPI>
+__device__ __forceinline__ void dma_epilogue(const I8GemmArgs &a, const i32x4 (&acc)[TI][TJ], int mt0, int nt0,
+                                             int lane) {
+    float rsc[TI][4], csc[TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rsc[i][e] = a.rowScale[min((mt0 + i) * 16 + 4 * (lane >> 4) + e, a.M - 1)];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
+    }
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        const bool colOk = col >= a.c0 && col < a.c1;
+        if constexpr (EPI != I8_EPI_SWIGLU) {
+            if (!colOk) continue;
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
+                const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], csc[j]), rsc[i][e]);
+                if constexpr (EPI == I8_EPI_STORE) {
+                    if (row < a.M) a.dst[(size_t)row * a.stride + col] = v;
+                } else if constexpr (EPI == I8_EPI_ADD) {
+                    if (row < a.M) __builtin_amdgcn_global_atomic_fadd_f32(a.dst + (size_t)row * a.stride + col, v);
+                } else {
+                    // Every lane runs the exchange (DPP quad_perm [1,0,3,2]: lane l ^ 1 holds column col ^ 1).
+                    const float u = __builtin_bit_cast(
+                        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+                    if (colOk && !(col & 1) && row < a.M)
+                        a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
+                }
+            }
+    }
+}
+
 // Direct-to-LDS variant: BM x BN block tiles (WGM x WGN wavefronts, each a
 // grid of 16 x 16 v_mfma_i32_16x16x64_i8 tiles), a ring of NS stages of one
 // 64-deep K-step, every operand fragment (the tile layout's 1 KiB group of
@@ -845,45 +889,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_dma_kernel(const I8Gemm
             for (int j = 0; j < TJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
-    // Epilogue as in i8gemm_kernel: lane l of a 16 x 16 tile holds rows
-    // 4 (l / 16) + e, column l % 16; scales first, then the stores.
-    const int mt0 = rt0 + wm * TI, nt0 = ct0 + wn * TJ;
-    float rsc[TI][4], csc[TJ];
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) rsc[i][e] = a.rowScale[min((mt0 + i) * 16 + 4 * (lane >> 4) + e, a.M - 1)];
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int col = (nt0 + j) * 16 + (lane & 15);
-        csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
-    }
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int col = (nt0 + j) * 16 + (lane & 15);
-        const bool colOk = col >= a.c0 && col < a.c1;
-        if constexpr (EPI != I8_EPI_SWIGLU) {
-            if (!colOk) continue;
-        }
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int row = (mt0 + i) * 16 + 4 * (lane >> 4) + e;
-                const float v = __fmul_rn(__fmul_rn((float)acc[i][j][e], csc[j]), rsc[i][e]);
-                if constexpr (EPI == I8_EPI_STORE) {
-                    if (row < a.M) a.dst[(size_t)row * a.stride + col] = v;
-                } else if constexpr (EPI == I8_EPI_ADD) {
-                    if (row < a.M) __builtin_amdgcn_global_atomic_fadd_f32(a.dst + (size_t)row * a.stride + col, v);
-                } else {
-                    // Every lane runs the exchange (DPP quad_perm [1,0,3,2]: lane l ^ 1 holds column col ^ 1).
-                    const float u = __builtin_bit_cast(
-                        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
-                    if (colOk && !(col & 1) && row < a.M)
-                        a.dst[(size_t)row * a.stride + (col >> 1)] = v / (1.0f + expf(-v)) * u;
-                }
-            }
-    }
+    dma_epilogue<TI, TJ, EPI>(a, acc, rt0 + wm * TI, ct0 + wn * TJ, lane);
 }
 
 template <int BM, int BN, int WGM, int WGN, int NS, bool BROWS = false, int EPI = I8_EPI_STORE>
@@ -892,6 +898,136 @@ static int launch_i8gemm_dma(I8GemmArgs a, hipStream_t stream) {
     a.gridN = (tiles * 16 + BN - 1) / BN;
     a.gridM = (a.M + BM - 1) / BM;
     hipLaunchKernelGGL((i8gemm_dma_kernel<BM, BN, WGM, WGN, NS, BROWS, EPI>), dim3((unsigned)(a.gridM * a.gridN)),
+                       dim3(64 * WGM * WGN), 0, stream, a);
+    return launch_status();
+}
+
+// vmcnt(PER * min(after, MAXA)) and lgkmcnt(0).
+template <int PER, int MAXA>
+__device__ __forceinline__ void wait_stages_n(int after) {
+    if constexpr (MAXA <= 0) {
+        wait_vm_lgkm0<0>();
+    } else {
+        if (after >= MAXA)
+            wait_vm_lgkm0<PER * MAXA>();
+        else
+            wait_stages_n<PER, MAXA - 1>(after);
+    }
+}
+
+// Ping-pong variant of i8gemm_dma_kernel (8 wavefronts, two per SIMD: a
+// probe of the hardware wave id on MI355X places wavefronts w and w + 4 of a
+// 512-thread block on one SIMD). The wavefronts of group 0 (0-3) and group 1
+// (4-7) run half a K step apart: while one group issues its MFMAs for a step
+// (at raised wave priority), the other requests the ring stage NS - 1 ahead,
+// reads its fragments of the step from LDS and waits for its share of the
+// next stage; a barrier ends each half. Group 1 starts one barrier late and
+// group 0 ends with one extra, so every wavefront passes the same number of
+// barriers (2 KT + 2). Ordering: a wavefront's share of stage s + 1 is
+// complete, and its reads of stage s returned, before the barrier that ends
+// its memory half of step s; so both groups' shares of a stage are in LDS
+// before the barrier after which group 0 reads it, and the slot that stage
+// s + NS - 1 overwrites (stage s - 1's) was last read before the barrier
+// preceding the memory half that requests it. Measured on MI355X against
+// i8gemm_dma_kernel: the 4096-row int8 pass 54.2-54.4 -> 53.4-53.7 ms (256 x
+// 256 tiles, NS = 5), config 2 at M = 512 43.6-44.0 -> 40.8-42.9 us (128 x
+// 192 tiles, NS = 6); NS = 4 for the pass gave no gain.
+template <int BM, int BN, int WGM, int WGN, int NS, bool BROWS, int EPI>
+__global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_pp_kernel(const I8GemmArgs a) {
+    constexpr int NW = WGM * WGN;
+    static_assert(NW == 8, "two groups of four wavefronts");
+    constexpr int FA = BM / 16, FB = BN / 16, F = FA + FB;
+    constexpr int DMAX = (F + NW - 1) / NW, DREM = F % NW;
+    constexpr int TI = BM / 16 / WGM, TJ = BN / 16 / WGN;
+    static_assert(TI * 16 * WGM == BM && TJ * 16 * WGN == BN, "wave grid");
+    static_assert(NS >= 3 && DMAX * (NS - 2) < 64, "ring depth");
+    __shared__ i32x4 ring[NS][F][64];
+    int bm, bn;
+    tile_order(blockIdx.x, a.gridM, a.gridN, bm, bn);
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = wv >> 2;
+    const int wm = wv / WGN, wn = wv % WGN;
+    const int rt0 = bm * FA, ct0 = a.tileN0 + bn * FB;
+    const int MT = (a.M + 15) >> 4, KT = a.KT;
+    const bool full = DREM == 0 || wv < DREM;
+    const int8_t *src[DMAX];
+    int dst[DMAX];
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d) {
+        const int f = min(wv + NW * d, F - 1);
+        dst[d] = f;
+        if (f < FA) {
+            src[d] = a.A + (size_t)min(rt0 + f, MT - 1) * KT * 1024 +
+                     (BROWS ? (size_t)(lane & 15) * 64 + (lane >> 4) * 16 : (size_t)lane * 16);
+        } else if constexpr (BROWS) {
+            src[d] = a.B + (size_t)min((ct0 + (f - FA)) * 16 + (lane & 15), a.N - 1) * a.K + (lane >> 4) * 16;
+        } else {
+            src[d] = a.B + (size_t)min(ct0 + (f - FA), a.NT - 1) * KT * 1024 + (size_t)lane * 16;
+        }
+    }
+    auto stage_load = [&](int s) {
+        const int slot = s % NS;
+#pragma unroll
+        for (int d = 0; d < DMAX; ++d)
+            if (d < DMAX - 1 || full)
+                lds_dma16(src[d] + (size_t)s * (BROWS && dst[d] >= FA ? 64 : 1024), &ring[slot][dst[d]][0]);
+    };
+    auto wait_stages = [&](int after) {
+        if (full)
+            wait_stages_n<DMAX, NS - 2>(after);
+        else
+            wait_stages_n<DMAX - 1, NS - 2>(after);
+    };
+    auto barrier = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        ring_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    i32x4 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p)
+        if (p < KT) stage_load(p);
+    wait_stages(min(KT - 1, NS - 2));
+    barrier();
+    if (grp == 1) barrier();
+    i32x4 fa[TI], fb[TJ];
+    for (int s = 0; s < KT; ++s) {
+        // Memory half: the stage NS - 1 ahead (its slot held stage s - 1, which
+        // every wavefront finished reading before the barrier that ended its
+        // previous memory half), this step's fragments, then a wait for this
+        // wavefront's share of stage s + 1 and for the fragment reads.
+        if (s + NS - 1 < KT) stage_load(s + NS - 1);
+        const int slot = s % NS;
+#pragma unroll
+        for (int i = 0; i < TI; ++i) fa[i] = ring[slot][wm * TI + i][lane];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) fb[j] = ring[slot][FA + wn * TJ + j][lane];
+        wait_stages(min(KT - 2 - s, NS - 2));
+        barrier();
+        // MFMA half.
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
+        barrier();
+    }
+    if (grp == 0) barrier();
+    dma_epilogue<TI, TJ, EPI>(a, acc, rt0 + wm * TI, ct0 + wn * TJ, lane);
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, bool BROWS = false, int EPI = I8_EPI_STORE>
+static int launch_i8gemm_pp(I8GemmArgs a, hipStream_t stream) {
+    const int tiles = (a.c1 + 15) / 16 - a.tileN0;
+    a.gridN = (tiles * 16 + BN - 1) / BN;
+    a.gridM = (a.M + BM - 1) / BM;
+    hipLaunchKernelGGL((i8gemm_pp_kernel<BM, BN, WGM, WGN, NS, BROWS, EPI>), dim3((unsigned)(a.gridM * a.gridN)),
                        dim3(64 * WGM * WGN), 0, stream, a);
     return launch_status();
 }
@@ -970,7 +1106,7 @@ int i8gemm_launch(const int8_t *A, const int8_t *B, const float *rowScale, const
         if (M <= 128) return launch_i8gemm_skinny<4, 2, 3, 4, 3>(a, stream);
     }
     if (M > 128 && M <= 256) return launch_i8gemm_dma<64, 192, 2, 4, 8>(a, stream);
-    if (M > 256 && M <= 512) return launch_i8gemm_dma<128, 192, 2, 4, 6>(a, stream);
+    if (M > 256 && M <= 512) return launch_i8gemm_pp<128, 192, 2, 4, 6>(a, stream);
     if (M <= 64) return launch_i8gemm<4, 1, 1, 2, 4, 4>(a, stream);
     if (M <= 128) return launch_i8gemm_lds<128, 64, 2, 2, 4>(a, stream);
     return launch_i8gemm_big<128, 192, 4, 2>(a, stream);
@@ -1044,10 +1180,11 @@ int lm_i8_mm(int epi, const int8_t *act, const float *a_scale, const int8_t *cod
     // 256 x 256 tiles on direct-to-LDS loads, the weights gathered from their
     // rows. Measured on MI355X at M = 4096 (Qwen3-8B's projections, store
     // epilogue) against the register-staged big-tile kernel on row-major
-    // operands: QKV 152 -> 141 us, gate/up 527 -> 479, down 207 -> 187.
-    if (epi == 0) return launch_i8gemm_dma<256, 256, 4, 2, 4, true, I8_EPI_STORE>(a, stream);
-    if (epi == 1) return launch_i8gemm_dma<256, 256, 4, 2, 4, true, I8_EPI_ADD>(a, stream);
-    return launch_i8gemm_dma<256, 256, 4, 2, 4, true, I8_EPI_SWIGLU>(a, stream);
+    // operands: QKV 152 -> 141 us, gate/up 527 -> 479, down 207 -> 187; the
+    // ping-pong schedule with a 5-stage ring then took the pass 1.5% lower.
+    if (epi == 0) return launch_i8gemm_pp<256, 256, 4, 2, 5, true, I8_EPI_STORE>(a, stream);
+    if (epi == 1) return launch_i8gemm_pp<256, 256, 4, 2, 5, true, I8_EPI_ADD>(a, stream);
+    return launch_i8gemm_pp<256, 256, 4, 2, 5, true, I8_EPI_SWIGLU>(a, stream);
 }
 
 int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int kt, hipStream_t stream) {
