@@ -753,6 +753,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
 // Epilogue of the direct-to-LDS kernels, as in i8gemm_kernel: lane l of a
 // 16 x 16 tile holds rows 4 (l / 16) + e, column l % 16; scales first, then
 // the stores. mt0 / nt0: the wavefront's first row and column tile.
+// Measured on MI355X (config 2, M = 512): stores of 16 columns per row wrote
+// 1.32x the output's bytes to HBM (WRITE_SIZE); whole 128-byte lines write
+// them once.
 template <int TI, int TJ, int EPI>
 __device__ __forceinline__ void dma_epilogue(const I8GemmArgs &a, const i32x4 (&acc)[TI][TJ], int mt0, int nt0,
                                              int lane) {
@@ -766,8 +769,43 @@ __device__ __forceinline__ void dma_epilogue(const I8GemmArgs &a, const i32x4 (&
         const int col = (nt0 + j) * 16 + (lane & 15);
         csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
     }
+    // Store and add epilogues take column tiles j and j + 1 in pairs:
+    // v_permlane16_swap exchanges lanes 16-31 of tile j's values with lanes
+    // 0-15 of tile j + 1's (and 48-63 with 32-47), so each store covers 32
+    // consecutive columns of two rows (two whole 128-byte lines) instead of 16
+    // columns of four rows. After the swap, lane l holds column (j + bit 4 of
+    // l) * 16 + l % 16; the first value is row 8 (l / 32) + e, the second row
+    // 4 more. An odd last tile is stored as it is.
+    constexpr int TJP = EPI == I8_EPI_SWIGLU ? 0 : TJ & ~1;
+    if constexpr (TJP > 0) {
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
+        for (int j = 0; j < TJP; j += 2) {
+            const int col = (nt0 + j + ((lane >> 4) & 1)) * 16 + (lane & 15);
+            const bool colOk = col >= a.c0 && col < a.c1;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v0 = __fmul_rn(__fmul_rn((float)acc[i][j][e], csc[j]), rsc[i][e]);
+                    const float v1 = __fmul_rn(__fmul_rn((float)acc[i][j + 1][e], csc[j + 1]), rsc[i][e]);
+                    const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v0),
+                                                                     __builtin_bit_cast(uint32_t, v1), false, false);
+                    const int row = (mt0 + i) * 16 + 8 * (lane >> 5) + e;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int r = row + 4 * h;
+                        const float v = __builtin_bit_cast(float, h ? sw[1] : sw[0]);
+                        if (!colOk || r >= a.M) continue;
+                        if constexpr (EPI == I8_EPI_STORE)
+                            a.dst[(size_t)r * a.stride + col] = v;
+                        else
+                            __builtin_amdgcn_global_atomic_fadd_f32(a.dst + (size_t)r * a.stride + col, v);
+                    }
+                }
+        }
+    }
+#pragma unroll
+    for (int j = TJP; j < TJ; ++j) {
         const int col = (nt0 + j) * 16 + (lane & 15);
         const bool colOk = col >= a.c0 && col < a.c1;
         if constexpr (EPI != I8_EPI_SWIGLU) {
