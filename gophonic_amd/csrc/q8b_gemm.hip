@@ -1,4 +1,4 @@
-// Block-32 int8 GEMM on MI355X: BASELINE configuration 2 as worded there
+// Block-32 int8 GEMM on MI355X: benchmark configuration 2 as worded there
 // (activations and weights each with one fp32 scale per 32-value block). The
 // reference has no such function: its q8gemm int8 path scales per row
 // (int8.go:106-211, gphq_q8gemm_*). Each 32-value block is quantized with

@@ -705,7 +705,7 @@ int gphq_prefill_arith(const gphq_prefill *ws);
 int gphq_prefill_project(gphq_prefill *ws, int64_t layer, int proj, const float *x_dev, int64_t rows, float *y_dev,
                          void *stream);
 
-/* ---- Block-32 int8 GEMM (BASELINE configuration 2 as worded there) -----------
+/* ---- Block-32 int8 GEMM (benchmark configuration 2 as worded there) -----------
  * No counterpart in the reference, whose q8gemm int8 path scales per row
  * (gphq_q8gemm_* above). Activations and weights carry one fp32 scale per
  * 32-value block; each block is quantized with WorkspaceI8's per-row rule

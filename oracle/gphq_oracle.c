@@ -234,7 +234,7 @@ float orc_q4_group_scale(const float *v, int64_t len) {
  * bound), not bit-exact targets.
  *
  * fmt: 8 = Q8 (int8 codes, fp32 scale per row), 9 = Q8B (int8 codes, f16 scale
- * per 32), 10 = Q8 with fp32 scale per 32 (the BASELINE config-1 variant),
+ * per 32), 10 = Q8 with fp32 scale per 32 (the benchmark config-1 variant),
  * 4 = Q4 (split nibbles, f16 scale per 32). */
 
 static float scale_of(int fmt, const void *scale, int64_t row, int64_t k, int64_t i) {
@@ -483,7 +483,7 @@ void orc_i8_mul_panels(float *dst, int64_t stride, const int8_t *act, const floa
     }
 }
 
-/* Block-32 int8 variant (BASELINE configuration 2's wording; the reference's
+/* Block-32 int8 variant (benchmark configuration 2's wording; the reference's
  * q8gemm int8 path scales per row): every 32-value block of a row takes the
  * per-row rule of WorkspaceI8 (int8.go:106-119: scale max/127, inverse 127/max,
  * both 0 unless 0 < max < inf) and quantize's codes (int8.go:163-168). q is

@@ -1,5 +1,5 @@
 """Workload-size parity of the decode provider and the batched pass, through
-the C ABI: BASELINE configurations 3, 4a and 4b at their real widths, context
+the C ABI: benchmark configurations 3, 4a and 4b at their real widths, context
 lengths and vocabulary.
 
 * One layer at Qwen3-8B widths with the real 151,936-row head, against the

@@ -111,7 +111,7 @@ def test_gptq_256_row_tiles_with_two_splits():
 @pytest.mark.parametrize("m,split", [(1, False), (256, False), (256, True)])
 @pytest.mark.parametrize("k,n", [(4096, 12288), (12288, 4096)])
 def test_gptq_g128_config5_within_2e3(m, split, k, n):
-    # BASELINE config 5 shapes. The north-star tolerance (2e-3 relative) is
+    # Benchmark config 5 shapes. The north-star tolerance (2e-3 relative) is
     # checked against float64 with un-rounded weights on a sample of columns;
     # the FP16-tile oracle bounds the same sample tightly.
     rng = np.random.default_rng(m + k)

@@ -62,7 +62,7 @@ def test_gemm_bit_exact(m, k, n):
 
 @pytest.mark.parametrize("m", [1, 16, 128, 512])
 def test_config2_shape_rows_bit_exact(m):
-    # BASELINE configuration 2 (K = 4096, N = 12288) at each bench M: sampled
+    # Benchmark configuration 2 (K = 4096, N = 12288) at each bench M: sampled
     # rows against the oracle (rows are independent).
     import torch
 

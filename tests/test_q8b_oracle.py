@@ -1,5 +1,5 @@
 """Pins the block-32 int8 oracle (oracle.q8b_quantize / q8b_gemm), the
-BASELINE configuration-2 variant with no counterpart in the reference:
+benchmark configuration-2 variant with no counterpart in the reference:
 
 * the quantizer equals the pinned per-row quantizer (WorkspaceI8,
   int8.go:106-168, pinned in test_oracle.py) applied to every 32-value block

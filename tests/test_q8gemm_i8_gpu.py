@@ -98,7 +98,7 @@ def test_mul_panels_i8_bit_exact(rows, k, n):
 
 @pytest.mark.parametrize("m", [1, 16, 32, 64, 100, 128, 192, 256, 320, 512])
 def test_config2_shapes_bit_exact(m):
-    # K = 4096, N = 12288; exact integer sums via a float64
+    # Benchmark config 2: K = 4096, N = 12288; exact integer sums via a float64
     # product of the integer codes (every partial sum is an integer < 2^53, so
     # float64 accumulation is exact in any order).
     import torch
