@@ -534,8 +534,8 @@ def test_attention_ranges_follow_the_context_not_the_capacity():
     # alone. A prefix with twice the rows it needs (the reference's callers
     # double capacity, qwen3/chat.go:760-769) decodes the same bits as one
     # sized to the need, step by step, eagerly, or replayed from one captured
-    # step; here the run crosses a change of range (2048 keys over 32 splits
-    # take 64 keys each, 2049 take 80), so a replayed step first loads the
+    # step; here the run crosses a change of range (2560 keys over 32 splits
+    # take 80 keys each, 2561 take 96), so a replayed step first loads the
     # range the capture expected and then its own. The first step matches the
     # float64 oracle over the same cache rows.
     import torch
@@ -545,7 +545,7 @@ def test_attention_ranges_follow_the_context_not_the_capacity():
     oracle = lc.oracle_for(model)
     lm = device_model(model)
     rng = np.random.default_rng(8)
-    ctx, steps = 2040, 16
+    ctx, steps = 2552, 16
     src = gphq.Prefix(lm, ctx + steps + 1)
     pf = gphq.Prefill(lm, 512)
     pf.extend(src, 0, list(rng.integers(0, g.vocab, ctx)), torch.empty(g.hidden, device="cuda"))
