@@ -72,11 +72,14 @@ __device__ __forceinline__ int rot_pad(int i) {
     return (i & ~15) + ((((i >> 2) + (i >> 6)) & 3) << 2) + (i & 3) + ((i >> 8) << 4);
 }
 
-template <int R, bool PAD = false>
+// NT: the block's thread count when the caller knows it (blockDim.x is read
+// from the dispatch packet, a memory round trip, at every use); 0 for any.
+template <int R, bool PAD = false, int NT = 0>
 __device__ __forceinline__ void fwht_round(float *v, int n, int s) {
     constexpr int r = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : 1;
     const int h = 1 << s;
-    for (int idx = threadIdx.x; idx < (n >> r); idx += blockDim.x) {
+    const int nt = NT ? NT : (int)blockDim.x;
+    for (int idx = threadIdx.x; idx < (n >> r); idx += nt) {
         const int base = ((idx >> s) << (s + r)) | (idx & (h - 1));
         float a[R];
 #pragma unroll
@@ -112,63 +115,110 @@ __device__ inline void lds_fwht(float *v, int n, int block) {
 }
 
 // A row held in registers by a one-block-per-row kernel of 256 threads
-// (thread t owns chunks of 16 values at 16 * (t + 256 c), c < CPT; values
-// past K are zero and stay so) is rotated in place: x * signs (the scale
+// (thread t owns chunks of 16 values at 16 * (t + 256 c), c < CPT; chunks
+// past K are left as they are) is rotated in place: x * signs (the scale
 // folded into signs), then lds_fwht over the row in blocks of `block`, in
-// rot_lds_bytes(K) of dynamic LDS (the row padded by rot_pad).
+// rot_lds_bytes(K) of dynamic LDS (a segment padded by rot_pad).
 //
-// The network's first stages (h = 1 .. 8, up to the block) pair values of one
-// thread's 16-value chunk, so they run in registers before the row goes to
-// LDS; the rest run as radix-16 rounds (then 8, 4, 2) from stage h = 16,
-// whose 16 consecutive items read consecutive words. Same butterflies in the
-// same stage order as lds_fwht, so the same bits.
-inline size_t rot_lds_bytes(int K) { return (size_t)(K + (K >> 8) * 16 + 16) * sizeof(float); }
+// Chunk c of every thread is segment c of the row, values 4096c .. 4096c +
+// 4095, and a block (a power of two up to 4096 dividing K) never straddles
+// two segments, so the segments are rotated one after another through the
+// same LDS: 16.6 KB however long the row (a 12288-value row took 49.9 KB,
+// which left room for three rows per CU). The network's first stages (h = 1
+// .. 8, up to the block) pair values of one thread's 16-value chunk, so they
+// run in registers before the segment goes to LDS; the rest run as radix-16
+// rounds (then 8, 4, 2) from stage h = 16, whose 16 consecutive items read
+// consecutive words. Same butterflies in the same stage order as lds_fwht, so
+// the same bits.
+inline size_t rot_lds_bytes(int K) {
+    const int n = K < 4096 ? K : 4096;
+    return (size_t)(n + (n >> 8) * 16 + 16) * sizeof(float);
+}
+
+// The signs of a thread's chunk at k (clamped into the row), for
+// rotate_row_lds: the caller loads segment 0's before the row itself, so the
+// first segment waits only for its own loads.
+__device__ __forceinline__ void rot_signs(float4 (&sg)[4], const float *__restrict__ signs, int k, int K) {
+    const int kk = k < K - 16 ? k : K - 16;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sg[q] = *(const float4 *)(signs + kk + 4 * q);
+}
 
 template <int CPT>
-__device__ __forceinline__ void rotate_row_lds(float4 (&v)[CPT][4], int K, const float *__restrict__ signs, int block) {
+__device__ __forceinline__ void rotate_row_lds(float4 (&v)[CPT][4], float4 (&sg)[4], int K,
+                                               const float *__restrict__ signs, int block) {
     extern __shared__ float rot_lds[];
     const int lb = __builtin_ctz((unsigned)block);
+    const int kl = 16 * (int)threadIdx.x;  // the thread's chunk within a segment
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-        const int k = 16 * ((int)threadIdx.x + 256 * c);
-        if (k >= K) continue;
+        const int seg = 4096 * c;
+        if (c > 0 && seg >= K) break;  // (K >= 16: segment 0 always exists)
+        const int n = K - seg < 4096 ? K - seg : 4096;
+        const int k = seg + kl;
+        if (c > 0) __syncthreads();  // the previous segment has been read back
         float a[16];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float4 s = *(const float4 *)(signs + k + 4 * q);
-            a[4 * q] = v[c][q].x * s.x;
-            a[4 * q + 1] = v[c][q].y * s.y;
-            a[4 * q + 2] = v[c][q].z * s.z;
-            a[4 * q + 3] = v[c][q].w * s.w;
+            a[4 * q] = v[c][q].x * sg[q].x;
+            a[4 * q + 1] = v[c][q].y * sg[q].y;
+            a[4 * q + 2] = v[c][q].z * sg[q].z;
+            a[4 * q + 3] = v[c][q].w * sg[q].w;
         }
+        if (c + 1 < CPT && seg + 4096 < K) rot_signs(sg, signs, k + 4096, K);  // the next segment's
+        if (k < K) {
 #pragma unroll
-        for (int m = 1; m < 16; m <<= 1) {
-            if (m >= block) break;
+            for (int m = 1; m < 16; m <<= 1) {
+                if (m >= block) break;
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
-                if (!(j & m)) {
-                    const float x = a[j], y = a[j + m];
-                    a[j] = x + y;
-                    a[j + m] = x - y;
-                }
+                for (int j = 0; j < 16; ++j)
+                    if (!(j & m)) {
+                        const float x = a[j], y = a[j + m];
+                        a[j] = x + y;
+                        a[j + m] = x - y;
+                    }
+            }
+            // Each quad of 4 values stays contiguous under rot_pad.
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *(float4 *)(rot_lds + rot_pad(kl + 4 * q)) = float4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
         }
-        // Each quad of 4 values stays contiguous under rot_pad.
+        __syncthreads();
+        int s = 4;
+        for (; s + 4 <= lb; s += 4) fwht_round<16, true, 256>(rot_lds, n, s);
+        if (lb - s == 3) fwht_round<8, true, 256>(rot_lds, n, s);
+        if (lb - s == 2) fwht_round<4, true, 256>(rot_lds, n, s);
+        if (lb - s == 1) fwht_round<2, true, 256>(rot_lds, n, s);
+        if (k < K) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            *(float4 *)(rot_lds + rot_pad(k + 4 * q)) = float4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+            for (int q = 0; q < 4; ++q) v[c][q] = *(const float4 *)(rot_lds + rot_pad(kl + 4 * q));
+        }
     }
-    __syncthreads();
-    int s = 4;
-    for (; s + 4 <= lb; s += 4) fwht_round<16, true>(rot_lds, K, s);
-    if (lb - s == 3) fwht_round<8, true>(rot_lds, K, s);
-    if (lb - s == 2) fwht_round<4, true>(rot_lds, K, s);
-    if (lb - s == 1) fwht_round<2, true>(rot_lds, K, s);
+}
+
+// Chunk c of a 256-thread row kernel: 16 values at k = 16 * (t + 256 c)
+// (K % 16 == 0). The load is issued on every path (the address clamped into
+// the row), so the compiler's waits count only the loads issued before the
+// ones a use needs; chunks past K hold a copy of the last chunk until
+// zero_past_end, which the kernel calls where it first needs the values.
+template <int CPT>
+__device__ __forceinline__ void load_row_chunks(float4 (&v)[CPT][4], const float *__restrict__ xr, int K) {
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
         const int k = 16 * ((int)threadIdx.x + 256 * c);
-        if (k >= K) continue;
+        const int kk = k < K - 16 ? k : K - 16;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = *(const float4 *)(rot_lds + rot_pad(k + 4 * q));
+        for (int q = 0; q < 4; ++q) v[c][q] = *(const float4 *)(xr + kk + 4 * q);
+    }
+}
+
+template <int CPT>
+__device__ __forceinline__ void zero_past_end(float4 (&v)[CPT][4], int K) {
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        if (16 * ((int)threadIdx.x + 256 * c) < K) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = float4{0.f, 0.f, 0.f, 0.f};
     }
 }
 

@@ -880,13 +880,14 @@ __global__ __launch_bounds__(256) void act_pack_rows_kernel(const float *__restr
     const int chunks = kt * 4;
     float4 v[CPT][4];
     float ss = 0.0f, mx = 0.0f;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-        const int k = 16 * ((int)threadIdx.x + 256 * c);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = k < K ? *(const float4 *)(xr + k + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
+    float4 sg[4];
+    if constexpr (ROT) {
+        rot_signs(sg, signs, 16 * (int)threadIdx.x, K);
+        __builtin_amdgcn_sched_barrier(0);  // the signs are requested first
     }
-    if constexpr (ROT) rotate_row_lds<CPT>(v, K, signs, block);
+    load_row_chunks<CPT>(v, xr, K);
+    if constexpr (ROT) rotate_row_lds<CPT>(v, sg, K, signs, block);
+    zero_past_end<CPT>(v, K);
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
 #pragma unroll
@@ -932,7 +933,7 @@ template <int MODE, bool ROT = false>
 static int launch_act_pack_rows(const float *x, long stride, int rows, int K, float eps, _Float16 *act,
                                 float *rowInv, hipStream_t stream, const float *signs = nullptr, int block = 0) {
     const int kt = (K + 63) / 64, chunks = kt * 4;
-    // A rotated row takes rot_lds_bytes(K) of dynamic LDS (69.7 KB at K = 16384).
+    // A rotated row takes rot_lds_bytes(K) of dynamic LDS (one 4096-value segment at a time, 16.6 KB).
     const size_t lds = ROT ? rot_lds_bytes(K) : 0;
 #define GPHQ_ACTPACK(CPT)                                                                                              \
     do {                                                                                                               \

@@ -184,13 +184,14 @@ __global__ __launch_bounds__(256) void i8_act_rows_kernel(const float *__restric
     float4 v[CPT][4];
     float ss = 0.0f, mx = 0.0f;
     int nan = 0;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-        const int k = 16 * ((int)threadIdx.x + 256 * c);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = k < K ? *(const float4 *)(xr + k + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
+    float4 sg[4];
+    if constexpr (ROT) {
+        rot_signs(sg, signs, 16 * (int)threadIdx.x, K);
+        __builtin_amdgcn_sched_barrier(0);  // the signs are requested first
     }
-    if constexpr (ROT) rotate_row_lds<CPT>(v, K, signs, block);
+    load_row_chunks<CPT>(v, xr, K);
+    if constexpr (ROT) rotate_row_lds<CPT>(v, sg, K, signs, block);
+    zero_past_end<CPT>(v, K);
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
 #pragma unroll
