@@ -47,13 +47,17 @@ __device__ __forceinline__ _Float16 i8h(uint32_t v, int i) { return (_Float16)(i
 struct RawB {
     u32x4 w;
     uint32_t sz;
+    bool ok;  // the fragment lies inside K (else it dequantizes to zeros)
 };
 
+// A fragment past K is loaded from the row's last 16 values instead and
+// zeroed by dequant, so the load is issued on every path and the compiler's
+// waits for a register set count only the loads issued before it.
 template <int WF>
 __device__ __forceinline__ RawB load_raw(const F16GemmArgs &a, int n, int kt, int g) {
-    const int k = kt * 64 + g * 16;
-    RawB r{u32x4{0, 0, 0, 0}, 0};
-    if (k >= a.K) return r;
+    const int k0 = kt * 64 + g * 16;
+    RawB r{u32x4{0, 0, 0, 0}, 0, k0 < a.K};
+    const int k = r.ok ? k0 : a.K - 16;
     if constexpr (WF == W_Q8_ROW || WF == W_Q8B_ROW || WF == W_Q8BF_ROW) {
         r.w = *(const u32x4 *)((const int8_t *)a.B + (size_t)n * a.K + k);
         if constexpr (WF == W_Q8B_ROW) r.sz = ((const uint16_t *)a.bScale)[(size_t)n * (a.K >> 5) + (k >> 5)];
@@ -151,6 +155,10 @@ __device__ __forceinline__ void dequant(const RawB &r, int g, f16x8 &lo, f16x8 &
         }
         lo = cat4(p[0], p[1], p[2], p[3]);
         hi = cat4(p[4], p[5], p[6], p[7]);
+    }
+    if (!r.ok) {
+        lo = f16x8{};
+        hi = f16x8{};
     }
 }
 
@@ -697,9 +705,10 @@ static int launch_by_m(F16GemmArgs a, hipStream_t stream) {
     if (a.M <= 64) return launch_f16gemm<WF, EPI, 4, 2, 1, 2, 4, 2>(a, stream);
     if constexpr (WF != W_I8_TILE && WF != W_F16_TILE) {
         const long width = a.c1 - a.tileN0 * 16;
-        // 256 x 256 block tiles when they fill the chip.
+        // 256 x 256 block tiles when they fill the chip, loads two K steps
+        // ahead (4096-row pass 78.0 -> 77.5 ms against one step; no spills).
         const long big = (long)((a.M + 255) / 256) * ((width + 255) / 256);
-        if (a.M >= 512 && big >= 256) return launch_f16gemm_big<WF, EPI, 256, 256, 4, 2, 1>(a, stream);
+        if (a.M >= 512 && big >= 256) return launch_f16gemm_big<WF, EPI, 256, 256, 4, 2, 2>(a, stream);
         // 128 x 128 tiles, with K split over extra blocks when the caller gave
         // scratch for the partial sums (store epilogues only).
         const long mid = (long)((a.M + 127) / 128) * ((width + 127) / 128);

@@ -460,19 +460,26 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_kernel(const FlashAr
 
 // lm_flash_kernel for a pass whose every key tile has an FP16 copy (no shared
 // prefix, copies from cache tile 0: a first pass, or any packed pass), with
-// the same arithmetic and results except the softmax sums: each lane keeps
-// the sum over its own 16 keys of a tile, and the lane pair (l, l ^ 32), which
-// shares every reference maximum, adds its two sums once at the end instead
-// of exchanging them per tile.
+// the same per-tile arithmetic, taking two 32-key tiles per step: one
+// barrier and one softmax update (one maximum exchange, one rescale) per 64
+// keys, and two independent score MFMA chains. The results equal
+// lm_flash_kernel's up to the rounding of the softmax sums and of the
+// reference maximum's moves, which now happen per 64 keys: each lane keeps
+// the sum over its own keys, and the lane pair (l, l ^ 32), which shares
+// every reference maximum, adds its two sums once at the end instead of
+// exchanging them per tile. A pair's second tile past the block's last is a
+// copy of the last tile, masked out.
 //
-// What differs is the load schedule. Every iteration loads exactly one tile
-// (the index clamped to the last tile, so the loop's last iterations reload
-// it), so the number of loads in flight is the same on every path and the
-// compiler's wait before each LDS store covers only that tile's loads; in the
-// general kernel, whose loads depend on the tile's source, the wait covered
-// the next tile's loads too (measured on MI355X at 4096 rows: 325 -> 260 us
-// per layer). The tiles pass through two LDS buffers: tile t is computed from
-// buffer t & 1 while tile t + 1 is stored into the other, one barrier per tile.
+// What differs most is the load schedule. Every step loads exactly one pair
+// (the index clamped to the last tile, so the last steps reload it), so the
+// number of loads in flight is the same on every path and the compiler's wait
+// before each LDS store covers only that pair's loads; in the general kernel,
+// whose loads depend on the tile's source, the wait covered the next tile's
+// loads too. Measured on MI355X at 4096 rows, per layer: 325 us before, 260
+// with the one-tile version of this schedule, 174 with the longest-first
+// block order (flash_block), 169 with two tiles per step. The pairs pass
+// through two LDS buffers: pair u is computed from buffer u & 1 while pair
+// u + 1 is stored into the other, one barrier per step.
 template <int GROUP, int RH>
 __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_half_kernel(const FlashArgs a) {
     constexpr int NT = 64 * RH * GROUP;
@@ -480,11 +487,11 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_half_kernel(const Fl
     constexpr int KB = 32;
     constexpr int KS = kHeadDim + 8;
     constexpr int VS = KB + 8;
-    constexpr int PF = 2;  // tiles in flight in registers (3 and 4 measured the same)
+    constexpr int PF = 2;
     constexpr int HITEMS = (32 * kHeadDim / 8 + NT - 1) / NT;
-    constexpr bool EVEN = (32 * kHeadDim / 8) % NT == 0;  // every thread loads every item
-    __shared__ _Float16 Ks2[2][KB * KS];
-    __shared__ _Float16 Vt2[2][kHeadDim * VS];
+    constexpr bool EVEN = (32 * kHeadDim / 8) % NT == 0;
+    __shared__ _Float16 Ks2[2][2 * KB * KS];
+    __shared__ _Float16 Vt2[2][2][kHeadDim * VS];
     const int nmb = (a.rows + RB - 1) / RB;
     int mb, g;
     flash_block(nmb, mb, g);
@@ -496,6 +503,7 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_half_kernel(const Fl
     const int off = packed ? 0 : a.base;
     const int tb0 = (packed ? a.rowstart[m0] : 0) / KB;
     const int tiles = (off + min(m0 + RB - 1, a.rows - 1)) / KB + 1 - tb0;
+    const int pairs = (tiles + 1) / 2;
     const int myLast = off + mw + q;
     const int myFirst = packed ? a.rowstart[min(mw + q, a.rows - 1)] : 0;
     const int waveLast = off + mw + 31;
@@ -517,99 +525,111 @@ __global__ __launch_bounds__(64 * RH * GROUP) void lm_flash_half_kernel(const Fl
         }
     }
     typedef int i32x4v __attribute__((ext_vector_type(4)));
-    i32x4v hk[PF][HITEMS], hv[PF][HITEMS];
-    auto load_half = [&](int t, auto set_c) __attribute__((always_inline)) {
+    i32x4v hk[PF][2][HITEMS], hv[PF][2][HITEMS];
+    auto load_pair = [&](int u, auto set_c) __attribute__((always_inline)) {
         constexpr int S = decltype(set_c)::value;
-        const _Float16 *hs = kvh + (size_t)min(t, tiles - 1) * tstride;
 #pragma unroll
-        for (int i = 0; i < HITEMS; ++i) {
-            const int idx = tid + i * NT;
-            if (EVEN || idx < 32 * kHeadDim / 8) {
-                hk[S][i] = *(const i32x4v *)(hs + 8 * idx);
-                hv[S][i] = *(const i32x4v *)(hs + 32 * kHeadDim + 8 * idx);
+        for (int h = 0; h < 2; ++h) {
+            const _Float16 *hs = kvh + (size_t)min(2 * u + h, tiles - 1) * tstride;
+#pragma unroll
+            for (int i = 0; i < HITEMS; ++i) {
+                const int idx = tid + i * NT;
+                if (EVEN || idx < 32 * kHeadDim / 8) {
+                    hk[S][h][i] = *(const i32x4v *)(hs + 8 * idx);
+                    hv[S][h][i] = *(const i32x4v *)(hs + 32 * kHeadDim + 8 * idx);
+                }
             }
         }
     };
-    auto store_tile = [&](auto set_c, int buf) __attribute__((always_inline)) {
+    auto store_pair = [&](auto set_c, int buf) __attribute__((always_inline)) {
         constexpr int S = decltype(set_c)::value;
 #pragma unroll
-        for (int i = 0; i < HITEMS; ++i) {
-            const int idx = tid + i * NT;
-            if (EVEN || idx < 32 * kHeadDim / 8) {
-                *(i32x4v *)(Ks2[buf] + (idx >> 4) * KS + 8 * (idx & 15)) = hk[S][i];
-                *(i32x4v *)(Vt2[buf] + (idx >> 2) * VS + 8 * (idx & 3)) = hv[S][i];
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < HITEMS; ++i) {
+                const int idx = tid + i * NT;
+                if (EVEN || idx < 32 * kHeadDim / 8) {
+                    *(i32x4v *)(Ks2[buf] + (32 * h + (idx >> 4)) * KS + 8 * (idx & 15)) = hk[S][h][i];
+                    *(i32x4v *)(Vt2[buf][h] + (idx >> 2) * VS + 8 * (idx & 3)) = hv[S][h][i];
+                }
             }
-        }
     };
 
     f32x16 o[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = f32x16{};
     float mrun = -INFINITY, lrun = 0.0f;
-    auto compute = [&](int t, int buf) __attribute__((always_inline)) {
-        const int jb = (tb0 + t) * KB;
-        const _Float16 *Ks = Ks2[buf], *Vt = Vt2[buf];
-        // Every key of the tile is outside this wave's rows' ranges.
-        if (jb > waveLast || jb + KB - 1 < waveFirst) return;
-        f32x16 s = f32x16{};
+    auto compute = [&](int u, int buf) __attribute__((always_inline)) {
+        const int jb = (tb0 + 2 * u) * KB;  // first key of the pair
+        // Every key of the pair is outside this wave's rows' ranges.
+        if (jb > waveLast || jb + 2 * KB - 1 < waveFirst) return;
+        f32x16 s[2];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const half8 kf = *(const half8 *)(Ks + q * KS + 16 * c + 8 * hi);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], s, 0, 0, 0);
-        }
-        if (jb + KB - 1 > off + mw || jb < waveFirstMax) {
+        for (int h = 0; h < 2; ++h) {
+            s[h] = f32x16{};
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = jb + 8 * (r >> 2) + 4 * hi + (r & 3);
-                if (key > myLast || key < myFirst) s[r] = -INFINITY;
+            for (int c = 0; c < 8; ++c) {
+                const half8 kf = *(const half8 *)(Ks2[buf] + (32 * h + q) * KS + 16 * c + 8 * hi);
+                s[h] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], s[h], 0, 0, 0);
             }
         }
-        float mx = s[0];
+        // The pair's second tile past the block's last is a copy of the last.
+        const int kend = (tb0 + tiles) * KB;
+        if (jb + 2 * KB - 1 > off + mw || jb < waveFirstMax || jb + 2 * KB > kend) {
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = jb + 32 * h + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    if (key > myLast || key < myFirst || key >= kend) s[h][r] = -INFINITY;
+                }
+        }
+        float mx = s[0][0];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[h][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const bool grew = mx > mrun + 8.0f;
         const float mnew = grew ? mx : mrun;
         const float msafe = mnew == -INFINITY ? 0.0f : mnew;
         const float corr = __builtin_amdgcn_exp2f(mrun - msafe);
         mrun = mnew;
-        float p[16], rs = 0.0f;
+        float rs = 0.0f;
+        half8 p[2][2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            p[r] = __builtin_amdgcn_exp2f(s[r] - msafe);
-            rs += p[r];
-        }
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = __builtin_amdgcn_exp2f(s[h][r] - msafe);
+                rs += e;
+                p[h][r >> 3][r & 7] = (_Float16)e;
+            }
         lrun = lrun * corr + rs;
-        half8 p0, p1;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            p0[i] = (_Float16)p[i];
-            p1[i] = (_Float16)p[8 + i];
-        }
         if (__any(grew)) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) o[c] *= corr;
         }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const _Float16 *vrow = Vt + (32 * c + q) * VS + 8 * hi;
-            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)vrow, p0, o[c], 0, 0, 0);
-            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)(vrow + 16), p1, o[c], 0, 0, 0);
-        }
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const _Float16 *vrow = Vt2[buf][h] + (32 * c + q) * VS + 8 * hi;
+                o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)vrow, p[h][0], o[c], 0, 0, 0);
+                o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const half8 *)(vrow + 16), p[h][1], o[c], 0, 0, 0);
+            }
     };
-    // Tile x sits in register set x % PF; iteration t computes tile t,
-    // stores tile t + 1 and loads tile t + 1 + PF into the set just stored.
-    static_for<PF>([&](auto set_c) { load_half(decltype(set_c)::value, set_c); });
-    store_tile(std::integral_constant<int, 0>{}, 0);
-    load_half(PF, std::integral_constant<int, 0>{});
+    static_for<PF>([&](auto set_c) { load_pair(decltype(set_c)::value, set_c); });
+    store_pair(std::integral_constant<int, 0>{}, 0);
+    load_pair(PF, std::integral_constant<int, 0>{});
     __syncthreads();
-    for (int t0 = 0; t0 < tiles; t0 += PF)
+    for (int u0 = 0; u0 < pairs; u0 += PF)
         static_for<PF>([&](auto set_c) {
             constexpr int SN = (decltype(set_c)::value + 1) % PF;
-            const int t = t0 + decltype(set_c)::value;
-            if (t < tiles) compute(t, t & 1);
-            store_tile(std::integral_constant<int, SN>{}, (t + 1) & 1);
-            load_half(t + 1 + PF, std::integral_constant<int, SN>{});
+            const int u = u0 + decltype(set_c)::value;
+            if (u < pairs) compute(u, u & 1);
+            store_pair(std::integral_constant<int, SN>{}, (u + 1) & 1);
+            load_pair(u + 1 + PF, std::integral_constant<int, SN>{});
             __syncthreads();
         });
     lrun += __shfl_xor(lrun, 32);
