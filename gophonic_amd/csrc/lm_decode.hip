@@ -459,10 +459,13 @@ __global__ __launch_bounds__(256) void lm_attend_kernel(const AttnArgs a) {
     for (int it0 = 0; it0 < iters; it0 += NB) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            if (it0 + b < iters) {
-                step(kb[b], vb[b], okb[b]);
-                if (it0 + b + NB < iters) load_keys(it0 + b + NB, kb[b], vb[b], okb[b]);
-            }
+            if (it0 + b < iters) step(kb[b], vb[b], okb[b]);
+            // Every slot refills, past the block's keys too (rows past jc read
+            // row 0 and are masked): with the same loads in flight on every
+            // path the compiler waits only for the slot it consumes, where a
+            // conditional refill made it wait for all of them (Qwen3-8B step
+            // 2.369 -> 2.357 ms).
+            load_keys(it0 + b + NB, kb[b], vb[b], okb[b]);
         }
     }
     if (owner) {  // the new key, on row group 0
