@@ -419,6 +419,96 @@ __global__ __launch_bounds__(64) void q8b_small_kernel(const Q8bArgs a) {
     }
 }
 
+// M = 1, K = 1024 KS: one wavefront per RG weight rows, streamed as whole
+// rows (lane l takes bytes 16 l..+16 of each 1 KiB segment, so a load
+// instruction covers 1 KiB of one row), RB rows of loads per batch and up to
+// 128 VGPRs of them in flight (at K = 4096 all four rows at once). A row's
+// block products are two lanes' sdot4 chains (exact int32) added by a lane
+// swap; float(dot_b) and the scale product da[b] * dw[r][b] go to LDS, formed
+// by the lanes that hold them, and once the RG rows are in, lane r runs
+// output r's chain in block order, acc = fmaf(float(dot_b), da[b] * dw[r][b],
+// acc): the same arithmetic as the tiled kernels, so the same bits. Measured
+// on MI355X at config 2's shape (K = 4096, N = 12288, 56.6 MB a launch):
+// 12.9-13.0 us with 4 rows per wavefront (3072 wavefronts), 13.2 with 8,
+// 14.1 with 16, 13.4 with 2, against 19.3-19.8 us for q8b_small_kernel, whose
+// wavefronts read 128 bytes of 16 rows per step.
+template <int KS, int RG>
+__global__ __launch_bounds__(64) void q8b_gemv_kernel(const Q8bArgs a) {
+    constexpr int KB = 32 * KS;                                  // blocks per row
+    constexpr int RB0 = KS >= 16 ? 1 : 16 / KS;
+    constexpr int RB = RB0 < RG ? RB0 : RG;                      // rows per batch (RB * KS 16-byte loads)
+    constexpr int NB = RG / RB;                                  // batches
+    constexpr int NBUF0 = 32 / (RB * KS) > 0 ? 32 / (RB * KS) : 1;  // at most 128 VGPRs of codes in flight
+    constexpr int NBUF = NB < NBUF0 ? NB : NBUF0;                // batches in flight
+    static_assert(NB * RB == RG, "whole batches");
+    constexpr int SPL = KB / 64;            // scale floats per lane and row
+    static_assert(KS % 2 == 0 && KS <= 16, "whole 64-lane scale rows");
+    __shared__ float dots[RG][KB + 1];      // float(dot); +1: lane r's chain reads stride KB + 1 words
+    __shared__ float sw[RG][KB + 1];
+    const int lane = threadIdx.x;
+    const int n0 = blockIdx.x * RG;
+    // The activation row: lane l's bytes of each segment, then its scales.
+    i32x4 xa[KS];
+#pragma unroll
+    for (int j = 0; j < KS; ++j) xa[j] = *(const i32x4 *)(a.qa + 1024 * j + 16 * lane);
+    i32x4 wr[NBUF][RB][KS];
+    float sr[NBUF][RB][SPL];
+    auto load = [&](int buf, int bt) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int row = min(n0 + bt * RB + r, a.n - 1);
+            const int8_t *wp = a.qw + (size_t)row * a.k + 16 * lane;
+#pragma unroll
+            for (int j = 0; j < KS; ++j) wr[buf][r][j] = __builtin_nontemporal_load((const i32x4 *)(wp + 1024 * j));
+            const float *sp = a.dw + (size_t)row * KB + SPL * lane;
+#pragma unroll
+            for (int i = 0; i < SPL; ++i) sr[buf][r][i] = sp[i];
+        }
+    };
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) load(b, b);
+    float dar[SPL];  // the activation's block scales of this lane's scale slots
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) dar[i] = a.da[SPL * lane + i];
+#pragma unroll
+    for (int bt = 0; bt < NB; ++bt) {
+        const int buf = bt % NBUF;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int rr = bt * RB + r;
+#pragma unroll
+            for (int j = 0; j < KS; ++j) {
+                int d = __builtin_amdgcn_sdot4(wr[buf][r][j][0], xa[j][0], 0, false);
+                d = __builtin_amdgcn_sdot4(wr[buf][r][j][1], xa[j][1], d, false);
+                d = __builtin_amdgcn_sdot4(wr[buf][r][j][2], xa[j][2], d, false);
+                d = __builtin_amdgcn_sdot4(wr[buf][r][j][3], xa[j][3], d, false);
+                // Lanes 2t and 2t + 1 hold the halves of block 32 j + t.
+                d += __builtin_amdgcn_mov_dpp(d, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
+                if (!(lane & 1)) dots[rr][32 * j + (lane >> 1)] = (float)d;
+            }
+            // The chain's scale products da[b] * dw[r][b], formed here in parallel.
+#pragma unroll
+            for (int i = 0; i < SPL; ++i) sw[rr][SPL * lane + i] = __fmul_rn(dar[i], sr[buf][r][i]);
+        }
+        if (bt + NBUF < NB) load(buf, bt + NBUF);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < RG && n0 + lane < a.n) {
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int b = 0; b < KB; ++b) acc = __builtin_fmaf(dots[lane][b], sw[lane][b], acc);
+        a.y[n0 + lane] = acc;
+    }
+}
+
+template <int KS, int RG = 4>
+int go_gemv(const Q8bArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL((q8b_gemv_kernel<KS, RG>), dim3((unsigned)((a.n + RG - 1) / RG)), dim3(64), 0, st, a);
+    return launch_status();
+}
+
 template <int TI, int D>
 int go_small(const Q8bArgs &a, hipStream_t st) {
     hipLaunchKernelGGL((q8b_small_kernel<TI, D>), dim3((unsigned)((a.n + 15) / 16)), dim3(64), 0, st, a);
@@ -467,12 +557,21 @@ int gphq_q8b_gemm(const int8_t *qa_dev, const float *da_dev, const int8_t *qw_de
     hipStream_t st = (hipStream_t)stream;
     // Shapes measured on MI355X at K = 4096, N = 12288: from M = 256,
     // 128 x 192 tiles of eight wavefronts (one per CU at M = 512); from
-    // M = 33, 64 x 64 tiles with 256-byte K steps; up to 32 rows (k a
-    // multiple of 128), one wavefront per 16 weight rows with a ring of
-    // steps in flight.
+    // M = 33, 64 x 64 tiles with 256-byte K steps; one row at K = 2048, 4096,
+    // 8192 or 12288, whole weight rows streamed per wavefront; otherwise up
+    // to 32 rows (k a multiple of 128), one wavefront per 16 weight rows with
+    // a ring of steps in flight.
     if (m >= 256) return launch_q8b<128, 192, 4, 2, 4>(a, st);
     if (m > 32) return launch_q8b<64, 64, 2, 2, 8>(a, st);
     if (k % 128) return launch_q8b<64, 64, 2, 2, 4>(a, st);
+    if (m == 1) {
+        switch (k) {
+        case 2048: return go_gemv<2>(a, st);
+        case 4096: return go_gemv<4>(a, st);
+        case 8192: return go_gemv<8>(a, st);
+        case 12288: return go_gemv<12>(a, st);
+        }
+    }
     if (m > 16) return launch_small<2>(a, st);
     return launch_small<1>(a, st);
 }

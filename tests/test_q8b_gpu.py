@@ -44,7 +44,8 @@ def test_quantize_bit_exact_with_special_blocks():
 
 @pytest.mark.parametrize("m,k,n", [(1, 64, 96), (5, 4096, 200), (37, 160, 130), (128, 4096, 384), (300, 1024, 257),
                                    (1, 4096, 1001), (16, 2048, 301), (3, 8192, 77), (2, 1024, 3), (17, 1024, 64),
-                                   (32, 4096, 130), (24, 96, 50), (33, 4096, 96), (255, 512, 100), (256, 160, 97)])
+                                   (32, 4096, 130), (24, 96, 50), (33, 4096, 96), (255, 512, 100), (256, 160, 97),
+                                   (1, 2048, 37), (1, 8192, 100), (1, 12288, 45), (1, 4096, 3)])
 def test_gemm_bit_exact(m, k, n):
     import torch
 
