@@ -24,6 +24,30 @@ inline int hip_status(hipError_t e) {
 // Checks the launch that was just enqueued.
 inline int launch_status() { return hip_status(hipGetLastError()); }
 
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// A grid of rows256 x cols256 tiles of 256 x 256 outputs that is not a whole
+// number of rounds of the chip (one tile per CU): the number of 256-wide
+// column tiles, from the left, whose tiles fill whole rounds (0 when the
+// grid is whole rounds already or smaller than one).
+inline long whole_round_cols256(long rows256, long cols256) {
+    const long cus = device_cus(), big = rows256 * cols256;
+    if (big % cus == 0 || big < cus) return 0;
+    const long full = (big / cus) * cus / rows256;
+    return full < cols256 ? full : 0;
+}
+
 // n floats of dst set to v by a fill kernel (util.hip); never hipMemsetAsync,
 // so the fill may be captured in a HIP graph.
 int fill_f32(float *dst, size_t n, float v, hipStream_t stream);

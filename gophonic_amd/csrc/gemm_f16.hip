@@ -707,8 +707,25 @@ static int launch_by_m(F16GemmArgs a, hipStream_t stream) {
         const long width = a.c1 - a.tileN0 * 16;
         // 256 x 256 block tiles when they fill the chip, loads two K steps
         // ahead (4096-row pass 78.0 -> 77.5 ms against one step; no spills).
+        // A grid that is not whole rounds of the chip takes 256 x 256 tiles on
+        // the columns that fill whole rounds and 256 x 128 tiles on the rest
+        // (Qwen3-8B QKV at 4096 rows: 384 tiles as 256 + 256 half tiles,
+        // 288.2 -> 159.9 + 99.1 us in a kernel trace; smaller tiles for the O
+        // projection's single round measured slower: 205 -> 238-246 us with
+        // its activation pack).
         const long big = (long)((a.M + 255) / 256) * ((width + 255) / 256);
-        if (a.M >= 512 && big >= 256) return launch_f16gemm_big<WF, EPI, 256, 256, 4, 2, 2>(a, stream);
+        if (a.M >= 512 && big >= 256) {
+            const long full = whole_round_cols256((a.M + 255) / 256, (width + 255) / 256);
+            if (full == 0) return launch_f16gemm_big<WF, EPI, 256, 256, 4, 2, 2>(a, stream);
+            F16GemmArgs b = a;
+            b.c1 = (int)std::min<long>(a.c1, (long)a.tileN0 * 16 + full * 256);
+            GPHQ_TRY((launch_f16gemm_big<WF, EPI, 256, 256, 4, 2, 2>(b, stream)));
+            F16GemmArgs c = a;
+            c.c0 = b.c1;
+            c.tileN0 = c.c0 / 16;
+            c.splits = 1;
+            return launch_f16gemm_big<WF, EPI, 256, 128, 4, 2, 1>(c, stream);
+        }
         // 128 x 128 tiles, with K split over extra blocks when the caller gave
         // scratch for the partial sums (store epilogues only).
         const long mid = (long)((a.M + 127) / 128) * ((width + 127) / 128);

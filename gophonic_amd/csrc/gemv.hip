@@ -694,8 +694,6 @@ __global__ __launch_bounds__(64 * WPB) void gemv_gptq_kernel(const uint32_t *__r
     }
 }
 
-static int device_cus();
-
 template <int NS, int RW, int SK, int WPB>
 static int go_gptq(const uint32_t *codes, const uint16_t *scales, const uint8_t *zeros, const float *x, float *y,
                    int K, int N, int bpc, hipStream_t stream) {
@@ -801,19 +799,6 @@ static bool persistent_shape(int K, int N, bool batch, PersistentShape &p) {
     case 6: case 8: case 12: case 16: p = {2, 2, K / 2048, K / 1024, 2}; return true;
     }
     return false;
-}
-
-// Compute units of the current device (cached per device).
-static int device_cus() {
-    static int cached[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (!cached[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
 }
 
 template <int FMT, int NS, int RW, int SK, int WPB, int PRO, int EPI, int MAXB>
