@@ -24,6 +24,16 @@ inline int hip_status(hipError_t e) {
 // Checks the launch that was just enqueued.
 inline int launch_status() { return hip_status(hipGetLastError()); }
 
+// A K-split multi-vector GEMV whose residual add is left to the next
+// activation preparation: its parts [parts][V][N], its vectors' scales and,
+// for Q8, its row scales. parts == 0: nothing pending.
+struct VecFold {
+    const float *part = nullptr;
+    const float *inv = nullptr;
+    const float *rowScale = nullptr;
+    int parts = 0;
+};
+
 // Compute units of the current device (cached per device).
 inline int device_cus() {
     static int cached[64];

@@ -320,7 +320,7 @@ constexpr int kVechCH = 8;         // tiles whose slice sums are reduced togethe
 constexpr int kPrepUnits = 8;
 __global__ __launch_bounds__(1024) void vech_prep_kernel(const float *__restrict__ x, long stride, int V, int K,
                                                          _Float16 *__restrict__ A, float *__restrict__ inv,
-                                                         float *__restrict__ ssq) {
+                                                         float *__restrict__ ssq, const VecFold f) {
     typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
     __shared__ float red[2][16];
     const int v = blockIdx.x;  // 16 blocks; rows v >= V are written as zero
@@ -332,6 +332,30 @@ __global__ __launch_bounds__(1024) void vech_prep_kernel(const float *__restrict
     for (int j = 0; j < kPrepUnits; ++j) {
         const int u = threadIdx.x + j * 1024;
         q[j] = (live && u < U) ? *(const float4 *)(xv + 4 * u) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    if (f.parts) {
+        // The pending residual add of a K-split GEMV: x += (sum of its parts
+        // in order) * its vector scale (* the Q8 row scale), in
+        // vech_finish_kernel's order, written back to x.
+        const float pinv = live ? f.inv[v] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < kPrepUnits; ++j) {
+            const int u = threadIdx.x + j * 1024;
+            if (!live || u >= U) continue;
+            float4 sum = float4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int pp = 0; pp < f.parts; ++pp) {
+                const float4 t = *(const float4 *)(f.part + ((size_t)pp * V + v) * K + 4 * u);
+                sum.x += t.x, sum.y += t.y, sum.z += t.z, sum.w += t.w;
+            }
+            float4 val{__fmul_rn(sum.x, pinv), __fmul_rn(sum.y, pinv), __fmul_rn(sum.z, pinv), __fmul_rn(sum.w, pinv)};
+            if (f.rowScale) {
+                const float4 rs = *(const float4 *)(f.rowScale + 4 * u);
+                val = float4{__fmul_rn(val.x, rs.x), __fmul_rn(val.y, rs.y), __fmul_rn(val.z, rs.z), __fmul_rn(val.w, rs.w)};
+            }
+            q[j] = float4{__fadd_rn(q[j].x, val.x), __fadd_rn(q[j].y, val.y), __fadd_rn(q[j].z, val.z),
+                          __fadd_rn(q[j].w, val.w)};
+            *(float4 *)(const_cast<float *>(xv) + 4 * u) = q[j];
+        }
     }
     float mx = 0.0f, ss = 0.0f;
 #pragma unroll
@@ -540,16 +564,17 @@ __global__ __launch_bounds__(256) void vech_finish_kernel(const Vec2Args a, int 
     auto row_value = [&](int col) {
         float sum = 0.0f;
         for (int p = 0; p < parts; ++p) sum += a.part[((size_t)p * a.V + v) * a.N + col];
-        float val = sum * a.inv[v];
-        if constexpr (NORM) val *= 1.0f / sqrtf(a.ssq[v] / (float)a.K + a.eps);
-        if constexpr (FMT == GPHQ_FMT_Q8) val *= ((const float *)a.scales)[col];
+        float val = __fmul_rn(sum, a.inv[v]);
+        if constexpr (NORM) val = __fmul_rn(val, 1.0f / sqrtf(a.ssq[v] / (float)a.K + a.eps));
+        if constexpr (FMT == GPHQ_FMT_Q8) val = __fmul_rn(val, ((const float *)a.scales)[col]);
         return val;
     };
     if constexpr (EPI == VEC_SWIGLU) {
         const float gate = row_value(2 * r), up = row_value(2 * r + 1);
         a.y[(size_t)v * a.ystride + r] = gate / (1.0f + expf(-gate)) * up;
     } else if constexpr (EPI == VEC_ADD) {
-        a.y[(size_t)v * a.ystride + r] += row_value(r);
+        float *yp = a.y + (size_t)v * a.ystride + r;
+        *yp = __fadd_rn(*yp, row_value(r));  // the same rounding as a folded add (vech_prep_kernel)
     } else {
         a.y[(size_t)v * a.ystride + r] = row_value(r);
     }
@@ -602,7 +627,7 @@ static int go_vech(const Vec2Args &a, hipStream_t stream) {
 // K-split stationary path: blocks of kVechMaxSlices slices, one grid row per
 // K part (about 8 wavefronts per CU in all), then the ordered finish.
 template <int FMT, int EPI, bool NORM>
-static int go_vech_split(const Vec2Args &a, int parts, hipStream_t stream) {
+static int go_vech_split(const Vec2Args &a, int parts, hipStream_t stream, bool finish) {
     constexpr int SK = kVechMaxSlices;
     const int tiles = (a.N + 15) / 16;
     const int blocks = std::max(1, std::min(tiles, vech_cus() / parts));
@@ -610,6 +635,7 @@ static int go_vech_split(const Vec2Args &a, int parts, hipStream_t stream) {
     hipLaunchKernelGGL((vech_kernel<FMT, SK, VEC_STORE, false, true>), dim3((unsigned)blocks, (unsigned)parts),
                        dim3(64 * SK), 0, stream, a, iters);
     GPHQ_TRY(launch_status());
+    if (!finish) return GPHQ_OK;  // the next preparation adds the parts (VecFold)
     const int per = EPI == VEC_SWIGLU ? a.N / 2 : a.N;
     hipLaunchKernelGGL((vech_finish_kernel<FMT, EPI, NORM>), dim3((unsigned)((a.V * per + 255) / 256)), dim3(256), 0,
                        stream, a, parts);
@@ -617,11 +643,11 @@ static int go_vech_split(const Vec2Args &a, int parts, hipStream_t stream) {
 }
 
 template <int EPI, bool NORM>
-static int launch_vech_split(int fmt, const Vec2Args &a, int parts, hipStream_t stream) {
+static int launch_vech_split(int fmt, const Vec2Args &a, int parts, hipStream_t stream, bool finish = true) {
     switch (fmt) {
-    case GPHQ_FMT_Q8: return go_vech_split<GPHQ_FMT_Q8, EPI, NORM>(a, parts, stream);
-    case GPHQ_FMT_Q8B: return go_vech_split<GPHQ_FMT_Q8B, EPI, NORM>(a, parts, stream);
-    case GPHQ_FMT_Q8B_F32: return go_vech_split<GPHQ_FMT_Q8B_F32, EPI, NORM>(a, parts, stream);
+    case GPHQ_FMT_Q8: return go_vech_split<GPHQ_FMT_Q8, EPI, NORM>(a, parts, stream, finish);
+    case GPHQ_FMT_Q8B: return go_vech_split<GPHQ_FMT_Q8B, EPI, NORM>(a, parts, stream, finish);
+    case GPHQ_FMT_Q8B_F32: return go_vech_split<GPHQ_FMT_Q8B_F32, EPI, NORM>(a, parts, stream, finish);
     }
     return GPHQ_ERR_UNSUPPORTED;
 }
@@ -698,20 +724,38 @@ static int launch_vec2_fmt(int fmt, const Vec2Args &a, hipStream_t stream) {
 // norm (0/1) selects PRO_NORM, epi is VEC_STORE, VEC_ADD or VEC_SWIGLU (y then
 // holds N/2 values per vector). V <= kMaxVecLanes, K % 32 == 0, x rows 16-byte
 // aligned; work holds gemv_vec_workspace_bytes(V, K). Validated by the caller.
+// Whether a preparation for (fmt, V, K) goes through vech_prep_kernel, so a
+// pending K-split residual add (VecFold) can be handed to it.
+bool gemv_vec_prep_folds(int fmt, int V, int K) {
+    return vech_split_parts(fmt, V, K) != 0 || vech_takes(fmt, V, K);
+}
+
+// fold: a K-split GEMV's residual add into x left pending by an earlier call
+// (applied by this call's preparation, before it reads x); defer: when this
+// call is a K-split residual add without a norm, its finish is left to the
+// caller's next preparation and described in *defer (parts 0 otherwise).
 int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const void *scales, const float *x,
                           long xstride, float *y, long ystride, int V, int K, int N, float eps, void *work,
-                          hipStream_t stream, float *split, size_t split_bytes) {
-    if (N == 0 || V == 0) return GPHQ_OK;
+                          hipStream_t stream, float *split, size_t split_bytes, const VecFold &fold, VecFold *defer) {
+    if (defer) *defer = VecFold{};
+    if (N == 0 || V == 0) return fold.parts ? GPHQ_ERR_UNSUPPORTED : GPHQ_OK;
     const int KB = K / 32;
     const int parts = vech_split_parts(fmt, V, K);
+    if (fold.parts && !gemv_vec_prep_folds(fmt, V, K)) return GPHQ_ERR_UNSUPPORTED;
     if (parts && split && split_bytes >= (size_t)parts * V * N * 4 && (epi != VEC_SWIGLU || N % 2 == 0)) {
         _Float16 *A = (_Float16 *)work;
         float *inv = (float *)((char *)work + (size_t)2 * KB * 1024);
         float *ssq = inv + V;
-        hipLaunchKernelGGL(vech_prep_kernel, dim3(16), dim3(1024), 0, stream, x, xstride, V, K, A, inv, ssq);
+        hipLaunchKernelGGL(vech_prep_kernel, dim3(16), dim3(1024), 0, stream, x, xstride, V, K, A, inv, ssq, fold);
         GPHQ_TRY(launch_status());
         Vec2Args a{codes, scales, A, inv, ssq, y, ystride, V, K, N, KB, eps};
         a.part = split;
+        if (epi == VEC_ADD && !norm && defer) {
+            const int rc = launch_vech_split<VEC_ADD, false>(fmt, a, parts, stream, false);
+            if (rc != GPHQ_OK) return rc;
+            *defer = VecFold{split, inv, fmt == GPHQ_FMT_Q8 ? (const float *)scales : nullptr, parts};
+            return GPHQ_OK;
+        }
         if (epi == VEC_ADD) return norm ? launch_vech_split<VEC_ADD, true>(fmt, a, parts, stream)
                                         : launch_vech_split<VEC_ADD, false>(fmt, a, parts, stream);
         if (epi == VEC_SWIGLU) return norm ? launch_vech_split<VEC_SWIGLU, true>(fmt, a, parts, stream)
@@ -723,7 +767,7 @@ int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const v
         _Float16 *A = (_Float16 *)work;
         float *inv = (float *)((char *)work + (size_t)2 * KB * 1024);
         float *ssq = inv + V;
-        hipLaunchKernelGGL(vech_prep_kernel, dim3(16), dim3(1024), 0, stream, x, xstride, V, K, A, inv, ssq);
+        hipLaunchKernelGGL(vech_prep_kernel, dim3(16), dim3(1024), 0, stream, x, xstride, V, K, A, inv, ssq, fold);
         GPHQ_TRY(launch_status());
         const Vec2Args a{codes, scales, A, inv, ssq, y, ystride, V, K, N, KB, eps};
         if (epi == VEC_ADD) return norm ? launch_vech<VEC_ADD, true>(fmt, a, stream)
@@ -755,7 +799,7 @@ int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const v
 int gemv_vec_launch(int fmt, const void *codes, const void *scales, const float *x, long xstride, float *y,
                     long ystride, int V, int K, int N, void *work, hipStream_t stream) {
     return gemv_vec_fused_launch(fmt, 0, VEC_STORE, codes, scales, x, xstride, y, ystride, V, K, N, 0.0f, work,
-                                 stream, nullptr, 0);
+                                 stream, nullptr, 0, VecFold{}, nullptr);
 }
 
 }  // namespace gphq

@@ -41,7 +41,8 @@ int gemv_fused_launch(int fmt, int pro, int epi, const void *codes, const void *
                       int K, int N, float eps, hipStream_t stream);
 int gemv_vec_fused_launch(int fmt, int norm, int epi, const void *codes, const void *scales, const float *x,
                           long xstride, float *y, long ystride, int V, int K, int N, float eps, void *work,
-                          hipStream_t stream, float *split, size_t split_bytes);
+                          hipStream_t stream, float *split, size_t split_bytes, const VecFold &fold, VecFold *defer);
+bool gemv_vec_prep_folds(int fmt, int V, int K);
 size_t gemv_vec_split_bytes(int V, int K, int N);
 size_t gemv_vec_workspace_bytes(int V, int K);
 }  // namespace gphq
@@ -716,18 +717,25 @@ int attention_splits(const gphq_lm *lm, int lanes) {
     return (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplits, 256 / work));
 }
 
-// One projection GEMV of the step, single- or multi-lane.
+// One projection GEMV of the step, single- or multi-lane. Multi-lane only:
+// fold is a residual add left pending by the previous call (added to x by
+// this call's preparation), and a K-split residual add given defer leaves
+// its own finish to the next call (*defer).
 int gemv(gphq_decode_batch *ws, int lanes, int fmt, int pro, int epi, const uint8_t *buf, int64_t codes,
-         int64_t scales, const float *x, int64_t xs, float *y, int64_t ys, int64_t K, int64_t N, hipStream_t st) {
+         int64_t scales, const float *x, int64_t xs, float *y, int64_t ys, int64_t K, int64_t N, hipStream_t st,
+         const VecFold &fold = VecFold{}, VecFold *defer = nullptr) {
     const float eps = (float)ws->lm->cfg.eps;
+    if (defer) *defer = VecFold{};
     if (lanes < ws->vec_min_lanes) {
+        if (fold.parts) return GPHQ_ERR_UNSUPPORTED;
         for (int l = 0; l < lanes; ++l)
             GPHQ_TRY(gemv_fused_launch(fmt, pro, epi, buf + codes, buf + scales, x + (size_t)l * xs,
                                        y + (size_t)l * ys, (int)K, (int)N, eps, st));
         return GPHQ_OK;
     }
     return gemv_vec_fused_launch(fmt, pro == PRO_NORM, epi, buf + codes, buf + scales, x, (long)xs, y, (long)ys, lanes,
-                                 (int)K, (int)N, eps, ws->vec_work, st, ws->vec_split, ws->vec_split_bytes);
+                                 (int)K, (int)N, eps, ws->vec_work, st, ws->vec_split, ws->vec_split_bytes, fold,
+                                 defer);
 }
 
 // Enqueues one decode step for `lanes` lanes whose tokens and positions are
@@ -760,11 +768,19 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, const
     aa.kvh = (int)c.kv_heads;
     aa.splits = attention_splits(lm, lanes);
     aa.sin_off = (int)(lm->positions * 64);
+    // Multi-lane steps leave the K-split down projection's residual add to the
+    // next layer's QKV preparation (one launch fewer per layer). Its partial
+    // sums and scales stay in the workspace: the QKV preparation's own
+    // fragments and scales (hidden-wide) end before the down projection's
+    // scales (intermediate-wide) start.
+    const bool fold_down = lanes >= ws->vec_min_lanes && H < I && gemv_vec_prep_folds(fmt, lanes, (int)H);
+    VecFold pending{};
     for (int layer = 0; layer < c.layers; ++layer) {
         const gphq_lm_layer &L = lm->layers[layer];
         const uint8_t *buf = (const uint8_t *)L.buf_dev;
         GPHQ_TRY(gemv(ws, lanes, fmt, PRO_NORM, EPI_STORE, buf, L.qkv, L.qkv_scale, ws->h, H, ws->qkv, qkvw, H, qkvw,
-                      st));
+                      st, pending));
+        pending = VecFold{};
         for (int l = 0; l < lanes; ++l) {
             const size_t off = (size_t)layer * kvs[l]->capacity * lm->kvd;
             aa.kc[l] = kvs[l]->kc + off;
@@ -787,7 +803,9 @@ int encode_step(gphq_decode_batch *ws, gphq_prefix *const *kvs, int lanes, const
                                lm->iblock * sizeof(float), st, ws->act, (int)I, lm->isigns, (int)lm->iblock);
             GPHQ_TRY(launch_status());
         }
-        GPHQ_TRY(gemv(ws, lanes, fmt, PRO_PLAIN, EPI_ADD, buf, L.d, L.d_scale, ws->act, I, ws->h, H, I, H, st));
+        const bool defer = fold_down && layer + 1 < c.layers;
+        GPHQ_TRY(gemv(ws, lanes, fmt, PRO_PLAIN, EPI_ADD, buf, L.d, L.d_scale, ws->act, I, ws->h, H, I, H, st,
+                      VecFold{}, defer ? &pending : nullptr));
     }
     if (!head) return GPHQ_OK;
     hipLaunchKernelGGL(lm_final_kernel, dim3(lanes), dim3(1024), H * sizeof(float), st, ws->h, (int)H, lm->hsigns,

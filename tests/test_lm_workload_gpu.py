@@ -247,6 +247,44 @@ def test_decode_at_context_4096_one_layer_8b(lanes):
         toks = seq[s].tolist()
 
 
+@pytest.mark.parametrize("fmt", [lo.FMT_Q8B, lo.FMT_Q8])
+def test_multi_lane_down_projection_folded_into_next_layer(fmt):
+    # Two Qwen3-8B-width layers at 3 lanes: the multi-vector step leaves layer
+    # 0's K-split down projection (K = 12288) to layer 1's QKV preparation,
+    # which adds its parts (and, for Q8, its row scales) into the residual.
+    # Hidden states and logits against the float64 oracle within 1e-5, for
+    # contexts built by teacher-forced steps.
+    import torch
+
+    lm, _, st = gphq.lm_random(dict(QWEN3_8B, layers=2), fmt, seed=83, host=True)
+    g = lo.Geometry(hidden=4096, layers=2, heads=32, kv_heads=8, head_dim=128, inter=12288, vocab=VOCAB, max_pos=8192)
+    layers = [lo.Layer(qkv=L["qkv"], o=L["o"], gu=L["gu"], down=L["down"], q_norm=L["q_norm"], k_norm=L["k_norm"])
+              for L in st["layers"]]
+    orc = lo.DecodeOracle(g, fmt, layers, st["embed"], st["final_norm"], st["head"])
+    lanes, ctx = 3, 5
+    rng = np.random.default_rng(7 + fmt)
+    forced = rng.integers(0, g.vocab, (ctx, lanes))
+    kvs = [gphq.Prefix(lm, ctx + 4) for _ in range(lanes)]
+    ws = gphq.DecodeBatch(lm, lanes)
+    ws.extend(kvs, [0] * lanes, forced)
+    caches = [orc.new_cache(ctx + 4) for _ in range(lanes)]
+    for i in range(lanes):
+        for p in range(ctx):
+            orc.layers(caches[i], p, orc.embed_row(int(forced[p, i])))
+    tokens = rng.integers(0, g.vocab, lanes)
+    hidden = torch.empty((lanes, g.hidden), device="cuda")
+    logits = torch.empty((lanes, g.vocab), device="cuda")
+    print(f"fold test fmt={fmt}", flush=True)
+    ws.into(kvs, [ctx] * lanes, tokens, hidden, logits)
+    ws.check()
+    hs = np.stack([orc.layers(caches[i], ctx, orc.embed_row(int(tokens[i]))) for i in range(lanes)])
+    want_h, want_l = orc.finish_rows(hs)
+    got_h, got_l = hidden.cpu().numpy(), logits.cpu().numpy()
+    for i in range(lanes):
+        rh, rl = rel_l2(want_h[i], got_h[i]), rel_l2(want_l[i], got_l[i])
+        assert rh <= REL and rl <= REL, (i, rh, rl)
+
+
 # ---- full depth: property checks ---------------------------------------------
 
 _FULL = {}
