@@ -178,6 +178,51 @@ __device__ __forceinline__ void rot_signs(float4 (&sg)[4], const float *__restri
     for (int q = 0; q < 4; ++q) sg[q] = *(const float4 *)(signs + kk + 4 * q);
 }
 
+// The two radix-16 rounds of a 4096-value block (stages h = 16 .. 2048) over
+// 256 threads, on the rot_pad layout, with each thread's addresses in closed
+// form: in the round from h = 16, thread t owns values 256 (t >> 4) + (t & 15)
+// + 16 j, which sit at words A + 64 (j >> 2) + 16 (j & 3) + 4 ((q + (j >> 2))
+// & 3) (A = 272 (t >> 4) + (t & 3), q = (t >> 2) & 3); in the round from
+// h = 256 it owns t + 256 j, at rot_pad(t) + 272 j. The same words, items and
+// butterflies as two fwht_round<16, true, 256> calls (s = 4, 8), so the same
+// bits; the generic rounds recompute rot_pad for every access.
+__device__ __forceinline__ void fwht4096_rounds_pad(float *v) {
+    const int t = (int)threadIdx.x;
+    float a[16];
+    auto butterflies = [&]() {
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1)
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (!(j & m)) {
+                    const float x = a[j], y = a[j + m];
+                    a[j] = x + y;
+                    a[j + m] = x - y;
+                }
+    };
+    {
+        const int A = 272 * (t >> 4) + (t & 3), q = (t >> 2) & 3;
+        int base[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) base[m] = A + 64 * m + (((q + m) & 3) << 2);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) a[j] = v[base[j >> 2] + 16 * (j & 3)];
+        butterflies();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[base[j >> 2] + 16 * (j & 3)] = a[j];
+        __syncthreads();
+    }
+    {
+        const int b = rot_pad(t);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) a[j] = v[b + 272 * j];
+        butterflies();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[b + 272 * j] = a[j];
+        __syncthreads();
+    }
+}
+
 template <int CPT>
 __device__ __forceinline__ void rotate_row_lds(float4 (&v)[CPT][4], float4 (&sg)[4], int K,
                                                const float *__restrict__ signs, int block) {
@@ -219,6 +264,10 @@ __device__ __forceinline__ void rotate_row_lds(float4 (&v)[CPT][4], float4 (&sg)
         }
         __syncthreads();
         int s = 4;
+        if (n == 4096 && lb == 12) {  // whole 4096-value blocks: both rounds with closed-form addresses
+            fwht4096_rounds_pad(rot_lds);
+            s = 12;
+        }
         for (; s + 4 <= lb; s += 4) fwht_round<16, true, 256>(rot_lds, n, s);
         if (lb - s == 3) fwht_round<8, true, 256>(rot_lds, n, s);
         if (lb - s == 2) fwht_round<4, true, 256>(rot_lds, n, s);
