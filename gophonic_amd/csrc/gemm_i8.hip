@@ -196,13 +196,14 @@ __global__ __launch_bounds__(256) void i8_act_rows_kernel(const float *__restric
     for (int c = 0; c < CPT; ++c) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            ss += v[c][q].x * v[c][q].x + v[c][q].y * v[c][q].y + v[c][q].z * v[c][q].z + v[c][q].w * v[c][q].w;
+            if constexpr (MODE == 2)
+                ss += v[c][q].x * v[c][q].x + v[c][q].y * v[c][q].y + v[c][q].z * v[c][q].z + v[c][q].w * v[c][q].w;
             mx = fmaxf(fmaxf(fmaxf(mx, fabsf(v[c][q].x)), fmaxf(fabsf(v[c][q].y), fabsf(v[c][q].z))), fabsf(v[c][q].w));
             nan |= (v[c][q].x != v[c][q].x) | (v[c][q].y != v[c][q].y) | (v[c][q].z != v[c][q].z) |
                    (v[c][q].w != v[c][q].w);
         }
     }
-    ss = wave_sum(ss);
+    if constexpr (MODE == 2) ss = wave_sum(ss);
     for (int off = 32; off > 0; off >>= 1) {
         mx = fmaxf(mx, __shfl_xor(mx, off));
         nan |= __shfl_xor(nan, off);
@@ -220,6 +221,11 @@ __global__ __launch_bounds__(256) void i8_act_rows_kernel(const float *__restric
     float scale, inv;
     i8_row_scale(m, scale, inv);
     if (threadIdx.x == 0) rowScale[row] = scale;
+    // A row with a finite, nonzero 127/max has only finite products, so
+    // quantize_i8's NaN test can go: rint, clamp (v_med3) and convert, the
+    // four bytes packed by v_perm. Other rows (NaN, infinite, zero or
+    // denormal-range maxima) take quantize_i8 itself. The same bytes either way.
+    const bool plain = inv > 0.0f && inv < INFINITY;  // the same for the whole block
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
         const int k = 16 * ((int)threadIdx.x + 256 * c);
@@ -228,13 +234,24 @@ __global__ __launch_bounds__(256) void i8_act_rows_kernel(const float *__restric
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float e[4] = {v[c][q].x, v[c][q].y, v[c][q].z, v[c][q].w};
-            uint32_t packed = 0;
+            if (plain) {
+                int b[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float y = MODE == 2 ? __fmul_rn(e[i], f) : e[i];
-                packed |= (uint32_t)(uint8_t)quantize_i8(__fmul_rn(y, inv)) << (8 * i);
+                for (int i = 0; i < 4; ++i) {
+                    const float y = MODE == 2 ? __fmul_rn(e[i], f) : e[i];
+                    b[i] = (int)__builtin_amdgcn_fmed3f(rintf(__fmul_rn(y, inv)), -128.0f, 127.0f);
+                }
+                w[q] = __builtin_amdgcn_perm((uint32_t)b[1], (uint32_t)b[0], 0x0c0c0400u) |
+                       __builtin_amdgcn_perm((uint32_t)b[3], (uint32_t)b[2], 0x04000c0cu);
+            } else {
+                uint32_t packed = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float y = MODE == 2 ? __fmul_rn(e[i], f) : e[i];
+                    packed |= (uint32_t)(uint8_t)quantize_i8(__fmul_rn(y, inv)) << (8 * i);
+                }
+                w[q] = packed;
             }
-            w[q] = packed;
         }
         *(uint4 *)(act + rowtile_offset(row, k, K >> 6)) = make_uint4(w[0], w[1], w[2], w[3]);
     }

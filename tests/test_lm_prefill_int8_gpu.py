@@ -102,6 +102,9 @@ def test_project_int8_residual_add_bit_exact(geom, proj, rows):
     if rows > 2:
         x[1] = 0.0  # no finite positive maximum: scale 0
         x[2, 5] = np.nan  # SetRowScale(NaN): the row quantizes to zero
+    if rows > 4:
+        x[3, 7] = np.inf  # an infinite maximum: scale 0
+        x[4] *= np.float32(1e-38)  # subnormal values: 127 / max overflows, products clamp
     y0 = rng.standard_normal((rows, n)).astype(np.float32)
     ws = gphq.Prefill(lm, max(rows, 16))
     ws.set_arith(gphq.PASS_INT8)
