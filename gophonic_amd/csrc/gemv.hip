@@ -714,13 +714,17 @@ int gemv_gptq_launch(const void *codes, const void *scales, const uint8_t *zeros
     if (K % 2048 || (uintptr_t)x % 16) return GPHQ_ERR_UNSUPPORTED;
     const uint32_t *c = (const uint32_t *)codes;
     const uint16_t *s = (const uint16_t *)scales;
-    // Launch shapes from a sweep on MI355X at the config-5 shapes.
+    // Launch shapes from sweeps on MI355X at the config-5 shapes (K = 4096 ->
+    // N = 12288: 9.8 -> 9.0 us with 4-wavefront blocks; K = 12288 -> N = 4096:
+    // 10.8 -> 9.5 us with 8 rows per wavefront group, one group per block).
+    // Issuing the next row group's loads before the current one is reduced
+    // measured slower at both.
     switch (K / 2048) {
     case 1: return go_gptq<1, 4, 1, 4>(c, s, zeros, x, y, K, N, 2, stream);
-    case 2: return go_gptq<1, 4, 2, 8>(c, s, zeros, x, y, K, N, 2, stream);
+    case 2: return go_gptq<1, 4, 2, 4>(c, s, zeros, x, y, K, N, 2, stream);
     case 3: return go_gptq<1, 2, 3, 6>(c, s, zeros, x, y, K, N, 2, stream);
     case 4: return go_gptq<1, 2, 4, 8>(c, s, zeros, x, y, K, N, 1, stream);
-    case 6: return go_gptq<1, 2, 6, 12>(c, s, zeros, x, y, K, N, 1, stream);
+    case 6: return go_gptq<1, 8, 6, 6>(c, s, zeros, x, y, K, N, 1, stream);
     case 8: return go_gptq<1, 2, 8, 16>(c, s, zeros, x, y, K, N, 1, stream);
     }
     return GPHQ_ERR_UNSUPPORTED;

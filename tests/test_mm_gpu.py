@@ -108,6 +108,26 @@ def test_gptq_256_row_tiles_with_two_splits():
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
 
 
+@pytest.mark.parametrize("k,n", [(2048, 37), (4096, 101), (6144, 9), (8192, 45), (12288, 77), (16384, 13),
+                                 (4096, 1), (12288, 8)])
+def test_gptq_one_row_every_k_step(k, n):
+    # gphq_mm at m = 1 takes the GEMV for K a multiple of 2048 up to 16384, one
+    # launch shape per K; row counts that do not fill the last row group must
+    # not be written past N (the output is NaN-filled) and equal the float64
+    # value with un-rounded weights within 1e-4 relative.
+    rng = np.random.default_rng(k + n)
+    codes, scales, zeros = weights(orc.FMT_GPTQ4_G128, rng, n, k)
+    x = rng.standard_normal(k).astype(np.float16).astype(np.float32)
+    got = run_mm(orc.FMT_GPTQ4_G128, codes, scales, x, 1, k, n, zeros)
+    q = ((codes.reshape(n, k // 8)[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15).reshape(n, k)
+    z = np.repeat(zeros.reshape(n, k // 128).astype(np.float64), 128, axis=1)
+    s = np.repeat(scales.reshape(n, k // 128).view(np.float16).astype(np.float64), 128, axis=1)
+    ref = ((q.astype(np.float64) - z) * s) @ x.astype(np.float64)
+    assert np.isfinite(got).all()
+    rel = np.sqrt(((got[0] - ref) ** 2).sum() / (ref ** 2).sum())
+    assert rel <= 1e-4
+
+
 @pytest.mark.parametrize("m,split", [(1, False), (256, False), (256, True)])
 @pytest.mark.parametrize("k,n", [(4096, 12288), (12288, 4096)])
 def test_gptq_g128_config5_within_2e3(m, split, k, n):
