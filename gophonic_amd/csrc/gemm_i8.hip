@@ -141,6 +141,78 @@ __global__ __launch_bounds__(256) void i8_pack_rows_kernel(const float *__restri
     }
 }
 
+// The same Pack for K a multiple of 16 and 16-byte aligned rows: the row is
+// read once, as 16-byte pieces, into registers (CPT chunks of 16 values per
+// thread, thread t holding columns 16 (t + 256 c) .. + 15, the chunks past K
+// zero), reduced for MaxAbs, and quantized from the registers. Rows with a
+// finite positive 127/max quantize without quantize_i8's NaN test (rint,
+// v_med3 clamp, v_perm byte packing); the others take quantize_i8 itself: the
+// same bytes either way.
+template <int CPT>
+__global__ __launch_bounds__(256) void i8_pack_rows_vec_kernel(const float *__restrict__ x, long stride, int K,
+                                                               int kt, int8_t *__restrict__ act,
+                                                               float *__restrict__ rowScale,
+                                                               float *__restrict__ rowInv) {
+    __shared__ float smx[4];
+    __shared__ int snan[4];
+    const int row = blockIdx.x;
+    float4 v[CPT][4];
+    load_row_chunks<CPT>(v, x + (size_t)row * stride, K);
+    zero_past_end<CPT>(v, K);
+    float mx = 0.0f;
+    int nan = 0;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            mx = fmaxf(fmaxf(fmaxf(mx, fabsf(v[c][q].x)), fmaxf(fabsf(v[c][q].y), fabsf(v[c][q].z))), fabsf(v[c][q].w));
+            nan |= (v[c][q].x != v[c][q].x) | (v[c][q].y != v[c][q].y) | (v[c][q].z != v[c][q].z) |
+                   (v[c][q].w != v[c][q].w);
+        }
+    for (int off = 32; off > 0; off >>= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+        nan |= __shfl_xor(nan, off);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        smx[threadIdx.x >> 6] = mx;
+        snan[threadIdx.x >> 6] = nan;
+    }
+    __syncthreads();
+    float m = fmaxf(fmaxf(smx[0], smx[1]), fmaxf(smx[2], smx[3]));
+    if (snan[0] | snan[1] | snan[2] | snan[3]) m = __builtin_nanf("");
+    float scale, inv;
+    i8_row_scale(m, scale, inv);
+    if (threadIdx.x == 0) {
+        rowScale[row] = scale;
+        rowInv[row] = inv;
+    }
+    const bool plain = inv > 0.0f && inv < INFINITY;  // the same for the whole block
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int kb = 16 * ((int)threadIdx.x + 256 * c);
+        if (kb >= kt * 64) continue;
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float e[4] = {v[c][q].x, v[c][q].y, v[c][q].z, v[c][q].w};
+            if (plain) {
+                int b[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    b[i] = (int)__builtin_amdgcn_fmed3f(rintf(__fmul_rn(e[i], inv)), -128.0f, 127.0f);
+                w[q] = __builtin_amdgcn_perm((uint32_t)b[1], (uint32_t)b[0], 0x0c0c0400u) |
+                       __builtin_amdgcn_perm((uint32_t)b[3], (uint32_t)b[2], 0x04000c0cu);
+            } else {
+                uint32_t packed = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) packed |= (uint32_t)(uint8_t)quantize_i8(__fmul_rn(e[i], inv)) << (8 * i);
+                w[q] = packed;
+            }
+        }
+        *(uint4 *)(act + tile_offset(row, kb, kt)) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 // PackRange (int8.go:116-163) with row scales already set: quantize columns
 // [k0, k1) of every prepared row; k1 == K also zeroes the K padding.
 __global__ __launch_bounds__(256) void i8_pack_range_kernel(const float *__restrict__ x, long stride, int K, int kt,
@@ -1275,6 +1347,22 @@ int i8_pack_tiles(const int8_t *src, int8_t *dst, int rows, int K, int row0, int
 int i8_pack_rows(const float *x, long stride, int rows, int K, int kt, int8_t *act, float *rowScale, float *rowInv,
                  hipStream_t stream) {
     if (rows == 0) return GPHQ_OK;
+    // Rows whose values can be read as 16-byte pieces are held in registers
+    // (one read of the row); other shapes take the two-pass kernel.
+    if (K % 16 == 0 && stride % 4 == 0 && (uintptr_t)x % 16 == 0 && kt <= 256) {
+        switch ((kt + 63) / 64) {
+#define GPHQ_PACK_VEC(C)                                                                                              \
+    case C:                                                                                                           \
+        hipLaunchKernelGGL(i8_pack_rows_vec_kernel<C>, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, act,       \
+                           rowScale, rowInv);                                                                         \
+        return launch_status();
+            GPHQ_PACK_VEC(1)
+            GPHQ_PACK_VEC(2)
+            GPHQ_PACK_VEC(3)
+            GPHQ_PACK_VEC(4)
+#undef GPHQ_PACK_VEC
+        }
+    }
     hipLaunchKernelGGL(i8_pack_rows_kernel, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, act, rowScale, rowInv);
     return launch_status();
 }

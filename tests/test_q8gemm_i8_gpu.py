@@ -246,6 +246,28 @@ def test_non_finite_rows_and_extremes():
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,k,stride", [(3, 16384, 16384), (4, 1024, 1028), (5, 992, 1000), (3, 1000, 1003),
+                                           (2, 16, 20)])
+def test_pack_row_stride_and_wide_rows(rows, k, stride):
+    # Pack with a row stride, from K = 16 to 16384 (rows held in registers
+    # where K is a multiple of 16 and rows are 16-byte aligned, the two-pass
+    # quantizer otherwise), an infinite value in one row: the same bytes and
+    # products as the oracle's quantizer.
+    n = 40
+    w, q, scales = int8_fixture(k, n, 4)
+    rng = np.random.default_rng(k + stride)
+    x = rng.standard_normal((rows - 1) * stride + k).astype(np.float32)
+    x[stride + 3] = np.inf
+    ws = gphq.WorkspaceI8(k, rows)
+    ws.pack(dev(x), rows, k, stride=stride)
+    got = fill(rows * n)
+    gphq.mul_panels_i8(got, n, ws, w, 0, w.panels())
+    xs = np.concatenate([x[r * stride:r * stride + k] for r in range(rows)])
+    want, rs, _ = oracle_out(xs, rows, k, q, scales, n)
+    assert rs[1] == 0
+    assert np.array_equal(host(got).view(np.uint32), want.view(np.uint32))
+
+
 def test_k_zero_clears_and_errors_match_reference():
     w = gphq.WeightsI8(0, 70)
     w.pack(np.zeros(0, np.int8), np.ones(70, np.float32))
