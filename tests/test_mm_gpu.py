@@ -106,6 +106,17 @@ def test_gptq_256_row_tiles_with_two_splits():
     assert np.all(np.abs(got - want) <= k * 2.0 ** -23 * absum + 1e-30)
     again = run_mm(fmt, codes, scales, x, m, k, n, zeros, split=True)
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    # Each split is the unsplit product over its half of K (one K loop in the
+    # same order), and the finish kernel's outputs are their fp32 sum, first
+    # half + second.
+    h = k // 2
+    c2, s2, z2 = codes.reshape(n, k // 8), scales.reshape(n, k // 128), zeros.reshape(n, k // 128)
+    x2 = x.reshape(m, k)
+    halves = [run_mm(fmt, np.ascontiguousarray(c2[:, i * h // 8:(i + 1) * h // 8]).ravel(),
+                     np.ascontiguousarray(s2[:, i * h // 128:(i + 1) * h // 128]).ravel(),
+                     np.ascontiguousarray(x2[:, i * h:(i + 1) * h]).ravel(), m, h, n,
+                     np.ascontiguousarray(z2[:, i * h // 128:(i + 1) * h // 128]).ravel()) for i in range(2)]
+    assert np.array_equal(got.view(np.uint32), (halves[0] + halves[1]).view(np.uint32))
 
 
 @pytest.mark.parametrize("k,n", [(2048, 37), (4096, 101), (6144, 9), (8192, 45), (12288, 77), (16384, 13),
