@@ -147,15 +147,19 @@ __global__ __launch_bounds__(256) void i8_pack_rows_kernel(const float *__restri
 // zero), reduced for MaxAbs, and quantized from the registers. Rows with a
 // finite positive 127/max quantize without quantize_i8's NaN test (rint,
 // v_med3 clamp, v_perm byte packing); the others take quantize_i8 itself: the
-// same bytes either way.
+// same bytes either way. The 8 rows whose 16-byte pieces share a 128-byte line
+// of the tile layout (rows 8q .. 8q + 7) go to blocks b, b + 8, .., b + 56,
+// which the dispatcher places on one XCD (round robin over 8), so each line is
+// completed in one L2.
 template <int CPT>
 __global__ __launch_bounds__(256) void i8_pack_rows_vec_kernel(const float *__restrict__ x, long stride, int K,
                                                                int kt, int8_t *__restrict__ act,
                                                                float *__restrict__ rowScale,
-                                                               float *__restrict__ rowInv) {
+                                                               float *__restrict__ rowInv, int rows) {
     __shared__ float smx[4];
     __shared__ int snan[4];
-    const int row = blockIdx.x;
+    const int bx = blockIdx.x, row = (bx & ~63) + 8 * (bx & 7) + ((bx >> 3) & 7);
+    if (row >= rows) return;
     float4 v[CPT][4];
     load_row_chunks<CPT>(v, x + (size_t)row * stride, K);
     zero_past_end<CPT>(v, K);
@@ -1353,8 +1357,8 @@ int i8_pack_rows(const float *x, long stride, int rows, int K, int kt, int8_t *a
         switch ((kt + 63) / 64) {
 #define GPHQ_PACK_VEC(C)                                                                                              \
     case C:                                                                                                           \
-        hipLaunchKernelGGL(i8_pack_rows_vec_kernel<C>, dim3(rows), dim3(256), 0, stream, x, stride, K, kt, act,       \
-                           rowScale, rowInv);                                                                         \
+        hipLaunchKernelGGL(i8_pack_rows_vec_kernel<C>, dim3((unsigned)((rows + 63) & ~63)), dim3(256), 0, stream, x,  \
+                           stride, K, kt, act, rowScale, rowInv, rows);                                               \
         return launch_status();
             GPHQ_PACK_VEC(1)
             GPHQ_PACK_VEC(2)
