@@ -850,30 +850,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void i8gemm_big_kernel(const I8Gemm
 // Measured on MI355X (config 2, M = 512): stores of 16 columns per row wrote
 // 1.32x the output's bytes to HBM (WRITE_SIZE); whole 128-byte lines write
 // them once.
-template <int TI, int TJ, int EPI>
-__device__ __forceinline__ void dma_epilogue(const I8GemmArgs &a, const i32x4 (&acc)[TI][TJ], int mt0, int nt0,
-                                             int lane) {
-    float rsc[TI][4], csc[TJ];
+// The stores of dma_epilogue with the column-tile pairs starting at tile P
+// of the wavefront (P = nt0 % 2, so that each pair's 32 columns are one
+// 128-byte line of every row): v_permlane16_swap exchanges lanes 16-31 of
+// tile j's values with lanes 0-15 of tile j + 1's (and 48-63 with 32-47), so
+// each store covers 32 consecutive columns of two rows (two whole 128-byte
+// lines) instead of 16 columns of four rows. After the swap, lane l holds
+// column (j + bit 4 of l) * 16 + l % 16; the first value is row 8 (l / 32) + e,
+// the second row 4 more. The tiles left out of the pairs (the first when P is
+// 1, an odd last one) are stored as they are, and their half lines meet the
+// neighbouring wavefront's in L2.
+template <int TI, int TJ, int EPI, int P>
+__device__ __forceinline__ void dma_epilogue_stores(const I8GemmArgs &a, const i32x4 (&acc)[TI][TJ], int mt0,
+                                                    int nt0, int lane, const float (&rsc)[TI][4],
+                                                    const float (&csc)[TJ]) {
+    constexpr int PE = EPI == I8_EPI_SWIGLU ? 0 : P + ((TJ - P) & ~1);  // pairs cover tiles [P, PE)
+    if constexpr (PE > P) {
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) rsc[i][e] = a.rowScale[min((mt0 + i) * 16 + 4 * (lane >> 4) + e, a.M - 1)];
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int col = (nt0 + j) * 16 + (lane & 15);
-        csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
-    }
-    // Store and add epilogues take column tiles j and j + 1 in pairs:
-    // v_permlane16_swap exchanges lanes 16-31 of tile j's values with lanes
-    // 0-15 of tile j + 1's (and 48-63 with 32-47), so each store covers 32
-    // consecutive columns of two rows (two whole 128-byte lines) instead of 16
-    // columns of four rows. After the swap, lane l holds column (j + bit 4 of
-    // l) * 16 + l % 16; the first value is row 8 (l / 32) + e, the second row
-    // 4 more. An odd last tile is stored as it is.
-    constexpr int TJP = EPI == I8_EPI_SWIGLU ? 0 : TJ & ~1;
-    if constexpr (TJP > 0) {
-#pragma unroll
-        for (int j = 0; j < TJP; j += 2) {
+        for (int j = P; j < PE; j += 2) {
             const int col = (nt0 + j + ((lane >> 4) & 1)) * 16 + (lane & 15);
             const bool colOk = col >= a.c0 && col < a.c1;
 #pragma unroll
@@ -899,7 +893,8 @@ __device__ __forceinline__ void dma_epilogue(const I8GemmArgs &a, const i32x4 (&
         }
     }
 #pragma unroll
-    for (int j = TJP; j < TJ; ++j) {
+    for (int j = 0; j < TJ; ++j) {
+        if (PE > P && j >= P && j < PE) continue;  // stored as a pair
         const int col = (nt0 + j) * 16 + (lane & 15);
         const bool colOk = col >= a.c0 && col < a.c1;
         if constexpr (EPI != I8_EPI_SWIGLU) {
@@ -924,6 +919,32 @@ __device__ __forceinline__ void dma_epilogue(const I8GemmArgs &a, const i32x4 (&
                 }
             }
     }
+}
+
+// Epilogue of the direct-to-LDS kernels, as in i8gemm_kernel: lane l of a
+// 16 x 16 tile holds rows 4 (l / 16) + e, column l % 16; scales first, then
+// the stores. mt0 / nt0: the wavefront's first row and column tile.
+// Measured on MI355X (config 2, M = 512): stores of 16 columns per row wrote
+// 1.32x the output's bytes to HBM (WRITE_SIZE); column-tile pairs from the
+// wavefront's first tile 1.19x (wavefronts of 48 columns starting at an odd
+// tile paired across lines); pairs that start on a line once.
+template <int TI, int TJ, int EPI>
+__device__ __forceinline__ void dma_epilogue(const I8GemmArgs &a, const i32x4 (&acc)[TI][TJ], int mt0, int nt0,
+                                             int lane) {
+    float rsc[TI][4], csc[TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rsc[i][e] = a.rowScale[min((mt0 + i) * 16 + 4 * (lane >> 4) + e, a.M - 1)];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int col = (nt0 + j) * 16 + (lane & 15);
+        csc[j] = a.colScale[col >= a.c0 && col < a.c1 ? col : a.c0];
+    }
+    if (EPI != I8_EPI_SWIGLU && TJ > 2 && (nt0 & 1))
+        dma_epilogue_stores<TI, TJ, EPI, 1>(a, acc, mt0, nt0, lane, rsc, csc);
+    else
+        dma_epilogue_stores<TI, TJ, EPI, 0>(a, acc, mt0, nt0, lane, rsc, csc);
 }
 
 // Direct-to-LDS variant: BM x BN block tiles (WGM x WGN wavefronts, each a
