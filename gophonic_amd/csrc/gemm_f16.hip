@@ -668,6 +668,34 @@ __global__ __launch_bounds__(256) void mm_finish_kernel(const F16GemmArgs a) {
     a.dst[(size_t)row * a.stride + a.c0 + c] = v;
 }
 
+// The same finish, four consecutive outputs of one row per thread (16-byte
+// loads and stores; the column range, the stride and the buffers 16-byte
+// aligned), the splits added in the same order.
+template <int EPI>
+__global__ __launch_bounds__(256) void mm_finish4_kernel(const F16GemmArgs a) {
+    const unsigned q = (unsigned)(a.c1 - a.c0) / 4u;  // quads per row
+    const unsigned idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= (unsigned)a.M * q) return;
+    const unsigned row = idx / q, c = 4u * (idx - row * q);
+    const size_t plane = (size_t)a.M * (a.c1 - a.c0);
+    float4 v = *(const float4 *)(a.part + 4 * (size_t)idx);
+    for (int s = 1; s < a.splits; ++s) {
+        const float4 p = *(const float4 *)(a.part + (size_t)s * plane + 4 * (size_t)idx);
+        v.x += p.x;
+        v.y += p.y;
+        v.z += p.z;
+        v.w += p.w;
+    }
+    if constexpr (EPI == EPI_ROWSCALE) {
+        const float4 cs = *(const float4 *)(a.colScale + a.c0 + c);
+        v.x = __fmul_rn(v.x, cs.x);
+        v.y = __fmul_rn(v.y, cs.y);
+        v.z = __fmul_rn(v.z, cs.z);
+        v.w = __fmul_rn(v.w, cs.w);
+    }
+    *(float4 *)(a.dst + (size_t)row * a.stride + a.c0 + c) = v;
+}
+
 template <int WF, int EPI, int BM, int BN, int WGM, int WGN, int PF>
 static int launch_f16gemm_big(F16GemmArgs a, hipStream_t stream) {
     a.gridN = (a.c1 - a.tileN0 * 16 + BN - 1) / BN;
@@ -678,7 +706,13 @@ static int launch_f16gemm_big(F16GemmArgs a, hipStream_t stream) {
     GPHQ_TRY(launch_status());
     if (a.splits == 1) return GPHQ_OK;
     const size_t outs = (size_t)a.M * (a.c1 - a.c0);
-    hipLaunchKernelGGL((mm_finish_kernel<EPI>), dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, stream, a);
+    const bool quads = (a.c1 - a.c0) % 4 == 0 && a.c0 % 4 == 0 && a.stride % 4 == 0 && (uintptr_t)a.dst % 16 == 0 &&
+                       (uintptr_t)a.part % 16 == 0 && outs / 4 < (size_t)UINT32_MAX - 256 &&
+                       (EPI != EPI_ROWSCALE || (uintptr_t)a.colScale % 16 == 0);
+    if (quads)
+        hipLaunchKernelGGL((mm_finish4_kernel<EPI>), dim3((unsigned)((outs / 4 + 255) / 256)), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((mm_finish_kernel<EPI>), dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, stream, a);
     return launch_status();
 }
 
